@@ -1,0 +1,182 @@
+/*
+ * polylora_hip.h — C ABI of the MI355X (gfx950) multi-LoRA SGMV library.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers, sizes and a
+ * hipStream_t (passed as `void*`), enqueues asynchronously on that stream and
+ * returns 0 on success or a nonzero PL_ERR_* code; `pl_last_error()` returns
+ * the message of the last failure on the calling thread.  No entry point
+ * allocates device memory: every buffer is owned by the caller.
+ *
+ * Reference interfaces replaced (Knowledgator/PolyLoRA, paths relative to the
+ * repository root):
+ *   pl_sgmv_lora_a_ref  <- src/polylora/sgmv.py:141-175  sgmv_lora_a_fwd
+ *   pl_sgmv_lora_b_ref  <- src/polylora/sgmv.py:278-328  sgmv_lora_b_fwd
+ *   pl_plan_build       <- src/polylora/sgmv.py:29-61    _build_flat_schedule
+ *                          (one device-side plan per forward instead of a
+ *                          host-synchronising schedule per layer)
+ *   pl_sgmv_shrink      <- src/polylora/sgmv.py:63-138   _sgmv_lora_a_kernel
+ *   pl_sgmv_expand      <- src/polylora/sgmv.py:178-275  _sgmv_lora_b_kernel
+ *   pl_lora_apply       <- src/polylora/layers.py:42-53  (shrink then expand,
+ *                          the LoRA half of MultiLoraLinear.forward)
+ *   pl_slot_upload      <- src/polylora/cache.py:119-150 _load_adapter_into_slot
+ *                          (host->device copy of one adapter into a slot)
+ *   pl_check_right_padded <- src/polylora/context.py:37-45 assert_right_padded
+ */
+#ifndef POLYLORA_HIP_H
+#define POLYLORA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of x, y and the adapter weights */
+enum pl_dtype { PL_F32 = 0, PL_BF16 = 1, PL_F16 = 2 };
+
+/* epilogue rounding order of the expand (scale and add-back) */
+enum pl_epilogue {
+  /* layers.py:127-128: d = T(acc); d = T(d * T(scale)); y = T(y + d) */
+  PL_EPI_FALLBACK = 0,
+  /* sgmv.py:268-275:   y = T(T(acc * scale) + y) */
+  PL_EPI_TRITON = 1
+};
+
+enum pl_status {
+  PL_OK = 0,
+  PL_ERR_ARG = 1,     /* invalid argument (null pointer, bad size, bad dtype) */
+  PL_ERR_ALIGN = 2,   /* shape or pointer alignment not supported by the tiled path */
+  PL_ERR_LAUNCH = 3,  /* kernel launch or HIP runtime failure */
+  PL_ERR_LIMIT = 4    /* a size exceeds a documented maximum */
+};
+
+/* One entry per (slot, module) of the slot table, 32 bytes.  The table is a
+ * device array laid out [num_slots][num_modules].  Slot 0 is the base
+ * adapter and always has rank 0.  `a_off` points (bytes from the arena base)
+ * at the adapter's A for this module, stored [rank][in_features] row-major;
+ * `b_off` points at B stored [out_features][rank8] row-major where
+ * rank8 = rank rounded up to a multiple of 8 and columns rank..rank8-1 are 0.
+ * Replaces the per-module A/B/ranks/scales tensors of cache.py:37-58. */
+typedef struct pl_slot_entry {
+  int32_t rank;
+  float scale;  /* lora_alpha / rank, fp32 (store.py:252) */
+  int32_t rank8;
+  int32_t reserved;
+  int64_t a_off;
+  int64_t b_off;
+} pl_slot_entry;
+
+/* One group of at most `group_tokens` tokens that all use the same slot.
+ * `start` indexes the sorted token list written by pl_plan_build. */
+typedef struct pl_group {
+  int32_t slot;
+  int32_t start;
+  int32_t len;
+  int32_t reserved;
+} pl_group;
+
+/* Maximum slot count accepted by pl_plan_build (slot 0 included). */
+#define PL_MAX_SLOTS 4096
+/* Token-group size used by the tiled kernels. */
+#define PL_GROUP_TOKENS 64
+
+/* Library version (major*10000 + minor*100 + patch). */
+int pl_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* pl_last_error(void);
+
+/* 1 if `ptr` is a device (or managed) pointer visible to the current HIP
+ * device, 0 if not, negative on a runtime error.  Used at load time to check
+ * that the caller's allocator and this library share one HIP runtime. */
+int pl_is_device_pointer(const void* ptr);
+
+/* Upper bound on the number of groups pl_plan_build can emit for `rows` rows
+ * of `row_len` tokens over `num_slots` slots: ceil(rows*row_len/64) + num_slots - 1. */
+int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t num_slots);
+
+/* Build the per-forward adapter-major plan on the device.
+ *   row_slot[rows]  int32 slot of each row (weight_indices, cache.py:77-84)
+ *   seq_lens[rows]  int32 valid length of each row; the row contributes
+ *                   min(max(seq_len,0), row_len) tokens (layers.py:127 slicing)
+ *   tok[rows*row_len]          out: token indices (row*row_len + m), grouped by slot
+ *   groups[group_cap]          out: pl_group list
+ *   meta[4]                    out: {num_groups, num_tokens, 0, 0}
+ * Rows with slot 0, slot >= num_slots, slot < 0 or length 0 are skipped.
+ * Token order inside one slot is unspecified; every consumer is order-free. */
+int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,
+                  int32_t row_len, int32_t num_slots, int32_t* tok, pl_group* groups,
+                  int32_t* meta, int64_t group_cap, void* stream);
+
+/* Shrink: tmp[p][j] (+)= sum_k x[tok[p]][k] * A_slot[j][k] for every planned
+ * token position p and j < rank(slot, module).  fp32 output.
+ *   x [*, ldx] of dtype; K = in_features
+ *   k_splits == 1: tmp is stored; k_splits > 1: tmp is accumulated with
+ *   atomics and must be zero on entry.
+ *   zero_ptr/zero_count: optional buffer of `zero_count` floats that the
+ *   kernel clears (used to clear the other half of a ping-pong workspace).
+ * Requires K % 8 == 0 (bf16/f16) or K % 4 == 0 (f32), 16-byte aligned x rows
+ * and arena parts; otherwise returns PL_ERR_ALIGN. */
+int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t K, const void* arena,
+                   const pl_slot_entry* table, int32_t num_modules, int32_t module,
+                   const int32_t* tok, const pl_group* groups, const int32_t* meta,
+                   int64_t group_cap, float* tmp, int32_t ldt, int32_t k_splits,
+                   float* zero_ptr, int64_t zero_count, void* stream);
+
+/* Expand: y[tok[p]][n] += scale * sum_{j<rank} T(tmp[p][j]) * B_slot[n][j]
+ * with the rounding order of `epilogue`.  y [*, ldy] of dtype, N % 4 == 0. */
+int pl_sgmv_expand(int32_t dtype, const float* tmp, int32_t ldt, const void* arena,
+                   const pl_slot_entry* table, int32_t num_modules, int32_t module,
+                   const int32_t* tok, const pl_group* groups, const int32_t* meta,
+                   int64_t group_cap, void* y, int64_t ldy, int32_t N, int32_t epilogue,
+                   void* stream);
+
+/* Shrink followed by expand on one stream (one call per wrapped Linear). */
+int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y, int64_t ldy,
+                  int32_t N, const void* arena, const pl_slot_entry* table,
+                  int32_t num_modules, int32_t module, const int32_t* tok,
+                  const pl_group* groups, const int32_t* meta, int64_t group_cap, float* tmp,
+                  int32_t ldt, int32_t k_splits, float* zero_ptr, int64_t zero_count,
+                  int32_t epilogue, void* stream);
+
+/* Row-based LoRA on the slot arena for shapes the tiled path rejects
+ * (any K, N, strides, alignment).  Writes y[b*row_len+m] for m < seq_len[b].
+ * tmp is [rows*row_len][ldt] fp32 scratch. */
+int pl_lora_apply_rows(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
+                       int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
+                       int32_t num_modules, int32_t module, const int32_t* row_slot,
+                       const int32_t* seq_lens, int32_t rows, int32_t row_len, float* tmp,
+                       int32_t ldt, int32_t epilogue, void* stream);
+
+/* Reference-layout shrink (sgmv.py:141-175): out[b][m][n] = T(sum_k x[b][m][k] *
+ * w[widx[b]][k][n]) for m < seq_lens[b], n < ranks[widx[b]] * stack_num.
+ * x [B][M][K] contiguous; w strides in elements; out [B][M][n_max] contiguous. */
+int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K,
+                       const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t n_max,
+                       const int32_t* seq_lens, const int32_t* weight_indices,
+                       const int32_t* lora_ranks, int32_t stack_num, void* out, void* stream);
+
+/* Reference-layout expand (sgmv.py:278-328): out[b][m][n] = T(T(scale * sum_{k<rank}
+ * x[b][m][k] * w[widx[b]][k][n]) + out[b][m][n]) for m < seq_lens[b], rank > 0.
+ * x [B][M][k_max] contiguous; out [B][M][N] contiguous (updated in place). */
+int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max,
+                       const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t N,
+                       const int32_t* seq_lens, const int32_t* weight_indices,
+                       const int32_t* lora_ranks, const float* scalings, void* out,
+                       void* stream);
+
+/* Copy one packed adapter (host, pinned) into its slot region and its table
+ * row into the slot table, both asynchronously on `stream`. */
+int pl_slot_upload(void* arena_dst, const void* host_src, int64_t nbytes, void* table_dst,
+                   const void* table_src, int64_t table_bytes, void* stream);
+
+/* flag[0] |= 1 if (mask[b][s] != 0) != (s < seq_lens[b]) for any element.
+ * mask_dtype: 0 int64, 1 int32, 2 uint8/bool, 3 f32, 4 bf16, 5 f16. */
+int pl_check_right_padded(const void* mask, int32_t mask_dtype, int32_t B, int32_t S,
+                          const int32_t* seq_lens, int32_t* flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* POLYLORA_HIP_H */

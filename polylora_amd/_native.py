@@ -1,0 +1,130 @@
+"""ctypes binding of ``libpolylora_hip.so`` (declared in ``include/polylora_hip.h``).
+
+The library is the only compute path of this package: when it is missing
+every LoRA entry point raises instead of computing anything on the CPU.
+torch is imported first so that the library binds to torch's HIP runtime.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_int32, c_int64, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime the library must share)
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolylora_hip.so"
+
+PL_F32, PL_BF16, PL_F16 = 0, 1, 2
+PL_EPI_FALLBACK, PL_EPI_TRITON = 0, 1
+PL_MAX_SLOTS = 4096
+PL_GROUP_TOKENS = 64
+SLOT_ENTRY_INT32S = 8  # sizeof(pl_slot_entry) / 4
+
+DTYPE_CODES = {torch.float32: PL_F32, torch.bfloat16: PL_BF16, torch.float16: PL_F16}
+MASK_DTYPE_CODES = {
+    torch.int64: 0,
+    torch.int32: 1,
+    torch.uint8: 2,
+    torch.bool: 2,
+    torch.float32: 3,
+    torch.bfloat16: 4,
+    torch.float16: 5,
+}
+
+# name -> argument types; every function returns int32 unless listed in _RESTYPES
+_SIGNATURES: dict[str, tuple] = {
+    "pl_version": (),
+    "pl_last_error": (),
+    "pl_is_device_pointer": (c_void_p,),
+    "pl_plan_group_capacity": (c_int32, c_int32, c_int32),
+    "pl_plan_build": (c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p),
+    "pl_sgmv_shrink": (
+        c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
+        c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p, c_int64, c_void_p,
+    ),
+    "pl_sgmv_expand": (
+        c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+        c_int64, c_void_p, c_int64, c_int32, c_int32, c_void_p,
+    ),
+    "pl_lora_apply": (
+        c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
+        c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p, c_int64,
+        c_int32, c_void_p,
+    ),
+    "pl_lora_apply_rows": (
+        c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
+        c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_int32, c_void_p,
+    ),
+    "pl_sgmv_lora_a_ref": (
+        c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
+        c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
+    ),
+    "pl_sgmv_lora_b_ref": (
+        c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
+        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+    ),
+    "pl_slot_upload": (c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p),
+    "pl_check_right_padded": (c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p),
+}
+_RESTYPES = {"pl_last_error": ctypes.c_char_p, "pl_plan_group_capacity": c_int64}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lib = None
+_checked_runtime = False
+
+
+class NativeLibraryMissing(RuntimeError):
+    """The HIP library has not been built (run ``python -m polylora_amd.build``)."""
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once and attach argument types."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise NativeLibraryMissing(
+            f"polylora_amd HIP library not found at {LIB_PATH}; build it with "
+            "`python -m polylora_amd.build` (the LoRA path has no CPU fallback)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, argtypes in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = list(argtypes)
+        fn.restype = _RESTYPES.get(name, c_int32)
+    _lib = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().pl_last_error().decode("utf-8", "replace")
+        raise RuntimeError(f"{what} failed (status {status}): {msg}")
+
+
+def check_runtime(tensor: torch.Tensor) -> None:
+    """Verify once that a torch device pointer is a device pointer to the library."""
+    global _checked_runtime
+    if _checked_runtime:
+        return
+    res = load().pl_is_device_pointer(tensor.data_ptr())
+    if res != 1:
+        msg = load().pl_last_error().decode("utf-8", "replace")
+        raise RuntimeError(
+            "polylora_amd HIP library does not see torch's device memory "
+            f"(pl_is_device_pointer={res}: {msg}); two HIP runtimes are loaded"
+        )
+    _checked_runtime = True
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"polylora_amd kernels support float32, bfloat16 and float16, not {dtype}") from None
+
+
+def current_stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,74 @@
+// C-ABI utilities: error reporting, version, pointer probe, slot upload.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "pl_common.h"
+
+namespace {
+thread_local char g_last_error[512] = {0};
+}
+
+void pl_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+int pl_launch_status(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    pl_set_error("%s: launch failed: %s", what, hipGetErrorString(err));
+    return PL_ERR_LAUNCH;
+  }
+  return PL_OK;
+}
+
+extern "C" int pl_version(void) { return 100; }
+
+extern "C" const char* pl_last_error(void) { return g_last_error; }
+
+extern "C" int pl_is_device_pointer(const void* ptr) {
+  hipPointerAttribute_t attr;
+  const hipError_t err = hipPointerGetAttributes(&attr, ptr);
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    pl_set_error("hipPointerGetAttributes: %s", hipGetErrorString(err));
+    return -1;
+  }
+  return (attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged) ? 1 : 0;
+}
+
+// cache.py:138-145 copies each module's A and B separately with .to(device)
+// and .copy_(); here one packed adapter image (all modules, compact ranks)
+// moves with one host->device copy, followed by its 32-byte-per-module table
+// row.  Both copies are ordered on `stream` (a side stream the caller orders
+// against compute with events), so the table row never becomes visible to a
+// kernel on that stream before the weights it points at.
+extern "C" int pl_slot_upload(void* arena_dst, const void* host_src, int64_t nbytes,
+                              void* table_dst, const void* table_src, int64_t table_bytes,
+                              void* stream) {
+  if (nbytes < 0 || table_bytes < 0 || (nbytes > 0 && (!arena_dst || !host_src)) ||
+      (table_bytes > 0 && (!table_dst || !table_src))) {
+    pl_set_error("pl_slot_upload: bad arguments");
+    return PL_ERR_ARG;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (nbytes > 0) {
+    const hipError_t err =
+        hipMemcpyAsync(arena_dst, host_src, (size_t)nbytes, hipMemcpyHostToDevice, s);
+    if (err != hipSuccess) {
+      pl_set_error("pl_slot_upload: weights copy failed: %s", hipGetErrorString(err));
+      return PL_ERR_LAUNCH;
+    }
+  }
+  if (table_bytes > 0) {
+    const hipError_t err =
+        hipMemcpyAsync(table_dst, table_src, (size_t)table_bytes, hipMemcpyHostToDevice, s);
+    if (err != hipSuccess) {
+      pl_set_error("pl_slot_upload: table copy failed: %s", hipGetErrorString(err));
+      return PL_ERR_LAUNCH;
+    }
+  }
+  return PL_OK;
+}

@@ -1,0 +1,101 @@
+// Shared device/host helpers of the gfx950 multi-LoRA SGMV library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/polylora_hip.h"
+
+typedef __bf16 pl_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 pl_f16x8 __attribute__((ext_vector_type(8)));
+typedef float pl_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pl_u32x4 __attribute__((ext_vector_type(4)));
+
+// Element traits.  E = elements per 16-byte chunk, the unit every lane loads.
+template <int DT>
+struct pl_traits;
+template <>
+struct pl_traits<PL_F32> {
+  typedef float T;
+  typedef float T4 __attribute__((ext_vector_type(4)));
+  typedef float T8 __attribute__((ext_vector_type(8)));
+  enum { E = 4 };
+};
+template <>
+struct pl_traits<PL_BF16> {
+  typedef __bf16 T;
+  typedef __bf16 T4 __attribute__((ext_vector_type(4)));
+  typedef __bf16 T8 __attribute__((ext_vector_type(8)));
+  enum { E = 8 };
+};
+template <>
+struct pl_traits<PL_F16> {
+  typedef _Float16 T;
+  typedef _Float16 T4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 T8 __attribute__((ext_vector_type(8)));
+  enum { E = 8 };
+};
+
+// Round an fp32 value to the element type (round-to-nearest-even) and back.
+template <int DT>
+__device__ __forceinline__ float pl_round(float v) {
+  typedef typename pl_traits<DT>::T T;
+  return (float)(T)v;
+}
+
+// Expand epilogue: combine the fp32 accumulator with the base output value.
+//   fallback order (layers.py:127-128): d = T(acc); d = T(d * T(scale)); y = T(y + d)
+//   triton order   (sgmv.py:268-275):   y = T(T(acc * scale) + y)
+template <int DT>
+__device__ __forceinline__ float pl_epilogue(float acc, float y, float scale, float scale_t,
+                                             int mode) {
+  if (mode == PL_EPI_FALLBACK) {
+    float d = pl_round<DT>(acc);
+    d = pl_round<DT>(d * scale_t);
+    return pl_round<DT>(y + d);
+  }
+  float d = pl_round<DT>(acc * scale);
+  return pl_round<DT>(d + y);
+}
+
+__device__ __forceinline__ pl_u32x4 pl_ld16(const void* p) {
+  return *reinterpret_cast<const pl_u32x4*>(p);
+}
+
+// One 16-byte chunk per lane on each operand of a 16x16 MFMA tile, fp32
+// accumulate.  Lane l supplies row (l % 16) of the A operand and column
+// (l % 16) of the B operand; its chunk covers the reduction slots owned by
+// lane group l / 16.  bf16/f16: one 16x16x32 MFMA (8 elements per lane).
+// f32: four 16x16x4 MFMAs, element i of both chunks feeding MFMA i.  Both
+// operands use the same lane -> reduction-index map, so any consistent
+// assignment of k to (lane group, element) yields the same contraction.
+template <int DT>
+__device__ __forceinline__ pl_f32x4 pl_mfma_chunk(pl_u32x4 a, pl_u32x4 b, pl_f32x4 c);
+
+template <>
+__device__ __forceinline__ pl_f32x4 pl_mfma_chunk<PL_BF16>(pl_u32x4 a, pl_u32x4 b,
+                                                           pl_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(pl_bf16x8, a),
+                                                 __builtin_bit_cast(pl_bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ pl_f32x4 pl_mfma_chunk<PL_F16>(pl_u32x4 a, pl_u32x4 b,
+                                                          pl_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(pl_f16x8, a),
+                                                __builtin_bit_cast(pl_f16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ pl_f32x4 pl_mfma_chunk<PL_F32>(pl_u32x4 a, pl_u32x4 b, pl_f32x4 c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), c, 0, 0, 0);
+  return c;
+}
+
+// ---------------------------------------------------------------- host side
+void pl_set_error(const char* fmt, ...);
+int pl_launch_status(const char* what);
+
+static inline int pl_elem_size(int dtype) { return dtype == PL_F32 ? 4 : 2; }
+static inline int pl_chunk_elems(int dtype) { return dtype == PL_F32 ? 4 : 8; }

@@ -1,0 +1,218 @@
+// Device-side per-forward plan: rows -> adapter-major token groups.
+//
+// Replaces the per-layer host schedule of sgmv.py:29-61 (two host syncs per
+// wrapped Linear) with one single-workgroup kernel per forward whose output
+// every wrapped Linear of that forward shares.  A row b with slot s > 0 and
+// length L = min(max(seq_len, 0), row_len) contributes the L tokens
+// b*row_len + m, m < L (the slicing x[b, :seq_len] of layers.py:127).
+//
+// Steps: per-slot token counts (LDS atomics), one block-wide exclusive scan
+// of counts and of group counts, group list emission, then each wave copies
+// the token indices of its rows to the slot's segment.  Row order inside a
+// segment follows LDS atomic order and is not fixed; no consumer depends on
+// it.
+#include "pl_common.h"
+
+namespace {
+
+constexpr int kPlanThreads = 1024;
+
+__global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
+    const int32_t* __restrict__ row_slot, const int32_t* __restrict__ seq_lens, int32_t rows,
+    int32_t row_len, int32_t num_slots, int32_t* __restrict__ tok, pl_group* __restrict__ groups,
+    int32_t* __restrict__ meta, int64_t group_cap) {
+  __shared__ int32_t cnt[PL_MAX_SLOTS];
+  __shared__ int32_t off[PL_MAX_SLOTS];
+  __shared__ int32_t goff[PL_MAX_SLOTS];
+  __shared__ int32_t wsum[2][kPlanThreads / 64];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int S = num_slots;
+
+  for (int s = tid; s < S; s += kPlanThreads) cnt[s] = 0;
+  __syncthreads();
+
+  for (int b = tid; b < rows; b += kPlanThreads) {
+    const int s = row_slot[b];
+    int L = seq_lens[b];
+    L = L < 0 ? 0 : (L > row_len ? row_len : L);
+    if (s > 0 && s < S && L > 0) atomicAdd(&cnt[s], L);
+  }
+  __syncthreads();
+
+  // Each thread owns 4 consecutive slots (PL_MAX_SLOTS == 4 * kPlanThreads).
+  int loc_t[4], loc_g[4];
+  int st = 0, sg = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int s = tid * 4 + q;
+    const int c = s < S ? cnt[s] : 0;
+    loc_t[q] = st;
+    loc_g[q] = sg;
+    st += c;
+    sg += (c + PL_GROUP_TOKENS - 1) / PL_GROUP_TOKENS;
+  }
+  int it = st, ig = sg;
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t1 = __shfl_up(it, d);
+    const int g1 = __shfl_up(ig, d);
+    if (lane >= d) {
+      it += t1;
+      ig += g1;
+    }
+  }
+  if (lane == 63) {
+    wsum[0][wave] = it;
+    wsum[1][wave] = ig;
+  }
+  __syncthreads();
+  int wt = 0, wg = 0, tt = 0, tg = 0;
+  for (int w = 0; w < kPlanThreads / 64; ++w) {
+    if (w < wave) {
+      wt += wsum[0][w];
+      wg += wsum[1][w];
+    }
+    tt += wsum[0][w];
+    tg += wsum[1][w];
+  }
+  const int ex_t = wt + it - st;
+  const int ex_g = wg + ig - sg;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int s = tid * 4 + q;
+    if (s < S) {
+      off[s] = ex_t + loc_t[q];
+      goff[s] = ex_g + loc_g[q];
+    }
+  }
+  if (tid == 0) {
+    meta[0] = tg;
+    meta[1] = tt;
+    meta[2] = 0;
+    meta[3] = 0;
+  }
+  __syncthreads();
+
+  for (int s = tid; s < S; s += kPlanThreads) {
+    const int c = cnt[s];
+    const int ng = (c + PL_GROUP_TOKENS - 1) / PL_GROUP_TOKENS;
+    for (int q = 0; q < ng; ++q) {
+      const int64_t gi = (int64_t)goff[s] + q;
+      if (gi < group_cap) {
+        pl_group gr;
+        gr.slot = s;
+        gr.start = off[s] + q * PL_GROUP_TOKENS;
+        gr.len = min(PL_GROUP_TOKENS, c - q * PL_GROUP_TOKENS);
+        gr.reserved = 0;
+        groups[gi] = gr;
+      }
+    }
+  }
+  __syncthreads();
+  for (int s = tid; s < S; s += kPlanThreads) cnt[s] = 0;  // reused as fill counters
+  __syncthreads();
+
+  for (int b = wave; b < rows; b += kPlanThreads / 64) {
+    const int s = row_slot[b];
+    int L = seq_lens[b];
+    L = L < 0 ? 0 : (L > row_len ? row_len : L);
+    if (s > 0 && s < S && L > 0) {
+      int p = 0;
+      if (lane == 0) p = off[s] + atomicAdd(&cnt[s], L);
+      p = __shfl(p, 0);
+      const int base = b * row_len;
+      for (int m = lane; m < L; m += 64) tok[p + m] = base + m;
+    }
+  }
+}
+
+template <typename M>
+__device__ __forceinline__ bool pl_mask_on(const void* mask, int64_t i) {
+  return reinterpret_cast<const M*>(mask)[i] != M(0);
+}
+
+__global__ __launch_bounds__(256) void pl_right_pad_kernel(const void* __restrict__ mask,
+                                                           int32_t mask_dtype, int32_t B,
+                                                           int32_t S,
+                                                           const int32_t* __restrict__ seq_lens,
+                                                           int32_t* __restrict__ flag) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)B * S) return;
+  const int b = (int)(i / S);
+  const int s = (int)(i - (int64_t)b * S);
+  bool on;
+  switch (mask_dtype) {
+    case 0: on = pl_mask_on<int64_t>(mask, i); break;
+    case 1: on = pl_mask_on<int32_t>(mask, i); break;
+    case 2: on = pl_mask_on<uint8_t>(mask, i); break;
+    case 3: on = pl_mask_on<float>(mask, i); break;
+    case 4: on = (reinterpret_cast<const uint16_t*>(mask)[i] & 0x7fffu) != 0; break;
+    default: on = (reinterpret_cast<const uint16_t*>(mask)[i] & 0x7fffu) != 0; break;
+  }
+  const bool expect = s < seq_lens[b];
+  if (on != expect) *flag = 1;  // every writer stores the same value
+}
+
+}  // namespace
+
+extern "C" int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t num_slots) {
+  if (rows < 0 || row_len < 0 || num_slots < 1) return 0;
+  const int64_t t = (int64_t)rows * row_len;
+  return (t + PL_GROUP_TOKENS - 1) / PL_GROUP_TOKENS + (num_slots - 1);
+}
+
+extern "C" int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,
+                             int32_t row_len, int32_t num_slots, int32_t* tok,
+                             pl_group* groups, int32_t* meta, int64_t group_cap, void* stream) {
+  if (!meta || (rows > 0 && (!row_slot || !seq_lens || !tok || !groups))) {
+    pl_set_error("pl_plan_build: null pointer");
+    return PL_ERR_ARG;
+  }
+  if (rows < 0 || row_len < 0 || num_slots < 1) {
+    pl_set_error("pl_plan_build: bad sizes rows=%d row_len=%d num_slots=%d", rows, row_len,
+                 num_slots);
+    return PL_ERR_ARG;
+  }
+  if (num_slots > PL_MAX_SLOTS) {
+    pl_set_error("pl_plan_build: %d slots exceed the maximum of %d", num_slots, PL_MAX_SLOTS);
+    return PL_ERR_LIMIT;
+  }
+  if ((int64_t)rows * row_len > 0x7fffffffLL) {
+    pl_set_error("pl_plan_build: rows*row_len exceeds 2^31-1");
+    return PL_ERR_LIMIT;
+  }
+  if (group_cap < pl_plan_group_capacity(rows, row_len, num_slots)) {
+    pl_set_error("pl_plan_build: group capacity %lld below the bound %lld", (long long)group_cap,
+                 (long long)pl_plan_group_capacity(rows, row_len, num_slots));
+    return PL_ERR_ARG;
+  }
+  hipLaunchKernelGGL(pl_plan_kernel, dim3(1), dim3(kPlanThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), row_slot, seq_lens, rows, row_len,
+                     num_slots, tok, groups, meta, group_cap);
+  return pl_launch_status("pl_plan_build");
+}
+
+extern "C" int pl_check_right_padded(const void* mask, int32_t mask_dtype, int32_t B, int32_t S,
+                                     const int32_t* seq_lens, int32_t* flag, void* stream) {
+  if (!flag || (B > 0 && S > 0 && (!mask || !seq_lens))) {
+    pl_set_error("pl_check_right_padded: null pointer");
+    return PL_ERR_ARG;
+  }
+  if (B < 0 || S < 0 || mask_dtype < 0 || mask_dtype > 5) {
+    pl_set_error("pl_check_right_padded: bad arguments");
+    return PL_ERR_ARG;
+  }
+  const int64_t n = (int64_t)B * S;
+  if (n == 0) return PL_OK;
+  const int64_t grid = (n + 255) / 256;
+  if (grid > 0x7fffffffLL) {
+    pl_set_error("pl_check_right_padded: mask too large");
+    return PL_ERR_LIMIT;
+  }
+  hipLaunchKernelGGL(pl_right_pad_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), mask, mask_dtype, B, S, seq_lens,
+                     flag);
+  return pl_launch_status("pl_check_right_padded");
+}

@@ -1,0 +1,119 @@
+"""MultiLoraLinear — drop-in wrapper of nn.Linear (src/polylora/layers.py:18-134).
+
+forward(x) = base_layer(x), then, when a LoRA batch context is active, the
+HIP SGMV shrink + expand adds ``scale * (x @ A^T) @ B^T`` in place into the
+base output for every row whose slot has rank > 0 in this module, over the
+first ``min(seq_len, M)`` tokens of the row.  Rank-0 rows and padding tokens
+keep the base output bit for bit.
+
+Where the reference picks Triton or its torch fallback (layers.py:42-58,
+:64-70), this layer always runs HIP kernels: the MFMA-tiled ones when
+``config.use_triton_kernels`` is True, the row-based ones otherwise.  A CPU
+input with an active LoRA context raises.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import sgmv
+from .cache import GpuAdapterCache
+from .context import LoraBatchContext, get_lora_context
+
+
+class MultiLoraLinear(nn.Module):
+    def __init__(self, base_layer: nn.Linear, module_name: str, cache: GpuAdapterCache) -> None:
+        super().__init__()
+        self.base_layer = base_layer
+        self.module_name = module_name
+        self.cache = cache
+
+    @property
+    def in_features(self) -> int:
+        return self.base_layer.in_features
+
+    @property
+    def out_features(self) -> int:
+        return self.base_layer.out_features
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        base = self.base_layer(x)
+        lora_ctx = get_lora_context()
+        if lora_ctx is None:
+            return base
+        original_shape = base.shape
+        x_3d, base_3d, seq_lens, weight_indices = self._prepare_batched_inputs(x, base, lora_ctx)
+        out = self._hip_forward(x_3d, base_3d, seq_lens, weight_indices, lora_ctx)
+        return out.reshape(original_shape)
+
+    @staticmethod
+    def _as_3d(x: torch.Tensor) -> torch.Tensor:
+        if x.dim() == 2:
+            return x.unsqueeze(1)
+        if x.dim() == 3:
+            return x
+        if x.dim() > 3:
+            return x.reshape(x.shape[0], -1, x.shape[-1])
+        raise ValueError("MultiLoraLinear expects a batched tensor")
+
+    def _prepare_batched_inputs(self, x: torch.Tensor, base: torch.Tensor, lora_ctx: LoraBatchContext):
+        """The three input shapes of layers.py:82-110.
+
+        Row lengths are returned unclamped; the plan (and the row kernels) use
+        min(seq_len, M), which is what the reference's slicing x[b, :seq_len]
+        and its explicit clamps compute.
+        """
+        batch = lora_ctx.weight_indices.shape[0]
+        if x.shape[0] == batch:
+            # (i) one row per context row: [B, K], [B, M, K] or [B, ..., K]
+            return (self._as_3d(x).contiguous(), self._as_3d(base).contiguous(), lora_ctx.seq_lens, lora_ctx.weight_indices)
+        if x.dim() == 3 and x.shape[0] == 1:
+            # (ii) a shared batch-1 tensor (e.g. DeBERTa relative position
+            # embeddings): row 0's adapter over its first min(seq_len, M) rows
+            return (x.contiguous(), base.contiguous(), lora_ctx.seq_lens[:1], lora_ctx.weight_indices[:1])
+        if x.dim() == 2 and x.shape[0] % batch == 0:
+            # (iii) flattened [B*S, K]
+            seq_len = x.shape[0] // batch
+            return (
+                x.reshape(batch, seq_len, x.shape[-1]).contiguous(),
+                base.reshape(batch, seq_len, base.shape[-1]).contiguous(),
+                lora_ctx.seq_lens,
+                lora_ctx.weight_indices,
+            )
+        raise ValueError("LoRA batch context batch size does not match layer input batch size")
+
+    def _hip_forward(
+        self,
+        x: torch.Tensor,
+        base: torch.Tensor,
+        seq_lens: torch.Tensor,
+        weight_indices: torch.Tensor,
+        lora_ctx: LoraBatchContext,
+    ) -> torch.Tensor:
+        if not x.is_cuda:
+            raise RuntimeError(
+                "MultiLoraLinear: the LoRA path of polylora_amd runs only on a ROCm GPU "
+                "(HIP kernels); move the model and inputs to a GPU device"
+            )
+        cache = self.cache
+        if x.dtype != cache.dtype or base.dtype != cache.dtype:
+            raise TypeError(
+                f"MultiLoraLinear {self.module_name!r}: input {x.dtype} / output {base.dtype} "
+                f"must match the adapter cache dtype {cache.dtype}"
+            )
+        rows, row_len, in_features = x.shape
+        if rows * row_len == 0:
+            return base
+        x2 = x.view(rows * row_len, in_features)
+        y2 = base.view(rows * row_len, base.shape[-1])
+        if cache.config.use_triton_kernels:
+            key = (rows, row_len)
+            plan = lora_ctx.plans.get(key)
+            if plan is None:
+                plan = sgmv.SgmvPlan(weight_indices, seq_lens, row_len, cache.num_slots)
+                lora_ctx.plans[key] = plan
+            sgmv.lora_apply(x2, y2, cache, self.module_name, plan)
+        else:
+            sgmv.lora_apply_rows(x2, y2, cache, self.module_name, weight_indices, seq_lens, row_len)
+        return base

@@ -1,0 +1,377 @@
+"""SGMV operators on the gfx950 HIP library (replaces src/polylora/sgmv.py).
+
+Two levels:
+
+* ``sgmv_lora_a_fwd`` / ``sgmv_lora_b_fwd`` keep the reference operator
+  signatures and tensor layouts (sgmv.py:141-175, :278-328): weights
+  ``[adapters, K, N]``, per-row ``seq_lens`` / ``weight_indices`` /
+  ``lora_ranks`` (/ ``scalings``).  They run the row-based HIP kernels.
+* ``SgmvPlan`` + ``lora_apply`` are what ``MultiLoraLinear`` uses: one device
+  plan per forward (no host sync) and the MFMA-tiled shrink/expand over the
+  packed slot arena of ``GpuAdapterCache``.
+
+There is no CPU path: CPU tensors raise.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+__all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "sgmv_lora_a_fwd", "sgmv_lora_b_fwd", "choose_k_splits"]
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"{what}: polylora_amd runs LoRA math only on a ROCm GPU through its HIP library; "
+            "got a CPU tensor (there is no CPU fallback)"
+        )
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.int32).contiguous()
+
+
+class SgmvPlan:
+    """Adapter-major token groups for one (rows, row_len) layer shape of a forward.
+
+    Built on the device by ``pl_plan_build`` from the int32 row -> slot map and
+    per-row lengths; every wrapped Linear of the forward with this shape reuses
+    it.  Buffers: ``tok`` [rows*row_len] sorted token indices, ``groups``
+    [group_cap, 4] (slot, start, len, 0), ``meta`` [4] (num_groups, num_tokens, 0, 0).
+    """
+
+    __slots__ = ("rows", "row_len", "num_slots", "tokens_cap", "group_cap", "tok", "groups", "meta", "row_slot", "seq_lens")
+
+    def __init__(self, row_slot: torch.Tensor, seq_lens: torch.Tensor, row_len: int, num_slots: int) -> None:
+        _require_gpu(row_slot, "SgmvPlan")
+        lib = _native.load()
+        row_slot = _i32(row_slot)
+        seq_lens = _i32(seq_lens)
+        rows = int(row_slot.numel())
+        if int(seq_lens.numel()) != rows:
+            raise ValueError("row_slot and seq_lens must have the same length")
+        self.rows, self.row_len, self.num_slots = rows, int(row_len), int(num_slots)
+        self.tokens_cap = rows * self.row_len
+        self.group_cap = int(lib.pl_plan_group_capacity(rows, self.row_len, self.num_slots))
+        dev = row_slot.device
+        self.tok = torch.empty(max(1, self.tokens_cap), dtype=torch.int32, device=dev)
+        self.groups = torch.empty((max(1, self.group_cap), 4), dtype=torch.int32, device=dev)
+        self.meta = torch.empty(4, dtype=torch.int32, device=dev)
+        self.row_slot, self.seq_lens = row_slot, seq_lens
+        _native.check(
+            lib.pl_plan_build(
+                row_slot.data_ptr(),
+                seq_lens.data_ptr(),
+                rows,
+                self.row_len,
+                self.num_slots,
+                self.tok.data_ptr(),
+                self.groups.data_ptr(),
+                self.meta.data_ptr(),
+                max(1, self.group_cap),
+                _stream(dev),
+            ),
+            "pl_plan_build",
+        )
+
+
+class _Workspace:
+    """Ping-pong fp32 intermediate for one (device, stream).
+
+    A split-K shrink accumulates with atomics and needs a zeroed buffer.  Call
+    i uses buffer i%2 (clean on entry) and its kernel clears what call i-1
+    left in the other buffer, so no separate clearing launch is ever needed.
+    """
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = device
+        self.cap = 0
+        self.bufs: list[torch.Tensor | None] = [None, None]
+        self.dirty = [0, 0]
+        self.cur = 0
+
+    def acquire(self, nfloats: int) -> tuple[int, torch.Tensor, int, int]:
+        nfloats = (max(nfloats, 4) + 3) // 4 * 4
+        if nfloats > self.cap:
+            self.cap = max(nfloats, 2 * self.cap)
+            self.bufs = [torch.zeros(self.cap, dtype=torch.float32, device=self.device) for _ in range(2)]
+            self.dirty = [0, 0]
+            self.cur = 0
+        i = self.cur
+        j = 1 - i
+        if self.dirty[i]:  # only after a failed launch
+            self.bufs[i][: self.dirty[i]].zero_()
+            self.dirty[i] = 0
+        zero_ptr, zero_count = 0, 0
+        if self.dirty[j]:
+            zero_ptr, zero_count = self.bufs[j].data_ptr(), self.dirty[j]
+        return i, self.bufs[i], zero_ptr, zero_count
+
+    def commit(self, i: int, used: int, ok: bool) -> None:
+        j = 1 - i
+        if not ok:
+            self.dirty = [self.cap, self.cap]
+            return
+        self.dirty[j] = 0
+        self.dirty[i] = (max(used, 4) + 3) // 4 * 4
+        self.cur = j
+
+
+_WORKSPACES: dict[tuple[int, int], _Workspace] = {}
+
+
+def _workspace(device: torch.device, stream: int) -> _Workspace:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        ws = _WORKSPACES[key] = _Workspace(device)
+    return ws
+
+
+def choose_k_splits(group_cap: int, K: int, dtype: torch.dtype) -> int:
+    """Split K across workgroups only when the group count alone cannot fill the GPU."""
+    chunk = 8 if dtype != torch.float32 else 4
+    k_per_wg_step = 4 * 16 * chunk  # four waves x one 16-chunk step each
+    max_splits = max(1, -(-K // k_per_wg_step))
+    if group_cap >= 512:
+        return 1
+    return max(1, min(max_splits, -(-1024 // max(1, group_cap))))
+
+
+def _tiled_ok(x: torch.Tensor, y: torch.Tensor) -> bool:
+    chunk = 4 if x.dtype == torch.float32 else 8
+    K = x.shape[1]
+    N = y.shape[1]
+    es = x.element_size()
+    return (
+        x.stride(1) == 1
+        and y.stride(1) == 1
+        and K % chunk == 0
+        and (x.stride(0) * es) % 16 == 0
+        and x.data_ptr() % 16 == 0
+        and N % 4 == 0
+        and y.stride(0) % 4 == 0
+        and y.data_ptr() % (4 * es) == 0
+    )
+
+
+def lora_apply(
+    x: torch.Tensor,
+    y: torch.Tensor,
+    cache,
+    module_name: str,
+    plan: SgmvPlan,
+    *,
+    epilogue: int = _native.PL_EPI_FALLBACK,
+    k_splits: int | None = None,
+) -> torch.Tensor:
+    """y[t] += scale * (x[t] @ A^T) @ B^T for every planned token t, in place.
+
+    x: [rows*row_len, in_features], y: [rows*row_len, out_features], both of
+    the cache's dtype, on the cache's device.  Falls back to the row-based HIP
+    kernels when x / y do not meet the tiled path's alignment.
+    """
+    _require_gpu(x, "lora_apply")
+    if not _tiled_ok(x, y):
+        return lora_apply_rows(x, y, cache, module_name, plan.row_slot, plan.seq_lens, plan.row_len, epilogue=epilogue)
+    lib = _native.load()
+    dt = _native.dtype_code(x.dtype)
+    K = int(x.shape[1])
+    N = int(y.shape[1])
+    ldt = cache.rank8_cap
+    stream = _stream(x.device)
+    splits = k_splits if k_splits is not None else choose_k_splits(plan.group_cap, K, x.dtype)
+    ws = _workspace(x.device, stream)
+    need = plan.tokens_cap * ldt
+    i, buf, zero_ptr, zero_count = ws.acquire(need)
+    status = lib.pl_lora_apply(
+        dt,
+        x.data_ptr(),
+        x.stride(0),
+        K,
+        y.data_ptr(),
+        y.stride(0),
+        N,
+        cache.arena.data_ptr(),
+        cache.table.data_ptr(),
+        len(cache.module_index),
+        cache.module_index[module_name],
+        plan.tok.data_ptr(),
+        plan.groups.data_ptr(),
+        plan.meta.data_ptr(),
+        max(1, plan.group_cap),
+        buf.data_ptr(),
+        ldt,
+        splits,
+        zero_ptr or None,
+        zero_count,
+        epilogue,
+        stream,
+    )
+    ws.commit(i, need, status == 0)
+    _native.check(status, "pl_lora_apply")
+    return y
+
+
+def lora_apply_rows(
+    x: torch.Tensor,
+    y: torch.Tensor,
+    cache,
+    module_name: str,
+    row_slot: torch.Tensor,
+    seq_lens: torch.Tensor,
+    row_len: int,
+    *,
+    epilogue: int = _native.PL_EPI_FALLBACK,
+) -> torch.Tensor:
+    """Row-based HIP kernels on the slot arena: any K, N, stride or alignment."""
+    _require_gpu(x, "lora_apply_rows")
+    lib = _native.load()
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    y_work = y if y.stride(-1) == 1 else y.contiguous()
+    rows = int(row_slot.numel())
+    T = rows * int(row_len)
+    ldt = max(1, cache.config.max_rank)
+    tmp = torch.empty(max(1, T * ldt), dtype=torch.float32, device=x.device)
+    row_slot = _i32(row_slot)
+    seq_lens = _i32(seq_lens)
+    _native.check(
+        lib.pl_lora_apply_rows(
+            _native.dtype_code(x.dtype),
+            x.data_ptr(),
+            x.stride(0),
+            int(x.shape[1]),
+            y_work.data_ptr(),
+            y_work.stride(0),
+            int(y_work.shape[1]),
+            cache.arena.data_ptr(),
+            cache.table.data_ptr(),
+            len(cache.module_index),
+            cache.module_index[module_name],
+            row_slot.data_ptr(),
+            seq_lens.data_ptr(),
+            rows,
+            int(row_len),
+            tmp.data_ptr(),
+            ldt,
+            epilogue,
+            _stream(x.device),
+        ),
+        "pl_lora_apply_rows",
+    )
+    if y_work is not y:
+        y.copy_(y_work)
+    return y
+
+
+def sgmv_lora_a_fwd(
+    x: torch.Tensor,  # (B, M, K)
+    weights: torch.Tensor,  # (num_adapters, K, N_max)
+    seq_lens: torch.Tensor,  # (B,)
+    weight_indices: torch.Tensor,  # (B,)
+    lora_ranks: torch.Tensor,  # (num_adapters,)
+    stack_num: int = 1,
+) -> torch.Tensor:
+    """Shrink with the reference signature: out[b, m, n] = x[b, m] @ weights[w_b][:, n].
+
+    Rows m >= seq_lens[b] and columns n >= ranks[w_b] * stack_num are left
+    unwritten, like the reference's ``torch.empty`` output.
+    """
+    assert x.is_contiguous() and weights.is_contiguous()
+    assert x.dim() == 3 and weights.dim() == 3
+    B, M, K = x.shape
+    _, Kw, N_max = weights.shape
+    assert Kw == K, f"K mismatch: x={K}, weights={Kw}"
+    output = torch.empty((B, M, N_max), device=x.device, dtype=x.dtype)
+    if B == 0 or M == 0 or N_max == 0:
+        return output
+    _require_gpu(x, "sgmv_lora_a_fwd")
+    if weights.dtype != x.dtype:
+        raise TypeError(f"weights dtype {weights.dtype} must match x dtype {x.dtype}")
+    seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
+    lib = _native.load()
+    _native.check(
+        lib.pl_sgmv_lora_a_ref(
+            _native.dtype_code(x.dtype),
+            x.data_ptr(),
+            B,
+            M,
+            K,
+            weights.data_ptr(),
+            weights.stride(0),
+            weights.stride(1),
+            weights.stride(2),
+            N_max,
+            seq_lens.data_ptr(),
+            weight_indices.data_ptr(),
+            lora_ranks.data_ptr(),
+            int(stack_num),
+            output.data_ptr(),
+            _stream(x.device),
+        ),
+        "pl_sgmv_lora_a_ref",
+    )
+    return output
+
+
+def sgmv_lora_b_fwd(
+    x: torch.Tensor,  # (B, M, K_max)
+    weights: torch.Tensor,  # (num_adapters, K_max, N)
+    seq_lens: torch.Tensor,  # (B,)
+    weight_indices: torch.Tensor,  # (B,)
+    lora_ranks: torch.Tensor,  # (num_adapters,)
+    scalings: torch.Tensor,  # (num_adapters,) fp32
+    base_output: torch.Tensor | None = None,  # (B, M, N) fused add target
+) -> torch.Tensor:
+    """Expand with the reference signature and fused add-back (sgmv.py:278-328)."""
+    assert x.is_contiguous() and weights.is_contiguous()
+    assert x.dim() == 3 and weights.dim() == 3
+    B, M, K_max = x.shape
+    _, Kw, N = weights.shape
+    assert Kw == K_max, f"K mismatch: x={K_max}, weights={Kw}"
+    if base_output is None:
+        output = torch.zeros((B, M, N), device=x.device, dtype=x.dtype)
+    else:
+        assert base_output.shape == (B, M, N)
+        output = base_output
+    if B == 0 or M == 0 or N == 0:
+        return output
+    _require_gpu(x, "sgmv_lora_b_fwd")
+    if weights.dtype != x.dtype or output.dtype != x.dtype:
+        raise TypeError("x, weights and base_output must share one dtype")
+    work = output if output.is_contiguous() else output.contiguous()
+    seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
+    scalings = scalings.to(torch.float32).contiguous()
+    lib = _native.load()
+    _native.check(
+        lib.pl_sgmv_lora_b_ref(
+            _native.dtype_code(x.dtype),
+            x.data_ptr(),
+            B,
+            M,
+            K_max,
+            weights.data_ptr(),
+            weights.stride(0),
+            weights.stride(1),
+            weights.stride(2),
+            N,
+            seq_lens.data_ptr(),
+            weight_indices.data_ptr(),
+            lora_ranks.data_ptr(),
+            scalings.data_ptr(),
+            work.data_ptr(),
+            _stream(x.device),
+        ),
+        "pl_sgmv_lora_b_ref",
+    )
+    if work is not output:
+        output.copy_(work)
+    return output

@@ -1,0 +1,161 @@
+"""GPU parity of the HIP kernels against the oracle (run with `-m gpu`)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.lora import reference_forward, sgmv_expand_reference, sgmv_shrink_reference
+from oracle.plan import check_plan
+from polylora_amd import sgmv
+from tests._util import make_cache, oracle_slot_tensors, peft_layer, tol_for
+
+pytestmark = pytest.mark.gpu
+
+
+def _announce(**kw):
+    print("case:", ", ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _adapters(gen, ranks, fin, fout, module="m", extra_module=None):
+    """One adapter per rank; rank 0 means the adapter lacks `module` (needs extra_module)."""
+    out = {}
+    for i, r in enumerate(ranks):
+        layers = {}
+        if r > 0:
+            layers[module] = peft_layer(gen, fin, fout, r, alpha=2.0 * r)
+        if extra_module is not None:
+            layers[extra_module] = peft_layer(gen, 8, 8, 2, alpha=4.0)
+        out[f"a{i:03d}"] = layers
+    return out
+
+
+@pytest.mark.parametrize(
+    "rows,row_len,num_slots,seed",
+    [(1, 1, 2, 0), (7, 3, 5, 1), (256, 1, 65, 2), (32, 1024, 9, 3), (4096, 1, 17, 4), (3, 200, 4096, 5), (0, 5, 3, 6)],
+)
+def test_plan_matches_oracle(gpu, rows, row_len, num_slots, seed):
+    _announce(test="plan", rows=rows, row_len=row_len, num_slots=num_slots)
+    g = torch.Generator().manual_seed(seed)
+    row_slot = torch.randint(-1, num_slots + 1, (rows,), generator=g, dtype=torch.int32)
+    seq_lens = torch.randint(-2, row_len + 3, (rows,), generator=g, dtype=torch.int32)
+    plan = sgmv.SgmvPlan(row_slot.to(gpu), seq_lens.to(gpu), row_len, num_slots)
+    torch.cuda.synchronize()
+    check_plan(
+        plan.tok.cpu().numpy(),
+        plan.groups.cpu().numpy(),
+        plan.meta.cpu().numpy(),
+        row_slot.tolist(),
+        seq_lens.tolist(),
+        row_len,
+        num_slots,
+    )
+
+
+CASES = [
+    # dtype, rows, M, K, N, ranks, max_rank, k_splits, seed
+    (torch.bfloat16, 8, 5, 64, 32, [2, 3, 4], 4, None, 10),
+    (torch.float32, 8, 5, 64, 32, [2, 3, 4], 4, None, 11),
+    (torch.float16, 8, 5, 64, 32, [2, 3, 4], 4, None, 12),
+    (torch.bfloat16, 256, 1, 4096, 4096, [8, 16, 32, 64], 64, None, 13),
+    (torch.bfloat16, 256, 1, 14336, 4096, [8, 16, 32, 64], 64, None, 14),
+    (torch.bfloat16, 64, 1, 4096, 14336, [8, 16, 32, 64], 64, None, 15),
+    (torch.bfloat16, 4, 300, 512, 1024, [16, 32], 64, None, 16),
+    (torch.bfloat16, 33, 7, 1024, 768, [1, 7, 9, 15, 17, 33, 63], 64, 3, 17),
+    (torch.float32, 33, 7, 768, 3072, [4, 8, 16], 16, 4, 18),
+    (torch.float32, 6, 128, 3072, 768, [4, 8, 8, 16, 16], 16, None, 19),
+    (torch.bfloat16, 16, 3, 4104, 1000, [80, 128], 128, 2, 20),
+    (torch.bfloat16, 300, 1, 256, 256, [16] * 5, 16, 1, 21),
+]
+
+
+@pytest.mark.parametrize("dtype,rows,M,K,N,ranks,max_rank,k_splits,seed", CASES)
+def test_lora_apply_matches_oracle(gpu, dtype, rows, M, K, N, ranks, max_rank, k_splits, seed):
+    _announce(test="lora_apply", dtype=dtype, rows=rows, M=M, K=K, N=N, ranks=ranks, k_splits=k_splits)
+    g = torch.Generator().manual_seed(seed)
+    adapters = _adapters(g, ranks, K, N)
+    ids = list(adapters) + ["__base__"]
+    cache = make_cache(adapters, {"m": (K, N)}, len(adapters), max_rank, gpu, dtype)
+    pick = torch.randint(0, len(ids), (rows,), generator=g).tolist()
+    adapter_ids = [ids[i] for i in pick]
+    row_slot = cache.ensure_resident(adapter_ids)
+    seq_lens = torch.randint(0, M + 2, (rows,), generator=g, dtype=torch.int32)
+    x = torch.randn(rows, M, K, generator=g).to(dtype)
+    base = torch.randn(rows, M, N, generator=g).to(dtype)
+    y = base.to(gpu)
+    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots)
+    sgmv.lora_apply(x.to(gpu).view(-1, K), y.view(-1, N), cache, "m", plan, k_splits=k_splits)
+    got = y.cpu()
+    A, B, rk, sc = oracle_slot_tensors(cache, adapters, "m", dtype)
+    expect = reference_forward(x, base, seq_lens, row_slot.cpu(), A, B, rk, sc)
+    torch.testing.assert_close(got, expect, **tol_for(dtype))
+    # untouched rows (base adapter, padding) are bit-identical to the base output
+    untouched = torch.ones(rows, M, dtype=torch.bool)
+    for b, aid in enumerate(adapter_ids):
+        if aid != "__base__":
+            untouched[b, : min(int(seq_lens[b]), M)] = False
+    assert torch.equal(got[untouched], base[untouched])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rows_kernels_match_oracle(gpu, dtype):
+    _announce(test="rows", dtype=dtype)
+    g = torch.Generator().manual_seed(30)
+    rows, M, K, N = 5, 9, 37, 30  # K, N not multiples of the 16-byte chunk
+    adapters = _adapters(g, [1, 3, 5], K, N)
+    cache = make_cache(adapters, {"m": (K, N)}, 3, 5, gpu, dtype, tiled=False)
+    ids = ["a000", "__base__", "a001", "a002", "a001"]
+    row_slot = cache.ensure_resident(ids)
+    seq_lens = torch.tensor([9, 9, 0, 4, 11], dtype=torch.int32)
+    x = torch.randn(rows, M, K, generator=g).to(dtype)
+    base = torch.randn(rows, M, N, generator=g).to(dtype)
+    y = base.to(gpu)
+    sgmv.lora_apply_rows(x.to(gpu).view(-1, K), y.view(-1, N), cache, "m", row_slot, seq_lens.to(gpu), M)
+    A, B, rk, sc = oracle_slot_tensors(cache, adapters, "m", dtype)
+    expect = reference_forward(x, base, seq_lens, row_slot.cpu(), A, B, rk, sc)
+    torch.testing.assert_close(y.cpu(), expect, **tol_for(dtype))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("stack_num", [1, 2])
+def test_reference_layout_ops_match_oracle(gpu, dtype, stack_num):
+    _announce(test="ref_ops", dtype=dtype, stack_num=stack_num)
+    g = torch.Generator().manual_seed(40 + stack_num)
+    Bt, M, K, N, S, R = 6, 10, 96, 80, 4, 8
+    x = torch.randn(Bt, M, K, generator=g).to(dtype)
+    wa = (torch.randn(S, K, R * stack_num, generator=g) * 0.05).to(dtype)
+    wb = (torch.randn(S, R, N, generator=g) * 0.05).to(dtype)
+    ranks = torch.tensor([0, 3, 8, 5], dtype=torch.int32)
+    scal = torch.tensor([0.0, 1.5, 2.0, 3.0], dtype=torch.float32)
+    seq = torch.tensor([10, 0, 7, 12, 3, 10], dtype=torch.int32)
+    widx = torch.tensor([1, 2, 0, 3, 2, 1], dtype=torch.int64)
+    tmp = sgmv.sgmv_lora_a_fwd(x.to(gpu), wa.to(gpu), seq.to(gpu), widx.to(gpu), ranks.to(gpu), stack_num)
+    exp_tmp, valid = sgmv_shrink_reference(x, wa, seq, widx, ranks, stack_num)
+    torch.testing.assert_close(tmp.cpu()[valid], exp_tmp[valid], **tol_for(dtype))
+    # expand over the oracle's intermediate (zeros outside the valid region)
+    base = torch.randn(Bt, M, N, generator=g).to(dtype)
+    xb = exp_tmp[:, :, :R].contiguous()
+    out = sgmv.sgmv_lora_b_fwd(xb.to(gpu), wb.to(gpu), seq.to(gpu), widx.to(gpu), ranks.to(gpu), scal.to(gpu), base.to(gpu))
+    expect = sgmv_expand_reference(xb, wb, seq, widx, ranks, scal, base)
+    torch.testing.assert_close(out.cpu(), expect, **tol_for(dtype))
+
+
+def test_isolated_sgmv_config_bf16(gpu):
+    """T=4096 tokens, K=N=4096, 16 slots + base, ranks cycling {0,4,8,16}, Dirichlet segments."""
+    _announce(test="isolated_sgmv_4096")
+    from bench import isolated_sgmv_workload
+
+    wl = isolated_sgmv_workload(gpu, seed=1002)
+    sgmv.lora_apply(wl.x, wl.y, wl.cache, "op", wl.plan)
+    torch.cuda.synchronize()
+    A, B, rk, sc = oracle_slot_tensors(wl.cache, wl.adapters, "op", torch.bfloat16)
+    A, B, rk, sc = A.to(gpu), B.to(gpu), rk.to(gpu), sc.to(gpu)
+    expect = reference_forward(
+        wl.x.view(-1, 1, 4096), wl.base.view(-1, 1, 4096), wl.seq_lens, wl.row_slot, A, B, rk, sc
+    ).view(-1, 4096)
+    torch.testing.assert_close(wl.y, expect, rtol=2e-2, atol=1e-2)
+    # tokens of rank-0 slots are untouched
+    zero = (rk[wl.row_slot.long()] == 0).cpu()
+    assert torch.equal(wl.y.cpu()[zero], wl.base.cpu()[zero])
+    np.testing.assert_array_equal(np.bincount(wl.row_slot.cpu().numpy(), minlength=17).sum(), 4096)
