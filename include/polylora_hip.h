@@ -116,8 +116,9 @@ int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows
  *   atomics and must be zero on entry.
  *   zero_ptr/zero_count: optional buffer of `zero_count` floats that the
  *   kernel clears (used to clear the other half of a ping-pong workspace).
- * Requires K % 8 == 0 (bf16/f16) or K % 4 == 0 (f32), 16-byte aligned x rows
- * and arena parts; otherwise returns PL_ERR_ALIGN. */
+ * tmp is [num_tokens][ldt] with ldt a multiple of 8 and >= every rank of
+ * this module.  Requires K % 8 == 0 (bf16/f16) or K % 4 == 0 (f32), 16-byte
+ * aligned x rows and arena parts; otherwise returns PL_ERR_ALIGN. */
 int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t K, const void* arena,
                    const pl_slot_entry* table, int32_t num_modules, int32_t module,
                    const int32_t* tok, const pl_group* groups, const int32_t* meta,
@@ -142,26 +143,34 @@ int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
 
 /* Row-based LoRA on the slot arena for shapes the tiled path rejects
  * (any K, N, strides, alignment).  Writes y[b*row_len+m] for m < seq_len[b].
- * tmp is [rows*row_len][ldt] fp32 scratch. */
+ * Rows whose slot is <= 0 or >= num_slots get no LoRA.  tmp is
+ * [rows*row_len][ldt] fp32 scratch with ldt >= the largest rank. */
 int pl_lora_apply_rows(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
                        int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
-                       int32_t num_modules, int32_t module, const int32_t* row_slot,
+                       int32_t num_slots, int32_t num_modules, int32_t module,
+                       const int32_t* row_slot,
                        const int32_t* seq_lens, int32_t rows, int32_t row_len, float* tmp,
                        int32_t ldt, int32_t epilogue, void* stream);
 
 /* Reference-layout shrink (sgmv.py:141-175): out[b][m][n] = T(sum_k x[b][m][k] *
  * w[widx[b]][k][n]) for m < seq_lens[b], n < ranks[widx[b]] * stack_num.
- * x [B][M][K] contiguous; w strides in elements; out [B][M][n_max] contiguous. */
+ * x [B][M][K] contiguous; w [num_adapters][K][n_max] with element strides;
+ * out [B][M][n_max] contiguous.  Rows with widx outside [0, num_adapters)
+ * are skipped. */
 int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K,
-                       const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t n_max,
+                       const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
+                       int32_t num_adapters, int32_t n_max,
                        const int32_t* seq_lens, const int32_t* weight_indices,
                        const int32_t* lora_ranks, int32_t stack_num, void* out, void* stream);
 
 /* Reference-layout expand (sgmv.py:278-328): out[b][m][n] = T(T(scale * sum_{k<rank}
  * x[b][m][k] * w[widx[b]][k][n]) + out[b][m][n]) for m < seq_lens[b], rank > 0.
- * x [B][M][k_max] contiguous; out [B][M][N] contiguous (updated in place). */
+ * x [B][M][k_max] contiguous; w [num_adapters][k_max][N] with element strides;
+ * out [B][M][N] contiguous (updated in place).  Rows with widx outside
+ * [0, num_adapters) are skipped. */
 int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max,
-                       const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t N,
+                       const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
+                       int32_t num_adapters, int32_t N,
                        const int32_t* seq_lens, const int32_t* weight_indices,
                        const int32_t* lora_ranks, const float* scalings, void* out,
                        void* stream);

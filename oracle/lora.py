@@ -23,20 +23,38 @@ def reference_forward(
 
     x [rows, M, K], base [rows, M, N]; A [slots, K, R] (lora_A^T per slot),
     B [slots, R, N] (lora_B^T), ranks int [slots], scales fp32 [slots].
-    Same op order as the reference: (x @ A[:, :r]) @ B[:r] in the model
-    dtype, times scale cast to the model dtype, added to a clone of base.
+    Same op order and rounding points as the reference (layers.py:127-128):
+    t = T(x @ A[:, :r]); d = T(t @ B[:r]); d = T(d * T(scale)); out = T(out + d)
+    on a clone of base, where T rounds to the model dtype.
+
+    Each product is computed as an fp32 matmul of the model-dtype values and
+    then rounded once to the model dtype, i.e. a model-dtype GEMM with fp32
+    accumulation, which is what the reference's torch matmul does on the GPU
+    for bf16/fp16.  For fp32 it is the reference op itself.  torch's CPU
+    bf16 matmul is deliberately not used: for a single strided column
+    (A[:, :1] of a [K, R] slot) it returns results off by more than 2 where
+    the exact product is below 1, so it cannot restate the GPU semantics.
     """
     out = base.clone()
+    dtype = out.dtype
     lengths = [int(v) for v in seq_lens.detach().cpu().tolist()]
     slots = [int(v) for v in weight_indices.detach().cpu().tolist()]
     for row, slot in enumerate(slots):
         rank = int(ranks[slot].item())
-        length = lengths[row]
+        length = min(max(lengths[row], 0), x.shape[1])
         if rank == 0 or length == 0:
             continue
-        delta = x[row, :length].matmul(A[slot, :, :rank]).matmul(B[slot, :rank, :])
-        out[row, :length] += delta * scales[slot].to(dtype=out.dtype)
+        t = _gemm(x[row, :length], A[slot, :, :rank], dtype)
+        delta = _gemm(t, B[slot, :rank, :], dtype)
+        out[row, :length] += delta * scales[slot].to(dtype=dtype)
     return out
+
+
+def _gemm(a: torch.Tensor, b: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """a @ b of model-dtype operands: fp32 (or fp64) accumulation, one rounding to `dtype`."""
+    if dtype in (torch.float32, torch.float64):
+        return a.matmul(b)
+    return a.float().matmul(b.float()).to(dtype)
 
 
 def as_3d(x: torch.Tensor) -> torch.Tensor:

@@ -54,15 +54,15 @@ _SIGNATURES: dict[str, tuple] = {
     ),
     "pl_lora_apply_rows": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
-        c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_int32, c_void_p,
+        c_int32, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_int32, c_void_p,
     ),
     "pl_sgmv_lora_a_ref": (
         c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
-        c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
+        c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
     ),
     "pl_sgmv_lora_b_ref": (
         c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
-        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+        c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
     ),
     "pl_slot_upload": (c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p),
     "pl_check_right_padded": (c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p),

@@ -9,14 +9,17 @@
 // Shrink: one wave per token row; lanes stride K, each rank column is a
 // wave-wide dot product finished with a butterfly reduction.
 // Expand: one thread per output element; loop over the adapter's rank.
+// Every kernel skips rows whose slot index is outside [0, num_slots), so a
+// corrupt row map cannot read outside the weight tensors.
 #include "pl_common.h"
 
 namespace {
 
-// Weight access for the two layouts.
+// Weight access for the reference layout [slot][k][n] (element strides).
 struct pl_ref_layout {
   const void* w;
-  int64_t s0, s1, s2;  // element strides of [slot][k][n]
+  int64_t s0, s1, s2;
+  int32_t num_slots;
 };
 
 template <int DT>
@@ -49,6 +52,7 @@ __global__ __launch_bounds__(256) void pl_ref_shrink(const void* __restrict__ x,
   const int m = (int)(row - (int64_t)b * M);
   if (m >= seq_lens[b]) return;
   const int s = widx[b];
+  if (s < 0 || s >= w.num_slots) return;
   const int n_eff = min(ranks[s] * stack_num, n_max);
   const int64_t xb = row * K;
   const int64_t wb = (int64_t)s * w.s0;
@@ -78,6 +82,7 @@ __global__ __launch_bounds__(256) void pl_ref_expand(const void* __restrict__ x,
   const int m = (int)(row - (int64_t)b * M);
   if (m >= seq_lens[b]) return;
   const int s = widx[b];
+  if (s < 0 || s >= w.num_slots) return;
   const int rank = min(ranks[s], k_max);
   if (rank <= 0) return;
   const int64_t xb = row * k_max;
@@ -91,77 +96,104 @@ __global__ __launch_bounds__(256) void pl_ref_expand(const void* __restrict__ x,
 
 // ---- slot arena layout ------------------------------------------------------
 
+struct pl_rows_args {
+  const void* x;
+  int64_t ldx;
+  int32_t K;
+  void* y;
+  int64_t ldy;
+  int32_t N;
+  const char* arena;
+  const pl_slot_entry* table;
+  int32_t num_slots;
+  int32_t num_modules;
+  int32_t module;
+  const int32_t* row_slot;
+  const int32_t* seq_lens;
+  int32_t rows;
+  int32_t row_len;
+  float* tmp;
+  int32_t ldt;
+  int32_t epilogue;
+  int32_t nblk;
+};
+
+// Slot-table entry of token t's row, or nullptr when the token gets no LoRA.
+__device__ __forceinline__ const pl_slot_entry* pl_row_entry(const pl_rows_args& a, int64_t t) {
+  const int b = (int)(t / a.row_len);
+  const int m = (int)(t - (int64_t)b * a.row_len);
+  if (m >= a.seq_lens[b]) return nullptr;
+  const int s = a.row_slot[b];
+  if (s <= 0 || s >= a.num_slots) return nullptr;
+  const pl_slot_entry* e = a.table + (int64_t)s * a.num_modules + a.module;
+  return e->rank > 0 ? e : nullptr;
+}
+
 template <int DT>
-__global__ __launch_bounds__(256) void pl_rows_shrink(
-    const void* __restrict__ x, int64_t ldx, int32_t K, const char* __restrict__ arena,
-    const pl_slot_entry* __restrict__ table, int32_t num_modules, int32_t module,
-    const int32_t* __restrict__ row_slot, const int32_t* __restrict__ seq_lens, int32_t rows,
-    int32_t row_len, float* __restrict__ tmp, int32_t ldt) {
+__global__ __launch_bounds__(256) void pl_rows_shrink(pl_rows_args a) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= (int64_t)rows * row_len) return;
-  const int b = (int)(t / row_len);
-  const int m = (int)(t - (int64_t)b * row_len);
-  if (m >= seq_lens[b]) return;
-  const int s = row_slot[b];
-  if (s <= 0) return;
-  const pl_slot_entry e = table[(int64_t)s * num_modules + module];
-  if (e.rank <= 0) return;
-  const void* A = arena + e.a_off;
-  for (int j = 0; j < e.rank; ++j) {
+  if (t >= (int64_t)a.rows * a.row_len) return;
+  const pl_slot_entry* e = pl_row_entry(a, t);
+  if (e == nullptr) return;
+  const int rank = min(e->rank, a.ldt);
+  const void* A = a.arena + e->a_off;
+  for (int j = 0; j < rank; ++j) {
     float acc = 0.f;
-    for (int k = lane; k < K; k += 64)
-      acc += pl_ld<DT>(x, t * ldx + k) * pl_ld<DT>(A, (int64_t)j * K + k);
+    for (int k = lane; k < a.K; k += 64)
+      acc += pl_ld<DT>(a.x, t * a.ldx + k) * pl_ld<DT>(A, (int64_t)j * a.K + k);
     acc = pl_wave_sum(acc);
-    if (lane == 0) tmp[t * ldt + j] = acc;
+    if (lane == 0) a.tmp[t * a.ldt + j] = acc;
   }
 }
 
 template <int DT>
-__global__ __launch_bounds__(256) void pl_rows_expand(
-    const float* __restrict__ tmp, int32_t ldt, const char* __restrict__ arena,
-    const pl_slot_entry* __restrict__ table, int32_t num_modules, int32_t module,
-    const int32_t* __restrict__ row_slot, const int32_t* __restrict__ seq_lens,
-    int32_t row_len, void* __restrict__ y, int64_t ldy, int32_t N, int32_t epilogue,
-    int32_t nblk) {
+__global__ __launch_bounds__(256) void pl_rows_expand(pl_rows_args a) {
   typedef typename pl_traits<DT>::T T;
-  const int64_t t = blockIdx.x / nblk;
-  const int n = (int)(blockIdx.x - t * nblk) * blockDim.x + threadIdx.x;
-  if (n >= N) return;
-  const int b = (int)(t / row_len);
-  const int m = (int)(t - (int64_t)b * row_len);
-  if (m >= seq_lens[b]) return;
-  const int s = row_slot[b];
-  if (s <= 0) return;
-  const pl_slot_entry e = table[(int64_t)s * num_modules + module];
-  if (e.rank <= 0) return;
-  const void* Bc = arena + e.b_off;
+  const int64_t t = blockIdx.x / a.nblk;
+  const int n = (int)(blockIdx.x - t * a.nblk) * blockDim.x + threadIdx.x;
+  if (n >= a.N) return;
+  const pl_slot_entry* e = pl_row_entry(a, t);
+  if (e == nullptr) return;
+  const int rank = min(e->rank, a.ldt);
+  const int r8 = e->rank8;
+  const void* Bc = a.arena + e->b_off;
   float acc = 0.f;
-  for (int j = 0; j < e.rank; ++j)
-    acc += pl_round<DT>(tmp[t * ldt + j]) * pl_ld<DT>(Bc, (int64_t)n * e.rank8 + j);
-  T* o = reinterpret_cast<T*>(y) + t * ldy + n;
-  *o = (T)pl_epilogue<DT>(acc, (float)*o, e.scale, pl_round<DT>(e.scale), epilogue);
+  for (int j = 0; j < rank; ++j)
+    acc += pl_round<DT>(a.tmp[t * a.ldt + j]) * pl_ld<DT>(Bc, (int64_t)n * r8 + j);
+  T* o = reinterpret_cast<T*>(a.y) + t * a.ldy + n;
+  *o = (T)pl_epilogue<DT>(acc, (float)*o, e->scale, pl_round<DT>(e->scale), a.epilogue);
 }
 
 bool valid_dtype(int32_t dtype) { return dtype == PL_F32 || dtype == PL_BF16 || dtype == PL_F16; }
+
+// Instantiate `launch<DT>()` for the runtime dtype code.
+template <typename F>
+void pl_dispatch(int32_t dtype, F&& launch) {
+  switch (dtype) {
+    case PL_BF16: launch(std::integral_constant<int, PL_BF16>()); break;
+    case PL_F16: launch(std::integral_constant<int, PL_F16>()); break;
+    default: launch(std::integral_constant<int, PL_F32>()); break;
+  }
+}
 
 }  // namespace
 
 extern "C" int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K,
                                   const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
-                                  int32_t n_max, const int32_t* seq_lens,
+                                  int32_t num_adapters, int32_t n_max, const int32_t* seq_lens,
                                   const int32_t* weight_indices, const int32_t* lora_ranks,
                                   int32_t stack_num, void* out, void* stream) {
   if (!valid_dtype(dtype)) {
     pl_set_error("unsupported dtype code %d", dtype);
     return PL_ERR_ARG;
   }
-  if (B < 0 || M < 0 || K < 0 || n_max < 0 || stack_num < 1) {
+  if (B < 0 || M < 0 || K < 0 || n_max < 0 || stack_num < 1 || num_adapters < 0) {
     pl_set_error("pl_sgmv_lora_a_ref: bad sizes");
     return PL_ERR_ARG;
   }
   const int64_t rows = (int64_t)B * M;
-  if (rows == 0 || n_max == 0) return PL_OK;
+  if (rows == 0 || n_max == 0 || num_adapters == 0) return PL_OK;
   if (!x || !w || !seq_lens || !weight_indices || !lora_ranks || !out) {
     pl_set_error("pl_sgmv_lora_a_ref: null pointer");
     return PL_ERR_ARG;
@@ -171,39 +203,31 @@ extern "C" int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32
     pl_set_error("pl_sgmv_lora_a_ref: too many rows");
     return PL_ERR_LIMIT;
   }
-  pl_ref_layout L{w, w_s0, w_s1, w_s2};
+  const pl_ref_layout L{w, w_s0, w_s1, w_s2, num_adapters};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case PL_BF16:
-      hipLaunchKernelGGL(pl_ref_shrink<PL_BF16>, dim3((unsigned)grid), dim3(256), 0, s, x, B, M, K,
-                         L, n_max, seq_lens, weight_indices, lora_ranks, stack_num, out);
-      break;
-    case PL_F16:
-      hipLaunchKernelGGL(pl_ref_shrink<PL_F16>, dim3((unsigned)grid), dim3(256), 0, s, x, B, M, K,
-                         L, n_max, seq_lens, weight_indices, lora_ranks, stack_num, out);
-      break;
-    default:
-      hipLaunchKernelGGL(pl_ref_shrink<PL_F32>, dim3((unsigned)grid), dim3(256), 0, s, x, B, M, K,
-                         L, n_max, seq_lens, weight_indices, lora_ranks, stack_num, out);
-  }
+  pl_dispatch(dtype, [&](auto dt) {
+    hipLaunchKernelGGL(pl_ref_shrink<decltype(dt)::value>, dim3((unsigned)grid), dim3(256), 0, s, x,
+                       B, M, K, L, n_max, seq_lens, weight_indices, lora_ranks, stack_num, out);
+  });
   return pl_launch_status("pl_sgmv_lora_a_ref");
 }
 
 extern "C" int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M,
                                   int32_t k_max, const void* w, int64_t w_s0, int64_t w_s1,
-                                  int64_t w_s2, int32_t N, const int32_t* seq_lens,
-                                  const int32_t* weight_indices, const int32_t* lora_ranks,
-                                  const float* scalings, void* out, void* stream) {
+                                  int64_t w_s2, int32_t num_adapters, int32_t N,
+                                  const int32_t* seq_lens, const int32_t* weight_indices,
+                                  const int32_t* lora_ranks, const float* scalings, void* out,
+                                  void* stream) {
   if (!valid_dtype(dtype)) {
     pl_set_error("unsupported dtype code %d", dtype);
     return PL_ERR_ARG;
   }
-  if (B < 0 || M < 0 || k_max < 0 || N < 0) {
+  if (B < 0 || M < 0 || k_max < 0 || N < 0 || num_adapters < 0) {
     pl_set_error("pl_sgmv_lora_b_ref: bad sizes");
     return PL_ERR_ARG;
   }
   const int64_t rows = (int64_t)B * M;
-  if (rows == 0 || N == 0) return PL_OK;
+  if (rows == 0 || N == 0 || num_adapters == 0) return PL_OK;
   if (!x || !w || !seq_lens || !weight_indices || !lora_ranks || !scalings || !out) {
     pl_set_error("pl_sgmv_lora_b_ref: null pointer");
     return PL_ERR_ARG;
@@ -213,29 +237,20 @@ extern "C" int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32
     pl_set_error("pl_sgmv_lora_b_ref: grid too large");
     return PL_ERR_LIMIT;
   }
-  pl_ref_layout L{w, w_s0, w_s1, w_s2};
-  dim3 grid((unsigned)(rows * nblk));
+  const pl_ref_layout L{w, w_s0, w_s1, w_s2, num_adapters};
+  const dim3 grid((unsigned)(rows * nblk));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case PL_BF16:
-      hipLaunchKernelGGL(pl_ref_expand<PL_BF16>, grid, dim3(256), 0, s, x, B, M, k_max, L, N,
-                         seq_lens, weight_indices, lora_ranks, scalings, out, nblk);
-      break;
-    case PL_F16:
-      hipLaunchKernelGGL(pl_ref_expand<PL_F16>, grid, dim3(256), 0, s, x, B, M, k_max, L, N,
-                         seq_lens, weight_indices, lora_ranks, scalings, out, nblk);
-      break;
-    default:
-      hipLaunchKernelGGL(pl_ref_expand<PL_F32>, grid, dim3(256), 0, s, x, B, M, k_max, L, N,
-                         seq_lens, weight_indices, lora_ranks, scalings, out, nblk);
-  }
+  pl_dispatch(dtype, [&](auto dt) {
+    hipLaunchKernelGGL(pl_ref_expand<decltype(dt)::value>, grid, dim3(256), 0, s, x, B, M, k_max,
+                       L, N, seq_lens, weight_indices, lora_ranks, scalings, out, nblk);
+  });
   return pl_launch_status("pl_sgmv_lora_b_ref");
 }
 
 extern "C" int pl_lora_apply_rows(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
                                   int64_t ldy, int32_t N, const void* arena,
-                                  const pl_slot_entry* table, int32_t num_modules,
-                                  int32_t module, const int32_t* row_slot,
+                                  const pl_slot_entry* table, int32_t num_slots,
+                                  int32_t num_modules, int32_t module, const int32_t* row_slot,
                                   const int32_t* seq_lens, int32_t rows, int32_t row_len,
                                   float* tmp, int32_t ldt, int32_t epilogue, void* stream) {
   if (!valid_dtype(dtype)) {
@@ -243,7 +258,8 @@ extern "C" int pl_lora_apply_rows(int32_t dtype, const void* x, int64_t ldx, int
     return PL_ERR_ARG;
   }
   if (rows < 0 || row_len < 0 || K <= 0 || N <= 0 || ldx < K || ldy < N || ldt <= 0 ||
-      num_modules <= 0 || module < 0 || module >= num_modules) {
+      num_slots < 1 || num_slots > PL_MAX_SLOTS || num_modules <= 0 || module < 0 ||
+      module >= num_modules) {
     pl_set_error("pl_lora_apply_rows: bad sizes");
     return PL_ERR_ARG;
   }
@@ -262,28 +278,32 @@ extern "C" int pl_lora_apply_rows(int32_t dtype, const void* x, int64_t ldx, int
     pl_set_error("pl_lora_apply_rows: grid too large");
     return PL_ERR_LIMIT;
   }
+  pl_rows_args a;
+  a.x = x;
+  a.ldx = ldx;
+  a.K = K;
+  a.y = y;
+  a.ldy = ldy;
+  a.N = N;
+  a.arena = reinterpret_cast<const char*>(arena);
+  a.table = table;
+  a.num_slots = num_slots;
+  a.num_modules = num_modules;
+  a.module = module;
+  a.row_slot = row_slot;
+  a.seq_lens = seq_lens;
+  a.rows = rows;
+  a.row_len = row_len;
+  a.tmp = tmp;
+  a.ldt = ldt;
+  a.epilogue = epilogue;
+  a.nblk = nblk;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const char* ar = reinterpret_cast<const char*>(arena);
-  dim3 g1((unsigned)((T + 3) / 4));
-  dim3 g2((unsigned)(T * nblk));
-  switch (dtype) {
-    case PL_BF16:
-      hipLaunchKernelGGL(pl_rows_shrink<PL_BF16>, g1, dim3(256), 0, s, x, ldx, K, ar, table,
-                         num_modules, module, row_slot, seq_lens, rows, row_len, tmp, ldt);
-      hipLaunchKernelGGL(pl_rows_expand<PL_BF16>, g2, dim3(256), 0, s, tmp, ldt, ar, table,
-                         num_modules, module, row_slot, seq_lens, row_len, y, ldy, N, epilogue, nblk);
-      break;
-    case PL_F16:
-      hipLaunchKernelGGL(pl_rows_shrink<PL_F16>, g1, dim3(256), 0, s, x, ldx, K, ar, table,
-                         num_modules, module, row_slot, seq_lens, rows, row_len, tmp, ldt);
-      hipLaunchKernelGGL(pl_rows_expand<PL_F16>, g2, dim3(256), 0, s, tmp, ldt, ar, table,
-                         num_modules, module, row_slot, seq_lens, row_len, y, ldy, N, epilogue, nblk);
-      break;
-    default:
-      hipLaunchKernelGGL(pl_rows_shrink<PL_F32>, g1, dim3(256), 0, s, x, ldx, K, ar, table,
-                         num_modules, module, row_slot, seq_lens, rows, row_len, tmp, ldt);
-      hipLaunchKernelGGL(pl_rows_expand<PL_F32>, g2, dim3(256), 0, s, tmp, ldt, ar, table,
-                         num_modules, module, row_slot, seq_lens, row_len, y, ldy, N, epilogue, nblk);
-  }
+  const dim3 g1((unsigned)((T + 3) / 4));
+  const dim3 g2((unsigned)(T * nblk));
+  pl_dispatch(dtype, [&](auto dt) {
+    hipLaunchKernelGGL(pl_rows_shrink<decltype(dt)::value>, g1, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(pl_rows_expand<decltype(dt)::value>, g2, dim3(256), 0, s, a);
+  });
   return pl_launch_status("pl_lora_apply_rows");
 }

@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void pl_shrink_tiled(pl_shrink_args a) {
   if (g >= a.meta[0]) return;
   const pl_group grp = a.groups[g];
   const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module];
-  const int rank = e.rank;
+  const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
   if (rank <= 0) return;
   const int len = grp.len;
   const int nrt = (len + 15) >> 4;
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(256) void pl_expand_tiled(pl_expand_args a) {
   if (g >= a.meta[0]) return;
   const pl_group grp = a.groups[g];
   const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module];
-  const int rank = e.rank;
+  const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
   if (rank <= 0) return;
   const int r8 = e.rank8;
   const int N = a.N;
@@ -344,7 +344,7 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
     pl_set_error("null x or tmp pointer");
     return PL_ERR_ARG;
   }
-  if (K <= 0 || ldx < K || ldt <= 0 || (ldt & 3) != 0 || k_splits < 1) {
+  if (K <= 0 || ldx < K || ldt <= 0 || (ldt & 7) != 0 || k_splits < 1) {
     pl_set_error("bad shrink sizes K=%d ldx=%lld ldt=%d k_splits=%d", K, (long long)ldx, ldt,
                  k_splits);
     return PL_ERR_ARG;
@@ -398,7 +398,7 @@ int prepare_expand(pl_expand_args& a, int32_t dtype, const float* tmp, int32_t l
     pl_set_error("null y or tmp pointer");
     return PL_ERR_ARG;
   }
-  if (N <= 0 || ldy < N || ldt <= 0 || (ldt & 3) != 0) {
+  if (N <= 0 || ldy < N || ldt <= 0 || (ldt & 7) != 0) {
     pl_set_error("bad expand sizes N=%d ldy=%lld ldt=%d", N, (long long)ldy, ldt);
     return PL_ERR_ARG;
   }

@@ -162,6 +162,26 @@ def _tiled_ok(x: torch.Tensor, y: torch.Tensor) -> bool:
     )
 
 
+def _check_operands(x: torch.Tensor, y: torch.Tensor, cache, module_name: str, tokens: int) -> None:
+    """Shapes, dtypes and devices the kernels assume; a mismatch would read outside the arena."""
+    spec = cache.module_specs.get(module_name)
+    if spec is None:
+        raise KeyError(f"module {module_name!r} is not in the adapter cache")
+    if x.dim() != 2 or y.dim() != 2:
+        raise ValueError("x and y must be 2-D [tokens, features]")
+    if x.shape[0] != tokens or y.shape[0] != tokens:
+        raise ValueError(f"x / y have {x.shape[0]} / {y.shape[0]} token rows; the plan covers {tokens}")
+    if x.shape[1] != spec.in_features or y.shape[1] != spec.out_features:
+        raise ValueError(
+            f"module {module_name!r} is {spec.in_features} -> {spec.out_features}, "
+            f"got x [.., {x.shape[1]}] and y [.., {y.shape[1]}]"
+        )
+    if x.dtype != cache.dtype or y.dtype != cache.dtype:
+        raise TypeError(f"x {x.dtype} / y {y.dtype} must match the adapter cache dtype {cache.dtype}")
+    if x.device != cache.device or y.device != cache.device:
+        raise ValueError(f"x / y must be on the adapter cache device {cache.device}")
+
+
 def lora_apply(
     x: torch.Tensor,
     y: torch.Tensor,
@@ -179,6 +199,7 @@ def lora_apply(
     kernels when x / y do not meet the tiled path's alignment.
     """
     _require_gpu(x, "lora_apply")
+    _check_operands(x, y, cache, module_name, plan.tokens_cap)
     if not _tiled_ok(x, y):
         return lora_apply_rows(x, y, cache, module_name, plan.row_slot, plan.seq_lens, plan.row_len, epilogue=epilogue)
     lib = _native.load()
@@ -233,6 +254,9 @@ def lora_apply_rows(
 ) -> torch.Tensor:
     """Row-based HIP kernels on the slot arena: any K, N, stride or alignment."""
     _require_gpu(x, "lora_apply_rows")
+    _check_operands(x, y, cache, module_name, int(row_slot.numel()) * int(row_len))
+    if int(seq_lens.numel()) != int(row_slot.numel()):
+        raise ValueError("row_slot and seq_lens must have the same length")
     lib = _native.load()
     if x.stride(-1) != 1:
         x = x.contiguous()
@@ -254,6 +278,7 @@ def lora_apply_rows(
             int(y_work.shape[1]),
             cache.arena.data_ptr(),
             cache.table.data_ptr(),
+            cache.num_slots,
             len(cache.module_index),
             cache.module_index[module_name],
             row_slot.data_ptr(),
@@ -270,6 +295,14 @@ def lora_apply_rows(
     if y_work is not y:
         y.copy_(y_work)
     return y
+
+
+def _check_row_meta(B: int, num_adapters: int, seq_lens, weight_indices, lora_ranks, scalings=None) -> None:
+    """Per-row and per-adapter vectors must cover every row and adapter the kernels index."""
+    if int(seq_lens.numel()) != B or int(weight_indices.numel()) != B:
+        raise ValueError(f"seq_lens / weight_indices must have {B} entries")
+    if int(lora_ranks.numel()) < num_adapters or (scalings is not None and int(scalings.numel()) < num_adapters):
+        raise ValueError(f"lora_ranks / scalings must have an entry for each of the {num_adapters} adapters")
 
 
 def sgmv_lora_a_fwd(
@@ -297,6 +330,7 @@ def sgmv_lora_a_fwd(
     if weights.dtype != x.dtype:
         raise TypeError(f"weights dtype {weights.dtype} must match x dtype {x.dtype}")
     seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
+    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks)
     lib = _native.load()
     _native.check(
         lib.pl_sgmv_lora_a_ref(
@@ -309,6 +343,7 @@ def sgmv_lora_a_fwd(
             weights.stride(0),
             weights.stride(1),
             weights.stride(2),
+            int(weights.shape[0]),
             N_max,
             seq_lens.data_ptr(),
             weight_indices.data_ptr(),
@@ -350,6 +385,7 @@ def sgmv_lora_b_fwd(
     work = output if output.is_contiguous() else output.contiguous()
     seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
     scalings = scalings.to(torch.float32).contiguous()
+    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, scalings)
     lib = _native.load()
     _native.check(
         lib.pl_sgmv_lora_b_ref(
@@ -362,6 +398,7 @@ def sgmv_lora_b_fwd(
             weights.stride(0),
             weights.stride(1),
             weights.stride(2),
+            int(weights.shape[0]),
             N,
             seq_lens.data_ptr(),
             weight_indices.data_ptr(),

@@ -382,7 +382,7 @@ class CpuAdapterStore:
     @staticmethod
     def _validate_peft_config(config: Any) -> None:
         for name in ("use_dora", "lora_bias", "use_rslora"):
-            if hasattr(config, name) and getattr(config, name) is not False:
+            if hasattr(config, name) and getattr(config, name) != False:  # noqa: E712 (store.py:397)
                 raise ValueError(f"Unsupported PEFT LoRA option: {name}={getattr(config, name)!r}")
         if getattr(config, "lora_dropout", 0.0) not in (0, 0.0):
             raise ValueError("LoRA dropout is not supported by the inference runtime")

@@ -1,0 +1,366 @@
+"""Host logic without a GPU: config, PEFT parsing, CPU/disk tiers, slot cache, C-ABI surface.
+
+The reference's tests (tests/test_polylora_peft.py) compare against PEFT,
+which is not installed; their assertions on slots, ranks, scales, errors and
+cache tiers are restated here on fixtures this suite writes in PEFT's file
+layout.  The slot cache runs on a CPU device here (its uploads become host
+copies), so the packed arena and the slot table can be checked byte for byte
+against the reference-layout tensors of the oracle.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.lora import dense_slot_tensors
+from oracle.slots import SlotCacheModel
+from polylora_amd import PolyLoraConfig, PolyLoraModel, _native
+from polylora_amd.cache import GpuAdapterCache, ModuleSpec, SlotLayout, pack_adapter
+from polylora_amd.context import LoraBatchContext, assert_right_padded, get_lora_context, use_lora_context
+from polylora_amd.store import CpuAdapterStore, CpuLayerWeights, DiskAdapterCache
+from tests import _peft
+
+ROOT = Path(__file__).resolve().parents[1]
+TARGETS = ["query_proj", "key_proj", "value_proj", "dense"]
+
+
+# --------------------------------------------------------------------------- config
+
+
+def test_config_validation_messages():
+    with pytest.raises(ValueError, match="max_gpu_adapters must be at least 1"):
+        PolyLoraConfig(max_gpu_adapters=0, max_rank=4)
+    with pytest.raises(ValueError, match="max_cpu_adapters must be at least max_gpu_adapters"):
+        PolyLoraConfig(max_gpu_adapters=3, max_rank=4, max_cpu_adapters=2)
+    with pytest.raises(ValueError, match="max_disk_adapters must be at least 1"):
+        PolyLoraConfig(max_gpu_adapters=1, max_rank=4, disk_cache_dir="/tmp/x", max_disk_adapters=0)
+    with pytest.raises(ValueError, match="disk_cache_dir must be set"):
+        PolyLoraConfig(max_gpu_adapters=1, max_rank=4, max_disk_adapters=2)
+    with pytest.raises(ValueError, match="max_rank must be at least 1"):
+        PolyLoraConfig(max_gpu_adapters=1, max_rank=0)
+    with pytest.raises(ValueError, match="target_modules must not be empty"):
+        PolyLoraConfig(max_gpu_adapters=1, max_rank=4, target_modules=[])
+    cfg = PolyLoraConfig(max_gpu_adapters=2, max_rank=8)
+    assert cfg.base_adapter_id == "__base__" and cfg.enforce_right_padding and cfg.use_triton_kernels
+    from polylora_amd import CustomLoraConfig, CustomPeftModel
+
+    assert CustomLoraConfig is PolyLoraConfig and CustomPeftModel is PolyLoraModel
+
+
+# --------------------------------------------------------------------------- store: PEFT parsing
+
+
+def _shapes():
+    return {"enc.q_proj": (6, 4), "enc.v_proj": (6, 5)}
+
+
+def test_peft_state_dict_layout_and_scale():
+    g = torch.Generator().manual_seed(0)
+    w = _peft.make_lora_weights(g, _shapes(), rank=3)
+    store = CpuAdapterStore()
+    for name in (None, "ad"):
+        store.add_adapter_from_peft_state_dict(
+            f"x{name}", _peft.state_dict(w, name), list(_shapes()), lora_alpha=9, peft_adapter_name=name or "default"
+        )
+        layers = store.adapters[f"x{name}"].layers
+        for mod, (a, b) in w.items():
+            assert torch.equal(layers[mod].A, a.t()) and torch.equal(layers[mod].B, b.t())
+            assert layers[mod].rank == 3 and layers[mod].scale == 3.0
+
+
+def test_peft_rejects_outside_module_set_and_incomplete_pair():
+    g = torch.Generator().manual_seed(1)
+    w = _peft.make_lora_weights(g, _shapes(), rank=2)
+    store = CpuAdapterStore()
+    with pytest.raises(ValueError, match="outside the configured module set"):
+        store.add_adapter_from_peft_state_dict("a", _peft.state_dict(w, "a"), ["enc.v_proj"], 4, "a")
+    sd = {k: v for k, v in _peft.state_dict(w, "a").items() if ".lora_B." not in k}
+    with pytest.raises(ValueError, match="incomplete LoRA weights"):
+        store.add_adapter_from_peft_state_dict("a", sd, list(_shapes()), 4, "a")
+    with pytest.raises(ValueError, match="reserved for base-only rows"):
+        store.add_adapter("__base__", {"m": CpuLayerWeights(torch.zeros(2, 1), torch.zeros(1, 2), 1, 1.0)})
+    with pytest.raises(ValueError, match="at least one target layer"):
+        store.add_adapter("e", {})
+
+
+def test_sparse_adapter_missing_modules_are_rank_zero():
+    g = torch.Generator().manual_seed(2)
+    w = _peft.make_lora_weights(g, _shapes(), rank=2, modules=["enc.v_proj"])
+    store = CpuAdapterStore()
+    store.add_adapter_from_peft_state_dict("s", _peft.state_dict(w, "s"), list(_shapes()), 4, "s")
+    cache = _cpu_cache(store, _shapes(), 1, 2)
+    cache.ensure_resident(["s"])
+    slot = cache.adapter_to_slot["s"]
+    assert int(cache.ranks["enc.q_proj"][slot]) == 0 and float(cache.scales["enc.q_proj"][slot]) == 0.0
+    assert int(cache.ranks["enc.v_proj"][slot]) == 2 and float(cache.scales["enc.v_proj"][slot]) == 2.0
+
+
+@pytest.mark.parametrize("fmt", ["safetensors", "bin"])
+def test_load_from_disk_formats(tmp_path, fmt):
+    g = torch.Generator().manual_seed(3)
+    w = _peft.make_lora_weights(g, _shapes(), rank=4)
+    path = _peft.write_adapter_dir(tmp_path / "ad", w, 4, 8, fmt=fmt)
+    store = CpuAdapterStore()
+    store.load_adapter_from_disk("a", path, list(_shapes()))
+    for mod, (a, b) in w.items():
+        assert torch.equal(store.adapters["a"].layers[mod].A, a.t())
+        assert store.adapters["a"].layers[mod].scale == 2.0
+
+
+@pytest.mark.parametrize(
+    "extra,msg",
+    [
+        ({"peft_type": "IA3"}, "Unsupported PEFT adapter type"),
+        ({"use_dora": True}, "DoRA adapters are not supported"),
+        ({"use_rslora": True}, "RS-LoRA adapters are not supported"),
+        ({"lora_bias": True}, "LoRA bias is not supported"),
+        ({"lora_dropout": 0.1}, "LoRA dropout is not supported"),
+    ],
+)
+def test_peft_config_validation(tmp_path, extra, msg):
+    g = torch.Generator().manual_seed(4)
+    w = _peft.make_lora_weights(g, _shapes(), rank=2)
+    path = _peft.write_adapter_dir(tmp_path / "ad", w, 2, 4, extra_config=extra)
+    with pytest.raises(ValueError, match=msg):
+        CpuAdapterStore().load_adapter_from_disk("a", path, list(_shapes()))
+
+
+def test_cpu_lru_and_disk_reload(tmp_path):
+    """tests/test_polylora_peft.py:484-550: a CPU miss reloads from the disk cache."""
+    g = torch.Generator().manual_seed(5)
+    disk = DiskAdapterCache(tmp_path / "disk", 2)
+    store = CpuAdapterStore(max_adapters=1, disk_cache=disk, module_names=list(_shapes()))
+    ws = {}
+    for aid in ("a", "b"):
+        ws[aid] = _peft.make_lora_weights(g, _shapes(), rank=2)
+        store.load_adapter_from_disk(aid, _peft.write_adapter_dir(tmp_path / f"src_{aid}", ws[aid], 2, 4, fmt="bin"), list(_shapes()))
+    assert "a" not in store.adapters and "a" in store
+    got = store.get("a")
+    assert "a" in store.adapters and "b" not in store.adapters
+    assert torch.equal(got.layers["enc.q_proj"].A, ws["a"]["enc.q_proj"][0].t())
+
+
+def test_disk_cache_evicts_oldest_directory(tmp_path):
+    """tests/test_polylora_peft.py:553-609."""
+    g = torch.Generator().manual_seed(6)
+    disk = DiskAdapterCache(tmp_path / "disk", 2)
+    store = CpuAdapterStore(max_adapters=1, disk_cache=disk, module_names=list(_shapes()))
+    src = {}
+    for aid in ("a", "b", "c"):
+        src[aid] = _peft.write_adapter_dir(tmp_path / f"src_{aid}", _peft.make_lora_weights(g, _shapes(), 2), 2, 4)
+        store.load_adapter_from_disk(aid, src[aid], list(_shapes()))
+    assert "a" not in store
+    assert list(disk.entries) == ["b", "c"]
+    dirs = [p for p in (tmp_path / "disk").iterdir() if p.is_dir()]
+    assert len(dirs) == 2 and all(p != src["a"] for p in dirs)
+    # the manifest survives a restart
+    again = DiskAdapterCache(tmp_path / "disk", 2)
+    assert list(again.entries) == ["b", "c"]
+
+
+def test_cpu_store_never_evicts_gpu_resident():
+    store = CpuAdapterStore(max_adapters=1)
+    lw = {"m": CpuLayerWeights(torch.zeros(2, 1), torch.zeros(1, 2), 1, 1.0)}
+    store.add_adapter("a", lw)
+    store.set_eviction_exclusions({"a"})
+    with pytest.raises(RuntimeError, match="No evictable CPU LoRA adapter"):
+        store.add_adapter("b", lw)
+
+
+# --------------------------------------------------------------------------- GPU slot cache (CPU device)
+
+
+def _cpu_cache(store, shapes, max_gpu, max_rank, dtype=torch.float32):
+    cfg = PolyLoraConfig(max_gpu_adapters=max_gpu, max_rank=max_rank)
+    specs = [ModuleSpec(n, i, o) for n, (i, o) in shapes.items()]
+    return GpuAdapterCache(store, specs, cfg, torch.device("cpu"), dtype)
+
+
+def _store_with(ws: dict, alphas: dict) -> CpuAdapterStore:
+    store = CpuAdapterStore()
+    for aid, w in ws.items():
+        store.add_adapter_from_peft_state_dict(aid, _peft.state_dict(w), sorted({m for m in w}), alphas[aid])
+    return store
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_slot_arena_matches_reference_layout_bit_exact(dtype):
+    g = torch.Generator().manual_seed(7)
+    shapes = {"l0.q": (24, 16), "l0.o": (16, 40), "l1.q": (24, 16)}
+    ranks = {"a": 3, "b": 8, "c": 5}
+    ws = {aid: _peft.make_lora_weights(g, shapes, r, modules=None if aid != "c" else ["l0.o"]) for aid, r in ranks.items()}
+    store = _store_with(ws, {"a": 6, "b": 4, "c": 5})
+    cache = _cpu_cache(store, shapes, 3, 8, dtype)
+    slots_ = cache.ensure_resident(["c", "__base__", "a", "b", "a"])
+    assert slots_.dtype == torch.int32
+    assert slots_.tolist() == [3, 0, 1, 2, 1]  # sorted load order into the lowest free slots
+    for mod, (fin, fout) in shapes.items():
+        per_slot = [None] + [
+            None if mod not in ws[cache.slot_to_adapter[s]] else (*ws[cache.slot_to_adapter[s]][mod], {"a": 6, "b": 4, "c": 5}[cache.slot_to_adapter[s]])
+            for s in range(1, 4)
+        ]
+        A, B, rk, sc = dense_slot_tensors(per_slot, fin, fout, 8, dtype)
+        assert torch.equal(cache.A[mod], A)
+        assert torch.equal(cache.B[mod], B)
+        assert torch.equal(cache.ranks[mod], rk)
+        assert torch.equal(cache.scales[mod], sc)
+    # base slot 0: rank 0 and scale 0 in every module (tests/test_polylora_peft.py:323-326)
+    assert cache.adapter_to_slot["__base__"] == 0
+    assert all(int(cache.ranks[m][0]) == 0 and float(cache.scales[m][0]) == 0.0 for m in shapes)
+
+
+def test_slot_cache_matches_slot_model_under_churn():
+    """Same slot trace as the restated bookkeeping for a long random id sequence."""
+    g = torch.Generator().manual_seed(8)
+    rng = np.random.default_rng(8)
+    shapes = {"m": (8, 8)}
+    ids = [f"ad{i:02d}" for i in range(12)]
+    ws = {aid: _peft.make_lora_weights(g, shapes, 1 + i % 4) for i, aid in enumerate(ids)}
+    store = _store_with(ws, {aid: 2.0 for aid in ids})
+    cache = _cpu_cache(store, shapes, 4, 4)
+    model = SlotCacheModel(4)
+    for step in range(60):
+        batch = [ids[int(i)] if rng.random() > 0.2 else "__base__" for i in rng.integers(0, 12, size=5)]
+        distinct = {a for a in batch if a != "__base__"}
+        if len(distinct) > 4:
+            with pytest.raises(RuntimeError, match="more adapters than GPU cache capacity"):
+                cache.ensure_resident(batch)
+            continue
+        got = cache.ensure_resident(batch).tolist()
+        want = model.ensure_resident(batch, set(ids))
+        assert got == want, step
+        assert cache.slot_to_adapter == model.slot_to_adapter
+        assert list(cache.lru) == list(model.lru)
+        for s, aid in enumerate(cache.slot_to_adapter):
+            want_rank = 0 if s == 0 or aid is None else ws[aid]["m"][0].shape[0]
+            assert int(cache.ranks["m"][s]) == want_rank
+
+
+def test_slot_reload_cycle_and_errors():
+    g = torch.Generator().manual_seed(9)
+    shapes = {"m": (8, 8)}
+    ws = {aid: _peft.make_lora_weights(g, shapes, 2) for aid in ("a", "b")}
+    cache = _cpu_cache(_store_with(ws, {"a": 4, "b": 4}), shapes, 1, 2)
+    for aid in ("a", "b", "a"):
+        cache.ensure_resident([aid])
+        assert cache.slot_to_adapter[1] == aid
+        assert torch.equal(cache.A["m"][1], ws[aid]["m"][0].t())
+    with pytest.raises(KeyError, match="Unknown LoRA adapter"):
+        cache.ensure_resident(["nope"])
+    with pytest.raises(RuntimeError, match="more adapters than GPU cache capacity"):
+        cache.ensure_resident(["a", "b"])
+    big = {"m": (torch.zeros(3, 8), torch.zeros(8, 3))}
+    store = _store_with({"r3": big}, {"r3": 3})
+    with pytest.raises(ValueError, match="exceeds max_rank"):
+        _cpu_cache(store, shapes, 1, 2).ensure_resident(["r3"])
+
+
+def test_pack_adapter_layout():
+    shapes = {"x": (16, 24), "y": (8, 8)}
+    a = torch.arange(3 * 16, dtype=torch.float32).reshape(3, 16)
+    b = torch.arange(24 * 3, dtype=torch.float32).reshape(24, 3)
+    store = CpuAdapterStore()
+    store.add_adapter("p", {"x": CpuLayerWeights(a.t().contiguous(), b.t().contiguous(), 3, 1.5)})
+    layout = SlotLayout([ModuleSpec(n, i, o) for n, (i, o) in shapes.items()], torch.bfloat16, 6)
+    packed = pack_adapter(store.adapters["p"], layout)
+    rows = packed.rows
+    assert rows[0, 0] == 3 and rows[0, 2] == 8 and rows.view(np.float32)[0, 1] == np.float32(1.5)
+    a_off, b_off = int(rows.view(np.int64)[0, 2]), int(rows.view(np.int64)[0, 3])
+    assert a_off % 256 == 0 and b_off % 256 == 0
+    img = packed.image
+    A = img[a_off : a_off + 3 * 16 * 2].view(torch.bfloat16).view(3, 16)
+    B = img[b_off : b_off + 24 * 8 * 2].view(torch.bfloat16).view(24, 8)
+    assert torch.equal(A, a.bfloat16()) and torch.equal(B[:, :3], b.bfloat16())
+    assert torch.equal(B[:, 3:], torch.zeros(24, 5, dtype=torch.bfloat16))  # rank padding is zero
+    assert rows[1].tolist() == [0] * 8  # module without weights: rank 0, scale 0
+    assert layout.rank8_cap == 8
+
+
+# --------------------------------------------------------------------------- context and model wrapper
+
+
+def test_context_var_protocol():
+    assert get_lora_context() is None
+    ctx = LoraBatchContext(["a"], torch.tensor([1], dtype=torch.int32), torch.tensor([3], dtype=torch.int32))
+    with use_lora_context(ctx):
+        assert get_lora_context() is ctx
+    assert get_lora_context() is None
+
+
+def test_assert_right_padded():
+    mask = torch.tensor([[1, 1, 0], [1, 1, 1]])
+    assert_right_padded(mask, mask.sum(-1))
+    with pytest.raises(ValueError, match="right-padded attention_mask"):
+        bad = torch.tensor([[0, 1, 1]])
+        assert_right_padded(bad, bad.sum(-1))
+    with pytest.raises(ValueError, match="2D batch mask"):
+        assert_right_padded(torch.ones(2, 2, 2), torch.tensor([2, 2]))
+
+
+def test_model_wrapping_and_cpu_lora_refuses():
+    model = _peft.tiny_deberta(0)
+    pm = PolyLoraModel(model, PolyLoraConfig(max_gpu_adapters=2, max_rank=3, target_modules=TARGETS))
+    names = pm.target_module_names
+    assert len(names) == 6  # q, k, v, attention.output.dense, intermediate.dense, output.dense
+    assert all(type(pm.base_model.get_submodule(n)).__name__ == "MultiLoraLinear" for n in names)
+    ids = torch.tensor([[1, 5, 6, 2]])
+    with torch.inference_mode():
+        base = pm(input_ids=ids).last_hidden_state  # no adapter_ids: plain base model
+    assert base.shape == (1, 4, 32)
+    g = torch.Generator().manual_seed(0)
+    w = _peft.make_lora_weights(g, {sp.name: (sp.in_features, sp.out_features) for sp in pm.module_specs}, 2)
+    pm.adapter_store.add_adapter_from_peft_state_dict("a", _peft.state_dict(w, "a"), names, 4, "a")
+    with pytest.raises(RuntimeError, match="only on a ROCm GPU"):
+        with torch.inference_mode():
+            pm(input_ids=ids, adapter_ids=["a"])
+    with pytest.raises(ValueError, match="adapter_ids length must match batch size"):
+        pm(input_ids=ids, adapter_ids=["a", "a"])
+    with pytest.raises(ValueError, match="No nn.Linear modules matched"):
+        PolyLoraModel(_peft.tiny_deberta(0), PolyLoraConfig(max_gpu_adapters=1, max_rank=2, target_modules=["nothing"]))
+
+
+# --------------------------------------------------------------------------- C-ABI surface
+
+
+def _header_functions() -> list[str]:
+    text = (ROOT / "include" / "polylora_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(pl_[a-z_0-9]+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_native.LIB_PATH))
+    declared = _header_functions()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_host_side_errors_without_gpu():
+    """Argument checks run before any HIP call, so they are testable on the CPU."""
+    lib = _native.load()
+    assert lib.pl_version() >= 100
+    assert lib.pl_plan_group_capacity(256, 1, 65) == 4 + 64
+    assert lib.pl_plan_group_capacity(32, 1024, 9) == 512 + 8
+    fake = ctypes.c_void_p(64)  # never dereferenced: the size check fails first
+    assert lib.pl_plan_build(fake, fake, 4, 1, 5000, fake, fake, fake, 100, None) == 4  # PL_ERR_LIMIT
+    assert b"exceed the maximum" in lib.pl_last_error()
+    st = lib.pl_sgmv_shrink(7, None, 0, 0, None, None, 1, 0, None, None, None, 1, None, 8, 1, None, 0, None)
+    assert st == 1 and b"dtype" in lib.pl_last_error()
+    with pytest.raises(RuntimeError, match="dtype"):
+        _native.check(st, "pl_sgmv_shrink")
+
+
+def test_no_cpu_fallback_in_product_ops():
+    from polylora_amd import sgmv
+
+    x = torch.randn(2, 3, 4)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        sgmv.sgmv_lora_a_fwd(x, torch.randn(2, 4, 2), torch.tensor([3, 3]), torch.tensor([0, 1]), torch.tensor([0, 2]))
