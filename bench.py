@@ -1,15 +1,27 @@
-"""Benchmark: SGMV achieved HBM GB/s on one MI355X (isolated op, bf16).
+"""Benchmark of the multi-LoRA SGMV path on one MI355X.
 
-Default workload: T=4096 tokens, K=N=4096, 16 adapter slots + the base slot,
-ranks cycling {0,4,8,16} by slot, alpha=32 (scale 32/r), tokens sorted into
-contiguous per-slot segments with Dirichlet(1) lengths, X and base Y ~N(0,1),
-A and B ~N(0,0.02).  One step = the LoRA shrink + expand of all tokens
-(``pl_lora_apply``) with the device plan already built (it is built once per
-forward and shared by every wrapped Linear).  Inputs rotate over enough X/Y
-sets (> 512 MB) that the 256 MB Infinity Cache cannot hold them.
+Headline (``value``): SGMV achieved HBM GB/s on the isolated op, bf16:
+T=4096 tokens, K=N=4096, 16 adapter slots + the base slot, ranks cycling
+{0,4,8,16} by slot, alpha=32 (scale 32/r), tokens sorted into contiguous
+per-slot segments with Dirichlet(1) lengths, X and base Y ~N(0,1), A and B
+~N(0,0.02).  One step = the LoRA shrink + expand of all tokens
+(``pl_lora_apply``) with the device plan already built (one plan per forward
+is shared by every wrapped Linear).  Inputs rotate over enough X/Y sets
+(> 512 MB) that the 256 MB Infinity Cache cannot hold them.
 
-Prints one JSON line (see ``--help``).  ``--gpus`` above 1 exits: this build
-measures one GPU.
+Also reported in the same JSON line (``workloads``):
+
+* ``decode``  Llama-3-8B-shaped decoder (32 layers, hidden 4096, 32/8 heads,
+  head_dim 128, FFN 14336, random init, bf16), LoRA on q/k/v/o/gate/up/down,
+  64 slots, max_rank 64, ranks {8,16,32,64}, alpha 2r; batch 256 rows x one
+  new token over a 512-token random KV cache; adapter_ids Zipf(1.1) over 64
+  adapters with 10% __base__ rows.  Multi-LoRA tokens/s against the same
+  model with no adapters (HIP-graph replay of one decode step, and eager),
+  and the 224 shrink+expand pairs of one step timed alone (HBM GB/s).
+* ``deberta`` DeBERTa-v3-base shape, fp32, 5 adapters, B=8, S=128 (tokens/s).
+* ``prefill`` / ``churn`` with ``--prefill`` / ``--churn``.
+
+``--gpus`` above 1 exits: this build measures one GPU.
 """
 
 from __future__ import annotations
@@ -20,16 +32,194 @@ import os
 import platform
 import sys
 import time
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 import torch
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+METRIC = "SGMV achieved HBM GB/s (% peak); multi-LoRA decode tokens/s, 1 MI355X"
+
+LLAMA_TARGETS = ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"]
+DEBERTA_TARGETS = ["query_proj", "key_proj", "value_proj", "dense"]
 
 
-# ----------------------------------------------------------------------------- workloads
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------------------- base-model attention
+def _safe_fp32_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """Attention in fp32 with contiguous operands (no bf16 batched product on a transposed view)."""
+    groups = query.shape[1] // key.shape[1]
+    q, k, v = query.float(), key.float(), value.float()
+    if groups > 1:
+        k = k.repeat_interleave(groups, dim=1)
+        v = v.repeat_interleave(groups, dim=1)
+    scale = scaling if scaling is not None else q.shape[-1] ** -0.5
+    w = torch.matmul(q, k.transpose(2, 3).contiguous()) * scale
+    if attention_mask is not None:
+        m = attention_mask[..., : k.shape[2]]
+        w = w.masked_fill(~m, float("-inf")) if m.dtype == torch.bool else w + m.float()
+    w = torch.softmax(w, dim=-1)
+    out = torch.matmul(w, v.contiguous()).transpose(1, 2).contiguous()
+    return out.to(query.dtype), None
+
+
+_GQA_NATIVE = {"ok": None}  # None: untried; True/False once a fused kernel accepted or refused enable_gqa
+
+
+def _fused_sdpa_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, is_causal=None,
+                          **kwargs):
+    """torch SDPA restricted to its fused kernels (raises instead of taking the math path).
+
+    Grouped-query heads go to the kernel as they are (enable_gqa) when it
+    accepts them; otherwise K/V are expanded to the query heads first.
+    """
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    groups = query.shape[1] // key.shape[1]
+    if is_causal is None:
+        is_causal = query.shape[2] > 1 and attention_mask is None and getattr(module, "is_causal", True)
+    kw = dict(attn_mask=attention_mask, dropout_p=0.0, scale=scaling, is_causal=bool(is_causal))
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        out = None
+        if groups > 1 and _GQA_NATIVE["ok"] is not False:
+            try:
+                out = F.scaled_dot_product_attention(query, key, value, enable_gqa=True, **kw)
+                _GQA_NATIVE["ok"] = True
+            except RuntimeError:
+                if _GQA_NATIVE["ok"]:
+                    raise
+                _GQA_NATIVE["ok"] = False
+        if out is None:
+            if groups > 1:
+                key = key.repeat_interleave(groups, dim=1)
+                value = value.repeat_interleave(groups, dim=1)
+            out = F.scaled_dot_product_attention(query, key, value, **kw)
+    return out.transpose(1, 2).contiguous(), None
+
+
+def _fused_sdpa_mask(*args, **kwargs):
+    """sdpa masks, except a single decode query with no padding mask gets none.
+
+    The decode workloads here attend over a cache that is exactly full (512
+    cached positions + the new one), so every key is visible and the mask
+    would be all true; passing none lets SDPA's flash kernel take the step.
+    """
+    from transformers.masking_utils import sdpa_mask
+
+    q_length = kwargs.get("q_length", args[1] if len(args) > 1 else None)
+    if kwargs.get("attention_mask") is None and q_length == 1:
+        return None
+    return sdpa_mask(*args, **kwargs)
+
+
+def register_attention() -> None:
+    """Register "pl_safe_fp32" (eager masks) and "pl_fused_sdpa" (sdpa masks) with transformers."""
+    from transformers import AttentionInterface
+    from transformers.masking_utils import AttentionMaskInterface, eager_mask
+
+    AttentionInterface.register("pl_safe_fp32", _safe_fp32_attention)
+    AttentionMaskInterface.register("pl_safe_fp32", eager_mask)
+    AttentionInterface.register("pl_fused_sdpa", _fused_sdpa_attention)
+    AttentionMaskInterface.register("pl_fused_sdpa", _fused_sdpa_mask)
+
+
+# ----------------------------------------------------------------------------- adapters
+def _lora_pair(gen, fin, fout, rank, std, device):
+    a = (torch.randn(rank, fin, generator=gen, device=device) * std).to(torch.bfloat16).cpu()
+    b = (torch.randn(fout, rank, generator=gen, device=device) * std).to(torch.bfloat16).cpu()
+    return a, b
+
+
+def add_random_adapters(pm, ranks: dict, std: float = 0.02, seed: int = 0, device="cpu", alpha_per_rank: float = 2.0):
+    """Random PEFT-layout adapters (all target modules) added to pm's CPU store; returns id -> rank."""
+    from polylora_amd.store import CpuLayerWeights
+
+    gen = torch.Generator(device=device).manual_seed(seed)
+    for aid, r in ranks.items():
+        layers = {}
+        for spec in pm.module_specs:
+            a, b = _lora_pair(gen, spec.in_features, spec.out_features, r, std, device)
+            layers[spec.name] = CpuLayerWeights(A=a.t().contiguous(), B=b.t().contiguous(), rank=r, scale=alpha_per_rank)
+        pm.adapter_store.add_adapter(aid, layers)
+    return ranks
+
+
+# ----------------------------------------------------------------------------- config 1: DeBERTa fp32
+@dataclass
+class DebertaWorkload:
+    model: object  # PolyLoraModel
+    base: object  # plain DebertaV2Model with the same weights
+    inputs: dict
+    adapter_ids: list
+    adapters: dict  # id -> ({module: (lora_A, lora_B)}, alpha)
+
+
+def deberta_workload(device, seed: int = 1001, layers: int = 12) -> DebertaWorkload:
+    """DeBERTa-v3-base shape fp32, q/k/v/dense targets, 5 adapters r {4,8,8,16,16} (last: q/v only), B=8, S=128."""
+    import copy
+
+    from transformers import DebertaV2Config, DebertaV2Model
+
+    from polylora_amd import PolyLoraConfig, PolyLoraModel
+
+    torch.manual_seed(seed)
+    cfg = DebertaV2Config(vocab_size=32000, hidden_size=768, num_hidden_layers=layers, num_attention_heads=12,
+                          intermediate_size=3072, hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0,
+                          initializer_range=0.02)
+    base = DebertaV2Model(cfg).to(device).eval()
+    pm = PolyLoraModel(copy.deepcopy(base), PolyLoraConfig(target_modules=DEBERTA_TARGETS, max_gpu_adapters=4, max_rank=16)).eval()
+    gen = torch.Generator().manual_seed(seed)
+    adapters = {}
+    for i, r in enumerate([4, 8, 8, 16, 16]):
+        mods = [s for s in pm.module_specs if i < 4 or s.name.endswith(("query_proj", "value_proj"))]
+        w = {s.name: (torch.randn(r, s.in_features, generator=gen) * 0.02, torch.randn(s.out_features, r, generator=gen) * 0.02) for s in mods}
+        aid = f"deb{i}"
+        from polylora_amd.store import CpuLayerWeights
+
+        pm.adapter_store.add_adapter(aid, {m: CpuLayerWeights(a.t().contiguous(), b.t().contiguous(), r, 2.0) for m, (a, b) in w.items()})
+        adapters[aid] = (w, 2.0 * r)
+    B, S = 8, 128
+    choices = list(adapters) + ["__base__"]
+    while True:  # at most 4 distinct adapters per batch (4 GPU slots)
+        pick = torch.randint(0, len(choices), (B,), generator=gen).tolist()
+        ids = [choices[i] for i in pick]
+        if len({a for a in ids if a != "__base__"}) <= 4:
+            break
+    lens = torch.randint(32, S + 1, (B,), generator=gen)
+    mask = (torch.arange(S)[None, :] < lens[:, None]).long()
+    input_ids = torch.randint(0, 32000, (B, S), generator=gen)
+    inputs = {"input_ids": input_ids.to(device), "attention_mask": mask.to(device)}
+    return DebertaWorkload(pm, base, inputs, ids, adapters)
+
+
+def run_deberta(device, reps: int = 20) -> dict:
+    wl = deberta_workload(device)
+    valid = int(wl.inputs["attention_mask"].sum())
+    with torch.inference_mode():
+        for _ in range(3):
+            wl.model(**wl.inputs, adapter_ids=wl.adapter_ids)
+            wl.model(**wl.inputs)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            wl.model(**wl.inputs, adapter_ids=wl.adapter_ids)
+        torch.cuda.synchronize()
+        lora_s = (time.perf_counter() - t0) / reps
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            wl.model(**wl.inputs)
+        torch.cuda.synchronize()
+        base_s = (time.perf_counter() - t0) / reps
+    return {"dtype": "f32", "valid_tokens": valid, "lora_tokens_per_s": round(valid / lora_s, 1),
+            "base_tokens_per_s": round(valid / base_s, 1), "ratio": round(base_s / lora_s, 4), "timing": "eager wall clock"}
+
+
+# ----------------------------------------------------------------------------- config 2: isolated SGMV
 @dataclass
 class IsolatedSgmv:
     cache: object
@@ -98,15 +288,13 @@ def isolated_sgmv_bytes(wl: IsolatedSgmv, K: int, N: int) -> dict:
     active = [s for s in range(len(wl.ranks)) if wl.ranks[s] > 0]
     t_active = int(sum(wl.seg_lens[s] for s in active))
     r_tok = int(sum(wl.seg_lens[s] * wl.ranks[s] for s in active))
-    ab = sum(2 * wl.ranks[s] * (K + N) for s in active)
     shrink = 2 * t_active * K + sum(2 * wl.ranks[s] * K for s in active)
     expand = 4 * t_active * N + sum(2 * wl.ranks[s] * N for s in active)
-    total = 2 * t_active * K + 4 * t_active * N + ab + 4 * len(wl.ranks) * 2
+    total = shrink + expand + 4 * len(wl.ranks) * 2
     flops = 2 * r_tok * (K + N)
     return {"total": total, "shrink": shrink, "expand": expand, "t_active": t_active, "flops": flops}
 
 
-# ----------------------------------------------------------------------------- CPU baseline
 def cpu_baseline_isolated(wl: IsolatedSgmv, nbytes: int, budget_s: float) -> dict:
     """The reference fallback (oracle restatement of layers.py:112-134) on the host.
 
@@ -151,51 +339,47 @@ def cpu_baseline_isolated(wl: IsolatedSgmv, nbytes: int, budget_s: float) -> dic
     }
 
 
-# ----------------------------------------------------------------------------- GPU timing
-def _time_isolated(wl_sets, steps: int, warmup: int, lib_apply) -> tuple[float, list]:
-    for i in range(warmup):
-        lib_apply(wl_sets[i % len(wl_sets)])
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        lib_apply(wl_sets[i % len(wl_sets)])
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, []
+class KernelTimer:
+    """Shrink and expand launched separately, each bracketed by events on the launch stream."""
 
+    def __init__(self):
+        from polylora_amd import _native
 
-def _kernel_times(wl_sets, reps: int) -> tuple[float, float]:
-    """Average shrink and expand durations, each bracketed by events on the launch stream."""
-    from polylora_amd import _native, sgmv
+        self.lib = _native.load()
+        self.native = _native
+        self.stream = torch.cuda.current_stream()
+        self.events = []
 
-    lib = _native.load()
-    stream = torch.cuda.current_stream()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
-    for i in range(reps):
-        wl = wl_sets[i % len(wl_sets)]
-        cache, plan = wl.cache, wl.plan
+    def run(self, x, y, cache, module, plan, k_splits=None):
+        from polylora_amd import sgmv
+
+        n = self.native
+        dt = n.dtype_code(x.dtype)
+        K, N = int(x.shape[1]), int(y.shape[1])
+        splits = k_splits if k_splits is not None else sgmv.choose_k_splits(plan.group_cap, K, x.dtype)
+        rows = max(1, plan.tokens_cap)
         ldt = cache.rank8_cap
-        ws = sgmv._workspace(wl.x.device, stream.cuda_stream)
-        splits = sgmv.choose_k_splits(plan.group_cap, wl.x.shape[1], wl.x.dtype)
-        need = plan.tokens_cap * ldt
-        slot, buf, zp, zc = ws.acquire(need)
-        common = (cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), cache.module_index["op"],
-                  plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), plan.group_cap)
-        ev[i][0].record(stream)
-        st = lib.pl_sgmv_shrink(_native.PL_BF16, wl.x.data_ptr(), wl.x.stride(0), wl.x.shape[1], *common,
-                                buf.data_ptr(), ldt, splits, zp or None, zc, stream.cuda_stream)
-        ev[i][1].record(stream)
-        st2 = lib.pl_sgmv_expand(_native.PL_BF16, buf.data_ptr(), ldt, *common, wl.y.data_ptr(), wl.y.stride(0),
-                                 wl.y.shape[1], _native.PL_EPI_FALLBACK, stream.cuda_stream)
-        ev[i][2].record(stream)
-        ws.commit(slot, need, st == 0 and st2 == 0)
-        _native.check(st, "pl_sgmv_shrink")
-        _native.check(st2, "pl_sgmv_expand")
-    torch.cuda.synchronize()
-    sh = sum(e[0].elapsed_time(e[1]) for e in ev) / reps
-    ex = sum(e[1].elapsed_time(e[2]) for e in ev) / reps
-    return sh, ex
+        nbytes = int(self.lib.pl_shrink_workspace_bytes(dt, K, splits, rows, ldt))
+        planes = int(self.lib.pl_shrink_planes(dt, K, splits))
+        buf = sgmv._workspace(x.device, self.stream.cuda_stream).get(nbytes)
+        common = (cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), cache.module_index[module],
+                  plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap))
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record(self.stream)
+        n.check(self.lib.pl_sgmv_shrink(dt, x.data_ptr(), x.stride(0), K, *common, buf.data_ptr(), buf.numel(),
+                                        ldt, rows, splits, self.stream.cuda_stream), "pl_sgmv_shrink")
+        ev[1].record(self.stream)
+        n.check(self.lib.pl_sgmv_expand(dt, buf.data_ptr(), ldt, rows, planes, *common, y.data_ptr(), y.stride(0), N,
+                                        n.PL_EPI_FALLBACK, self.stream.cuda_stream), "pl_sgmv_expand")
+        ev[2].record(self.stream)
+        self.events.append(ev)
+
+    def times_ms(self):
+        torch.cuda.synchronize()
+        sh = [e[0].elapsed_time(e[1]) for e in self.events]
+        ex = [e[1].elapsed_time(e[2]) for e in self.events]
+        self.events = []
+        return sh, ex
 
 
 def run_isolated(args) -> dict:
@@ -207,7 +391,7 @@ def run_isolated(args) -> dict:
     set_bytes = 2 * base_set.x.numel() * base_set.x.element_size()
     n_sets = max(3, int(np.ceil(600e6 / set_bytes)))
     sets = [base_set]
-    for i in range(1, n_sets):
+    for _ in range(1, n_sets):
         sets.append(IsolatedSgmv(base_set.cache, base_set.adapters, base_set.ranks,
                                  torch.randn_like(base_set.x), base_set.base, torch.randn_like(base_set.y),
                                  base_set.row_slot, base_set.seq_lens, base_set.plan, base_set.seg_lens))
@@ -216,23 +400,29 @@ def run_isolated(args) -> dict:
     def apply(wl):
         sgmv.lora_apply(wl.x, wl.y, wl.cache, "op", wl.plan)
 
-    ms, _ = _time_isolated(sets, args.steps, args.warmup, apply)
-    sh_ms, ex_ms = _kernel_times(sets, max(20, args.steps))
+    for i in range(args.warmup):
+        apply(sets[i % n_sets])
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        apply(sets[i % n_sets])
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+
+    timer = KernelTimer()
+    for i in range(max(20, args.steps)):
+        wl = sets[i % n_sets]
+        timer.run(wl.x, wl.y, wl.cache, "op", wl.plan)
+    sh, ex = timer.times_ms()
+    sh_ms, ex_ms = float(np.mean(sh)), float(np.mean(ex))
     value = nb["total"] / (ms * 1e-3) / 1e9
+    kern_gbs = nb["total"] / ((sh_ms + ex_ms) * 1e-3) / 1e9
     exp_gbs = nb["expand"] / (ex_ms * 1e-3) / 1e9
-    result = {
-        "metric": "SGMV achieved HBM GB/s (% peak); multi-LoRA decode tokens/s, 1 MI355X",
+    out = {
         "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
         "config": {
             "workload": "isolated SGMV shrink+expand, T=4096 tokens, K=N=4096, 16 slots + base, ranks {0,4,8,16}, "
                         "Dirichlet(1) segments, alpha 32",
@@ -242,6 +432,8 @@ def run_isolated(args) -> dict:
             "input_sets_rotated": n_sets,
             "shrink_ms": round(sh_ms, 5),
             "expand_ms": round(ex_ms, 5),
+            "shrink_plus_expand_kernel_gbs": round(kern_gbs, 1),
+            "shrink_gbs": round(nb["shrink"] / (sh_ms * 1e-3) / 1e9, 1),
         },
         "roofline": {
             "kernel": "pl_expand_tiled<bf16>",
@@ -252,13 +444,251 @@ def run_isolated(args) -> dict:
             "frac": round(exp_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
             "algorithmic_bytes_per_launch": nb["expand"],
+            "avg_launch_ms": round(ex_ms, 5),
         },
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_isolated(base_set, nb["total"], args.cpu_seconds)
-    return result
+        out["cpu_baseline"] = cpu_baseline_isolated(base_set, nb["total"], args.cpu_seconds)
+    return out
 
 
+# ----------------------------------------------------------------------------- Llama-3-8B shape
+def llama_config(layers: int = 32, attn: str = "pl_fused_sdpa"):
+    from transformers import LlamaConfig
+
+    cfg = LlamaConfig(hidden_size=4096, num_hidden_layers=layers, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=128, intermediate_size=14336, vocab_size=128256, max_position_embeddings=8192,
+                      rms_norm_eps=1e-5, rope_theta=500000.0)
+    cfg._attn_implementation = attn
+    return cfg
+
+
+def build_llama(device, layers: int = 32, seed: int = 0, attn: str = "pl_fused_sdpa"):
+    """Random-init Llama-3-8B-shaped LlamaModel, built directly on the GPU in bf16."""
+    from transformers import LlamaModel
+
+    register_attention()
+    torch.manual_seed(seed)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            model = LlamaModel(llama_config(layers, attn))
+    finally:
+        torch.set_default_dtype(prev)
+    return model.eval()
+
+
+def zipf_ids(rng: np.random.Generator, n_rows: int, n_adapters: int, s: float, base_frac: float, names: list) -> list:
+    w = 1.0 / np.arange(1, n_adapters + 1) ** s
+    w /= w.sum()
+    picks = rng.choice(n_adapters, size=n_rows, p=w)
+    base = rng.random(n_rows) < base_frac
+    return ["__base__" if b else names[int(p)] for p, b in zip(picks, base)]
+
+
+@dataclass
+class DecodeWorkload:
+    model: object  # PolyLoraModel over the Llama stack
+    cache: object  # transformers StaticCache with 512 filled positions + 1 free
+    input_ids: torch.Tensor
+    cache_position: torch.Tensor
+    adapter_ids: list
+    ranks: dict
+    past: int
+    extra: dict = field(default_factory=dict)
+
+
+def decode_workload(device, layers: int = 32, batch: int = 256, past: int = 512, slots: int = 64, seed: int = 1003,
+                    attn: str = "pl_fused_sdpa") -> DecodeWorkload:
+    from transformers import StaticCache
+
+    from polylora_amd import PolyLoraConfig, PolyLoraModel
+
+    rng = np.random.default_rng(seed)
+    model = build_llama(device, layers, seed, attn)
+    pm = PolyLoraModel(model, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=slots, max_rank=64)).eval()
+    names = [f"ad{i:02d}" for i in range(slots)]
+    ranks = {n: int(rng.choice([8, 16, 32, 64])) for n in names}
+    _log(f"decode: generating {slots} adapters")
+    add_random_adapters(pm, ranks, seed=seed, device=device)
+    ids = zipf_ids(rng, batch, slots, 1.1, 0.10, names)
+    cfg = model.config
+    kv = StaticCache(config=cfg, max_cache_len=past + 1)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    for layer in range(cfg.num_hidden_layers):
+        k = torch.randn(batch, cfg.num_key_value_heads, past, cfg.head_dim, generator=gen, device=device, dtype=torch.bfloat16)
+        v = torch.randn(batch, cfg.num_key_value_heads, past, cfg.head_dim, generator=gen, device=device, dtype=torch.bfloat16)
+        kv.update(k, v, layer)
+    input_ids = torch.randint(0, cfg.vocab_size, (batch, 1), generator=gen, device=device)
+    cache_position = torch.tensor([past], device=device)
+    return DecodeWorkload(pm, kv, input_ids, cache_position, ids, ranks, past)
+
+
+def _reset_kv(wl: DecodeWorkload) -> None:
+    for layer in wl.cache.layers:
+        layer.cumulative_length.fill_(wl.past)
+
+
+def _decode_step(wl: DecodeWorkload, lora: bool):
+    _reset_kv(wl)
+    return wl.model.base_model(input_ids=wl.input_ids, past_key_values=wl.cache, cache_position=wl.cache_position,
+                               use_cache=True).last_hidden_state
+
+
+def decode_lora_bytes(pm, adapter_ids: list, rows: int) -> dict:
+    """Algorithmic bytes of one decode step's 224 shrink+expand pairs: active X, Y RMW, unique A+B once."""
+    base_id = pm.config.base_adapter_id
+    active = [a for a in adapter_ids if a != base_id]
+    uniq = sorted(set(active))
+    es = 2
+    total = xy = ab = flops = 0
+    for spec in pm.module_specs:
+        for aid in uniq:
+            w = pm.adapter_store.adapters[aid].layers.get(spec.name)
+            if w is None:
+                continue
+            ab += es * w.rank * (spec.in_features + spec.out_features)
+        t_act = sum(1 for a in active if pm.adapter_store.adapters[a].layers.get(spec.name) is not None)
+        xy += es * t_act * spec.in_features + 2 * es * t_act * spec.out_features
+        flops += sum(2 * pm.adapter_store.adapters[a].layers[spec.name].rank * (spec.in_features + spec.out_features) for a in active)
+    total = xy + ab
+    return {"total": total, "xy": xy, "ab": ab, "flops": flops, "active_rows": len(active), "distinct": len(uniq)}
+
+
+def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Tensor, reps: int, seed: int = 0) -> dict:
+    """Every wrapped Linear's shrink+expand over one batch, launched alone (no base model), events per op."""
+    from polylora_amd import sgmv
+
+    device = pm.adapter_cache.device
+    cache = pm.adapter_cache
+    row_slot = cache.ensure_resident(adapter_ids)
+    plan = sgmv.SgmvPlan(row_slot, seq_lens, tokens_per_row, cache.num_slots)
+    T = len(adapter_ids) * tokens_per_row
+    gen = torch.Generator(device=device).manual_seed(seed)
+    shapes = sorted({(s.in_features, s.out_features) for s in pm.module_specs})
+    xs = {k: torch.randn(T, k, generator=gen, device=device, dtype=torch.bfloat16) for k, _ in shapes}
+    ys = {n: torch.randn(T, n, generator=gen, device=device, dtype=torch.bfloat16) for _, n in shapes}
+    timer = KernelTimer()
+    for spec in pm.module_specs:  # warm-up pass
+        timer.run(xs[spec.in_features], ys[spec.out_features], cache, spec.name, plan)
+    timer.times_ms()
+    per_type: dict = {}
+    tot_sh = tot_ex = 0.0
+    for _ in range(reps):
+        for spec in pm.module_specs:
+            timer.run(xs[spec.in_features], ys[spec.out_features], cache, spec.name, plan)
+        sh, ex = timer.times_ms()
+        tot_sh += sum(sh)
+        tot_ex += sum(ex)
+        for spec, a, b in zip(pm.module_specs, sh, ex):
+            key = spec.name.rsplit(".", 1)[-1]
+            d = per_type.setdefault(key, [0.0, 0.0, 0])
+            d[0] += a
+            d[1] += b
+            d[2] += 1
+    return {"shrink_ms": tot_sh / reps, "expand_ms": tot_ex / reps,
+            "per_type_us": {k: [round(1e3 * v[0] / v[2], 2), round(1e3 * v[1] / v[2], 2)] for k, v in per_type.items()}}
+
+
+def _graph_ms(fn, reps: int) -> float:
+    """Capture fn() in a HIP graph (after eager warm-up) and time replays."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / reps
+
+
+def _eager_ms(fn, reps: int) -> float:
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def run_decode(args) -> dict:
+    from polylora_amd.context import use_lora_context
+
+    device = torch.device("cuda", 0)
+    t_build = time.perf_counter()
+    wl = decode_workload(device, layers=args.decode_layers)
+    pm = wl.model
+    B = len(wl.adapter_ids)
+    ctx = pm.prepare_lora_context(wl.adapter_ids, None, B, 1, device)  # uploads the step's adapters
+    torch.cuda.synchronize()
+    _log(f"decode: model + adapters ready in {time.perf_counter() - t_build:.1f}s")
+    nb = decode_lora_bytes(pm, wl.adapter_ids, B)
+    out = {"rows": B, "layers": args.decode_layers, "distinct_adapters": nb["distinct"], "active_rows": nb["active_rows"],
+           "lora_bytes_per_step": nb["total"], "lora_adapter_bytes_per_step": nb["ab"], "lora_flops_per_step": nb["flops"]}
+
+    def base_step():
+        return _decode_step(wl, False)
+
+    def lora_step():
+        with use_lora_context(ctx):
+            return _decode_step(wl, True)
+
+    with torch.inference_mode():
+        kt = time_lora_ops(pm, wl.adapter_ids, 1, torch.ones(B, dtype=torch.int32, device=device), reps=5)
+        kern_ms = kt["shrink_ms"] + kt["expand_ms"]
+        out["lora_kernels_ms"] = round(kern_ms, 4)
+        out["lora_kernels_gbs"] = round(nb["total"] / (kern_ms * 1e-3) / 1e9, 1)
+        out["lora_kernels_pct_hbm"] = round(100 * nb["total"] / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
+        out["lora_kernels_shrink_ms"] = round(kt["shrink_ms"], 4)
+        out["lora_kernels_expand_ms"] = round(kt["expand_ms"], 4)
+        out["per_op_us_shrink_expand"] = kt["per_type_us"]
+        _log(f"decode: kernels {out['lora_kernels_gbs']} GB/s")
+        e_base = _eager_ms(base_step, args.decode_steps)
+        e_lora = _eager_ms(lora_step, args.decode_steps)
+        out["eager_ms_base"] = round(e_base, 3)
+        out["eager_ms_lora"] = round(e_lora, 3)
+        out["eager_tokens_per_s_lora"] = round(B / e_lora * 1e3, 1)
+        out["eager_tokens_per_s_base"] = round(B / e_base * 1e3, 1)
+        _log(f"decode: eager base {e_base:.2f} ms, lora {e_lora:.2f} ms")
+        try:
+            g_base = _graph_ms(base_step, args.decode_steps)
+            g_lora = _graph_ms(lora_step, args.decode_steps)
+            out["graph_ms_base"] = round(g_base, 3)
+            out["graph_ms_lora"] = round(g_lora, 3)
+            out["tokens_per_s_lora"] = round(B / g_lora * 1e3, 1)
+            out["tokens_per_s_base"] = round(B / g_base * 1e3, 1)
+            out["ratio_lora_to_base"] = round(g_base / g_lora, 4)
+            out["timing"] = "HIP graph replay of one decode step"
+            out["attention"] = "torch SDPA fused kernel, " + ("native GQA" if _GQA_NATIVE["ok"] else "K/V expanded to 32 heads")
+            _log(f"decode: graph base {g_base:.2f} ms, lora {g_lora:.2f} ms")
+        except Exception as exc:  # noqa: BLE001 - report and keep the eager numbers
+            out["graph_error"] = f"{type(exc).__name__}: {str(exc)[:300]}"
+            out["tokens_per_s_lora"] = out["eager_tokens_per_s_lora"]
+            out["tokens_per_s_base"] = out["eager_tokens_per_s_base"]
+            out["ratio_lora_to_base"] = round(e_base / e_lora, 4)
+            out["timing"] = "eager wall clock (graph capture failed)"
+    del wl, pm, ctx
+    torch.cuda.empty_cache()
+    return out
+
+
+# ----------------------------------------------------------------------------- main
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
@@ -266,6 +696,10 @@ def main(argv=None) -> int:
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--only-isolated", action="store_true", help="skip the model workloads")
+    p.add_argument("--decode-layers", type=int, default=32)
+    p.add_argument("--decode-steps", type=int, default=20)
+    p.add_argument("--no-deberta", action="store_true")
     args = p.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path; run with --gpus 1", file=sys.stderr)
@@ -273,7 +707,32 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
-    result = run_isolated(args)
+    iso = run_isolated(args)
+    _log(f"isolated: {iso['value']} GB/s")
+    result = {
+        "metric": METRIC,
+        "value": iso["value"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": iso["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": iso["config"],
+        "roofline": iso["roofline"],
+    }
+    if "cpu_baseline" in iso:
+        result["cpu_baseline"] = iso["cpu_baseline"]
+    if not args.only_isolated:
+        workloads = {}
+        workloads["decode"] = run_decode(args)
+        if not args.no_deberta:
+            workloads["deberta"] = run_deberta(torch.device("cuda", 0))
+        result["workloads"] = workloads
     print(json.dumps(result), flush=True)
     return 0
 

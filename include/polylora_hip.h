@@ -15,6 +15,8 @@
  *                          (one device-side plan per forward instead of a
  *                          host-synchronising schedule per layer)
  *   pl_sgmv_shrink      <- src/polylora/sgmv.py:63-138   _sgmv_lora_a_kernel
+ *   pl_shrink_planes, pl_shrink_workspace_bytes
+ *                          (sizes of the shrink -> expand workspace)
  *   pl_sgmv_expand      <- src/polylora/sgmv.py:178-275  _sgmv_lora_b_kernel
  *   pl_lora_apply       <- src/polylora/layers.py:42-53  (shrink then expand,
  *                          the LoRA half of MultiLoraLinear.forward)
@@ -109,36 +111,49 @@ int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows
                   int32_t row_len, int32_t num_slots, int32_t* tok, pl_group* groups,
                   int32_t* meta, int64_t group_cap, void* stream);
 
-/* Shrink: tmp[p][j] (+)= sum_k x[tok[p]][k] * A_slot[j][k] for every planned
- * token position p and j < rank(slot, module).  fp32 output.
+/* Number of K splits pl_sgmv_shrink uses for a requested count: the K range
+ * is cut into at most k_splits pieces of whole MFMA steps. */
+int32_t pl_shrink_planes(int32_t dtype, int32_t K, int32_t k_splits);
+
+/* Bytes of the workspace `ws` that pl_sgmv_shrink / pl_lora_apply need for
+ * these sizes: fp32 partial planes [planes][tmp_rows][ldt]. */
+int64_t pl_shrink_workspace_bytes(int32_t dtype, int32_t K, int32_t k_splits, int64_t tmp_rows,
+                                  int32_t ldt);
+
+/* Shrink: planes[c][p][j] = sum_{k in split c} x[tok[p]][k] * A_slot[j][k]
+ * for every planned token position p, j < rank(slot, module) and split
+ * c < pl_shrink_planes(dtype, K, k_splits).  fp32 accumulation, plain stores
+ * (no atomics); entries outside (p, j < rank) are not written and nothing
+ * needs clearing between calls.
  *   x [*, ldx] of dtype; K = in_features
- *   k_splits == 1: tmp is stored; k_splits > 1: tmp is accumulated with
- *   atomics and must be zero on entry.
- *   zero_ptr/zero_count: optional buffer of `zero_count` floats that the
- *   kernel clears (used to clear the other half of a ping-pong workspace).
- * tmp is [num_tokens][ldt] with ldt a multiple of 8 and >= every rank of
- * this module.  Requires K % 8 == 0 (bf16/f16) or K % 4 == 0 (f32), 16-byte
- * aligned x rows and arena parts; otherwise returns PL_ERR_ALIGN. */
+ *   ws / ws_bytes: at least pl_shrink_workspace_bytes(...) bytes
+ *   tmp_rows >= the plan's token count; ldt a multiple of 8 and >= every
+ *     rank8 of this module.
+ * Requires K % 8 == 0 (bf16/f16) or K % 4 == 0 (f32) and 16-byte aligned x
+ * rows and arena parts; otherwise returns PL_ERR_ALIGN. */
 int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t K, const void* arena,
                    const pl_slot_entry* table, int32_t num_modules, int32_t module,
                    const int32_t* tok, const pl_group* groups, const int32_t* meta,
-                   int64_t group_cap, float* tmp, int32_t ldt, int32_t k_splits,
-                   float* zero_ptr, int64_t zero_count, void* stream);
+                   int64_t group_cap, void* ws, int64_t ws_bytes, int32_t ldt, int64_t tmp_rows,
+                   int32_t k_splits, void* stream);
 
-/* Expand: y[tok[p]][n] += scale * sum_{j<rank} T(tmp[p][j]) * B_slot[n][j]
- * with the rounding order of `epilogue`.  y [*, ldy] of dtype, N % 4 == 0. */
-int pl_sgmv_expand(int32_t dtype, const float* tmp, int32_t ldt, const void* arena,
-                   const pl_slot_entry* table, int32_t num_modules, int32_t module,
-                   const int32_t* tok, const pl_group* groups, const int32_t* meta,
-                   int64_t group_cap, void* y, int64_t ldy, int32_t N, int32_t epilogue,
-                   void* stream);
+/* Expand: y[tok[p]][n] = T(y + d), d = scale * sum_{j<rank} T(sum_c
+ * planes[c][p][j]) * B_slot[n][j] rounded in the order of `epilogue`; the
+ * `planes` partial sums the shrink left in `ws` are added in split order, so
+ * results are bitwise reproducible.  y [*, ldy] of dtype; requires
+ * N % 8 == 0 (bf16/f16) or N % 4 == 0 (f32) and 16-byte aligned y rows. */
+int pl_sgmv_expand(int32_t dtype, const void* ws, int32_t ldt, int64_t tmp_rows, int32_t planes,
+                   const void* arena, const pl_slot_entry* table, int32_t num_modules,
+                   int32_t module, const int32_t* tok, const pl_group* groups,
+                   const int32_t* meta, int64_t group_cap, void* y, int64_t ldy, int32_t N,
+                   int32_t epilogue, void* stream);
 
 /* Shrink followed by expand on one stream (one call per wrapped Linear). */
 int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y, int64_t ldy,
                   int32_t N, const void* arena, const pl_slot_entry* table,
                   int32_t num_modules, int32_t module, const int32_t* tok,
-                  const pl_group* groups, const int32_t* meta, int64_t group_cap, float* tmp,
-                  int32_t ldt, int32_t k_splits, float* zero_ptr, int64_t zero_count,
+                  const pl_group* groups, const int32_t* meta, int64_t group_cap, void* ws,
+                  int64_t ws_bytes, int32_t ldt, int64_t tmp_rows, int32_t k_splits,
                   int32_t epilogue, void* stream);
 
 /* Row-based LoRA on the slot arena for shapes the tiled path rejects

@@ -39,17 +39,19 @@ _SIGNATURES: dict[str, tuple] = {
     "pl_is_device_pointer": (c_void_p,),
     "pl_plan_group_capacity": (c_int32, c_int32, c_int32),
     "pl_plan_build": (c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p),
+    "pl_shrink_planes": (c_int32, c_int32, c_int32),
+    "pl_shrink_workspace_bytes": (c_int32, c_int32, c_int32, c_int64, c_int32),
     "pl_sgmv_shrink": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
-        c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p, c_int64, c_void_p,
+        c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int64, c_int32, c_void_p,
     ),
     "pl_sgmv_expand": (
-        c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
-        c_int64, c_void_p, c_int64, c_int32, c_int32, c_void_p,
+        c_int32, c_void_p, c_int32, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
+        c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_void_p,
     ),
     "pl_lora_apply": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
-        c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p, c_int64,
+        c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int64, c_int32,
         c_int32, c_void_p,
     ),
     "pl_lora_apply_rows": (
@@ -67,7 +69,7 @@ _SIGNATURES: dict[str, tuple] = {
     "pl_slot_upload": (c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p),
     "pl_check_right_padded": (c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p),
 }
-_RESTYPES = {"pl_last_error": ctypes.c_char_p, "pl_plan_group_capacity": c_int64}
+_RESTYPES = {"pl_last_error": ctypes.c_char_p, "pl_plan_group_capacity": c_int64, "pl_shrink_workspace_bytes": c_int64}
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

@@ -43,19 +43,20 @@ __device__ __forceinline__ float pl_round(float v) {
   return (float)(T)v;
 }
 
-// Expand epilogue: combine the fp32 accumulator with the base output value.
-//   fallback order (layers.py:127-128): d = T(acc); d = T(d * T(scale)); y = T(y + d)
-//   triton order   (sgmv.py:268-275):   y = T(T(acc * scale) + y)
+// Expand epilogue: the scaled delta added to the base output, y = T(y + d), with
+//   fallback order (layers.py:127-128): d = T(T(acc) * T(scale))
+//   triton order   (sgmv.py:268-275):   d = T(acc * scale)
+// pl_delta returns d (exactly representable in the element type).
+template <int DT>
+__device__ __forceinline__ float pl_delta(float acc, float scale, float scale_t, int mode) {
+  if (mode == PL_EPI_FALLBACK) return pl_round<DT>(pl_round<DT>(acc) * scale_t);
+  return pl_round<DT>(acc * scale);
+}
+
 template <int DT>
 __device__ __forceinline__ float pl_epilogue(float acc, float y, float scale, float scale_t,
                                              int mode) {
-  if (mode == PL_EPI_FALLBACK) {
-    float d = pl_round<DT>(acc);
-    d = pl_round<DT>(d * scale_t);
-    return pl_round<DT>(y + d);
-  }
-  float d = pl_round<DT>(acc * scale);
-  return pl_round<DT>(d + y);
+  return pl_round<DT>(y + pl_delta<DT>(acc, scale, scale_t, mode));
 }
 
 __device__ __forceinline__ pl_u32x4 pl_ld16(const void* p) {

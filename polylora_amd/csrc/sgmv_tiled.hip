@@ -5,31 +5,41 @@
 // which other tokens share its group, so the plan's order inside a slot is
 // free.
 //
-// Shrink (replaces sgmv.py:63-138): one workgroup per (group, K-chunk).  Its
-// four waves split the chunk along K; each lane streams 64 contiguous bytes
-// of one token row of x and of one rank row of A per step, feeding 16x16
-// MFMA tiles [tokens x ranks].  The four wave partials are summed in LDS in
-// a fixed order, then stored (one K-chunk) or added atomically (split-K) to
-// the fp32 intermediate tmp[position][rank].
+// Shrink (replaces sgmv.py:63-138): one workgroup per (group, K split).  Its
+// four waves split the split's K range; per step each lane loads two
+// 16-byte chunks of one token row of x and of one rank row of A, and the
+// four lanes that share a row read 64 contiguous bytes per load.  16x16 MFMA
+// tiles [tokens x ranks] accumulate in fp32, the four wave partials are
+// summed in LDS in a fixed order, and the block stores its sum with plain
+// stores into its own fp32 plane planes[split][position][rank].
 //
-// Expand (replaces sgmv.py:178-275): one workgroup per (group, 256 output
-// columns), each wave owns 64 columns.  The MFMA computes the transposed
-// tile [columns x tokens] so that B (stored [out][rank8], rank contiguous)
-// and tmp (stored [position][ldt], rank contiguous) are both read as 16-byte
-// rank chunks, and every lane ends up with 4 consecutive output columns of
-// one token for the fused scale + add-back read-modify-write of y.
+// Expand (replaces sgmv.py:178-275): one workgroup per (group, column chunk
+// of 256 bf16/f16 or 128 f32 output columns), one 16-token row tile at a
+// time.  The intermediate is the shrink planes summed in split order (four
+// planes' loads in flight together) and rounded once to the model dtype; the
+// MFMA runs on the transposed tile [columns x tokens] so that B (stored
+// [out][rank8], rank contiguous) and the planes (rank contiguous) are both
+// read in contiguous 16-byte rank chunks.  Split-K therefore needs no
+// atomics, no cross-workgroup signalling and no cleared buffers: results are
+// bitwise reproducible and every launch can be recorded in a HIP graph.
+// The scaled, rounded delta goes through LDS to the row-major layout of y,
+// and the fused add-back reads and writes y once with 16-byte accesses (512
+// contiguous bytes per row).  Registers stay near 128 per lane so that four
+// workgroups share a CU and hide each other's memory latency.
 #include "pl_common.h"
 
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kChunksPerLane = 4;  // 64 contiguous bytes per lane per step
+constexpr int kChunksPerLane = 2;  // 16-byte chunks per lane per shrink step
+constexpr int kJT = 2;             // 16-rank column tiles per shrink pass
+constexpr int kYRowsPerPass = 8;   // 256 threads, 32 lanes per tile row
 
 struct pl_shrink_args {
   const void* x;
   int64_t ldx;
   int32_t K;
-  int32_t kw;  // K per wave, multiple of the step span
+  int32_t kw;  // K per wave, a multiple of the step span
   const char* arena;
   const pl_slot_entry* table;
   int32_t num_modules;
@@ -37,17 +47,17 @@ struct pl_shrink_args {
   const int32_t* tok;
   const pl_group* groups;
   const int32_t* meta;
-  float* tmp;
+  float* planes;  // [k_splits][tmp_rows][ldt] fp32
   int32_t ldt;
   int32_t k_splits;
-  int32_t atomic;
-  float* zero_ptr;
-  int64_t zero_count;
+  int64_t plane;  // floats between split planes
 };
 
 struct pl_expand_args {
-  const float* tmp;
+  const float* planes;
   int32_t ldt;
+  int32_t k_splits;
+  int64_t plane;
   const char* arena;
   const pl_slot_entry* table;
   int32_t num_modules;
@@ -62,12 +72,23 @@ struct pl_expand_args {
   int32_t epilogue;
 };
 
+// Columns of y one expand wave owns: 64 for 2-byte types, 32 for fp32, so
+// that a block's tile row is always 512 bytes.
 template <int DT>
-__global__ __launch_bounds__(256) void pl_shrink_tiled(pl_shrink_args a) {
+struct pl_expand_shape {
+  enum { kColsWave = DT == PL_F32 ? 32 : 64 };
+  enum { kCT = kColsWave / 16 };
+  enum { kChunk = kWaves * kColsWave };
+  enum { kPad = DT == PL_F32 ? 4 : 8 };  // 16 bytes of LDS row padding
+  enum { kLdsRow = kChunk + kPad };
+};
+
+template <int DT>
+__global__ __launch_bounds__(256, 4) void pl_shrink_tiled(pl_shrink_args a) {
   typedef typename pl_traits<DT>::T T;
   constexpr int E = pl_traits<DT>::E;
-  constexpr int kLaneSpan = kChunksPerLane * E;  // k covered by one lane per step
-  constexpr int kStep = 4 * kLaneSpan;           // k covered by one wave per step
+  constexpr int kInstr = 4 * E;                   // k covered by one wave load (4 lane groups)
+  constexpr int kStep = kChunksPerLane * kInstr;  // k covered by one wave step
   __shared__ pl_f32x4 red[kWaves][4][64];
 
   const int tid = threadIdx.x;
@@ -75,14 +96,6 @@ __global__ __launch_bounds__(256) void pl_shrink_tiled(pl_shrink_args a) {
   const int lane = tid & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;
-
-  if (a.zero_ptr != nullptr) {
-    pl_f32x4* z = reinterpret_cast<pl_f32x4*>(a.zero_ptr);
-    const int64_t n4 = a.zero_count >> 2;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + tid; i < n4; i += stride)
-      z[i] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
-  }
 
   const int g = blockIdx.x / a.k_splits;
   const int c = blockIdx.x - g * a.k_splits;
@@ -96,6 +109,7 @@ __global__ __launch_bounds__(256) void pl_shrink_tiled(pl_shrink_args a) {
   const int K = a.K;
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
   const T* __restrict__ A = reinterpret_cast<const T*>(a.arena + e.a_off);
+  float* __restrict__ out = a.planes + (int64_t)c * a.plane;
 
   const T* xrow[4];
   bool xok[4];
@@ -104,40 +118,41 @@ __global__ __launch_bounds__(256) void pl_shrink_tiled(pl_shrink_args a) {
     const int p = rt * 16 + li;
     xok[rt] = p < len;
     const int t = xok[rt] ? a.tok[grp.start + p] : 0;
-    xrow[rt] = x + (int64_t)t * a.ldx;
+    xrow[rt] = x + (int64_t)t * a.ldx + lg * E;
   }
   const int k0 = (c * kWaves + wave) * a.kw;
   const int k1 = min(K, k0 + a.kw);
 
-  for (int rb = 0; rb < rank; rb += 64) {
-    pl_f32x4 acc[4][4];
+  for (int rb = 0; rb < rank; rb += 16 * kJT) {
+    pl_f32x4 acc[4][kJT];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) acc[rt][jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int jt = 0; jt < kJT; ++jt) acc[rt][jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
 
     for (int kb = k0; kb < k1; kb += kStep) {
-      const int kl = kb + lg * kLaneSpan;
+      // chunk cc of lane (li, lg) covers k = kb + cc*kInstr + lg*E .. +E
       pl_u32x4 xf[4][kChunksPerLane];
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
         for (int cc = 0; cc < kChunksPerLane; ++cc) {
-          const int k = kl + cc * E;
+          const int k = kb + cc * kInstr;
           pl_u32x4 v = {0u, 0u, 0u, 0u};
-          if (xok[rt] && k < k1) v = pl_ld16(xrow[rt] + k);
+          if (xok[rt] && k + lg * E < k1) v = pl_ld16(xrow[rt] + k);
           xf[rt][cc] = v;
         }
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
+      for (int jt = 0; jt < kJT; ++jt) {
         if (rb + jt * 16 < rank) {
           const int j = rb + jt * 16 + li;
+          const T* arow = A + (int64_t)j * K + lg * E;
           pl_u32x4 af[kChunksPerLane];
 #pragma unroll
           for (int cc = 0; cc < kChunksPerLane; ++cc) {
-            const int k = kl + cc * E;
+            const int k = kb + cc * kInstr;
             pl_u32x4 v = {0u, 0u, 0u, 0u};
-            if (j < rank && k < k1) v = pl_ld16(A + (int64_t)j * K + k);
+            if (j < rank && k + lg * E < k1) v = pl_ld16(arow + k);
             af[cc] = v;
           }
 #pragma unroll
@@ -151,29 +166,27 @@ __global__ __launch_bounds__(256) void pl_shrink_tiled(pl_shrink_args a) {
     }
 
     // Sum the four wave partials of each row tile in a fixed order.
-    // acc[rt][jt][v] holds tile element (row 4*lg+v, column li).
+    // acc[rt][jt][v] holds tile element (row 4*lg+v, column li).  Thread
+    // (wave, lane) finishes row tile rt0 + wave / kJT, column tile wave % kJT.
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      if (rt < nrt) {
+    for (int rt0 = 0; rt0 < 4; rt0 += 4 / kJT) {
+      if (rt0 < nrt) {
         __syncthreads();
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) red[wave][jt][lane] = acc[rt][jt];
+        for (int q = 0; q < 4 / kJT; ++q)
+#pragma unroll
+          for (int jt = 0; jt < kJT; ++jt) red[wave][q * kJT + jt][lane] = acc[rt0 + q][jt];
         __syncthreads();
-        const int jt = wave;  // thread (wave, lane) finishes tile column block jt
+        const int rt = rt0 + wave / kJT;
+        const int jt = wave % kJT;
         const int j = rb + jt * 16 + li;
-        const pl_f32x4 s = red[0][jt][lane] + red[1][jt][lane] + red[2][jt][lane] +
-                           red[3][jt][lane];
-        if (j < rank) {
+        const pl_f32x4 s = red[0][wave][lane] + red[1][wave][lane] + red[2][wave][lane] +
+                           red[3][wave][lane];
+        if (j < rank && rt < nrt) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int prow = rt * 16 + lg * 4 + v;
-            if (prow < len) {
-              float* dst = a.tmp + (int64_t)(grp.start + prow) * a.ldt + j;
-              if (a.atomic)
-                atomicAdd(dst, s[v]);
-              else
-                *dst = s[v];
-            }
+            if (prow < len) out[(int64_t)(grp.start + prow) * a.ldt + j] = s[v];
           }
         }
       }
@@ -181,13 +194,57 @@ __global__ __launch_bounds__(256) void pl_shrink_tiled(pl_shrink_args a) {
   }
 }
 
+// Intermediate chunk of one token for an MFMA operand: planes summed in split
+// order, entries at or beyond `rank` zero, rounded once to T.  Four planes'
+// loads are issued before any of them is added.
+template <int DT, int E>
+__device__ __forceinline__ pl_u32x4 pl_sum_planes(const float* __restrict__ src, int64_t plane,
+                                                  int planes, int jl, int rank) {
+  typedef typename pl_traits<DT>::T T;
+  typedef typename pl_traits<DT>::T8 T8;
+  pl_f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+  int q = 0;
+  for (; q + 4 <= planes; q += 4) {
+    pl_f32x4 l[4], h[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      l[u] = *reinterpret_cast<const pl_f32x4*>(src + (q + u) * plane);
+      if constexpr (E == 8) h[u] = *reinterpret_cast<const pl_f32x4*>(src + (q + u) * plane + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      lo += l[u];
+      if constexpr (E == 8) hi += h[u];
+    }
+  }
+  for (; q < planes; ++q) {
+    lo += *reinterpret_cast<const pl_f32x4*>(src + q * plane);
+    if constexpr (E == 8) hi += *reinterpret_cast<const pl_f32x4*>(src + q * plane + 4);
+  }
+  if constexpr (E == 8) {
+    T8 h8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h8[i] = (T)((jl + i < rank) ? lo[i] : 0.f);
+      h8[i + 4] = (T)((jl + i + 4 < rank) ? hi[i] : 0.f);
+    }
+    return __builtin_bit_cast(pl_u32x4, h8);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo[i] = (jl + i < rank) ? lo[i] : 0.f;
+    return __builtin_bit_cast(pl_u32x4, lo);
+  }
+}
+
 template <int DT>
-__global__ __launch_bounds__(256) void pl_expand_tiled(pl_expand_args a) {
+__global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
   typedef typename pl_traits<DT>::T T;
   typedef typename pl_traits<DT>::T4 T4;
   typedef typename pl_traits<DT>::T8 T8;
+  typedef pl_expand_shape<DT> S;
   constexpr int E = pl_traits<DT>::E;
   constexpr int kStep = 4 * E;  // rank slots per MFMA step
+  __shared__ __attribute__((aligned(16))) T delta[64 * S::kLdsRow];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -204,84 +261,82 @@ __global__ __launch_bounds__(256) void pl_expand_tiled(pl_expand_args a) {
   if (rank <= 0) return;
   const int r8 = e.rank8;
   const int N = a.N;
-  const int n0 = c * 256 + wave * 64;
-  if (n0 >= N) return;
+  const int n_base = c * S::kChunk;
   const int len = grp.len;
   const int nrt = (len + 15) >> 4;
-  const T* __restrict__ Bc = reinterpret_cast<const T*>(a.arena + e.b_off);
-
-  int trow[4];
-  bool tok_ok[4];
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
-    const int p = rt * 16 + li;
-    tok_ok[rt] = p < len;
-    trow[rt] = grp.start + (tok_ok[rt] ? p : 0);
-  }
-
-  pl_f32x4 acc[4][4];
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int j0 = 0; j0 < r8; j0 += kStep) {
-    const int jl = j0 + lg * E;
-    pl_u32x4 tf[4];
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      pl_u32x4 v = {0u, 0u, 0u, 0u};
-      if (tok_ok[rt] && jl < rank) {
-        const float* src = a.tmp + (int64_t)trow[rt] * a.ldt + jl;
-        if constexpr (E == 8) {
-          const pl_f32x4 lo = *reinterpret_cast<const pl_f32x4*>(src);
-          const pl_f32x4 hi = *reinterpret_cast<const pl_f32x4*>(src + 4);
-          T8 h;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            h[i] = (T)((jl + i < rank) ? lo[i] : 0.f);
-            h[i + 4] = (T)((jl + i + 4 < rank) ? hi[i] : 0.f);
-          }
-          v = __builtin_bit_cast(pl_u32x4, h);
-        } else {
-          pl_f32x4 f = *reinterpret_cast<const pl_f32x4*>(src);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) f[i] = (jl + i < rank) ? f[i] : 0.f;
-          v = __builtin_bit_cast(pl_u32x4, f);
-        }
-      }
-      tf[rt] = v;
-    }
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const int n = n0 + ct * 16 + li;
-      pl_u32x4 bf = {0u, 0u, 0u, 0u};
-      if (n < N && jl < r8) bf = pl_ld16(Bc + (int64_t)n * r8 + jl);
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-        if (rt < nrt) acc[rt][ct] = pl_mfma_chunk<DT>(bf, tf[rt], acc[rt][ct]);
-    }
-  }
-
-  // acc[rt][ct][v] = delta(column n0 + ct*16 + 4*lg + v, token row rt*16 + li)
   const float scale = e.scale;
   const float scale_t = pl_round<DT>(scale);
+  const int n0 = n_base + wave * S::kColsWave;
+  const T* __restrict__ Bc = reinterpret_cast<const T*>(a.arena + e.b_off);
+
+  // 1. delta^T tiles [columns x tokens] on the MFMA, one 16-token row tile at
+  // a time; acc[ct][v] = delta(column n0 + ct*16 + 4*lg + v, token rt*16 + li).
+  for (int rt = 0; rt < nrt; ++rt) {
+    const int p = rt * 16 + li;
+    const bool tok_ok = p < len;
+    const float* prow = a.planes + (int64_t)(grp.start + (tok_ok ? p : 0)) * a.ldt;
+    pl_f32x4 acc[S::kCT];
+#pragma unroll
+    for (int ct = 0; ct < S::kCT; ++ct) acc[ct] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < r8; j0 += kStep) {
+      const int jl = j0 + lg * E;
+      pl_u32x4 bf[S::kCT];
+#pragma unroll
+      for (int ct = 0; ct < S::kCT; ++ct) {
+        const int n = n0 + ct * 16 + li;
+        bf[ct] = pl_u32x4{0u, 0u, 0u, 0u};
+        if (n < N && jl < r8) bf[ct] = pl_ld16(Bc + (int64_t)n * r8 + jl);
+      }
+      pl_u32x4 tf = {0u, 0u, 0u, 0u};
+      if (tok_ok && jl < rank) tf = pl_sum_planes<DT, E>(prow + jl, a.plane, a.k_splits, jl, rank);
+#pragma unroll
+      for (int ct = 0; ct < S::kCT; ++ct) acc[ct] = pl_mfma_chunk<DT>(bf[ct], tf, acc[ct]);
+    }
+    // 2. scale and round in the epilogue's order, stage in LDS as [token][column]
+    T* drow = delta + p * S::kLdsRow + wave * S::kColsWave;
+#pragma unroll
+    for (int ct = 0; ct < S::kCT; ++ct) {
+      T4 d;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) d[v] = (T)pl_delta<DT>(acc[ct][v], scale, scale_t, a.epilogue);
+      *reinterpret_cast<T4*>(drow + ct * 16 + lg * 4) = d;
+    }
+  }
+  __syncthreads();
+
+  // 3. y = T(y + delta): thread (row t/32 + 8*i, columns (t%32)*E .. +E), full-width
+  // loads and stores, all of a thread's rows in flight together.
+  const int yq = tid & 31;
+  const int yr0 = tid >> 5;
+  const int ycol = n_base + yq * E;
+  if (ycol >= N) return;
   T* __restrict__ y = reinterpret_cast<T*>(a.y);
+  pl_u32x4 yv[64 / kYRowsPerPass];
+  T* yptr[64 / kYRowsPerPass];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
-    if (rt < nrt && tok_ok[rt]) {
-      const int t = a.tok[trow[rt]];
-      T* yrow = y + (int64_t)t * a.ldy;
+  for (int i = 0; i < 64 / kYRowsPerPass; ++i) {
+    const int r = yr0 + kYRowsPerPass * i;
+    yptr[i] = nullptr;
+    if (r < len) {
+      yptr[i] = y + (int64_t)a.tok[grp.start + r] * a.ldy + ycol;
+      yv[i] = pl_ld16(yptr[i]);
+    }
+  }
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const int nb = n0 + ct * 16 + lg * 4;
-        if (nb < N) {
-          T4 yv = *reinterpret_cast<const T4*>(yrow + nb);
+  for (int i = 0; i < 64 / kYRowsPerPass; ++i) {
+    if (yptr[i] != nullptr) {
+      const int r = yr0 + kYRowsPerPass * i;
+      const pl_u32x4 dv = *reinterpret_cast<const pl_u32x4*>(delta + r * S::kLdsRow + yq * E);
+      if constexpr (E == 8) {
+        T8 yy = __builtin_bit_cast(T8, yv[i]);
+        const T8 dd = __builtin_bit_cast(T8, dv);
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            yv[v] = (T)pl_epilogue<DT>(acc[rt][ct][v], (float)yv[v], scale, scale_t, a.epilogue);
-          *reinterpret_cast<T4*>(yrow + nb) = yv;
-        }
+        for (int q = 0; q < 8; ++q) yy[q] = (T)((float)yy[q] + (float)dd[q]);
+        *reinterpret_cast<pl_u32x4*>(yptr[i]) = __builtin_bit_cast(pl_u32x4, yy);
+      } else {
+        pl_f32x4 yy = __builtin_bit_cast(pl_f32x4, yv[i]);
+        yy += __builtin_bit_cast(pl_f32x4, dv);
+        *reinterpret_cast<pl_f32x4*>(yptr[i]) = yy;
       }
     }
   }
@@ -331,41 +386,76 @@ int check_common(int32_t dtype, const void* arena, const pl_slot_entry* table,
   return PL_OK;
 }
 
+// K per wave for a requested split count: a multiple of the wave step.
+int64_t shrink_kw(int32_t dtype, int32_t K, int32_t k_splits) {
+  const int64_t step = (int64_t)kChunksPerLane * 4 * pl_chunk_elems(dtype);
+  const int64_t per_split = (K + (int64_t)k_splits - 1) / k_splits;
+  const int64_t kw = (per_split + kWaves - 1) / kWaves;
+  return (kw + step - 1) / step * step;
+}
+
+int32_t shrink_planes(int32_t dtype, int32_t K, int32_t k_splits) {
+  const int64_t kw = shrink_kw(dtype, K, k_splits);
+  return (int32_t)((K + kWaves * kw - 1) / (kWaves * kw));
+}
+
+// Workspace of the shrink -> expand hand-off: fp32 planes [planes][tmp_rows][ldt].
+int64_t workspace_bytes(int32_t planes, int64_t tmp_rows, int32_t ldt) {
+  return (int64_t)planes * tmp_rows * ldt * 4;
+}
+
+int check_ws(const void* ws, int32_t ldt, int64_t tmp_rows) {
+  if (!ws) {
+    pl_set_error("null workspace pointer");
+    return PL_ERR_ARG;
+  }
+  if (ldt <= 0 || (ldt & 7) != 0 || tmp_rows < 0) {
+    pl_set_error("workspace needs ldt a positive multiple of 8 (got %d) and tmp_rows >= 0", ldt);
+    return PL_ERR_ARG;
+  }
+  if (!aligned16(ws)) {
+    pl_set_error("workspace is not 16-byte aligned");
+    return PL_ERR_ALIGN;
+  }
+  return PL_OK;
+}
+
 int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx, int32_t K,
                    const void* arena, const pl_slot_entry* table, int32_t num_modules,
                    int32_t module, const int32_t* tok, const pl_group* groups,
-                   const int32_t* meta, int64_t group_cap, float* tmp, int32_t ldt,
-                   int32_t k_splits, float* zero_ptr, int64_t zero_count) {
+                   const int32_t* meta, int64_t group_cap, void* ws, int64_t ws_bytes,
+                   int32_t ldt, int64_t tmp_rows, int32_t k_splits) {
   int st = check_common(dtype, arena, table, num_modules, module, tok, groups, meta, group_cap);
   if (st) return st;
+  if ((st = check_ws(ws, ldt, tmp_rows))) return st;
   const int E = pl_chunk_elems(dtype);
   const int es = pl_elem_size(dtype);
-  if (!x || !tmp) {
-    pl_set_error("null x or tmp pointer");
+  if (!x) {
+    pl_set_error("null x pointer");
     return PL_ERR_ARG;
   }
-  if (K <= 0 || ldx < K || ldt <= 0 || (ldt & 7) != 0 || k_splits < 1) {
-    pl_set_error("bad shrink sizes K=%d ldx=%lld ldt=%d k_splits=%d", K, (long long)ldx, ldt,
-                 k_splits);
+  if (K <= 0 || ldx < K || k_splits < 1 || k_splits > 4096) {
+    pl_set_error("bad shrink sizes K=%d ldx=%lld k_splits=%d", K, (long long)ldx, k_splits);
     return PL_ERR_ARG;
   }
-  if (K % E != 0 || (ldx * es) % 16 != 0 || !aligned16(x) || !aligned16(tmp)) {
-    pl_set_error("shrink needs K %% %d == 0 and 16-byte aligned rows", E);
+  if (K % E != 0 || (ldx * es) % 16 != 0 || !aligned16(x)) {
+    pl_set_error("shrink needs K %% %d == 0 and 16-byte aligned x rows", E);
     return PL_ERR_ALIGN;
   }
-  if (zero_ptr && ((zero_count & 3) != 0 || !aligned16(zero_ptr) || zero_count < 0)) {
-    pl_set_error("zero buffer must be 16-byte aligned with a multiple of 4 floats");
+  const int32_t planes = shrink_planes(dtype, K, k_splits);
+  if (group_cap * planes > 0x7fffffffLL) {
+    pl_set_error("shrink grid too large");
+    return PL_ERR_LIMIT;
+  }
+  if (ws_bytes < workspace_bytes(planes, tmp_rows, ldt)) {
+    pl_set_error("workspace of %lld bytes is below the %lld this call needs", (long long)ws_bytes,
+                 (long long)workspace_bytes(planes, tmp_rows, ldt));
     return PL_ERR_ARG;
   }
-  const int step = 16 * E;  // k per wave per step
-  const int64_t per_split = (K + (int64_t)k_splits - 1) / k_splits;
-  int64_t kw = (per_split + kWaves - 1) / kWaves;
-  kw = (kw + step - 1) / step * step;
-  const int64_t eff_splits = (K + kWaves * kw - 1) / (kWaves * kw);
   a.x = x;
   a.ldx = ldx;
   a.K = K;
-  a.kw = (int32_t)kw;
+  a.kw = (int32_t)shrink_kw(dtype, K, k_splits);
   a.arena = reinterpret_cast<const char*>(arena);
   a.table = table;
   a.num_modules = num_modules;
@@ -373,51 +463,49 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
   a.tok = tok;
   a.groups = groups;
   a.meta = meta;
-  a.tmp = tmp;
+  a.planes = reinterpret_cast<float*>(ws);
   a.ldt = ldt;
-  a.k_splits = (int32_t)eff_splits;
-  a.atomic = k_splits > 1 ? 1 : 0;
-  a.zero_ptr = zero_count > 0 ? zero_ptr : nullptr;
-  a.zero_count = zero_count;
-  if (group_cap * eff_splits > 0x7fffffffLL) {
-    pl_set_error("shrink grid too large");
-    return PL_ERR_LIMIT;
-  }
+  a.k_splits = planes;
+  a.plane = tmp_rows * ldt;
   return PL_OK;
 }
 
-int prepare_expand(pl_expand_args& a, int32_t dtype, const float* tmp, int32_t ldt,
-                   const void* arena, const pl_slot_entry* table, int32_t num_modules,
-                   int32_t module, const int32_t* tok, const pl_group* groups,
-                   const int32_t* meta, int64_t group_cap, void* y, int64_t ldy, int32_t N,
-                   int32_t epilogue) {
+int prepare_expand(pl_expand_args& a, int32_t dtype, const void* ws, int32_t ldt,
+                   int64_t tmp_rows, int32_t planes, const void* arena, const pl_slot_entry* table,
+                   int32_t num_modules, int32_t module, const int32_t* tok,
+                   const pl_group* groups, const int32_t* meta, int64_t group_cap, void* y,
+                   int64_t ldy, int32_t N, int32_t epilogue) {
   int st = check_common(dtype, arena, table, num_modules, module, tok, groups, meta, group_cap);
   if (st) return st;
+  if ((st = check_ws(ws, ldt, tmp_rows))) return st;
+  const int E = pl_chunk_elems(dtype);
   const int es = pl_elem_size(dtype);
-  if (!y || !tmp) {
-    pl_set_error("null y or tmp pointer");
+  if (!y) {
+    pl_set_error("null y pointer");
     return PL_ERR_ARG;
   }
-  if (N <= 0 || ldy < N || ldt <= 0 || (ldt & 7) != 0) {
-    pl_set_error("bad expand sizes N=%d ldy=%lld ldt=%d", N, (long long)ldy, ldt);
+  if (N <= 0 || ldy < N || planes < 1 || planes > 4096) {
+    pl_set_error("bad expand sizes N=%d ldy=%lld planes=%d", N, (long long)ldy, planes);
     return PL_ERR_ARG;
   }
   if (epilogue != PL_EPI_FALLBACK && epilogue != PL_EPI_TRITON) {
     pl_set_error("bad epilogue mode %d", epilogue);
     return PL_ERR_ARG;
   }
-  if (N % 4 != 0 || (ldy % 4) != 0 || (reinterpret_cast<uintptr_t>(y) % (4 * es)) != 0 ||
-      !aligned16(tmp)) {
-    pl_set_error("expand needs N %% 4 == 0 and %d-byte aligned y rows", 4 * es);
+  if (N % E != 0 || (ldy * es) % 16 != 0 || !aligned16(y)) {
+    pl_set_error("expand needs N %% %d == 0 and 16-byte aligned y rows", E);
     return PL_ERR_ALIGN;
   }
-  const int64_t n_chunks = (N + 255) / 256;
+  const int chunk = 4 * (dtype == PL_F32 ? 32 : 64);
+  const int64_t n_chunks = (N + chunk - 1) / chunk;
   if (group_cap * n_chunks > 0x7fffffffLL) {
     pl_set_error("expand grid too large");
     return PL_ERR_LIMIT;
   }
-  a.tmp = tmp;
+  a.planes = reinterpret_cast<const float*>(ws);
   a.ldt = ldt;
+  a.k_splits = planes;
+  a.plane = tmp_rows * ldt;
   a.arena = reinterpret_cast<const char*>(arena);
   a.table = table;
   a.num_modules = num_modules;
@@ -453,27 +541,38 @@ int dispatch_expand(int32_t dtype, const pl_expand_args& a, int64_t group_cap,
 
 }  // namespace
 
+extern "C" int32_t pl_shrink_planes(int32_t dtype, int32_t K, int32_t k_splits) {
+  if (K <= 0 || k_splits < 1) return 0;
+  return shrink_planes(dtype, K, k_splits);
+}
+
+extern "C" int64_t pl_shrink_workspace_bytes(int32_t dtype, int32_t K, int32_t k_splits,
+                                             int64_t tmp_rows, int32_t ldt) {
+  if (K <= 0 || k_splits < 1 || tmp_rows < 0 || ldt <= 0) return 0;
+  return workspace_bytes(shrink_planes(dtype, K, k_splits), tmp_rows, ldt);
+}
+
 extern "C" int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t K,
                               const void* arena, const pl_slot_entry* table,
                               int32_t num_modules, int32_t module, const int32_t* tok,
                               const pl_group* groups, const int32_t* meta, int64_t group_cap,
-                              float* tmp, int32_t ldt, int32_t k_splits, float* zero_ptr,
-                              int64_t zero_count, void* stream) {
+                              void* ws, int64_t ws_bytes, int32_t ldt, int64_t tmp_rows,
+                              int32_t k_splits, void* stream) {
   pl_shrink_args a;
   int st = prepare_shrink(a, dtype, x, ldx, K, arena, table, num_modules, module, tok, groups,
-                          meta, group_cap, tmp, ldt, k_splits, zero_ptr, zero_count);
+                          meta, group_cap, ws, ws_bytes, ldt, tmp_rows, k_splits);
   if (st) return st;
   return dispatch_shrink(dtype, a, group_cap, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int pl_sgmv_expand(int32_t dtype, const float* tmp, int32_t ldt, const void* arena,
-                              const pl_slot_entry* table, int32_t num_modules, int32_t module,
-                              const int32_t* tok, const pl_group* groups, const int32_t* meta,
-                              int64_t group_cap, void* y, int64_t ldy, int32_t N,
-                              int32_t epilogue, void* stream) {
+extern "C" int pl_sgmv_expand(int32_t dtype, const void* ws, int32_t ldt, int64_t tmp_rows,
+                              int32_t planes, const void* arena, const pl_slot_entry* table,
+                              int32_t num_modules, int32_t module, const int32_t* tok,
+                              const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                              void* y, int64_t ldy, int32_t N, int32_t epilogue, void* stream) {
   pl_expand_args a;
-  int st = prepare_expand(a, dtype, tmp, ldt, arena, table, num_modules, module, tok, groups,
-                          meta, group_cap, y, ldy, N, epilogue);
+  int st = prepare_expand(a, dtype, ws, ldt, tmp_rows, planes, arena, table, num_modules, module,
+                          tok, groups, meta, group_cap, y, ldy, N, epilogue);
   if (st) return st;
   return dispatch_expand(dtype, a, group_cap, reinterpret_cast<hipStream_t>(stream));
 }
@@ -482,16 +581,16 @@ extern "C" int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t 
                              int64_t ldy, int32_t N, const void* arena,
                              const pl_slot_entry* table, int32_t num_modules, int32_t module,
                              const int32_t* tok, const pl_group* groups, const int32_t* meta,
-                             int64_t group_cap, float* tmp, int32_t ldt, int32_t k_splits,
-                             float* zero_ptr, int64_t zero_count, int32_t epilogue,
+                             int64_t group_cap, void* ws, int64_t ws_bytes, int32_t ldt,
+                             int64_t tmp_rows, int32_t k_splits, int32_t epilogue,
                              void* stream) {
   pl_shrink_args sa;
   pl_expand_args ea;
   int st = prepare_shrink(sa, dtype, x, ldx, K, arena, table, num_modules, module, tok, groups,
-                          meta, group_cap, tmp, ldt, k_splits, zero_ptr, zero_count);
+                          meta, group_cap, ws, ws_bytes, ldt, tmp_rows, k_splits);
   if (st) return st;
-  st = prepare_expand(ea, dtype, tmp, ldt, arena, table, num_modules, module, tok, groups, meta,
-                      group_cap, y, ldy, N, epilogue);
+  st = prepare_expand(ea, dtype, ws, ldt, tmp_rows, sa.k_splits, arena, table, num_modules,
+                      module, tok, groups, meta, group_cap, y, ldy, N, epilogue);
   if (st) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   st = dispatch_shrink(dtype, sa, group_cap, s);

@@ -83,45 +83,27 @@ class SgmvPlan:
 
 
 class _Workspace:
-    """Ping-pong fp32 intermediate for one (device, stream).
+    """fp32 shrink planes for one (device, stream), grown on demand.
 
-    A split-K shrink accumulates with atomics and needs a zeroed buffer.  Call
-    i uses buffer i%2 (clean on entry) and its kernel clears what call i-1
-    left in the other buffer, so no separate clearing launch is ever needed.
+    The shrink writes every entry the expand reads, so the buffer is never
+    cleared.  Buffers are only ever replaced by larger ones, and replaced
+    buffers stay allocated for the life of the process, so a HIP graph that
+    recorded a launch keeps a valid pointer.
     """
 
     def __init__(self, device: torch.device) -> None:
         self.device = device
-        self.cap = 0
-        self.bufs: list[torch.Tensor | None] = [None, None]
-        self.dirty = [0, 0]
-        self.cur = 0
+        self.buf: torch.Tensor | None = None
+        self.retired: list[torch.Tensor] = []
 
-    def acquire(self, nfloats: int) -> tuple[int, torch.Tensor, int, int]:
-        nfloats = (max(nfloats, 4) + 3) // 4 * 4
-        if nfloats > self.cap:
-            self.cap = max(nfloats, 2 * self.cap)
-            self.bufs = [torch.zeros(self.cap, dtype=torch.float32, device=self.device) for _ in range(2)]
-            self.dirty = [0, 0]
-            self.cur = 0
-        i = self.cur
-        j = 1 - i
-        if self.dirty[i]:  # only after a failed launch
-            self.bufs[i][: self.dirty[i]].zero_()
-            self.dirty[i] = 0
-        zero_ptr, zero_count = 0, 0
-        if self.dirty[j]:
-            zero_ptr, zero_count = self.bufs[j].data_ptr(), self.dirty[j]
-        return i, self.bufs[i], zero_ptr, zero_count
-
-    def commit(self, i: int, used: int, ok: bool) -> None:
-        j = 1 - i
-        if not ok:
-            self.dirty = [self.cap, self.cap]
-            return
-        self.dirty[j] = 0
-        self.dirty[i] = (max(used, 4) + 3) // 4 * 4
-        self.cur = j
+    def get(self, nbytes: int) -> torch.Tensor:
+        nbytes = max(256, (nbytes + 255) // 256 * 256)
+        if self.buf is None or self.buf.numel() < nbytes:
+            if self.buf is not None:
+                self.retired.append(self.buf)
+                nbytes = max(nbytes, 2 * self.buf.numel())
+            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self.buf
 
 
 _WORKSPACES: dict[tuple[int, int], _Workspace] = {}
@@ -135,14 +117,16 @@ def _workspace(device: torch.device, stream: int) -> _Workspace:
     return ws
 
 
+# Active shrink workgroups to aim for (256 CUs, several per CU).
+_TARGET_SHRINK_BLOCKS = 2048
+
+
 def choose_k_splits(group_cap: int, K: int, dtype: torch.dtype) -> int:
-    """Split K across workgroups only when the group count alone cannot fill the GPU."""
+    """K splits of the shrink: enough (group, split) workgroups to fill the GPU, none for big batches."""
     chunk = 8 if dtype != torch.float32 else 4
-    k_per_wg_step = 4 * 16 * chunk  # four waves x one 16-chunk step each
-    max_splits = max(1, -(-K // k_per_wg_step))
-    if group_cap >= 512:
-        return 1
-    return max(1, min(max_splits, -(-1024 // max(1, group_cap))))
+    k_per_block_step = 4 * 2 * 4 * chunk  # four waves x two loads x four lane groups x one chunk
+    max_splits = max(1, -(-K // k_per_block_step))
+    return max(1, min(max_splits, -(-_TARGET_SHRINK_BLOCKS // max(1, group_cap))))
 
 
 def _tiled_ok(x: torch.Tensor, y: torch.Tensor) -> bool:
@@ -154,11 +138,11 @@ def _tiled_ok(x: torch.Tensor, y: torch.Tensor) -> bool:
         x.stride(1) == 1
         and y.stride(1) == 1
         and K % chunk == 0
+        and N % chunk == 0
         and (x.stride(0) * es) % 16 == 0
+        and (y.stride(0) * es) % 16 == 0
         and x.data_ptr() % 16 == 0
-        and N % 4 == 0
-        and y.stride(0) % 4 == 0
-        and y.data_ptr() % (4 * es) == 0
+        and y.data_ptr() % 16 == 0
     )
 
 
@@ -209,9 +193,10 @@ def lora_apply(
     ldt = cache.rank8_cap
     stream = _stream(x.device)
     splits = k_splits if k_splits is not None else choose_k_splits(plan.group_cap, K, x.dtype)
-    ws = _workspace(x.device, stream)
-    need = plan.tokens_cap * ldt
-    i, buf, zero_ptr, zero_count = ws.acquire(need)
+    rows = max(1, plan.tokens_cap)
+    group_cap = max(1, plan.group_cap)
+    nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, rows, ldt))
+    buf = _workspace(x.device, stream).get(nbytes)
     status = lib.pl_lora_apply(
         dt,
         x.data_ptr(),
@@ -227,16 +212,15 @@ def lora_apply(
         plan.tok.data_ptr(),
         plan.groups.data_ptr(),
         plan.meta.data_ptr(),
-        max(1, plan.group_cap),
+        group_cap,
         buf.data_ptr(),
+        buf.numel(),
         ldt,
+        rows,
         splits,
-        zero_ptr or None,
-        zero_count,
         epilogue,
         stream,
     )
-    ws.commit(i, need, status == 0)
     _native.check(status, "pl_lora_apply")
     return y
 

@@ -159,3 +159,109 @@ def test_isolated_sgmv_config_bf16(gpu):
     zero = (rk[wl.row_slot.long()] == 0).cpu()
     assert torch.equal(wl.y.cpu()[zero], wl.base.cpu()[zero])
     np.testing.assert_array_equal(np.bincount(wl.row_slot.cpu().numpy(), minlength=17).sum(), 4096)
+
+
+def _small_case(gpu, dtype=torch.bfloat16, rows=40, M=3, K=1024, N=512, ranks=(4, 16, 33, 64), seed=50):
+    g = torch.Generator().manual_seed(seed)
+    adapters = _adapters(g, list(ranks), K, N)
+    ids = list(adapters) + ["__base__"]
+    cache = make_cache(adapters, {"m": (K, N)}, len(adapters), 64, gpu, dtype)
+    adapter_ids = [ids[i] for i in torch.randint(0, len(ids), (rows,), generator=g).tolist()]
+    row_slot = cache.ensure_resident(adapter_ids)
+    seq_lens = torch.randint(0, M + 1, (rows,), generator=g, dtype=torch.int32)
+    x = torch.randn(rows, M, K, generator=g).to(dtype)
+    base = torch.randn(rows, M, N, generator=g).to(dtype)
+    return adapters, cache, row_slot, seq_lens, x, base
+
+
+def test_split_k_bitwise_reproducible(gpu):
+    _announce(test="reproducible")
+    adapters, cache, row_slot, seq_lens, x, base = _small_case(gpu)
+    M, K, N = x.shape[1], x.shape[2], base.shape[2]
+    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots)
+    outs = []
+    for _ in range(3):
+        y = base.to(gpu)
+        sgmv.lora_apply(x.to(gpu).view(-1, K), y.view(-1, N), cache, "m", plan, k_splits=4)
+        outs.append(y.cpu())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    A, B, rk, sc = oracle_slot_tensors(cache, adapters, "m", torch.bfloat16)
+    expect = reference_forward(x, base, seq_lens, row_slot.cpu(), A, B, rk, sc)
+    torch.testing.assert_close(outs[0], expect, **tol_for(torch.bfloat16))
+
+
+def test_separate_shrink_expand_equal_fused(gpu):
+    """pl_sgmv_shrink + pl_sgmv_expand (planes from pl_shrink_planes) == pl_lora_apply, bit for bit."""
+    _announce(test="separate_vs_fused")
+    from bench import KernelTimer
+
+    _, cache, row_slot, seq_lens, x, base = _small_case(gpu, seed=51)
+    M, K, N = x.shape[1], x.shape[2], base.shape[2]
+    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots)
+    for splits in (1, 2, 5):
+        y1 = base.to(gpu)
+        sgmv.lora_apply(x.to(gpu).view(-1, K), y1.view(-1, N), cache, "m", plan, k_splits=splits)
+        y2 = base.to(gpu)
+        timer = KernelTimer()
+        timer.run(x.to(gpu).view(-1, K), y2.view(-1, N), cache, "m", plan, k_splits=splits)
+        timer.times_ms()
+        assert torch.equal(y1.cpu(), y2.cpu()), splits
+
+
+def test_triton_epilogue_order(gpu):
+    """PL_EPI_TRITON: y = T(T(acc * scale) + y) over T(x @ A) (sgmv.py:130-134, :268-275)."""
+    _announce(test="triton_epilogue")
+    from oracle.lora import dense_slot_tensors
+    from polylora_amd import _native
+
+    adapters, cache, row_slot, seq_lens, x, base = _small_case(gpu, seed=52)
+    M, K, N = x.shape[1], x.shape[2], base.shape[2]
+    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots)
+    y = base.to(gpu)
+    sgmv.lora_apply(x.to(gpu).view(-1, K), y.view(-1, N), cache, "m", plan, epilogue=_native.PL_EPI_TRITON)
+    A, B, rk, sc = oracle_slot_tensors(cache, adapters, "m", torch.bfloat16)
+    tmp, _ = sgmv_shrink_reference(x, A, seq_lens, row_slot.cpu(), rk)
+    expect = sgmv_expand_reference(tmp, B, seq_lens, row_slot.cpu(), rk, sc, base)
+    torch.testing.assert_close(y.cpu(), expect, **tol_for(torch.bfloat16))
+
+
+def test_lora_apply_graph_replays(gpu):
+    """Plan + two modules captured in a HIP graph; every replay equals the eager result bit for bit."""
+    _announce(test="graph_replay")
+    g = torch.Generator().manual_seed(53)
+    K, N, rows = 1024, 768, 48
+    shapes = {"q": (K, N), "o": (N, K)}
+    adapters = {f"a{i}": {m: peft_layer(g, fi, fo, r, 2.0 * r) for m, (fi, fo) in shapes.items()} for i, r in enumerate([8, 16, 64])}
+    cache = make_cache(adapters, shapes, 3, 64, gpu, torch.bfloat16)
+    ids = list(adapters) + ["__base__"]
+    row_slot = cache.ensure_resident([ids[i] for i in torch.randint(0, 4, (rows,), generator=g).tolist()])
+    seq_lens = torch.ones(rows, dtype=torch.int32, device=gpu)
+    x = torch.randn(rows, K, generator=g).to(torch.bfloat16).to(gpu)
+    y0 = torch.randn(rows, N, generator=g).to(torch.bfloat16).to(gpu)
+    z0 = torch.randn(rows, K, generator=g).to(torch.bfloat16).to(gpu)
+    y, z = y0.clone(), z0.clone()
+
+    def step():
+        y.copy_(y0)
+        z.copy_(z0)
+        plan = sgmv.SgmvPlan(row_slot, seq_lens, 1, cache.num_slots)
+        sgmv.lora_apply(x, y, cache, "q", plan)
+        sgmv.lora_apply(y, z, cache, "o", plan)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    want_y, want_z = y.clone(), z.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for i in range(4):
+        y.fill_(float(i))  # eager work between replays
+        z.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want_y) and torch.equal(z, want_z), i
