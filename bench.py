@@ -279,7 +279,7 @@ def isolated_sgmv_workload(device, seed: int = 1002, T: int = 4096, K: int = 409
     seq_lens = torch.ones(T, dtype=torch.int32, device=device)
     x = torch.randn(T, K, generator=gen).to(dtype).to(device)
     base = torch.randn(T, N, generator=gen).to(dtype).to(device)
-    plan = sgmv.SgmvPlan(row_slot, seq_lens, 1, cache.num_slots)
+    plan = sgmv.SgmvPlan(row_slot, seq_lens, 1, cache.num_slots, distinct_slots=slots)
     return IsolatedSgmv(cache, adapters, ranks, x, base, base.clone(), row_slot, seq_lens, plan, seg)
 
 
@@ -339,47 +339,53 @@ def cpu_baseline_isolated(wl: IsolatedSgmv, nbytes: int, budget_s: float) -> dic
     }
 
 
-class KernelTimer:
-    """Shrink and expand launched separately, each bracketed by events on the launch stream."""
+class SgmvLaunch:
+    """The shrink and the expand of one wrapped Linear as separate launches (pl_sgmv_shrink, pl_sgmv_expand)."""
 
-    def __init__(self):
-        from polylora_amd import _native
+    def __init__(self, x, y, cache, module, plan, k_splits=None):
+        from polylora_amd import _native, sgmv
 
-        self.lib = _native.load()
-        self.native = _native
+        self.lib, self.n = _native.load(), _native
         self.stream = torch.cuda.current_stream()
-        self.events = []
-
-    def run(self, x, y, cache, module, plan, k_splits=None):
-        from polylora_amd import sgmv
-
-        n = self.native
-        dt = n.dtype_code(x.dtype)
+        dt = _native.dtype_code(x.dtype)
         K, N = int(x.shape[1]), int(y.shape[1])
         splits = k_splits if k_splits is not None else sgmv.choose_k_splits(plan.group_cap, K, x.dtype)
         rows = max(1, plan.tokens_cap)
         ldt = cache.rank8_cap
-        nbytes = int(self.lib.pl_shrink_workspace_bytes(dt, K, splits, rows, ldt))
-        planes = int(self.lib.pl_shrink_planes(dt, K, splits))
+        gt = plan.group_tokens
+        nbytes = int(self.lib.pl_shrink_workspace_bytes(dt, K, splits, gt, rows, ldt))
+        planes = int(self.lib.pl_shrink_planes(dt, K, splits, gt))
         buf = sgmv._workspace(x.device, self.stream.cuda_stream).get(nbytes)
         common = (cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), cache.module_index[module],
-                  plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap))
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        ev[0].record(self.stream)
-        n.check(self.lib.pl_sgmv_shrink(dt, x.data_ptr(), x.stride(0), K, *common, buf.data_ptr(), buf.numel(),
-                                        ldt, rows, splits, self.stream.cuda_stream), "pl_sgmv_shrink")
-        ev[1].record(self.stream)
-        n.check(self.lib.pl_sgmv_expand(dt, buf.data_ptr(), ldt, rows, planes, *common, y.data_ptr(), y.stride(0), N,
-                                        n.PL_EPI_FALLBACK, self.stream.cuda_stream), "pl_sgmv_expand")
-        ev[2].record(self.stream)
-        self.events.append(ev)
+                  plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap), gt)
+        s = self.stream.cuda_stream
+        self.shrink_args = (dt, x.data_ptr(), x.stride(0), K, *common, buf.data_ptr(), buf.numel(), ldt, rows, splits, s)
+        self.expand_args = (dt, buf.data_ptr(), ldt, rows, planes, *common, y.data_ptr(), y.stride(0), N,
+                            _native.PL_EPI_FALLBACK, s)
+        self.keep = (x, y, buf, plan)
 
-    def times_ms(self):
-        torch.cuda.synchronize()
-        sh = [e[0].elapsed_time(e[1]) for e in self.events]
-        ex = [e[1].elapsed_time(e[2]) for e in self.events]
-        self.events = []
-        return sh, ex
+    def shrink(self):
+        self.n.check(self.lib.pl_sgmv_shrink(*self.shrink_args), "pl_sgmv_shrink")
+
+    def expand(self):
+        self.n.check(self.lib.pl_sgmv_expand(*self.expand_args), "pl_sgmv_expand")
+
+
+def time_launches(fns: list, reps: int, warmup: int = 2) -> float:
+    """Milliseconds per pass over `fns`, launched back to back on the current stream between two events."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        for f in fns:
+            f()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(reps):
+        for f in fns:
+            f()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / reps
 
 
 def run_isolated(args) -> dict:
@@ -411,12 +417,10 @@ def run_isolated(args) -> dict:
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
 
-    timer = KernelTimer()
-    for i in range(max(20, args.steps)):
-        wl = sets[i % n_sets]
-        timer.run(wl.x, wl.y, wl.cache, "op", wl.plan)
-    sh, ex = timer.times_ms()
-    sh_ms, ex_ms = float(np.mean(sh)), float(np.mean(ex))
+    launches = [SgmvLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets]
+    reps = max(10, args.steps // n_sets)
+    sh_ms = time_launches([l.shrink for l in launches], reps) / n_sets
+    ex_ms = time_launches([l.expand for l in launches], reps) / n_sets
     value = nb["total"] / (ms * 1e-3) / 1e9
     kern_gbs = nb["total"] / ((sh_ms + ex_ms) * 1e-3) / 1e9
     exp_gbs = nb["expand"] / (ex_ms * 1e-3) / 1e9
@@ -557,38 +561,31 @@ def decode_lora_bytes(pm, adapter_ids: list, rows: int) -> dict:
 
 
 def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Tensor, reps: int, seed: int = 0) -> dict:
-    """Every wrapped Linear's shrink+expand over one batch, launched alone (no base model), events per op."""
+    """Every wrapped Linear's shrink+expand over one batch, launched back to back without the base model."""
     from polylora_amd import sgmv
 
     device = pm.adapter_cache.device
     cache = pm.adapter_cache
     row_slot = cache.ensure_resident(adapter_ids)
-    plan = sgmv.SgmvPlan(row_slot, seq_lens, tokens_per_row, cache.num_slots)
+    distinct = len({a for a in adapter_ids if a != pm.config.base_adapter_id})
+    plan = sgmv.SgmvPlan(row_slot, seq_lens, tokens_per_row, cache.num_slots, distinct_slots=distinct)
     T = len(adapter_ids) * tokens_per_row
     gen = torch.Generator(device=device).manual_seed(seed)
     shapes = sorted({(s.in_features, s.out_features) for s in pm.module_specs})
     xs = {k: torch.randn(T, k, generator=gen, device=device, dtype=torch.bfloat16) for k, _ in shapes}
     ys = {n: torch.randn(T, n, generator=gen, device=device, dtype=torch.bfloat16) for _, n in shapes}
-    timer = KernelTimer()
-    for spec in pm.module_specs:  # warm-up pass
-        timer.run(xs[spec.in_features], ys[spec.out_features], cache, spec.name, plan)
-    timer.times_ms()
-    per_type: dict = {}
-    tot_sh = tot_ex = 0.0
-    for _ in range(reps):
-        for spec in pm.module_specs:
-            timer.run(xs[spec.in_features], ys[spec.out_features], cache, spec.name, plan)
-        sh, ex = timer.times_ms()
-        tot_sh += sum(sh)
-        tot_ex += sum(ex)
-        for spec, a, b in zip(pm.module_specs, sh, ex):
-            key = spec.name.rsplit(".", 1)[-1]
-            d = per_type.setdefault(key, [0.0, 0.0, 0])
-            d[0] += a
-            d[1] += b
-            d[2] += 1
-    return {"shrink_ms": tot_sh / reps, "expand_ms": tot_ex / reps,
-            "per_type_us": {k: [round(1e3 * v[0] / v[2], 2), round(1e3 * v[1] / v[2], 2)] for k, v in per_type.items()}}
+    launches = [SgmvLaunch(xs[s.in_features], ys[s.out_features], cache, s.name, plan) for s in pm.module_specs]
+    pairs = [f for l in launches for f in (l.shrink, l.expand)]
+    total_ms = time_launches(pairs, reps)
+    sh_ms = time_launches([l.shrink for l in launches], reps)
+    ex_ms = time_launches([l.expand for l in launches], reps)
+    per_type = {}
+    for key in sorted({s.name.rsplit(".", 1)[-1] for s in pm.module_specs}):
+        sel = [l for l, s in zip(launches, pm.module_specs) if s.name.rsplit(".", 1)[-1] == key]
+        per_type[key] = [round(1e3 * time_launches([l.shrink for l in sel], reps) / len(sel), 2),
+                         round(1e3 * time_launches([l.expand for l in sel], reps) / len(sel), 2)]
+    return {"pairs_ms": total_ms, "shrink_ms": sh_ms, "expand_ms": ex_ms, "per_type_us": per_type,
+            "group_tokens": plan.group_tokens}
 
 
 def _graph_ms(fn, reps: int) -> float:
@@ -651,7 +648,8 @@ def run_decode(args) -> dict:
 
     with torch.inference_mode():
         kt = time_lora_ops(pm, wl.adapter_ids, 1, torch.ones(B, dtype=torch.int32, device=device), reps=5)
-        kern_ms = kt["shrink_ms"] + kt["expand_ms"]
+        kern_ms = kt["pairs_ms"]
+        out["plan_group_tokens"] = kt["group_tokens"]
         out["lora_kernels_ms"] = round(kern_ms, 4)
         out["lora_kernels_gbs"] = round(nb["total"] / (kern_ms * 1e-3) / 1e9, 1)
         out["lora_kernels_pct_hbm"] = round(100 * nb["total"] / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)

@@ -80,8 +80,11 @@ typedef struct pl_group {
 
 /* Maximum slot count accepted by pl_plan_build (slot 0 included). */
 #define PL_MAX_SLOTS 4096
-/* Token-group size used by the tiled kernels. */
-#define PL_GROUP_TOKENS 64
+/* Token-group sizes of a plan: short groups for short adapter segments
+ * (decode), long groups for long segments (prefill).  The tiled kernels are
+ * called with the group size of the plan they walk. */
+#define PL_GROUP_TOKENS_SHORT 16
+#define PL_GROUP_TOKENS_LONG 64
 
 /* Library version (major*10000 + minor*100 + patch). */
 int pl_version(void);
@@ -95,30 +98,33 @@ const char* pl_last_error(void);
 int pl_is_device_pointer(const void* ptr);
 
 /* Upper bound on the number of groups pl_plan_build can emit for `rows` rows
- * of `row_len` tokens over `num_slots` slots: ceil(rows*row_len/64) + num_slots - 1. */
-int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t num_slots);
+ * of `row_len` tokens over `num_slots` slots:
+ * ceil(rows*row_len/group_tokens) + num_slots - 1. */
+int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t num_slots,
+                               int32_t group_tokens);
 
 /* Build the per-forward adapter-major plan on the device.
  *   row_slot[rows]  int32 slot of each row (weight_indices, cache.py:77-84)
  *   seq_lens[rows]  int32 valid length of each row; the row contributes
  *                   min(max(seq_len,0), row_len) tokens (layers.py:127 slicing)
+ *   group_tokens    16 or 64: tokens per group at most
  *   tok[rows*row_len]          out: token indices (row*row_len + m), grouped by slot
  *   groups[group_cap]          out: pl_group list
- *   meta[4]                    out: {num_groups, num_tokens, 0, 0}
+ *   meta[4]                    out: {num_groups, num_tokens, group_tokens, 0}
  * Rows with slot 0, slot >= num_slots, slot < 0 or length 0 are skipped.
  * Token order inside one slot is unspecified; every consumer is order-free. */
 int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,
-                  int32_t row_len, int32_t num_slots, int32_t* tok, pl_group* groups,
-                  int32_t* meta, int64_t group_cap, void* stream);
+                  int32_t row_len, int32_t num_slots, int32_t group_tokens, int32_t* tok,
+                  pl_group* groups, int32_t* meta, int64_t group_cap, void* stream);
 
 /* Number of K splits pl_sgmv_shrink uses for a requested count: the K range
  * is cut into at most k_splits pieces of whole MFMA steps. */
-int32_t pl_shrink_planes(int32_t dtype, int32_t K, int32_t k_splits);
+int32_t pl_shrink_planes(int32_t dtype, int32_t K, int32_t k_splits, int32_t group_tokens);
 
 /* Bytes of the workspace `ws` that pl_sgmv_shrink / pl_lora_apply need for
  * these sizes: fp32 partial planes [planes][tmp_rows][ldt]. */
-int64_t pl_shrink_workspace_bytes(int32_t dtype, int32_t K, int32_t k_splits, int64_t tmp_rows,
-                                  int32_t ldt);
+int64_t pl_shrink_workspace_bytes(int32_t dtype, int32_t K, int32_t k_splits,
+                                  int32_t group_tokens, int64_t tmp_rows, int32_t ldt);
 
 /* Shrink: planes[c][p][j] = sum_{k in split c} x[tok[p]][k] * A_slot[j][k]
  * for every planned token position p, j < rank(slot, module) and split
@@ -126,6 +132,7 @@ int64_t pl_shrink_workspace_bytes(int32_t dtype, int32_t K, int32_t k_splits, in
  * (no atomics); entries outside (p, j < rank) are not written and nothing
  * needs clearing between calls.
  *   x [*, ldx] of dtype; K = in_features
+ *   group_tokens: the group size the plan was built with (16 or 64)
  *   ws / ws_bytes: at least pl_shrink_workspace_bytes(...) bytes
  *   tmp_rows >= the plan's token count; ldt a multiple of 8 and >= every
  *     rank8 of this module.
@@ -134,8 +141,8 @@ int64_t pl_shrink_workspace_bytes(int32_t dtype, int32_t K, int32_t k_splits, in
 int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t K, const void* arena,
                    const pl_slot_entry* table, int32_t num_modules, int32_t module,
                    const int32_t* tok, const pl_group* groups, const int32_t* meta,
-                   int64_t group_cap, void* ws, int64_t ws_bytes, int32_t ldt, int64_t tmp_rows,
-                   int32_t k_splits, void* stream);
+                   int64_t group_cap, int32_t group_tokens, void* ws, int64_t ws_bytes,
+                   int32_t ldt, int64_t tmp_rows, int32_t k_splits, void* stream);
 
 /* Expand: y[tok[p]][n] = T(y + d), d = scale * sum_{j<rank} T(sum_c
  * planes[c][p][j]) * B_slot[n][j] rounded in the order of `epilogue`; the
@@ -145,16 +152,16 @@ int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t K, const v
 int pl_sgmv_expand(int32_t dtype, const void* ws, int32_t ldt, int64_t tmp_rows, int32_t planes,
                    const void* arena, const pl_slot_entry* table, int32_t num_modules,
                    int32_t module, const int32_t* tok, const pl_group* groups,
-                   const int32_t* meta, int64_t group_cap, void* y, int64_t ldy, int32_t N,
-                   int32_t epilogue, void* stream);
+                   const int32_t* meta, int64_t group_cap, int32_t group_tokens, void* y,
+                   int64_t ldy, int32_t N, int32_t epilogue, void* stream);
 
 /* Shrink followed by expand on one stream (one call per wrapped Linear). */
 int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y, int64_t ldy,
                   int32_t N, const void* arena, const pl_slot_entry* table,
                   int32_t num_modules, int32_t module, const int32_t* tok,
-                  const pl_group* groups, const int32_t* meta, int64_t group_cap, void* ws,
-                  int64_t ws_bytes, int32_t ldt, int64_t tmp_rows, int32_t k_splits,
-                  int32_t epilogue, void* stream);
+                  const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                  int32_t group_tokens, void* ws, int64_t ws_bytes, int32_t ldt,
+                  int64_t tmp_rows, int32_t k_splits, int32_t epilogue, void* stream);
 
 /* Row-based LoRA on the slot arena for shapes the tiled path rejects
  * (any K, N, strides, alignment).  Writes y[b*row_len+m] for m < seq_len[b].

@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import numpy as np
 
-GROUP_TOKENS = 64
+GROUP_TOKENS = 64  # default group size; check_plan takes the plan's own
 
 
 def expected_tokens(row_slot, seq_lens, row_len: int, num_slots: int) -> dict[int, list[int]]:
@@ -25,19 +25,21 @@ def expected_tokens(row_slot, seq_lens, row_len: int, num_slots: int) -> dict[in
     return per_slot
 
 
-def check_plan(tok: np.ndarray, groups: np.ndarray, meta: np.ndarray, row_slot, seq_lens, row_len: int, num_slots: int) -> None:
+def check_plan(tok: np.ndarray, groups: np.ndarray, meta: np.ndarray, row_slot, seq_lens, row_len: int, num_slots: int,
+               group_tokens: int = GROUP_TOKENS) -> None:
     """Assert a device plan is a valid grouping of exactly the expected tokens."""
     expect = expected_tokens(row_slot, seq_lens, row_len, num_slots)
     n_tokens = sum(len(v) for v in expect.values())
-    n_groups = sum(-(-len(v) // GROUP_TOKENS) for v in expect.values())
+    n_groups = sum(-(-len(v) // group_tokens) for v in expect.values())
     assert int(meta[0]) == n_groups, (int(meta[0]), n_groups)
     assert int(meta[1]) == n_tokens, (int(meta[1]), n_tokens)
+    assert int(meta[2]) == group_tokens, (int(meta[2]), group_tokens)
     seen: dict[int, list[int]] = {}
     covered = np.zeros(n_tokens, dtype=np.int64)
     for g in range(n_groups):
         slot, start, length, _ = (int(v) for v in groups[g])
         assert 0 < slot < num_slots
-        assert 1 <= length <= GROUP_TOKENS
+        assert 1 <= length <= group_tokens
         assert 0 <= start and start + length <= n_tokens
         covered[start : start + length] += 1
         seen.setdefault(slot, []).extend(int(t) for t in tok[start : start + length])
@@ -48,4 +50,4 @@ def check_plan(tok: np.ndarray, groups: np.ndarray, meta: np.ndarray, row_slot, 
     # groups of one slot: all full except possibly one
     for slot in expect:
         lens = sorted((int(groups[g][2]) for g in range(n_groups) if int(groups[g][0]) == slot), reverse=True)
-        assert all(v == GROUP_TOKENS for v in lens[:-1])
+        assert all(v == group_tokens for v in lens[:-1])

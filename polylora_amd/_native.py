@@ -18,7 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolylora_hip.so"
 PL_F32, PL_BF16, PL_F16 = 0, 1, 2
 PL_EPI_FALLBACK, PL_EPI_TRITON = 0, 1
 PL_MAX_SLOTS = 4096
-PL_GROUP_TOKENS = 64
+PL_GROUP_TOKENS_SHORT, PL_GROUP_TOKENS_LONG = 16, 64
 SLOT_ENTRY_INT32S = 8  # sizeof(pl_slot_entry) / 4
 
 DTYPE_CODES = {torch.float32: PL_F32, torch.bfloat16: PL_BF16, torch.float16: PL_F16}
@@ -37,22 +37,22 @@ _SIGNATURES: dict[str, tuple] = {
     "pl_version": (),
     "pl_last_error": (),
     "pl_is_device_pointer": (c_void_p,),
-    "pl_plan_group_capacity": (c_int32, c_int32, c_int32),
-    "pl_plan_build": (c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p),
-    "pl_shrink_planes": (c_int32, c_int32, c_int32),
-    "pl_shrink_workspace_bytes": (c_int32, c_int32, c_int32, c_int64, c_int32),
+    "pl_plan_group_capacity": (c_int32, c_int32, c_int32, c_int32),
+    "pl_plan_build": (c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p),
+    "pl_shrink_planes": (c_int32, c_int32, c_int32, c_int32),
+    "pl_shrink_workspace_bytes": (c_int32, c_int32, c_int32, c_int32, c_int64, c_int32),
     "pl_sgmv_shrink": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
-        c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int64, c_int32, c_void_p,
+        c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_int64, c_int32, c_void_p,
     ),
     "pl_sgmv_expand": (
         c_int32, c_void_p, c_int32, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
-        c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_void_p,
+        c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_int32, c_void_p,
     ),
     "pl_lora_apply": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
-        c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int64, c_int32,
-        c_int32, c_void_p,
+        c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_int64,
+        c_int32, c_int32, c_void_p,
     ),
     "pl_lora_apply_rows": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,

@@ -19,8 +19,8 @@ constexpr int kPlanThreads = 1024;
 
 __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     const int32_t* __restrict__ row_slot, const int32_t* __restrict__ seq_lens, int32_t rows,
-    int32_t row_len, int32_t num_slots, int32_t* __restrict__ tok, pl_group* __restrict__ groups,
-    int32_t* __restrict__ meta, int64_t group_cap) {
+    int32_t row_len, int32_t num_slots, int32_t group_tokens, int32_t* __restrict__ tok,
+    pl_group* __restrict__ groups, int32_t* __restrict__ meta, int64_t group_cap) {
   __shared__ int32_t cnt[PL_MAX_SLOTS];
   __shared__ int32_t off[PL_MAX_SLOTS];
   __shared__ int32_t goff[PL_MAX_SLOTS];
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     loc_t[q] = st;
     loc_g[q] = sg;
     st += c;
-    sg += (c + PL_GROUP_TOKENS - 1) / PL_GROUP_TOKENS;
+    sg += (c + group_tokens - 1) / group_tokens;
   }
   int it = st, ig = sg;
   for (int d = 1; d < 64; d <<= 1) {
@@ -90,21 +90,21 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   if (tid == 0) {
     meta[0] = tg;
     meta[1] = tt;
-    meta[2] = 0;
+    meta[2] = group_tokens;
     meta[3] = 0;
   }
   __syncthreads();
 
   for (int s = tid; s < S; s += kPlanThreads) {
     const int c = cnt[s];
-    const int ng = (c + PL_GROUP_TOKENS - 1) / PL_GROUP_TOKENS;
+    const int ng = (c + group_tokens - 1) / group_tokens;
     for (int q = 0; q < ng; ++q) {
       const int64_t gi = (int64_t)goff[s] + q;
       if (gi < group_cap) {
         pl_group gr;
         gr.slot = s;
-        gr.start = off[s] + q * PL_GROUP_TOKENS;
-        gr.len = min(PL_GROUP_TOKENS, c - q * PL_GROUP_TOKENS);
+        gr.start = off[s] + q * group_tokens;
+        gr.len = min(group_tokens, c - q * group_tokens);
         gr.reserved = 0;
         groups[gi] = gr;
       }
@@ -157,15 +157,17 @@ __global__ __launch_bounds__(256) void pl_right_pad_kernel(const void* __restric
 
 }  // namespace
 
-extern "C" int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t num_slots) {
-  if (rows < 0 || row_len < 0 || num_slots < 1) return 0;
+extern "C" int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t num_slots,
+                                          int32_t group_tokens) {
+  if (rows < 0 || row_len < 0 || num_slots < 1 || group_tokens < 1) return 0;
   const int64_t t = (int64_t)rows * row_len;
-  return (t + PL_GROUP_TOKENS - 1) / PL_GROUP_TOKENS + (num_slots - 1);
+  return (t + group_tokens - 1) / group_tokens + (num_slots - 1);
 }
 
 extern "C" int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,
-                             int32_t row_len, int32_t num_slots, int32_t* tok,
-                             pl_group* groups, int32_t* meta, int64_t group_cap, void* stream) {
+                             int32_t row_len, int32_t num_slots, int32_t group_tokens,
+                             int32_t* tok, pl_group* groups, int32_t* meta, int64_t group_cap,
+                             void* stream) {
   if (!meta || (rows > 0 && (!row_slot || !seq_lens || !tok || !groups))) {
     pl_set_error("pl_plan_build: null pointer");
     return PL_ERR_ARG;
@@ -173,6 +175,10 @@ extern "C" int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, i
   if (rows < 0 || row_len < 0 || num_slots < 1) {
     pl_set_error("pl_plan_build: bad sizes rows=%d row_len=%d num_slots=%d", rows, row_len,
                  num_slots);
+    return PL_ERR_ARG;
+  }
+  if (group_tokens != 16 && group_tokens != 64) {
+    pl_set_error("pl_plan_build: group_tokens must be 16 or 64 (got %d)", group_tokens);
     return PL_ERR_ARG;
   }
   if (num_slots > PL_MAX_SLOTS) {
@@ -183,14 +189,14 @@ extern "C" int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, i
     pl_set_error("pl_plan_build: rows*row_len exceeds 2^31-1");
     return PL_ERR_LIMIT;
   }
-  if (group_cap < pl_plan_group_capacity(rows, row_len, num_slots)) {
+  if (group_cap < pl_plan_group_capacity(rows, row_len, num_slots, group_tokens)) {
     pl_set_error("pl_plan_build: group capacity %lld below the bound %lld", (long long)group_cap,
-                 (long long)pl_plan_group_capacity(rows, row_len, num_slots));
+                 (long long)pl_plan_group_capacity(rows, row_len, num_slots, group_tokens));
     return PL_ERR_ARG;
   }
   hipLaunchKernelGGL(pl_plan_kernel, dim3(1), dim3(kPlanThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), row_slot, seq_lens, rows, row_len,
-                     num_slots, tok, groups, meta, group_cap);
+                     num_slots, group_tokens, tok, groups, meta, group_cap);
   return pl_launch_status("pl_plan_build");
 }
 

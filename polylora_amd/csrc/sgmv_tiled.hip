@@ -1,17 +1,21 @@
 // Adapter-major tiled SGMV kernels for gfx950 (MFMA 16x16, wave64).
 //
 // Both kernels walk the plan written by pl_plan_build: a list of groups of
-// at most 64 tokens that share one slot.  A token's result never depends on
-// which other tokens share its group, so the plan's order inside a slot is
-// free.
+// at most G tokens that share one slot, G = 16 * RT with RT = 1 (short
+// adapter segments, e.g. decode) or RT = 4 (long segments, e.g. prefill).
+// RT is a template parameter so that registers are sized for the group:
+// short segments get more K and more ranks in flight per wave instead of
+// accumulators for rows that do not exist.  A token's result never depends
+// on which other tokens share its group, so the plan's order inside a slot
+// is free.
 //
 // Shrink (replaces sgmv.py:63-138): one workgroup per (group, K split).  Its
-// four waves split the split's K range; per step each lane loads two
-// 16-byte chunks of one token row of x and of one rank row of A, and the
-// four lanes that share a row read 64 contiguous bytes per load.  16x16 MFMA
-// tiles [tokens x ranks] accumulate in fp32, the four wave partials are
-// summed in LDS in a fixed order, and the block stores its sum with plain
-// stores into its own fp32 plane planes[split][position][rank].
+// four waves split the split's K range; per step each lane loads CC 16-byte
+// chunks of one token row of x and of one rank row of A, and the four lanes
+// that share a row read 64 contiguous bytes per load.  16x16 MFMA tiles
+// [tokens x ranks] accumulate in fp32 (16*JT ranks per pass), the four wave
+// partials are summed in LDS in a fixed order, and the block stores its sum
+// with plain stores into its own fp32 plane planes[split][position][rank].
 //
 // Expand (replaces sgmv.py:178-275): one workgroup per (group, column chunk
 // of 256 bf16/f16 or 128 f32 output columns), one 16-token row tile at a
@@ -24,16 +28,28 @@
 // bitwise reproducible and every launch can be recorded in a HIP graph.
 // The scaled, rounded delta goes through LDS to the row-major layout of y,
 // and the fused add-back reads and writes y once with 16-byte accesses (512
-// contiguous bytes per row).  Registers stay near 128 per lane so that four
+// contiguous bytes per row).  With RT = 1 the y rows are loaded up front, in
+// parallel with B.  Registers stay at or below 128 per lane so that four
 // workgroups share a CU and hide each other's memory latency.
 #include "pl_common.h"
 
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kChunksPerLane = 2;  // 16-byte chunks per lane per shrink step
-constexpr int kJT = 2;             // 16-rank column tiles per shrink pass
-constexpr int kYRowsPerPass = 8;   // 256 threads, 32 lanes per tile row
+constexpr int kYRowsPerPass = 8;  // 256 threads, 32 lanes per tile row
+
+// Shrink shape per row-tile count: CC 16-byte chunks per lane per step and
+// JT 16-rank column tiles per pass.
+template <int RT>
+struct pl_shrink_shape;
+template <>
+struct pl_shrink_shape<1> {
+  enum { CC = 4, JT = 4 };
+};
+template <>
+struct pl_shrink_shape<4> {
+  enum { CC = 2, JT = 2 };
+};
 
 struct pl_shrink_args {
   const void* x;
@@ -83,13 +99,15 @@ struct pl_expand_shape {
   enum { kLdsRow = kChunk + kPad };
 };
 
-template <int DT>
+template <int DT, int RT>
 __global__ __launch_bounds__(256, 4) void pl_shrink_tiled(pl_shrink_args a) {
   typedef typename pl_traits<DT>::T T;
+  typedef pl_shrink_shape<RT> S;
   constexpr int E = pl_traits<DT>::E;
-  constexpr int kInstr = 4 * E;                   // k covered by one wave load (4 lane groups)
-  constexpr int kStep = kChunksPerLane * kInstr;  // k covered by one wave step
-  __shared__ pl_f32x4 red[kWaves][4][64];
+  constexpr int kInstr = 4 * E;          // k covered by one wave load (4 lane groups)
+  constexpr int kStep = S::CC * kInstr;  // k covered by one wave step
+  constexpr int kSlots = RT * S::JT;     // 16x16 tiles per pass
+  __shared__ pl_f32x4 red[kWaves][kWaves][64];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -104,17 +122,17 @@ __global__ __launch_bounds__(256, 4) void pl_shrink_tiled(pl_shrink_args a) {
   const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module];
   const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
   if (rank <= 0) return;
-  const int len = grp.len;
+  const int len = min(grp.len, 16 * RT);  // the host pairs the plan's group size with RT
   const int nrt = (len + 15) >> 4;
   const int K = a.K;
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
   const T* __restrict__ A = reinterpret_cast<const T*>(a.arena + e.a_off);
   float* __restrict__ out = a.planes + (int64_t)c * a.plane;
 
-  const T* xrow[4];
-  bool xok[4];
+  const T* xrow[RT];
+  bool xok[RT];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     const int p = rt * 16 + li;
     xok[rt] = p < len;
     const int t = xok[rt] ? a.tok[grp.start + p] : 0;
@@ -123,63 +141,64 @@ __global__ __launch_bounds__(256, 4) void pl_shrink_tiled(pl_shrink_args a) {
   const int k0 = (c * kWaves + wave) * a.kw;
   const int k1 = min(K, k0 + a.kw);
 
-  for (int rb = 0; rb < rank; rb += 16 * kJT) {
-    pl_f32x4 acc[4][kJT];
+  for (int rb = 0; rb < rank; rb += 16 * S::JT) {
+    pl_f32x4 acc[RT][S::JT];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int jt = 0; jt < kJT; ++jt) acc[rt][jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int jt = 0; jt < S::JT; ++jt) acc[rt][jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
 
     for (int kb = k0; kb < k1; kb += kStep) {
       // chunk cc of lane (li, lg) covers k = kb + cc*kInstr + lg*E .. +E
-      pl_u32x4 xf[4][kChunksPerLane];
+      pl_u32x4 xf[RT][S::CC];
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
+      for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int cc = 0; cc < kChunksPerLane; ++cc) {
+        for (int cc = 0; cc < S::CC; ++cc) {
           const int k = kb + cc * kInstr;
           pl_u32x4 v = {0u, 0u, 0u, 0u};
           if (xok[rt] && k + lg * E < k1) v = pl_ld16(xrow[rt] + k);
           xf[rt][cc] = v;
         }
 #pragma unroll
-      for (int jt = 0; jt < kJT; ++jt) {
+      for (int jt = 0; jt < S::JT; ++jt) {
         if (rb + jt * 16 < rank) {
           const int j = rb + jt * 16 + li;
           const T* arow = A + (int64_t)j * K + lg * E;
-          pl_u32x4 af[kChunksPerLane];
+          pl_u32x4 af[S::CC];
 #pragma unroll
-          for (int cc = 0; cc < kChunksPerLane; ++cc) {
+          for (int cc = 0; cc < S::CC; ++cc) {
             const int k = kb + cc * kInstr;
             pl_u32x4 v = {0u, 0u, 0u, 0u};
             if (j < rank && k + lg * E < k1) v = pl_ld16(arow + k);
             af[cc] = v;
           }
 #pragma unroll
-          for (int rt = 0; rt < 4; ++rt)
+          for (int rt = 0; rt < RT; ++rt)
             if (rt < nrt)
 #pragma unroll
-              for (int cc = 0; cc < kChunksPerLane; ++cc)
+              for (int cc = 0; cc < S::CC; ++cc)
                 acc[rt][jt] = pl_mfma_chunk<DT>(xf[rt][cc], af[cc], acc[rt][jt]);
         }
       }
     }
 
-    // Sum the four wave partials of each row tile in a fixed order.
-    // acc[rt][jt][v] holds tile element (row 4*lg+v, column li).  Thread
-    // (wave, lane) finishes row tile rt0 + wave / kJT, column tile wave % kJT.
+    // Sum the four wave partials of each tile in a fixed order, four tiles
+    // (one per finishing wave) at a time.  acc[rt][jt][v] holds tile element
+    // (row 4*lg+v, column li); tile index = rt*JT + jt.
 #pragma unroll
-    for (int rt0 = 0; rt0 < 4; rt0 += 4 / kJT) {
-      if (rt0 < nrt) {
+    for (int t0 = 0; t0 < kSlots; t0 += kWaves) {
+      if (t0 / S::JT < nrt) {
         __syncthreads();
 #pragma unroll
-        for (int q = 0; q < 4 / kJT; ++q)
-#pragma unroll
-          for (int jt = 0; jt < kJT; ++jt) red[wave][q * kJT + jt][lane] = acc[rt0 + q][jt];
+        for (int q = 0; q < kWaves; ++q) {
+          const int t = t0 + q;
+          red[wave][q][lane] = acc[t / S::JT][t % S::JT];
+        }
         __syncthreads();
-        const int rt = rt0 + wave / kJT;
-        const int jt = wave % kJT;
-        const int j = rb + jt * 16 + li;
+        const int t = t0 + wave;  // tile this wave finishes
+        const int rt = t / S::JT;
+        const int j = rb + (t % S::JT) * 16 + li;
         const pl_f32x4 s = red[0][wave][lane] + red[1][wave][lane] + red[2][wave][lane] +
                            red[3][wave][lane];
         if (j < rank && rt < nrt) {
@@ -236,7 +255,7 @@ __device__ __forceinline__ pl_u32x4 pl_sum_planes(const float* __restrict__ src,
   }
 }
 
-template <int DT>
+template <int DT, int RT>
 __global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
   typedef typename pl_traits<DT>::T T;
   typedef typename pl_traits<DT>::T4 T4;
@@ -244,7 +263,9 @@ __global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
   typedef pl_expand_shape<DT> S;
   constexpr int E = pl_traits<DT>::E;
   constexpr int kStep = 4 * E;  // rank slots per MFMA step
-  __shared__ __attribute__((aligned(16))) T delta[64 * S::kLdsRow];
+  constexpr int kRows = 16 * RT;
+  constexpr int kYPer = kRows / kYRowsPerPass;  // y rows per thread
+  __shared__ __attribute__((aligned(16))) T delta[kRows * S::kLdsRow];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -262,12 +283,27 @@ __global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
   const int r8 = e.rank8;
   const int N = a.N;
   const int n_base = c * S::kChunk;
-  const int len = grp.len;
+  const int len = min(grp.len, kRows);  // the host pairs the plan's group size with RT
   const int nrt = (len + 15) >> 4;
   const float scale = e.scale;
   const float scale_t = pl_round<DT>(scale);
   const int n0 = n_base + wave * S::kColsWave;
   const T* __restrict__ Bc = reinterpret_cast<const T*>(a.arena + e.b_off);
+
+  // y tile rows of this thread: rows t/32 + 8*i, columns (t%32)*E .. +E.
+  const int yq = tid & 31;
+  const int yr0 = tid >> 5;
+  const int ycol = n_base + yq * E;
+  T* __restrict__ y = reinterpret_cast<T*>(a.y);
+  pl_u32x4 yv[kYPer];
+  T* yptr[kYPer];
+#pragma unroll
+  for (int i = 0; i < kYPer; ++i) {
+    const int r = yr0 + kYRowsPerPass * i;
+    yptr[i] = (r < len && ycol < N) ? y + (int64_t)a.tok[grp.start + r] * a.ldy + ycol : nullptr;
+    yv[i] = pl_u32x4{0u, 0u, 0u, 0u};
+    if (RT == 1 && yptr[i] != nullptr) yv[i] = pl_ld16(yptr[i]);  // short tiles: load y early
+  }
 
   // 1. delta^T tiles [columns x tokens] on the MFMA, one 16-token row tile at
   // a time; acc[ct][v] = delta(column n0 + ct*16 + 4*lg + v, token rt*16 + li).
@@ -304,26 +340,14 @@ __global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
   }
   __syncthreads();
 
-  // 3. y = T(y + delta): thread (row t/32 + 8*i, columns (t%32)*E .. +E), full-width
-  // loads and stores, all of a thread's rows in flight together.
-  const int yq = tid & 31;
-  const int yr0 = tid >> 5;
-  const int ycol = n_base + yq * E;
-  if (ycol >= N) return;
-  T* __restrict__ y = reinterpret_cast<T*>(a.y);
-  pl_u32x4 yv[64 / kYRowsPerPass];
-  T* yptr[64 / kYRowsPerPass];
+  // 3. y = T(y + delta) with full-width stores.
+  if (RT != 1) {
 #pragma unroll
-  for (int i = 0; i < 64 / kYRowsPerPass; ++i) {
-    const int r = yr0 + kYRowsPerPass * i;
-    yptr[i] = nullptr;
-    if (r < len) {
-      yptr[i] = y + (int64_t)a.tok[grp.start + r] * a.ldy + ycol;
-      yv[i] = pl_ld16(yptr[i]);
-    }
+    for (int i = 0; i < kYPer; ++i)
+      if (yptr[i] != nullptr) yv[i] = pl_ld16(yptr[i]);
   }
 #pragma unroll
-  for (int i = 0; i < 64 / kYRowsPerPass; ++i) {
+  for (int i = 0; i < kYPer; ++i) {
     if (yptr[i] != nullptr) {
       const int r = yr0 + kYRowsPerPass * i;
       const pl_u32x4 dv = *reinterpret_cast<const pl_u32x4*>(delta + r * S::kLdsRow + yq * E);
@@ -342,19 +366,19 @@ __global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
   }
 }
 
-template <int DT>
+template <int DT, int RT>
 int launch_shrink(const pl_shrink_args& a, int64_t group_cap, hipStream_t stream) {
   const int64_t grid = group_cap * a.k_splits;
   if (grid <= 0) return PL_OK;
-  hipLaunchKernelGGL(pl_shrink_tiled<DT>, dim3((unsigned)grid), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((pl_shrink_tiled<DT, RT>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   return pl_launch_status("pl_sgmv_shrink");
 }
 
-template <int DT>
+template <int DT, int RT>
 int launch_expand(const pl_expand_args& a, int64_t group_cap, hipStream_t stream) {
   const int64_t grid = group_cap * a.n_chunks;
   if (grid <= 0) return PL_OK;
-  hipLaunchKernelGGL(pl_expand_tiled<DT>, dim3((unsigned)grid), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((pl_expand_tiled<DT, RT>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   return pl_launch_status("pl_sgmv_expand");
 }
 
@@ -362,7 +386,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int check_common(int32_t dtype, const void* arena, const pl_slot_entry* table,
                  int32_t num_modules, int32_t module, const int32_t* tok,
-                 const pl_group* groups, const int32_t* meta, int64_t group_cap) {
+                 const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                 int32_t group_tokens) {
   if (dtype != PL_F32 && dtype != PL_BF16 && dtype != PL_F16) {
     pl_set_error("unsupported dtype code %d", dtype);
     return PL_ERR_ARG;
@@ -379,6 +404,10 @@ int check_common(int32_t dtype, const void* arena, const pl_slot_entry* table,
     pl_set_error("group capacity %lld out of range", (long long)group_cap);
     return PL_ERR_LIMIT;
   }
+  if (group_tokens != 16 && group_tokens != 64) {
+    pl_set_error("group_tokens must be 16 or 64 (got %d)", group_tokens);
+    return PL_ERR_ARG;
+  }
   if (!aligned16(arena)) {
     pl_set_error("arena base is not 16-byte aligned");
     return PL_ERR_ALIGN;
@@ -387,15 +416,16 @@ int check_common(int32_t dtype, const void* arena, const pl_slot_entry* table,
 }
 
 // K per wave for a requested split count: a multiple of the wave step.
-int64_t shrink_kw(int32_t dtype, int32_t K, int32_t k_splits) {
-  const int64_t step = (int64_t)kChunksPerLane * 4 * pl_chunk_elems(dtype);
+int64_t shrink_kw(int32_t dtype, int32_t K, int32_t k_splits, int32_t group_tokens) {
+  const int cc = group_tokens == 16 ? pl_shrink_shape<1>::CC : pl_shrink_shape<4>::CC;
+  const int64_t step = (int64_t)cc * 4 * pl_chunk_elems(dtype);
   const int64_t per_split = (K + (int64_t)k_splits - 1) / k_splits;
   const int64_t kw = (per_split + kWaves - 1) / kWaves;
   return (kw + step - 1) / step * step;
 }
 
-int32_t shrink_planes(int32_t dtype, int32_t K, int32_t k_splits) {
-  const int64_t kw = shrink_kw(dtype, K, k_splits);
+int32_t shrink_planes(int32_t dtype, int32_t K, int32_t k_splits, int32_t group_tokens) {
+  const int64_t kw = shrink_kw(dtype, K, k_splits, group_tokens);
   return (int32_t)((K + kWaves * kw - 1) / (kWaves * kw));
 }
 
@@ -423,9 +453,10 @@ int check_ws(const void* ws, int32_t ldt, int64_t tmp_rows) {
 int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx, int32_t K,
                    const void* arena, const pl_slot_entry* table, int32_t num_modules,
                    int32_t module, const int32_t* tok, const pl_group* groups,
-                   const int32_t* meta, int64_t group_cap, void* ws, int64_t ws_bytes,
-                   int32_t ldt, int64_t tmp_rows, int32_t k_splits) {
-  int st = check_common(dtype, arena, table, num_modules, module, tok, groups, meta, group_cap);
+                   const int32_t* meta, int64_t group_cap, int32_t group_tokens, void* ws,
+                   int64_t ws_bytes, int32_t ldt, int64_t tmp_rows, int32_t k_splits) {
+  int st = check_common(dtype, arena, table, num_modules, module, tok, groups, meta, group_cap,
+                        group_tokens);
   if (st) return st;
   if ((st = check_ws(ws, ldt, tmp_rows))) return st;
   const int E = pl_chunk_elems(dtype);
@@ -442,7 +473,7 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
     pl_set_error("shrink needs K %% %d == 0 and 16-byte aligned x rows", E);
     return PL_ERR_ALIGN;
   }
-  const int32_t planes = shrink_planes(dtype, K, k_splits);
+  const int32_t planes = shrink_planes(dtype, K, k_splits, group_tokens);
   if (group_cap * planes > 0x7fffffffLL) {
     pl_set_error("shrink grid too large");
     return PL_ERR_LIMIT;
@@ -455,7 +486,7 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
   a.x = x;
   a.ldx = ldx;
   a.K = K;
-  a.kw = (int32_t)shrink_kw(dtype, K, k_splits);
+  a.kw = (int32_t)shrink_kw(dtype, K, k_splits, group_tokens);
   a.arena = reinterpret_cast<const char*>(arena);
   a.table = table;
   a.num_modules = num_modules;
@@ -471,11 +502,13 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
 }
 
 int prepare_expand(pl_expand_args& a, int32_t dtype, const void* ws, int32_t ldt,
-                   int64_t tmp_rows, int32_t planes, const void* arena, const pl_slot_entry* table,
-                   int32_t num_modules, int32_t module, const int32_t* tok,
-                   const pl_group* groups, const int32_t* meta, int64_t group_cap, void* y,
-                   int64_t ldy, int32_t N, int32_t epilogue) {
-  int st = check_common(dtype, arena, table, num_modules, module, tok, groups, meta, group_cap);
+                   int64_t tmp_rows, int32_t planes, const void* arena,
+                   const pl_slot_entry* table, int32_t num_modules, int32_t module,
+                   const int32_t* tok, const pl_group* groups, const int32_t* meta,
+                   int64_t group_cap, int32_t group_tokens, void* y, int64_t ldy, int32_t N,
+                   int32_t epilogue) {
+  int st = check_common(dtype, arena, table, num_modules, module, tok, groups, meta, group_cap,
+                        group_tokens);
   if (st) return st;
   if ((st = check_ws(ws, ldt, tmp_rows))) return st;
   const int E = pl_chunk_elems(dtype);
@@ -521,79 +554,98 @@ int prepare_expand(pl_expand_args& a, int32_t dtype, const void* ws, int32_t ldt
   return PL_OK;
 }
 
-int dispatch_shrink(int32_t dtype, const pl_shrink_args& a, int64_t group_cap,
-                    hipStream_t s) {
+template <int RT>
+int dispatch_shrink_rt(int32_t dtype, const pl_shrink_args& a, int64_t group_cap,
+                       hipStream_t s) {
   switch (dtype) {
-    case PL_BF16: return launch_shrink<PL_BF16>(a, group_cap, s);
-    case PL_F16: return launch_shrink<PL_F16>(a, group_cap, s);
-    default: return launch_shrink<PL_F32>(a, group_cap, s);
+    case PL_BF16: return launch_shrink<PL_BF16, RT>(a, group_cap, s);
+    case PL_F16: return launch_shrink<PL_F16, RT>(a, group_cap, s);
+    default: return launch_shrink<PL_F32, RT>(a, group_cap, s);
   }
 }
 
-int dispatch_expand(int32_t dtype, const pl_expand_args& a, int64_t group_cap,
-                    hipStream_t s) {
+template <int RT>
+int dispatch_expand_rt(int32_t dtype, const pl_expand_args& a, int64_t group_cap,
+                       hipStream_t s) {
   switch (dtype) {
-    case PL_BF16: return launch_expand<PL_BF16>(a, group_cap, s);
-    case PL_F16: return launch_expand<PL_F16>(a, group_cap, s);
-    default: return launch_expand<PL_F32>(a, group_cap, s);
+    case PL_BF16: return launch_expand<PL_BF16, RT>(a, group_cap, s);
+    case PL_F16: return launch_expand<PL_F16, RT>(a, group_cap, s);
+    default: return launch_expand<PL_F32, RT>(a, group_cap, s);
   }
+}
+
+int dispatch_shrink(int32_t dtype, int32_t group_tokens, const pl_shrink_args& a,
+                    int64_t group_cap, hipStream_t s) {
+  return group_tokens == 16 ? dispatch_shrink_rt<1>(dtype, a, group_cap, s)
+                            : dispatch_shrink_rt<4>(dtype, a, group_cap, s);
+}
+
+int dispatch_expand(int32_t dtype, int32_t group_tokens, const pl_expand_args& a,
+                    int64_t group_cap, hipStream_t s) {
+  return group_tokens == 16 ? dispatch_expand_rt<1>(dtype, a, group_cap, s)
+                            : dispatch_expand_rt<4>(dtype, a, group_cap, s);
 }
 
 }  // namespace
 
-extern "C" int32_t pl_shrink_planes(int32_t dtype, int32_t K, int32_t k_splits) {
-  if (K <= 0 || k_splits < 1) return 0;
-  return shrink_planes(dtype, K, k_splits);
+extern "C" int32_t pl_shrink_planes(int32_t dtype, int32_t K, int32_t k_splits,
+                                    int32_t group_tokens) {
+  if (K <= 0 || k_splits < 1 || (group_tokens != 16 && group_tokens != 64)) return 0;
+  return shrink_planes(dtype, K, k_splits, group_tokens);
 }
 
 extern "C" int64_t pl_shrink_workspace_bytes(int32_t dtype, int32_t K, int32_t k_splits,
-                                             int64_t tmp_rows, int32_t ldt) {
-  if (K <= 0 || k_splits < 1 || tmp_rows < 0 || ldt <= 0) return 0;
-  return workspace_bytes(shrink_planes(dtype, K, k_splits), tmp_rows, ldt);
+                                             int32_t group_tokens, int64_t tmp_rows,
+                                             int32_t ldt) {
+  if (K <= 0 || k_splits < 1 || tmp_rows < 0 || ldt <= 0 ||
+      (group_tokens != 16 && group_tokens != 64))
+    return 0;
+  return workspace_bytes(shrink_planes(dtype, K, k_splits, group_tokens), tmp_rows, ldt);
 }
 
 extern "C" int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t K,
                               const void* arena, const pl_slot_entry* table,
                               int32_t num_modules, int32_t module, const int32_t* tok,
                               const pl_group* groups, const int32_t* meta, int64_t group_cap,
-                              void* ws, int64_t ws_bytes, int32_t ldt, int64_t tmp_rows,
-                              int32_t k_splits, void* stream) {
+                              int32_t group_tokens, void* ws, int64_t ws_bytes, int32_t ldt,
+                              int64_t tmp_rows, int32_t k_splits, void* stream) {
   pl_shrink_args a;
   int st = prepare_shrink(a, dtype, x, ldx, K, arena, table, num_modules, module, tok, groups,
-                          meta, group_cap, ws, ws_bytes, ldt, tmp_rows, k_splits);
+                          meta, group_cap, group_tokens, ws, ws_bytes, ldt, tmp_rows, k_splits);
   if (st) return st;
-  return dispatch_shrink(dtype, a, group_cap, reinterpret_cast<hipStream_t>(stream));
+  return dispatch_shrink(dtype, group_tokens, a, group_cap, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int pl_sgmv_expand(int32_t dtype, const void* ws, int32_t ldt, int64_t tmp_rows,
                               int32_t planes, const void* arena, const pl_slot_entry* table,
                               int32_t num_modules, int32_t module, const int32_t* tok,
                               const pl_group* groups, const int32_t* meta, int64_t group_cap,
-                              void* y, int64_t ldy, int32_t N, int32_t epilogue, void* stream) {
+                              int32_t group_tokens, void* y, int64_t ldy, int32_t N,
+                              int32_t epilogue, void* stream) {
   pl_expand_args a;
   int st = prepare_expand(a, dtype, ws, ldt, tmp_rows, planes, arena, table, num_modules, module,
-                          tok, groups, meta, group_cap, y, ldy, N, epilogue);
+                          tok, groups, meta, group_cap, group_tokens, y, ldy, N, epilogue);
   if (st) return st;
-  return dispatch_expand(dtype, a, group_cap, reinterpret_cast<hipStream_t>(stream));
+  return dispatch_expand(dtype, group_tokens, a, group_cap, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
                              int64_t ldy, int32_t N, const void* arena,
                              const pl_slot_entry* table, int32_t num_modules, int32_t module,
                              const int32_t* tok, const pl_group* groups, const int32_t* meta,
-                             int64_t group_cap, void* ws, int64_t ws_bytes, int32_t ldt,
-                             int64_t tmp_rows, int32_t k_splits, int32_t epilogue,
+                             int64_t group_cap, int32_t group_tokens, void* ws, int64_t ws_bytes,
+                             int32_t ldt, int64_t tmp_rows, int32_t k_splits, int32_t epilogue,
                              void* stream) {
   pl_shrink_args sa;
   pl_expand_args ea;
   int st = prepare_shrink(sa, dtype, x, ldx, K, arena, table, num_modules, module, tok, groups,
-                          meta, group_cap, ws, ws_bytes, ldt, tmp_rows, k_splits);
+                          meta, group_cap, group_tokens, ws, ws_bytes, ldt, tmp_rows, k_splits);
   if (st) return st;
   st = prepare_expand(ea, dtype, ws, ldt, tmp_rows, sa.k_splits, arena, table, num_modules,
-                      module, tok, groups, meta, group_cap, y, ldy, N, epilogue);
+                      module, tok, groups, meta, group_cap, group_tokens, y, ldy, N, epilogue);
   if (st) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  st = dispatch_shrink(dtype, sa, group_cap, s);
+  st = dispatch_shrink(dtype, group_tokens, sa, group_cap, s);
   if (st) return st;
-  return dispatch_expand(dtype, ea, group_cap, s);
+  return dispatch_expand(dtype, group_tokens, ea, group_cap, s);
 }

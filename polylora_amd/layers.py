@@ -111,7 +111,8 @@ class MultiLoraLinear(nn.Module):
             key = (rows, row_len)
             plan = lora_ctx.plans.get(key)
             if plan is None:
-                plan = sgmv.SgmvPlan(weight_indices, seq_lens, row_len, cache.num_slots)
+                distinct = len({a for a in lora_ctx.adapter_ids if a != cache.config.base_adapter_id})
+                plan = sgmv.SgmvPlan(weight_indices, seq_lens, row_len, cache.num_slots, distinct_slots=distinct)
                 lora_ctx.plans[key] = plan
             sgmv.lora_apply(x2, y2, cache, self.module_name, plan)
         else:

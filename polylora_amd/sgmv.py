@@ -19,7 +19,8 @@ import torch
 
 from . import _native
 
-__all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "sgmv_lora_a_fwd", "sgmv_lora_b_fwd", "choose_k_splits"]
+__all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "sgmv_lora_a_fwd", "sgmv_lora_b_fwd", "choose_k_splits",
+           "choose_group_tokens"]
 
 
 def _stream(device: torch.device) -> int:
@@ -38,18 +39,35 @@ def _i32(t: torch.Tensor) -> torch.Tensor:
     return t.to(torch.int32).contiguous()
 
 
+def choose_group_tokens(tokens: int, distinct_slots: int | None) -> int:
+    """Plan group size: 16-token groups when adapter segments average at most 32 tokens (decode).
+
+    Short groups let the kernels keep one 16-row tile per workgroup; long
+    segments use 64-token groups so each adapter's weights are read once per
+    64 tokens.
+    """
+    if distinct_slots is not None and tokens <= 32 * max(1, distinct_slots):
+        return _native.PL_GROUP_TOKENS_SHORT
+    return _native.PL_GROUP_TOKENS_LONG
+
+
 class SgmvPlan:
     """Adapter-major token groups for one (rows, row_len) layer shape of a forward.
 
     Built on the device by ``pl_plan_build`` from the int32 row -> slot map and
     per-row lengths; every wrapped Linear of the forward with this shape reuses
     it.  Buffers: ``tok`` [rows*row_len] sorted token indices, ``groups``
-    [group_cap, 4] (slot, start, len, 0), ``meta`` [4] (num_groups, num_tokens, 0, 0).
+    [group_cap, 4] (slot, start, len, 0), ``meta`` [4] (num_groups,
+    num_tokens, group_tokens, 0).  ``distinct_slots`` (the number of different
+    adapters in the batch, known on the host) picks the group size; without
+    it the plan uses 64-token groups.
     """
 
-    __slots__ = ("rows", "row_len", "num_slots", "tokens_cap", "group_cap", "tok", "groups", "meta", "row_slot", "seq_lens")
+    __slots__ = ("rows", "row_len", "num_slots", "group_tokens", "tokens_cap", "group_cap", "tok", "groups", "meta",
+                 "row_slot", "seq_lens")
 
-    def __init__(self, row_slot: torch.Tensor, seq_lens: torch.Tensor, row_len: int, num_slots: int) -> None:
+    def __init__(self, row_slot: torch.Tensor, seq_lens: torch.Tensor, row_len: int, num_slots: int,
+                 distinct_slots: int | None = None, group_tokens: int | None = None) -> None:
         _require_gpu(row_slot, "SgmvPlan")
         lib = _native.load()
         row_slot = _i32(row_slot)
@@ -59,7 +77,12 @@ class SgmvPlan:
             raise ValueError("row_slot and seq_lens must have the same length")
         self.rows, self.row_len, self.num_slots = rows, int(row_len), int(num_slots)
         self.tokens_cap = rows * self.row_len
-        self.group_cap = int(lib.pl_plan_group_capacity(rows, self.row_len, self.num_slots))
+        if group_tokens is None:
+            group_tokens = choose_group_tokens(self.tokens_cap, distinct_slots)
+        if group_tokens not in (_native.PL_GROUP_TOKENS_SHORT, _native.PL_GROUP_TOKENS_LONG):
+            raise ValueError(f"group_tokens must be 16 or 64, not {group_tokens}")
+        self.group_tokens = int(group_tokens)
+        self.group_cap = int(lib.pl_plan_group_capacity(rows, self.row_len, self.num_slots, self.group_tokens))
         dev = row_slot.device
         self.tok = torch.empty(max(1, self.tokens_cap), dtype=torch.int32, device=dev)
         self.groups = torch.empty((max(1, self.group_cap), 4), dtype=torch.int32, device=dev)
@@ -72,6 +95,7 @@ class SgmvPlan:
                 rows,
                 self.row_len,
                 self.num_slots,
+                self.group_tokens,
                 self.tok.data_ptr(),
                 self.groups.data_ptr(),
                 self.meta.data_ptr(),
@@ -117,16 +141,19 @@ def _workspace(device: torch.device, stream: int) -> _Workspace:
     return ws
 
 
-# Active shrink workgroups to aim for (256 CUs, several per CU).
+# K elements per shrink split, and the active shrink workgroups to aim for.
+# Measured on MI355X (bf16, K=4096/14336): more splits feed the shrink more
+# workgroups, but every expand workgroup re-reads every split's partial sums,
+# so about one split per 1024 of K balances the two kernels.
+_K_PER_SPLIT = 1024
 _TARGET_SHRINK_BLOCKS = 2048
 
 
 def choose_k_splits(group_cap: int, K: int, dtype: torch.dtype) -> int:
-    """K splits of the shrink: enough (group, split) workgroups to fill the GPU, none for big batches."""
-    chunk = 8 if dtype != torch.float32 else 4
-    k_per_block_step = 4 * 2 * 4 * chunk  # four waves x two loads x four lane groups x one chunk
-    max_splits = max(1, -(-K // k_per_block_step))
-    return max(1, min(max_splits, -(-_TARGET_SHRINK_BLOCKS // max(1, group_cap))))
+    """K splits of the shrink: about one per 1024 of K, fewer when the group count alone fills the GPU."""
+    by_k = max(1, -(-K // _K_PER_SPLIT))
+    by_groups = max(1, -(-_TARGET_SHRINK_BLOCKS // max(1, group_cap)))
+    return min(by_k, by_groups)
 
 
 def _tiled_ok(x: torch.Tensor, y: torch.Tensor) -> bool:
@@ -195,7 +222,7 @@ def lora_apply(
     splits = k_splits if k_splits is not None else choose_k_splits(plan.group_cap, K, x.dtype)
     rows = max(1, plan.tokens_cap)
     group_cap = max(1, plan.group_cap)
-    nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, rows, ldt))
+    nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, plan.group_tokens, rows, ldt))
     buf = _workspace(x.device, stream).get(nbytes)
     status = lib.pl_lora_apply(
         dt,
@@ -213,6 +240,7 @@ def lora_apply(
         plan.groups.data_ptr(),
         plan.meta.data_ptr(),
         group_cap,
+        plan.group_tokens,
         buf.data_ptr(),
         buf.numel(),
         ldt,

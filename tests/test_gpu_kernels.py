@@ -31,16 +31,17 @@ def _adapters(gen, ranks, fin, fout, module="m", extra_module=None):
     return out
 
 
+@pytest.mark.parametrize("group_tokens", [16, 64])
 @pytest.mark.parametrize(
     "rows,row_len,num_slots,seed",
     [(1, 1, 2, 0), (7, 3, 5, 1), (256, 1, 65, 2), (32, 1024, 9, 3), (4096, 1, 17, 4), (3, 200, 4096, 5), (0, 5, 3, 6)],
 )
-def test_plan_matches_oracle(gpu, rows, row_len, num_slots, seed):
-    _announce(test="plan", rows=rows, row_len=row_len, num_slots=num_slots)
+def test_plan_matches_oracle(gpu, rows, row_len, num_slots, seed, group_tokens):
+    _announce(test="plan", rows=rows, row_len=row_len, num_slots=num_slots, group_tokens=group_tokens)
     g = torch.Generator().manual_seed(seed)
     row_slot = torch.randint(-1, num_slots + 1, (rows,), generator=g, dtype=torch.int32)
     seq_lens = torch.randint(-2, row_len + 3, (rows,), generator=g, dtype=torch.int32)
-    plan = sgmv.SgmvPlan(row_slot.to(gpu), seq_lens.to(gpu), row_len, num_slots)
+    plan = sgmv.SgmvPlan(row_slot.to(gpu), seq_lens.to(gpu), row_len, num_slots, group_tokens=group_tokens)
     torch.cuda.synchronize()
     check_plan(
         plan.tok.cpu().numpy(),
@@ -50,6 +51,7 @@ def test_plan_matches_oracle(gpu, rows, row_len, num_slots, seed):
         seq_lens.tolist(),
         row_len,
         num_slots,
+        group_tokens=group_tokens,
     )
 
 
@@ -83,19 +85,20 @@ def test_lora_apply_matches_oracle(gpu, dtype, rows, M, K, N, ranks, max_rank, k
     seq_lens = torch.randint(0, M + 2, (rows,), generator=g, dtype=torch.int32)
     x = torch.randn(rows, M, K, generator=g).to(dtype)
     base = torch.randn(rows, M, N, generator=g).to(dtype)
-    y = base.to(gpu)
-    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots)
-    sgmv.lora_apply(x.to(gpu).view(-1, K), y.view(-1, N), cache, "m", plan, k_splits=k_splits)
-    got = y.cpu()
     A, B, rk, sc = oracle_slot_tensors(cache, adapters, "m", dtype)
     expect = reference_forward(x, base, seq_lens, row_slot.cpu(), A, B, rk, sc)
-    torch.testing.assert_close(got, expect, **tol_for(dtype))
     # untouched rows (base adapter, padding) are bit-identical to the base output
     untouched = torch.ones(rows, M, dtype=torch.bool)
     for b, aid in enumerate(adapter_ids):
         if aid != "__base__":
             untouched[b, : min(int(seq_lens[b]), M)] = False
-    assert torch.equal(got[untouched], base[untouched])
+    for group_tokens in (16, 64):
+        y = base.to(gpu)
+        plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots, group_tokens=group_tokens)
+        sgmv.lora_apply(x.to(gpu).view(-1, K), y.view(-1, N), cache, "m", plan, k_splits=k_splits)
+        got = y.cpu()
+        torch.testing.assert_close(got, expect, **tol_for(dtype))
+        assert torch.equal(got[untouched], base[untouched])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -178,7 +181,7 @@ def test_split_k_bitwise_reproducible(gpu):
     _announce(test="reproducible")
     adapters, cache, row_slot, seq_lens, x, base = _small_case(gpu)
     M, K, N = x.shape[1], x.shape[2], base.shape[2]
-    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots)
+    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots, group_tokens=16)
     outs = []
     for _ in range(3):
         y = base.to(gpu)
@@ -193,19 +196,20 @@ def test_split_k_bitwise_reproducible(gpu):
 def test_separate_shrink_expand_equal_fused(gpu):
     """pl_sgmv_shrink + pl_sgmv_expand (planes from pl_shrink_planes) == pl_lora_apply, bit for bit."""
     _announce(test="separate_vs_fused")
-    from bench import KernelTimer
+    from bench import SgmvLaunch
 
     _, cache, row_slot, seq_lens, x, base = _small_case(gpu, seed=51)
     M, K, N = x.shape[1], x.shape[2], base.shape[2]
-    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots)
-    for splits in (1, 2, 5):
+    for splits, group_tokens in ((1, 64), (2, 16), (5, 64), (3, 16)):
+        plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots, group_tokens=group_tokens)
         y1 = base.to(gpu)
         sgmv.lora_apply(x.to(gpu).view(-1, K), y1.view(-1, N), cache, "m", plan, k_splits=splits)
         y2 = base.to(gpu)
-        timer = KernelTimer()
-        timer.run(x.to(gpu).view(-1, K), y2.view(-1, N), cache, "m", plan, k_splits=splits)
-        timer.times_ms()
-        assert torch.equal(y1.cpu(), y2.cpu()), splits
+        launch = SgmvLaunch(x.to(gpu).view(-1, K), y2.view(-1, N), cache, "m", plan, k_splits=splits)
+        launch.shrink()
+        launch.expand()
+        torch.cuda.synchronize()
+        assert torch.equal(y1.cpu(), y2.cpu()), (splits, group_tokens)
 
 
 def test_triton_epilogue_order(gpu):

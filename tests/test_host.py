@@ -347,22 +347,26 @@ def test_library_host_side_errors_without_gpu():
     """Argument checks run before any HIP call, so they are testable on the CPU."""
     lib = _native.load()
     assert lib.pl_version() >= 100
-    assert lib.pl_plan_group_capacity(256, 1, 65) == 4 + 64
-    assert lib.pl_plan_group_capacity(32, 1024, 9) == 512 + 8
-    # split planes: whole 256-element block steps (bf16), at most the requested count
-    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 8) == 8
-    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 100) == 16
-    assert lib.pl_shrink_planes(_native.PL_BF16, 14336, 16) == 14
-    assert lib.pl_shrink_planes(_native.PL_F32, 768, 4) == 3
-    assert lib.pl_shrink_planes(_native.PL_BF16, 32, 1) == 1
+    assert lib.pl_plan_group_capacity(256, 1, 65, 64) == 4 + 64
+    assert lib.pl_plan_group_capacity(256, 1, 65, 16) == 16 + 64
+    assert lib.pl_plan_group_capacity(32, 1024, 9, 64) == 512 + 8
+    # split planes: whole block steps (bf16: 256 elements with 64-token groups,
+    # 512 with 16-token groups), at most the requested count
+    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 8, 64) == 8
+    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 100, 64) == 16
+    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 100, 16) == 8
+    assert lib.pl_shrink_planes(_native.PL_BF16, 14336, 16, 64) == 14
+    assert lib.pl_shrink_planes(_native.PL_F32, 768, 4, 64) == 3
+    assert lib.pl_shrink_planes(_native.PL_BF16, 32, 1, 16) == 1
+    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 4, 32) == 0  # only 16 or 64
     # workspace: fp32 planes [planes][rows][ldt]
-    assert lib.pl_shrink_workspace_bytes(_native.PL_BF16, 4096, 1, 100, 16) == 100 * 16 * 4
-    assert lib.pl_shrink_workspace_bytes(_native.PL_BF16, 4096, 8, 100, 16) == 8 * 100 * 16 * 4
-    assert lib.pl_shrink_workspace_bytes(_native.PL_F32, 768, 4, 10, 8) == 3 * 10 * 8 * 4
+    assert lib.pl_shrink_workspace_bytes(_native.PL_BF16, 4096, 1, 64, 100, 16) == 100 * 16 * 4
+    assert lib.pl_shrink_workspace_bytes(_native.PL_BF16, 4096, 8, 64, 100, 16) == 8 * 100 * 16 * 4
+    assert lib.pl_shrink_workspace_bytes(_native.PL_F32, 768, 4, 64, 10, 8) == 3 * 10 * 8 * 4
     fake = ctypes.c_void_p(64)  # never dereferenced: the size check fails first
-    assert lib.pl_plan_build(fake, fake, 4, 1, 5000, fake, fake, fake, 100, None) == 4  # PL_ERR_LIMIT
+    assert lib.pl_plan_build(fake, fake, 4, 1, 5000, 64, fake, fake, fake, 100, None) == 4  # PL_ERR_LIMIT
     assert b"exceed the maximum" in lib.pl_last_error()
-    st = lib.pl_sgmv_shrink(7, None, 0, 0, None, None, 1, 0, None, None, None, 1, None, 0, 8, 1, 1, None)
+    st = lib.pl_sgmv_shrink(7, None, 0, 0, None, None, 1, 0, None, None, None, 1, 64, None, 0, 8, 1, 1, None)
     assert st == 1 and b"dtype" in lib.pl_last_error()
     with pytest.raises(RuntimeError, match="dtype"):
         _native.check(st, "pl_sgmv_shrink")

@@ -279,7 +279,7 @@ def _plan_from_expected(row_slot, seq_lens, row_len, num_slots):
             chunk = toks[q : q + plan.GROUP_TOKENS]
             groups.append((slot, len(tok), len(chunk), 0))
             tok.extend(chunk)
-    meta = np.array([len(groups), len(tok), 0, 0])
+    meta = np.array([len(groups), len(tok), plan.GROUP_TOKENS, 0])
     return np.array(tok, dtype=np.int64), np.array(groups, dtype=np.int64).reshape(-1, 4), meta
 
 
