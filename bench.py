@@ -698,6 +698,8 @@ def main(argv=None) -> int:
     p.add_argument("--decode-layers", type=int, default=32)
     p.add_argument("--decode-steps", type=int, default=20)
     p.add_argument("--no-deberta", action="store_true")
+    p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                   help="only copy a BYTES-sized device buffer 5 times (calibrates HBM byte counters) and exit")
     args = p.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path; run with --gpus 1", file=sys.stderr)
@@ -705,6 +707,14 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": args.copy_probe, "copies": 5}), flush=True)
+        return 0
     iso = run_isolated(args)
     _log(f"isolated: {iso['value']} GB/s")
     result = {

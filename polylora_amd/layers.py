@@ -4,7 +4,9 @@ forward(x) = base_layer(x), then, when a LoRA batch context is active, the
 HIP SGMV shrink + expand adds ``scale * (x @ A^T) @ B^T`` in place into the
 base output for every row whose slot has rank > 0 in this module, over the
 first ``min(seq_len, M)`` tokens of the row.  Rank-0 rows and padding tokens
-keep the base output bit for bit.
+keep the base output bit for bit.  On the tiled path, layers with many
+tokens run the shrink on a side stream concurrently with the base GEMM (it
+needs only x); the expand joins back on the caller's stream.
 
 Where the reference picks Triton or its torch fallback (layers.py:42-58,
 :64-70), this layer always runs HIP kernels: the MFMA-tiled ones when
@@ -20,6 +22,14 @@ from torch import nn
 from . import sgmv
 from .cache import GpuAdapterCache
 from .context import LoraBatchContext, get_lora_context
+
+
+# Layers with at least this many tokens run the shrink on a side stream while
+# the base GEMM computes.  Measured on MI355X: in decode (a few hundred
+# tokens) the concurrent shrink slows the memory-bound base GEMM and the
+# cross-stream joins cost more than the overlap saves, so small layers run
+# the shrink and expand back to back on the caller's stream.
+OVERLAP_MIN_TOKENS = 2048
 
 
 class MultiLoraLinear(nn.Module):
@@ -38,14 +48,75 @@ class MultiLoraLinear(nn.Module):
         return self.base_layer.out_features
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        base = self.base_layer(x)
         lora_ctx = get_lora_context()
         if lora_ctx is None:
-            return base
+            return self.base_layer(x)
+        if x.is_cuda and self.cache.config.use_triton_kernels and x.numel() >= OVERLAP_MIN_TOKENS * x.shape[-1]:
+            out = self._overlapped_forward(x, lora_ctx)
+            if out is not None:
+                return out
+        base = self.base_layer(x)
         original_shape = base.shape
         x_3d, base_3d, seq_lens, weight_indices = self._prepare_batched_inputs(x, base, lora_ctx)
         out = self._hip_forward(x_3d, base_3d, seq_lens, weight_indices, lora_ctx)
         return out.reshape(original_shape)
+
+    def _overlapped_forward(self, x: torch.Tensor, lora_ctx: LoraBatchContext) -> torch.Tensor | None:
+        """Tiled path with the shrink on a side stream, concurrent with the base GEMM.
+
+        The shrink reads only x, so it forks from the current stream as soon
+        as x is ready and runs while the base Linear computes; the expand,
+        which adds into the base output, joins back on the current stream.
+        Returns None when the shapes do not suit the tiled kernels (the
+        caller then takes the sequential path).
+        """
+        cache = self.cache
+        x_3d, seq_lens, weight_indices, reshape = self._batched_view(x, lora_ctx)
+        rows, row_len, in_features = x_3d.shape
+        if rows * row_len == 0 or x.dtype != cache.dtype:
+            return None
+        x2 = x_3d.reshape(rows * row_len, in_features)
+        if not sgmv.tiled_shapes_ok(x2, self.out_features):
+            return None
+        plan = self._plan(lora_ctx, rows, row_len, seq_lens, weight_indices)
+        main = torch.cuda.current_stream(x.device)
+        side = sgmv.side_stream(x.device)
+        side.wait_stream(main)  # x is ready, and every earlier expand has read the side workspace
+        with torch.cuda.stream(side):
+            shrunk = sgmv.lora_shrink(x2, cache, self.module_name, plan)
+        base = self.base_layer(x)
+        original_shape = base.shape
+        base_3d = reshape(base)
+        main.wait_stream(side)
+        sgmv.lora_expand(shrunk, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name)
+        return base_3d.reshape(original_shape)
+
+    def _plan(self, lora_ctx: LoraBatchContext, rows: int, row_len: int, seq_lens, weight_indices):
+        key = (rows, row_len)
+        plan = lora_ctx.plans.get(key)
+        if plan is None:
+            cache = self.cache
+            distinct = len({a for a in lora_ctx.adapter_ids if a != cache.config.base_adapter_id})
+            plan = sgmv.SgmvPlan(weight_indices, seq_lens, row_len, cache.num_slots, distinct_slots=distinct)
+            lora_ctx.plans[key] = plan
+        return plan
+
+    def _batched_view(self, x: torch.Tensor, lora_ctx: LoraBatchContext):
+        """_prepare_batched_inputs for x alone, plus the function that shapes the base output the same way."""
+        batch = lora_ctx.weight_indices.shape[0]
+        if x.shape[0] == batch:
+            return self._as_3d(x).contiguous(), lora_ctx.seq_lens, lora_ctx.weight_indices, lambda t: self._as_3d(t).contiguous()
+        if x.dim() == 3 and x.shape[0] == 1:
+            return x.contiguous(), lora_ctx.seq_lens[:1], lora_ctx.weight_indices[:1], lambda t: t.contiguous()
+        if x.dim() == 2 and x.shape[0] % batch == 0:
+            seq_len = x.shape[0] // batch
+            return (
+                x.reshape(batch, seq_len, x.shape[-1]).contiguous(),
+                lora_ctx.seq_lens,
+                lora_ctx.weight_indices,
+                lambda t: t.reshape(batch, seq_len, t.shape[-1]).contiguous(),
+            )
+        raise ValueError("LoRA batch context batch size does not match layer input batch size")
 
     @staticmethod
     def _as_3d(x: torch.Tensor) -> torch.Tensor:
@@ -108,12 +179,7 @@ class MultiLoraLinear(nn.Module):
         x2 = x.view(rows * row_len, in_features)
         y2 = base.view(rows * row_len, base.shape[-1])
         if cache.config.use_triton_kernels:
-            key = (rows, row_len)
-            plan = lora_ctx.plans.get(key)
-            if plan is None:
-                distinct = len({a for a in lora_ctx.adapter_ids if a != cache.config.base_adapter_id})
-                plan = sgmv.SgmvPlan(weight_indices, seq_lens, row_len, cache.num_slots, distinct_slots=distinct)
-                lora_ctx.plans[key] = plan
+            plan = self._plan(lora_ctx, rows, row_len, seq_lens, weight_indices)
             sgmv.lora_apply(x2, y2, cache, self.module_name, plan)
         else:
             sgmv.lora_apply_rows(x2, y2, cache, self.module_name, weight_indices, seq_lens, row_len)

@@ -19,8 +19,8 @@ import torch
 
 from . import _native
 
-__all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "sgmv_lora_a_fwd", "sgmv_lora_b_fwd", "choose_k_splits",
-           "choose_group_tokens"]
+__all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "lora_shrink", "lora_expand", "sgmv_lora_a_fwd",
+           "sgmv_lora_b_fwd", "choose_k_splits", "choose_group_tokens", "side_stream"]
 
 
 def _stream(device: torch.device) -> int:
@@ -250,6 +250,95 @@ def lora_apply(
         stream,
     )
     _native.check(status, "pl_lora_apply")
+    return y
+
+
+class ShrinkResult:
+    """Where a shrink left its partial sums: the workspace of the stream it ran on."""
+
+    __slots__ = ("buf", "planes", "rows", "ldt", "plan", "K")
+
+    def __init__(self, buf, planes, rows, ldt, plan, K) -> None:
+        self.buf, self.planes, self.rows, self.ldt, self.plan, self.K = buf, planes, rows, ldt, plan, K
+
+
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def side_stream(device: torch.device) -> torch.cuda.Stream:
+    """The per-device stream shrinks run on while the base GEMM runs on the current stream (default priority)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    st = _SIDE_STREAMS.get(idx)
+    if st is None:
+        st = _SIDE_STREAMS[idx] = torch.cuda.Stream(device=torch.device("cuda", idx))
+    return st
+
+
+def tiled_shapes_ok(x: torch.Tensor, out_features: int) -> bool:
+    """Whether x [tokens, K] and a fresh contiguous output of out_features columns suit the tiled kernels."""
+    chunk = 4 if x.dtype == torch.float32 else 8
+    return (
+        x.is_cuda
+        and x.dim() == 2
+        and x.stride(1) == 1
+        and x.shape[1] % chunk == 0
+        and out_features % chunk == 0
+        and (x.stride(0) * x.element_size()) % 16 == 0
+        and x.data_ptr() % 16 == 0
+    )
+
+
+def lora_shrink(x: torch.Tensor, cache, module_name: str, plan: SgmvPlan, *, k_splits: int | None = None) -> ShrinkResult:
+    """Launch the shrink of one wrapped Linear on the current stream; the expand reads the result later."""
+    _require_gpu(x, "lora_shrink")
+    spec = cache.module_specs.get(module_name)
+    if spec is None:
+        raise KeyError(f"module {module_name!r} is not in the adapter cache")
+    if x.dim() != 2 or x.shape[0] != plan.tokens_cap or x.shape[1] != spec.in_features:
+        raise ValueError(f"x must be [{plan.tokens_cap}, {spec.in_features}], got {list(x.shape)}")
+    if x.dtype != cache.dtype or x.device != cache.device:
+        raise TypeError(f"x {x.dtype} on {x.device} must match the adapter cache ({cache.dtype} on {cache.device})")
+    lib = _native.load()
+    dt = _native.dtype_code(x.dtype)
+    K = int(x.shape[1])
+    ldt = cache.rank8_cap
+    stream = _stream(x.device)
+    splits = k_splits if k_splits is not None else choose_k_splits(plan.group_cap, K, x.dtype)
+    rows = max(1, plan.tokens_cap)
+    planes = int(lib.pl_shrink_planes(dt, K, splits, plan.group_tokens))
+    nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, plan.group_tokens, rows, ldt))
+    buf = _workspace(x.device, stream).get(nbytes)
+    _native.check(
+        lib.pl_sgmv_shrink(
+            dt, x.data_ptr(), x.stride(0), K, cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index),
+            cache.module_index[module_name], plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(),
+            max(1, plan.group_cap), plan.group_tokens, buf.data_ptr(), buf.numel(), ldt, rows, splits, stream,
+        ),
+        "pl_sgmv_shrink",
+    )
+    return ShrinkResult(buf, planes, rows, ldt, plan, K)
+
+
+def lora_expand(res: ShrinkResult, y: torch.Tensor, cache, module_name: str, *,
+                epilogue: int = _native.PL_EPI_FALLBACK) -> torch.Tensor:
+    """Launch the expand on the current stream, which must already be ordered after the shrink."""
+    _require_gpu(y, "lora_expand")
+    spec = cache.module_specs[module_name]
+    plan = res.plan
+    if y.dim() != 2 or y.shape[0] != plan.tokens_cap or y.shape[1] != spec.out_features:
+        raise ValueError(f"y must be [{plan.tokens_cap}, {spec.out_features}], got {list(y.shape)}")
+    if y.dtype != cache.dtype or y.device != cache.device:
+        raise TypeError(f"y {y.dtype} on {y.device} must match the adapter cache ({cache.dtype} on {cache.device})")
+    lib = _native.load()
+    _native.check(
+        lib.pl_sgmv_expand(
+            _native.dtype_code(y.dtype), res.buf.data_ptr(), res.ldt, res.rows, res.planes, cache.arena.data_ptr(),
+            cache.table.data_ptr(), len(cache.module_index), cache.module_index[module_name], plan.tok.data_ptr(),
+            plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap), plan.group_tokens, y.data_ptr(),
+            y.stride(0), int(y.shape[1]), epilogue, _stream(y.device),
+        ),
+        "pl_sgmv_expand",
+    )
     return y
 
 

@@ -322,8 +322,8 @@ def test_deberta_base_shape_fp32_config(gpu):
     torch.testing.assert_close(got, want, **FP32)
 
 
-def _tiny_llama(seed, dtype, device):
-    """Tiny Llama whose attention runs in fp32 on contiguous operands (no bf16 batched product)."""
+def _tiny_llama(seed, dtype, device, attn="pl_safe_fp32"):
+    """Tiny Llama; attention in fp32 on contiguous operands (no bf16 batched product) unless `attn` says otherwise."""
     from transformers import LlamaConfig, LlamaModel
 
     from bench import register_attention
@@ -332,7 +332,7 @@ def _tiny_llama(seed, dtype, device):
     torch.manual_seed(seed)
     cfg = LlamaConfig(hidden_size=128, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2, head_dim=32,
                       intermediate_size=256, vocab_size=211)
-    cfg._attn_implementation = "pl_safe_fp32"
+    cfg._attn_implementation = attn
     return LlamaModel(cfg).to(device=device, dtype=dtype).eval(), cfg
 
 
@@ -422,3 +422,62 @@ def test_adapter_churn_matches_fallback(gpu):
             got = pm(input_ids=ids, adapter_ids=adapter_ids).last_hidden_state
             want = oracle_model.run(om, bank, adapter_ids, input_ids=ids).last_hidden_state
             torch.testing.assert_close(got.float(), want.float(), **BF16)
+
+
+def test_llama_decode_step_graph_replays(gpu):
+    """A decode step (shrinks on the side stream, expands joined back) captured in a HIP graph:
+    every replay, with eager work between replays, equals the eager step bit for bit."""
+    _announce(test="decode_graph_replay")
+    from transformers import StaticCache
+
+    from polylora_amd.context import use_lora_context
+
+    # torch's fused SDPA kernels (never the math path); a single decode query gets no mask, so
+    # the step has no host-side mask work and can be captured
+    base, cfg = _tiny_llama(14, torch.bfloat16, gpu, attn="pl_fused_sdpa")
+    pm = PolyLoraModel(base, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=6, max_rank=32)).eval()
+    g = torch.Generator().manual_seed(14)
+    ads = {f"d{i}": (_peft.make_lora_weights(g, _shapes(pm), r, std=0.05), 2.0 * r) for i, r in enumerate([8, 16, 32, 4])}
+    for aid, (w, alpha) in ads.items():
+        pm.adapter_store.add_adapter_from_peft_state_dict(aid, _peft.state_dict(w), pm.target_module_names, alpha)
+    B, past = 24, 40
+    adapter_ids = [["__base__", *ads][int(i)] for i in torch.randint(0, 5, (B,), generator=g)]
+    kv = StaticCache(config=cfg, max_cache_len=past + 1)
+    for layer in range(cfg.num_hidden_layers):
+        kv.update(torch.randn(B, 2, past, 32, generator=g).to(gpu, torch.bfloat16),
+                  torch.randn(B, 2, past, 32, generator=g).to(gpu, torch.bfloat16), layer)
+    ids = torch.randint(0, 211, (B, 1), generator=g).to(gpu)
+    pos = torch.tensor([past], device=gpu)
+    with torch.inference_mode():
+        ctx = pm.prepare_lora_context(adapter_ids, None, B, 1, gpu)
+
+        def step():
+            for layer in kv.layers:
+                layer.cumulative_length.fill_(past)
+            with use_lora_context(ctx):
+                return pm.base_model(input_ids=ids, past_key_values=kv, cache_position=pos, use_cache=True).last_hidden_state
+
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            want = step().clone()
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = step()
+        for i in range(3):
+            out.fill_(float(i))  # eager work between replays
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, want), i
+        # and the step still equals the fallback forward
+        om, bank = _oracle(_tiny_llama(14, torch.bfloat16, gpu, attn="pl_fused_sdpa")[0], LLAMA_TARGETS, ads, 32,
+                           torch.bfloat16, gpu)
+        for layer in kv.layers:
+            layer.cumulative_length.fill_(past)
+        ref = oracle_model.run(om, bank, adapter_ids, input_ids=ids, past_key_values=kv, cache_position=pos,
+                               use_cache=True).last_hidden_state
+    torch.testing.assert_close(want.float(), ref.float(), **BF16)
