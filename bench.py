@@ -388,6 +388,16 @@ def time_launches(fns: list, reps: int, warmup: int = 2) -> float:
     return t0.elapsed_time(t1) / reps
 
 
+def _profiled_traffic():
+    """HBM bytes per expand launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs, or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "sgmv_isolated_traffic.json")
+    try:
+        with open(path, encoding="utf-8") as fh:
+            return int(json.load(fh)["traffic_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def run_isolated(args) -> dict:
     from polylora_amd import sgmv
 
@@ -446,7 +456,7 @@ def run_isolated(args) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(exp_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": _profiled_traffic(),
             "algorithmic_bytes_per_launch": nb["expand"],
             "avg_launch_ms": round(ex_ms, 5),
         },
