@@ -355,7 +355,9 @@ class SgmvLaunch:
         gt = plan.group_tokens
         nbytes = int(self.lib.pl_shrink_workspace_bytes(dt, K, splits, gt, rows, ldt))
         planes = int(self.lib.pl_shrink_planes(dt, K, splits, gt))
-        buf = sgmv._workspace(x.device, self.stream.cuda_stream).get(nbytes)
+        ws = sgmv._workspace(x.device, self.stream.cuda_stream)
+        buf = ws.get(nbytes)
+        ws.owner = None
         common = (cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), cache.module_index[module],
                   plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap), gt)
         s = self.stream.cuda_stream

@@ -78,6 +78,9 @@ typedef struct pl_group {
   int32_t reserved;
 } pl_group;
 
+/* Modules one pl_sgmv_shrink_stacked launch can serve. */
+#define PL_MAX_STACKED_MODULES 4
+
 /* Maximum slot count accepted by pl_plan_build (slot 0 included). */
 #define PL_MAX_SLOTS 4096
 /* Token-group sizes of a plan: short groups for short adapter segments
@@ -143,6 +146,21 @@ int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t K, const v
                    const int32_t* tok, const pl_group* groups, const int32_t* meta,
                    int64_t group_cap, int32_t group_tokens, void* ws, int64_t ws_bytes,
                    int32_t ldt, int64_t tmp_rows, int32_t k_splits, void* stream);
+
+/* Shrink for up to PL_MAX_STACKED_MODULES wrapped Linears that read the same
+ * x (e.g. q/k/v or gate/up projections): one launch, x read once per group
+ * and split, module j's planes written to its own workspace ws[j] (each at
+ * least pl_shrink_workspace_bytes(...) bytes and distinct).  modules[] and
+ * ws[] are host arrays of n_modules entries; every other argument is as for
+ * pl_sgmv_shrink, which is this call with one module.  No counterpart in the
+ * reference, whose sgmv_lora_a_fwd (sgmv.py:141-175) serves one weight
+ * tensor per call (its stack_num packs modules along N instead). */
+int pl_sgmv_shrink_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K, const void* arena,
+                           const pl_slot_entry* table, int32_t num_modules, int32_t n_modules,
+                           const int32_t* modules, void* const* ws, const int32_t* tok,
+                           const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                           int32_t group_tokens, int64_t ws_bytes, int32_t ldt, int64_t tmp_rows,
+                           int32_t k_splits, void* stream);
 
 /* Expand: y[tok[p]][n] = T(y + d), d = scale * sum_{j<rank} T(sum_c
  * planes[c][p][j]) * B_slot[n][j] rounded in the order of `epilogue`; the

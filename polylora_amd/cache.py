@@ -161,6 +161,9 @@ class GpuAdapterCache:
         self.lru: OrderedDict[str, None] = OrderedDict()
         self.module_specs = {spec.name: spec for spec in module_specs}
         self.module_index = {spec.name: i for i, spec in enumerate(module_specs)}
+        # (first module, input shape) -> modules called back to back on that
+        # same input tensor; learned by MultiLoraLinear, used to stack shrinks
+        self.stacked_runs: dict[tuple, tuple[str, ...]] = {}
         self._allocate()
 
     # ------------------------------------------------------------------ storage

@@ -27,6 +27,9 @@ class LoraBatchContext:
     attention_mask: torch.Tensor | None = None
     # (rows, row_len) -> SgmvPlan, filled lazily by the first layer of that shape
     plans: dict = field(default_factory=dict, compare=False, repr=False)
+    # shrinks computed ahead for sibling Linears fed the same input, and the
+    # run of consecutive calls on one input used to learn such siblings
+    stack: dict = field(default_factory=dict, compare=False, repr=False)
 
 
 _CURRENT_LORA_CONTEXT: ContextVar[LoraBatchContext | None] = ContextVar(

@@ -51,6 +51,9 @@ struct pl_shrink_shape<4> {
   enum { CC = 2, JT = 2 };
 };
 
+// Modules one shrink launch serves: wrapped Linears fed the same input x.
+constexpr int kMaxJobs = PL_MAX_STACKED_MODULES;
+
 struct pl_shrink_args {
   const void* x;
   int64_t ldx;
@@ -59,11 +62,12 @@ struct pl_shrink_args {
   const char* arena;
   const pl_slot_entry* table;
   int32_t num_modules;
-  int32_t module;
+  int32_t n_jobs;                // modules served, 1..kMaxJobs
+  int32_t module[kMaxJobs];      // table column of each served module
+  float* planes[kMaxJobs];       // its fp32 planes [k_splits][tmp_rows][ldt]
   const int32_t* tok;
   const pl_group* groups;
   const int32_t* meta;
-  float* planes;  // [k_splits][tmp_rows][ldt] fp32
   int32_t ldt;
   int32_t k_splits;
   int64_t plane;  // floats between split planes
@@ -115,11 +119,15 @@ __global__ __launch_bounds__(256, 4) void pl_shrink_tiled(pl_shrink_args a) {
   const int li = lane & 15;
   const int lg = lane >> 4;
 
-  const int g = blockIdx.x / a.k_splits;
-  const int c = blockIdx.x - g * a.k_splits;
+  // block -> (group g, split c, served module job); the modules of one
+  // (group, split) are adjacent so their shared x rows are fetched together
+  const int job = blockIdx.x % a.n_jobs;
+  const int gc = blockIdx.x / a.n_jobs;
+  const int g = gc / a.k_splits;
+  const int c = gc - g * a.k_splits;
   if (g >= a.meta[0]) return;
   const pl_group grp = a.groups[g];
-  const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module];
+  const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module[job]];
   const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
   if (rank <= 0) return;
   const int len = min(grp.len, 16 * RT);  // the host pairs the plan's group size with RT
@@ -127,7 +135,7 @@ __global__ __launch_bounds__(256, 4) void pl_shrink_tiled(pl_shrink_args a) {
   const int K = a.K;
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
   const T* __restrict__ A = reinterpret_cast<const T*>(a.arena + e.a_off);
-  float* __restrict__ out = a.planes + (int64_t)c * a.plane;
+  float* __restrict__ out = a.planes[job] + (int64_t)c * a.plane;
 
   const T* xrow[RT];
   bool xok[RT];
@@ -368,7 +376,7 @@ __global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
 
 template <int DT, int RT>
 int launch_shrink(const pl_shrink_args& a, int64_t group_cap, hipStream_t stream) {
-  const int64_t grid = group_cap * a.k_splits;
+  const int64_t grid = group_cap * a.k_splits * a.n_jobs;
   if (grid <= 0) return PL_OK;
   hipLaunchKernelGGL((pl_shrink_tiled<DT, RT>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   return pl_launch_status("pl_sgmv_shrink");
@@ -452,13 +460,26 @@ int check_ws(const void* ws, int32_t ldt, int64_t tmp_rows) {
 
 int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx, int32_t K,
                    const void* arena, const pl_slot_entry* table, int32_t num_modules,
-                   int32_t module, const int32_t* tok, const pl_group* groups,
-                   const int32_t* meta, int64_t group_cap, int32_t group_tokens, void* ws,
-                   int64_t ws_bytes, int32_t ldt, int64_t tmp_rows, int32_t k_splits) {
-  int st = check_common(dtype, arena, table, num_modules, module, tok, groups, meta, group_cap,
-                        group_tokens);
-  if (st) return st;
-  if ((st = check_ws(ws, ldt, tmp_rows))) return st;
+                   int32_t n_jobs, const int32_t* modules, void* const* ws, const int32_t* tok,
+                   const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                   int32_t group_tokens, int64_t ws_bytes, int32_t ldt, int64_t tmp_rows,
+                   int32_t k_splits) {
+  if (n_jobs < 1 || n_jobs > kMaxJobs || !modules || !ws) {
+    pl_set_error("shrink serves 1..%d modules (got %d) with one workspace each", kMaxJobs, n_jobs);
+    return PL_ERR_ARG;
+  }
+  int st = PL_OK;
+  for (int j = 0; j < n_jobs; ++j) {
+    st = check_common(dtype, arena, table, num_modules, modules[j], tok, groups, meta, group_cap,
+                      group_tokens);
+    if (st) return st;
+    if ((st = check_ws(ws[j], ldt, tmp_rows))) return st;
+    for (int i = 0; i < j; ++i)
+      if (ws[i] == ws[j]) {
+        pl_set_error("each module of a stacked shrink needs its own workspace");
+        return PL_ERR_ARG;
+      }
+  }
   const int E = pl_chunk_elems(dtype);
   const int es = pl_elem_size(dtype);
   if (!x) {
@@ -474,7 +495,7 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
     return PL_ERR_ALIGN;
   }
   const int32_t planes = shrink_planes(dtype, K, k_splits, group_tokens);
-  if (group_cap * planes > 0x7fffffffLL) {
+  if (group_cap * planes * n_jobs > 0x7fffffffLL) {
     pl_set_error("shrink grid too large");
     return PL_ERR_LIMIT;
   }
@@ -490,11 +511,14 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
   a.arena = reinterpret_cast<const char*>(arena);
   a.table = table;
   a.num_modules = num_modules;
-  a.module = module;
+  a.n_jobs = n_jobs;
+  for (int j = 0; j < kMaxJobs; ++j) {
+    a.module[j] = j < n_jobs ? modules[j] : 0;
+    a.planes[j] = j < n_jobs ? reinterpret_cast<float*>(ws[j]) : nullptr;
+  }
   a.tok = tok;
   a.groups = groups;
   a.meta = meta;
-  a.planes = reinterpret_cast<float*>(ws);
   a.ldt = ldt;
   a.k_splits = planes;
   a.plane = tmp_rows * ldt;
@@ -609,9 +633,23 @@ extern "C" int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t
                               const pl_group* groups, const int32_t* meta, int64_t group_cap,
                               int32_t group_tokens, void* ws, int64_t ws_bytes, int32_t ldt,
                               int64_t tmp_rows, int32_t k_splits, void* stream) {
+  return pl_sgmv_shrink_stacked(dtype, x, ldx, K, arena, table, num_modules, 1, &module, &ws,
+                                tok, groups, meta, group_cap, group_tokens, ws_bytes, ldt,
+                                tmp_rows, k_splits, stream);
+}
+
+extern "C" int pl_sgmv_shrink_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K,
+                                      const void* arena, const pl_slot_entry* table,
+                                      int32_t num_modules, int32_t n_modules,
+                                      const int32_t* modules, void* const* ws,
+                                      const int32_t* tok, const pl_group* groups,
+                                      const int32_t* meta, int64_t group_cap,
+                                      int32_t group_tokens, int64_t ws_bytes, int32_t ldt,
+                                      int64_t tmp_rows, int32_t k_splits, void* stream) {
   pl_shrink_args a;
-  int st = prepare_shrink(a, dtype, x, ldx, K, arena, table, num_modules, module, tok, groups,
-                          meta, group_cap, group_tokens, ws, ws_bytes, ldt, tmp_rows, k_splits);
+  int st = prepare_shrink(a, dtype, x, ldx, K, arena, table, num_modules, n_modules, modules, ws,
+                          tok, groups, meta, group_cap, group_tokens, ws_bytes, ldt, tmp_rows,
+                          k_splits);
   if (st) return st;
   return dispatch_shrink(dtype, group_tokens, a, group_cap, reinterpret_cast<hipStream_t>(stream));
 }
@@ -638,8 +676,8 @@ extern "C" int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t 
                              void* stream) {
   pl_shrink_args sa;
   pl_expand_args ea;
-  int st = prepare_shrink(sa, dtype, x, ldx, K, arena, table, num_modules, module, tok, groups,
-                          meta, group_cap, group_tokens, ws, ws_bytes, ldt, tmp_rows, k_splits);
+  int st = prepare_shrink(sa, dtype, x, ldx, K, arena, table, num_modules, 1, &module, &ws, tok,
+                          groups, meta, group_cap, group_tokens, ws_bytes, ldt, tmp_rows, k_splits);
   if (st) return st;
   st = prepare_expand(ea, dtype, ws, ldt, tmp_rows, sa.k_splits, arena, table, num_modules,
                       module, tok, groups, meta, group_cap, group_tokens, y, ldy, N, epilogue);

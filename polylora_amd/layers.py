@@ -32,6 +32,14 @@ from .context import LoraBatchContext, get_lora_context
 OVERLAP_MIN_TOKENS = 2048
 
 
+def _version_of(x: torch.Tensor):
+    """In-place modification counter of x, or None for inference tensors (they keep none)."""
+    try:
+        return x._version
+    except RuntimeError:
+        return None
+
+
 class MultiLoraLinear(nn.Module):
     def __init__(self, base_layer: nn.Linear, module_name: str, cache: GpuAdapterCache) -> None:
         super().__init__()
@@ -51,8 +59,8 @@ class MultiLoraLinear(nn.Module):
         lora_ctx = get_lora_context()
         if lora_ctx is None:
             return self.base_layer(x)
-        if x.is_cuda and self.cache.config.use_triton_kernels and x.numel() >= OVERLAP_MIN_TOKENS * x.shape[-1]:
-            out = self._overlapped_forward(x, lora_ctx)
+        if x.is_cuda and self.cache.config.use_triton_kernels:
+            out = self._tiled_forward(x, lora_ctx)
             if out is not None:
                 return out
         base = self.base_layer(x)
@@ -61,14 +69,11 @@ class MultiLoraLinear(nn.Module):
         out = self._hip_forward(x_3d, base_3d, seq_lens, weight_indices, lora_ctx)
         return out.reshape(original_shape)
 
-    def _overlapped_forward(self, x: torch.Tensor, lora_ctx: LoraBatchContext) -> torch.Tensor | None:
-        """Tiled path with the shrink on a side stream, concurrent with the base GEMM.
+    def _tiled_forward(self, x: torch.Tensor, lora_ctx: LoraBatchContext) -> torch.Tensor | None:
+        """Tiled path: shrink (shared with sibling Linears when it can be), base GEMM, expand.
 
-        The shrink reads only x, so it forks from the current stream as soon
-        as x is ready and runs while the base Linear computes; the expand,
-        which adds into the base output, joins back on the current stream.
-        Returns None when the shapes do not suit the tiled kernels (the
-        caller then takes the sequential path).
+        Returns None when the shapes do not suit the tiled kernels; the caller
+        then takes the sequential path (row kernels).
         """
         cache = self.cache
         x_3d, seq_lens, weight_indices, reshape = self._batched_view(x, lora_ctx)
@@ -80,16 +85,62 @@ class MultiLoraLinear(nn.Module):
             return None
         plan = self._plan(lora_ctx, rows, row_len, seq_lens, weight_indices)
         main = torch.cuda.current_stream(x.device)
-        side = sgmv.side_stream(x.device)
-        side.wait_stream(main)  # x is ready, and every earlier expand has read the side workspace
-        with torch.cuda.stream(side):
-            shrunk = sgmv.lora_shrink(x2, cache, self.module_name, plan)
-        base = self.base_layer(x)
-        original_shape = base.shape
+        if rows * row_len >= OVERLAP_MIN_TOKENS:
+            side = sgmv.side_stream(x.device)
+            side.wait_stream(main)  # x is ready, and every earlier expand has read the side workspaces
+            with torch.cuda.stream(side):
+                shrunk = self._shrink(x, x2, plan, lora_ctx)
+            base = self.base_layer(x)
+            main.wait_stream(side)
+        else:
+            shrunk = self._shrink(x, x2, plan, lora_ctx)
+            base = self.base_layer(x)
         base_3d = reshape(base)
-        main.wait_stream(side)
         sgmv.lora_expand(shrunk, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name)
-        return base_3d.reshape(original_shape)
+        return base_3d.reshape(base.shape)
+
+    def _shrink(self, x: torch.Tensor, x2: torch.Tensor, plan, lora_ctx: LoraBatchContext):
+        """This module's shrink result: computed ahead by a sibling, stacked with siblings, or alone.
+
+        Siblings are wrapped Linears that the model calls back to back on the
+        very same input tensor (q/k/v, gate/up).  The first forward learns them
+        from the call sequence; later forwards let the first of them shrink for
+        all in one launch.  A precomputed result is used only if this call's
+        input is that same tensor object, unmodified (same version counter;
+        inference-mode tensors keep none, so for them object identity alone),
+        with the same plan, and its workspace still holds it; otherwise the
+        module computes its own.
+        """
+        stack = lora_ctx.stack
+        shared = stack.setdefault("shared", {})
+        hit = shared.pop(self.module_name, None)
+        self._observe_call(x, stack)
+        if hit is not None:
+            hx, version, res = hit
+            if hx is x and version == _version_of(x) and res.plan is plan and res.valid:
+                return res
+        run = self.cache.stacked_runs.get((self.module_name, tuple(x.shape)))
+        if run is not None and len(run) > 1:
+            results = sgmv.lora_shrink_stacked(x2, self.cache, list(run), plan)
+            for name, res in zip(run[1:], results[1:]):
+                shared[name] = (x, _version_of(x), res)
+            return results[0]
+        return sgmv.lora_shrink(x2, self.cache, self.module_name, plan)
+
+    def _observe_call(self, x: torch.Tensor, stack: dict) -> None:
+        """Extend the current run of calls on one input tensor, recording it as a sibling set."""
+        run = stack.get("run")
+        if (
+            run is not None
+            and stack.get("run_x") is x
+            and stack.get("run_version") == _version_of(x)
+            and self.module_name not in run
+            and len(run) < sgmv.MAX_STACKED_MODULES
+        ):
+            run.append(self.module_name)
+            self.cache.stacked_runs[(run[0], tuple(x.shape))] = tuple(run)
+        else:
+            stack["run"], stack["run_x"], stack["run_version"] = [self.module_name], x, _version_of(x)
 
     def _plan(self, lora_ctx: LoraBatchContext, rows: int, row_len: int, seq_lens, weight_indices):
         key = (rows, row_len)

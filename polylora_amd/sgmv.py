@@ -15,12 +15,14 @@ There is no CPU path: CPU tensors raise.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _native
 
 __all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "lora_shrink", "lora_expand", "sgmv_lora_a_fwd",
-           "sgmv_lora_b_fwd", "choose_k_splits", "choose_group_tokens", "side_stream"]
+           "sgmv_lora_b_fwd", "choose_k_splits", "choose_group_tokens", "side_stream", "lora_shrink_stacked"]
 
 
 def _stream(device: torch.device) -> int:
@@ -119,6 +121,7 @@ class _Workspace:
         self.device = device
         self.buf: torch.Tensor | None = None
         self.retired: list[torch.Tensor] = []
+        self.owner: object | None = None  # the ShrinkResult whose planes the buffer holds
 
     def get(self, nbytes: int) -> torch.Tensor:
         nbytes = max(256, (nbytes + 255) // 256 * 256)
@@ -130,11 +133,12 @@ class _Workspace:
         return self.buf
 
 
-_WORKSPACES: dict[tuple[int, int], _Workspace] = {}
+_WORKSPACES: dict[tuple[int, int, int], _Workspace] = {}
 
 
-def _workspace(device: torch.device, stream: int) -> _Workspace:
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+def _workspace(device: torch.device, stream: int, position: int = 0) -> _Workspace:
+    """Workspace `position` of (device, stream); a stacked shrink writes module i to position i."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream, position)
     ws = _WORKSPACES.get(key)
     if ws is None:
         ws = _WORKSPACES[key] = _Workspace(device)
@@ -223,7 +227,9 @@ def lora_apply(
     rows = max(1, plan.tokens_cap)
     group_cap = max(1, plan.group_cap)
     nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, plan.group_tokens, rows, ldt))
-    buf = _workspace(x.device, stream).get(nbytes)
+    ws = _workspace(x.device, stream)
+    buf = ws.get(nbytes)
+    ws.owner = None  # planes of an earlier separate shrink on this workspace are gone
     status = lib.pl_lora_apply(
         dt,
         x.data_ptr(),
@@ -254,13 +260,23 @@ def lora_apply(
 
 
 class ShrinkResult:
-    """Where a shrink left its partial sums: the workspace of the stream it ran on."""
+    """Where a shrink left its partial sums: a workspace of the stream it ran on.
 
-    __slots__ = ("buf", "planes", "rows", "ldt", "plan", "K")
+    ``valid`` turns False once a later shrink has reused that workspace.
+    """
 
-    def __init__(self, buf, planes, rows, ldt, plan, K) -> None:
-        self.buf, self.planes, self.rows, self.ldt, self.plan, self.K = buf, planes, rows, ldt, plan, K
+    __slots__ = ("ws", "buf", "planes", "rows", "ldt", "plan", "K")
 
+    def __init__(self, ws, buf, planes, rows, ldt, plan, K) -> None:
+        self.ws, self.buf, self.planes, self.rows, self.ldt, self.plan, self.K = ws, buf, planes, rows, ldt, plan, K
+        ws.owner = self
+
+    @property
+    def valid(self) -> bool:
+        return self.ws.owner is self
+
+
+MAX_STACKED_MODULES = _native.PL_MAX_STACKED_MODULES
 
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
 
@@ -290,33 +306,51 @@ def tiled_shapes_ok(x: torch.Tensor, out_features: int) -> bool:
 
 def lora_shrink(x: torch.Tensor, cache, module_name: str, plan: SgmvPlan, *, k_splits: int | None = None) -> ShrinkResult:
     """Launch the shrink of one wrapped Linear on the current stream; the expand reads the result later."""
+    return lora_shrink_stacked(x, cache, [module_name], plan, k_splits=k_splits)[0]
+
+
+def lora_shrink_stacked(x: torch.Tensor, cache, module_names: list, plan: SgmvPlan, *,
+                        k_splits: int | None = None) -> list:
+    """One shrink launch for wrapped Linears that read the same x (pl_sgmv_shrink_stacked).
+
+    Module i's partial sums go to workspace position i of the current stream.
+    """
     _require_gpu(x, "lora_shrink")
-    spec = cache.module_specs.get(module_name)
-    if spec is None:
-        raise KeyError(f"module {module_name!r} is not in the adapter cache")
-    if x.dim() != 2 or x.shape[0] != plan.tokens_cap or x.shape[1] != spec.in_features:
-        raise ValueError(f"x must be [{plan.tokens_cap}, {spec.in_features}], got {list(x.shape)}")
+    n = len(module_names)
+    if not 1 <= n <= _native.PL_MAX_STACKED_MODULES:
+        raise ValueError(f"a shrink serves 1..{_native.PL_MAX_STACKED_MODULES} modules, got {n}")
+    specs = []
+    for name in module_names:
+        spec = cache.module_specs.get(name)
+        if spec is None:
+            raise KeyError(f"module {name!r} is not in the adapter cache")
+        specs.append(spec)
+    K = int(x.shape[1]) if x.dim() == 2 else -1
+    if x.dim() != 2 or x.shape[0] != plan.tokens_cap or any(sp.in_features != K for sp in specs):
+        raise ValueError(f"x must be [{plan.tokens_cap}, in_features] for every module, got {list(x.shape)}")
     if x.dtype != cache.dtype or x.device != cache.device:
         raise TypeError(f"x {x.dtype} on {x.device} must match the adapter cache ({cache.dtype} on {cache.device})")
     lib = _native.load()
     dt = _native.dtype_code(x.dtype)
-    K = int(x.shape[1])
     ldt = cache.rank8_cap
     stream = _stream(x.device)
     splits = k_splits if k_splits is not None else choose_k_splits(plan.group_cap, K, x.dtype)
     rows = max(1, plan.tokens_cap)
     planes = int(lib.pl_shrink_planes(dt, K, splits, plan.group_tokens))
     nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, plan.group_tokens, rows, ldt))
-    buf = _workspace(x.device, stream).get(nbytes)
+    wss = [_workspace(x.device, stream, i) for i in range(n)]
+    bufs = [ws.get(nbytes) for ws in wss]
+    modules = (ctypes.c_int32 * n)(*(cache.module_index[name] for name in module_names))
+    ptrs = (ctypes.c_void_p * n)(*(b.data_ptr() for b in bufs))
     _native.check(
-        lib.pl_sgmv_shrink(
+        lib.pl_sgmv_shrink_stacked(
             dt, x.data_ptr(), x.stride(0), K, cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index),
-            cache.module_index[module_name], plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(),
-            max(1, plan.group_cap), plan.group_tokens, buf.data_ptr(), buf.numel(), ldt, rows, splits, stream,
+            n, modules, ptrs, plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(),
+            max(1, plan.group_cap), plan.group_tokens, min(b.numel() for b in bufs), ldt, rows, splits, stream,
         ),
-        "pl_sgmv_shrink",
+        "pl_sgmv_shrink_stacked",
     )
-    return ShrinkResult(buf, planes, rows, ldt, plan, K)
+    return [ShrinkResult(ws, b, planes, rows, ldt, plan, K) for ws, b in zip(wss, bufs)]
 
 
 def lora_expand(res: ShrinkResult, y: torch.Tensor, cache, module_name: str, *,
@@ -329,6 +363,8 @@ def lora_expand(res: ShrinkResult, y: torch.Tensor, cache, module_name: str, *,
         raise ValueError(f"y must be [{plan.tokens_cap}, {spec.out_features}], got {list(y.shape)}")
     if y.dtype != cache.dtype or y.device != cache.device:
         raise TypeError(f"y {y.dtype} on {y.device} must match the adapter cache ({cache.dtype} on {cache.device})")
+    if not res.valid:
+        raise RuntimeError("the shrink result was overwritten by a later shrink on the same workspace")
     lib = _native.load()
     _native.check(
         lib.pl_sgmv_expand(

@@ -269,3 +269,44 @@ def test_lora_apply_graph_replays(gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, want_y) and torch.equal(z, want_z), i
+
+
+@pytest.mark.parametrize("group_tokens", [16, 64])
+def test_stacked_shrink_equals_separate(gpu, group_tokens):
+    """pl_sgmv_shrink_stacked over q/k/v-like modules == one pl_sgmv_shrink per module, bit for bit."""
+    _announce(test="stacked_shrink", group_tokens=group_tokens)
+    g = torch.Generator().manual_seed(60)
+    K, rows = 512, 70
+    shapes = {"q": (K, 512), "k": (K, 128), "v": (K, 136)}
+    adapters = {}
+    for i, r in enumerate([8, 24, 64]):
+        adapters[f"s{i}"] = {m: peft_layer(g, fi, fo, r, 2.0 * r) for m, (fi, fo) in shapes.items() if not (i == 1 and m == "k")}
+    cache = make_cache(adapters, shapes, 3, 64, gpu, torch.bfloat16)
+    ids = list(adapters) + ["__base__"]
+    row_slot = cache.ensure_resident([ids[i] for i in torch.randint(0, 4, (rows,), generator=g).tolist()])
+    seq = torch.ones(rows, dtype=torch.int32, device=gpu)
+    plan = sgmv.SgmvPlan(row_slot, seq, 1, cache.num_slots, group_tokens=group_tokens)
+    x = torch.randn(rows, K, generator=g).to(torch.bfloat16).to(gpu)
+    base = {m: torch.randn(rows, fo, generator=g).to(torch.bfloat16).to(gpu) for m, (fi, fo) in shapes.items()}
+    # separate
+    sep = {}
+    for m in shapes:
+        y = base[m].clone()
+        res = sgmv.lora_shrink(x, cache, m, plan)
+        sgmv.lora_expand(res, y, cache, m)
+        sep[m] = y
+    # stacked
+    results = sgmv.lora_shrink_stacked(x, cache, list(shapes), plan)
+    for m, res in zip(shapes, results):
+        y = base[m].clone()
+        sgmv.lora_expand(res, y, cache, m)
+        assert torch.equal(y, sep[m]), m
+    # a later shrink on position 0 invalidates the first stacked result only
+    sgmv.lora_shrink(x, cache, "q", plan)
+    assert not results[0].valid and results[1].valid and results[2].valid
+    with pytest.raises(RuntimeError, match="overwritten"):
+        sgmv.lora_expand(results[0], base["q"].clone(), cache, "q")
+    for m in shapes:
+        A, B, rk, sc = oracle_slot_tensors(cache, adapters, m, torch.bfloat16)
+        expect = reference_forward(x.cpu().view(rows, 1, K), base[m].cpu().view(rows, 1, -1), seq.cpu(), row_slot.cpu(), A, B, rk, sc)
+        torch.testing.assert_close(sep[m].cpu(), expect.view(rows, -1), **tol_for(torch.bfloat16))

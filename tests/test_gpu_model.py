@@ -481,3 +481,29 @@ def test_llama_decode_step_graph_replays(gpu):
         ref = oracle_model.run(om, bank, adapter_ids, input_ids=ids, past_key_values=kv, cache_position=pos,
                                use_cache=True).last_hidden_state
     torch.testing.assert_close(want.float(), ref.float(), **BF16)
+
+
+def test_sibling_shrinks_are_stacked(gpu):
+    """q/k/v and gate/up are learned as siblings in the first forward; the second forward stacks their
+    shrinks and gives the same output bit for bit; both match the fallback."""
+    _announce(test="stacked_siblings")
+    base, cfg = _tiny_llama(15, torch.bfloat16, gpu)
+    pm = PolyLoraModel(copy.deepcopy(base), PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=4, max_rank=32)).eval()
+    g = torch.Generator().manual_seed(15)
+    ads = {f"t{i}": (_peft.make_lora_weights(g, _shapes(pm), r, std=0.05), 2.0 * r) for i, r in enumerate([8, 32, 16])}
+    for aid, (w, alpha) in ads.items():
+        pm.adapter_store.add_adapter_from_peft_state_dict(aid, _peft.state_dict(w), pm.target_module_names, alpha)
+    ids = torch.randint(0, 211, (12, 1), generator=g).to(gpu)
+    adapter_ids = [["__base__", *ads][int(i)] for i in torch.randint(0, 4, (12,), generator=g)]
+    with torch.inference_mode():
+        first = pm(input_ids=ids, adapter_ids=adapter_ids).last_hidden_state.clone()
+        runs = set(pm.adapter_cache.stacked_runs.values())
+        for layer in range(cfg.num_hidden_layers):
+            p = f"layers.{layer}."
+            assert (p + "self_attn.q_proj", p + "self_attn.k_proj", p + "self_attn.v_proj") in runs
+            assert (p + "mlp.gate_proj", p + "mlp.up_proj") in runs
+        second = pm(input_ids=ids, adapter_ids=adapter_ids).last_hidden_state
+        om, bank = _oracle(base, LLAMA_TARGETS, ads, 32, torch.bfloat16, gpu)
+        want = oracle_model.run(om, bank, adapter_ids, input_ids=ids).last_hidden_state
+    assert torch.equal(first, second)
+    torch.testing.assert_close(second.float(), want.float(), **BF16)
