@@ -18,8 +18,12 @@ Also reported in the same JSON line (``workloads``):
   adapters with 10% __base__ rows.  Multi-LoRA tokens/s against the same
   model with no adapters (HIP-graph replay of one decode step, and eager),
   and the 224 shrink+expand pairs of one step timed alone (HBM GB/s).
+* ``prefill`` the same model, 8 adapters (r16 x4, r32 x4), B=32, S=1024
+  right-padded, U[512,1024] lengths: LoRA kernel GB/s and MFMA fraction,
+  forward time with and without adapters.
+* ``churn`` 1024 rank-16 adapters through 32 slots, batch 128, Zipf(0.9):
+  tokens/s against an all-resident hot set, H2D bytes, copy/compute overlap.
 * ``deberta`` DeBERTa-v3-base shape, fp32, 5 adapters, B=8, S=128 (tokens/s).
-* ``prefill`` / ``churn`` with ``--prefill`` / ``--churn``.
 
 ``--gpus`` above 1 exits: this build measures one GPU.
 """
@@ -693,7 +697,176 @@ def run_decode(args) -> dict:
             out["tokens_per_s_base"] = out["eager_tokens_per_s_base"]
             out["ratio_lora_to_base"] = round(e_base / e_lora, 4)
             out["timing"] = "eager wall clock (graph capture failed)"
-    del wl, pm, ctx
+    if getattr(args, "keep_model", False):
+        out["_model"] = pm
+    del wl, ctx
+    torch.cuda.empty_cache()
+    return out
+
+
+def prefill_bytes(pm, adapter_ids: list, lens: list) -> dict:
+    """Algorithmic bytes and flops of one prefill forward's 224 shrink+expand pairs over the valid tokens."""
+    es = 2
+    xy = ab = flops = 0
+    uniq = sorted(set(adapter_ids))
+    for spec in pm.module_specs:
+        for aid, n in zip(adapter_ids, lens):
+            w = pm.adapter_store.adapters[aid].layers[spec.name]
+            xy += es * n * spec.in_features + 2 * es * n * spec.out_features
+            flops += 2 * n * w.rank * (spec.in_features + spec.out_features)
+        for aid in uniq:
+            w = pm.adapter_store.adapters[aid].layers[spec.name]
+            ab += es * w.rank * (spec.in_features + spec.out_features)
+    return {"total": xy + ab, "flops": flops}
+
+
+def run_prefill(args, pm) -> dict:
+    """Prefill: 8 adapters (4 x r16, 4 x r32), B=32, S=1024, right-padded, lengths U[512,1024], 4 rows per adapter.
+
+    The base model runs causal attention without the padding mask: rows are
+    right-padded, so every valid token attends exactly the same keys, and
+    torch's flash kernel (no masks) takes the step.  LoRA lengths come from
+    the mask, as in the reference (model.py:99-104).
+    """
+    from polylora_amd.context import use_lora_context
+
+    device = torch.device("cuda", 0)
+    rng = np.random.default_rng(1004)
+    names = [f"pf{i}" for i in range(8)]
+    add_random_adapters(pm, {n: (16 if i < 4 else 32) for i, n in enumerate(names)}, seed=1004, device=device)
+    B, S = 32, 1024
+    lens = rng.integers(512, S + 1, size=B)
+    adapter_ids = [names[i // 4] for i in range(B)]
+    mask = (torch.arange(S)[None, :] < torch.as_tensor(lens)[:, None]).long().to(device)
+    ids = torch.randint(0, pm.base_model.config.vocab_size, (B, S), device=device)
+    ctx = pm.prepare_lora_context(adapter_ids, mask, B, S, device)
+    nb = prefill_bytes(pm, adapter_ids, [int(v) for v in lens])
+    out = {"rows": B, "seq": S, "valid_tokens": int(lens.sum()), "lora_bytes_per_forward": nb["total"],
+           "lora_flops_per_forward": nb["flops"]}
+    with torch.inference_mode():
+        kt = time_lora_ops(pm, adapter_ids, S, torch.as_tensor(lens, dtype=torch.int32, device=device), reps=2)
+        kern_ms = kt["pairs_ms"]
+        out["plan_group_tokens"] = kt["group_tokens"]
+        out["lora_kernels_ms"] = round(kern_ms, 3)
+        out["lora_kernels_gbs"] = round(nb["total"] / (kern_ms * 1e-3) / 1e9, 1)
+        out["lora_kernels_pct_hbm"] = round(100 * nb["total"] / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
+        out["lora_kernels_mfma_tflops"] = round(nb["flops"] / (kern_ms * 1e-3) / 1e12, 2)
+        out["lora_kernels_pct_mfma_bf16"] = round(100 * nb["flops"] / (kern_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 3)
+        out["lora_kernels_shrink_ms"] = round(kt["shrink_ms"], 3)
+        out["lora_kernels_expand_ms"] = round(kt["expand_ms"], 3)
+
+        def base_fwd():
+            return pm.base_model(input_ids=ids, use_cache=False).last_hidden_state
+
+        def lora_fwd():
+            with use_lora_context(ctx):
+                return pm.base_model(input_ids=ids, use_cache=False).last_hidden_state
+
+        out["ms_base"] = round(_eager_ms(base_fwd, 3), 2)
+        out["ms_lora"] = round(_eager_ms(lora_fwd, 3), 2)
+        out["tokens_per_s_base"] = round(int(lens.sum()) / out["ms_base"] * 1e3, 1)
+        out["tokens_per_s_lora"] = round(int(lens.sum()) / out["ms_lora"] * 1e3, 1)
+        out["ratio_lora_to_base"] = round(out["ms_base"] / out["ms_lora"], 4)
+        out["timing"] = "eager wall clock of one forward (valid tokens per second)"
+    _log(f"prefill: kernels {out['lora_kernels_gbs']} GB/s, base {out['ms_base']} ms, lora {out['ms_lora']} ms")
+    return out
+
+
+def run_churn(args) -> dict:
+    """Adapter churn: 1024 rank-16 adapters on all 7 targets, 32 GPU slots, batch 128, Zipf(0.9) ids.
+
+    Each step's rows are split, in row order, into sub-batches of at most 32
+    distinct adapters (the reference raises beyond its slot count,
+    cache.py:65-66).  Every sub-batch is one forward of one new token per row
+    (no KV cache), preceded by the loads its adapters need; loads go to the
+    side stream and overlap the previous sub-batch's compute.  The catalog
+    aliases 64 distinct random weight images (adapter i uses image i % 64) so
+    that the pinned host catalog is 5.4 GB instead of 86 GB; every load still
+    copies the full 84 MB image.  Compared with the same rows restricted to 32
+    resident adapters (no loads).
+    """
+    from polylora_amd import PolyLoraConfig, PolyLoraModel
+    from polylora_amd.store import CpuAdapter
+
+    device = torch.device("cuda", 0)
+    rng = np.random.default_rng(1005)
+    model = build_llama(device, args.decode_layers, seed=1005)
+    pm = PolyLoraModel(model, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=32, max_rank=16)).eval()
+    images = [f"img{i:02d}" for i in range(64)]
+    add_random_adapters(pm, {n: 16 for n in images}, seed=1005, device=device)
+    store = pm.adapter_store
+    catalog = [f"cat{i:04d}" for i in range(1024)]
+    for i, aid in enumerate(catalog):
+        src = store.adapters[images[i % 64]]
+        store.adapters[aid] = CpuAdapter(aid, {}, src.layers, packed=src.packed)
+    for n in images:
+        store.adapters.pop(n)
+    w = 1.0 / np.arange(1, 1025) ** 0.9
+    w /= w.sum()
+    B = 128
+    steps = [[catalog[int(i)] for i in rng.choice(1024, size=B, p=w)] for _ in range(args.churn_steps)]
+
+    def sub_batches(ids):
+        out, cur, seen = [], [], set()
+        for a in ids:
+            if a not in seen and len(seen) == 32:
+                out.append(cur)
+                cur, seen = [], set()
+            cur.append(a)
+            seen.add(a)
+        out.append(cur)
+        return out
+
+    vocab = pm.base_model.config.vocab_size
+    gen = torch.Generator(device=device).manual_seed(1005)
+
+    def run(all_steps):
+        n_tok = 0
+        loads0 = pm.adapter_cache.loads
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.inference_mode():
+            for ids in all_steps:
+                for sub in sub_batches(ids):
+                    x = torch.randint(0, vocab, (len(sub), 1), generator=gen, device=device)
+                    pm(input_ids=x, adapter_ids=sub, use_cache=False)
+                    n_tok += len(sub)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, n_tok, pm.adapter_cache.loads - loads0
+
+    # pack every image once and touch the pinned copies before timing
+    for n in range(64):
+        pm.adapter_cache._packed(store.adapters[catalog[n]])
+    run(steps[:2])
+    churn_s, n_tok, loads = run(steps)
+    hot = catalog[:32]
+    hot_steps = [[hot[int(i) % 32] for i in rng.choice(1024, size=B, p=w)] for _ in range(args.churn_steps)]
+    run(hot_steps[:2])
+    hot_s, hot_tok, hot_loads = run(hot_steps)
+    image_bytes = int(pm.adapter_cache._packed(store.adapters[catalog[0]]).image.numel())
+    # pinned host -> device bandwidth of one adapter image
+    img = pm.adapter_cache._packed(store.adapters[catalog[0]]).image
+    dst = torch.empty(image_bytes, dtype=torch.uint8, device=device)
+    for _ in range(3):
+        dst.copy_(img, non_blocking=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        dst.copy_(img, non_blocking=True)
+    torch.cuda.synchronize()
+    h2d_gbs = 10 * image_bytes / (time.perf_counter() - t0) / 1e9
+    copy_s = loads * image_bytes / (h2d_gbs * 1e9)
+    overlap = (copy_s + hot_s - churn_s) / max(1e-9, min(copy_s, hot_s))
+    out = {"steps": args.churn_steps, "batch": B, "slots": 32, "catalog": 1024, "distinct_images": 64,
+           "slot_loads": loads, "loads_per_step": round(loads / args.churn_steps, 1), "adapter_image_bytes": image_bytes,
+           "h2d_bytes_per_step": round(loads * image_bytes / args.churn_steps), "pinned_h2d_gbs": round(h2d_gbs, 1),
+           "tokens_per_s_churn": round(n_tok / churn_s, 1), "tokens_per_s_hot_set": round(hot_tok / hot_s, 1),
+           "ratio_churn_to_hot": round(hot_s / churn_s * n_tok / hot_tok, 4),
+           "copy_s_at_measured_h2d": round(copy_s, 3), "compute_s_hot": round(hot_s, 3), "wall_s_churn": round(churn_s, 3),
+           "overlap_efficiency": round(overlap, 3), "hot_set_loads": hot_loads,
+           "timing": "eager wall clock; one new token per row, no KV cache"}
+    _log(f"churn: {out['tokens_per_s_churn']} tok/s vs hot {out['tokens_per_s_hot_set']}, overlap {out['overlap_efficiency']}")
+    del pm, model
     torch.cuda.empty_cache()
     return out
 
@@ -710,6 +883,9 @@ def main(argv=None) -> int:
     p.add_argument("--decode-layers", type=int, default=32)
     p.add_argument("--decode-steps", type=int, default=20)
     p.add_argument("--no-deberta", action="store_true")
+    p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-churn", action="store_true")
+    p.add_argument("--churn-steps", type=int, default=10, help="decode steps of the churn workload (200 in the full config)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                    help="only copy a BYTES-sized device buffer 5 times (calibrates HBM byte counters) and exit")
     args = p.parse_args(argv)
@@ -749,7 +925,15 @@ def main(argv=None) -> int:
         result["cpu_baseline"] = iso["cpu_baseline"]
     if not args.only_isolated:
         workloads = {}
+        args.keep_model = not args.no_prefill
         workloads["decode"] = run_decode(args)
+        pm = workloads["decode"].pop("_model", None)
+        if pm is not None:
+            workloads["prefill"] = run_prefill(args, pm)
+            del pm
+            torch.cuda.empty_cache()
+        if not args.no_churn:
+            workloads["churn"] = run_churn(args)
         if not args.no_deberta:
             workloads["deberta"] = run_deberta(torch.device("cuda", 0))
         result["workloads"] = workloads

@@ -164,6 +164,7 @@ class GpuAdapterCache:
         # (first module, input shape) -> modules called back to back on that
         # same input tensor; learned by MultiLoraLinear, used to stack shrinks
         self.stacked_runs: dict[tuple, tuple[str, ...]] = {}
+        self.loads = 0  # adapters copied into a slot since construction
         self._allocate()
 
     # ------------------------------------------------------------------ storage
@@ -296,6 +297,7 @@ class GpuAdapterCache:
     def _load_adapter_into_slot(self, adapter_id: str, slot: int) -> None:
         adapter = self.store.get(adapter_id)
         self._write_slot(slot, self._packed(adapter))
+        self.loads += 1
         self.adapter_to_slot[adapter_id] = slot
         self.slot_to_adapter[slot] = adapter_id
         self._touch(adapter_id)
