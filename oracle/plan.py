@@ -44,6 +44,8 @@ def check_plan(tok: np.ndarray, groups: np.ndarray, meta: np.ndarray, row_slot, 
         covered[start : start + length] += 1
         seen.setdefault(slot, []).extend(int(t) for t in tok[start : start + length])
     assert (covered == 1).all(), "groups must tile the sorted token list exactly once"
+    for g in range(n_groups, len(groups)):  # the rest of the capacity: empty groups
+        assert int(groups[g][0]) == 0 and int(groups[g][2]) == 0, (g, groups[g])
     assert set(seen) == set(expect)
     for slot, toks in expect.items():
         assert sorted(seen[slot]) == sorted(toks), f"slot {slot} token set differs"

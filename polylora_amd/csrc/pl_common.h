@@ -63,6 +63,16 @@ __device__ __forceinline__ pl_u32x4 pl_ld16(const void* p) {
   return *reinterpret_cast<const pl_u32x4*>(p);
 }
 
+// Sixteen zero bytes in device memory: the source of every masked-off lane.
+static __device__ __attribute__((aligned(16))) uint32_t pl_zero16[4];
+
+// Branch-free guarded load: lanes with !ok read pl_zero16 instead of p.  The
+// guard only selects an address, so no exec-masked branch and no select on
+// the loaded value: the compiler can keep a wave's loads in flight together.
+__device__ __forceinline__ pl_u32x4 pl_ld16_or0(const void* p, bool ok) {
+  return pl_ld16(ok ? p : static_cast<const void*>(pl_zero16));
+}
+
 // One 16-byte chunk per lane on each operand of a 16x16 MFMA tile, fp32
 // accumulate.  Lane l supplies row (l % 16) of the A operand and column
 // (l % 16) of the B operand; its chunk covers the reduction slots owned by

@@ -7,7 +7,8 @@
 // b*row_len + m, m < L (the slicing x[b, :seq_len] of layers.py:127).
 //
 // Steps: per-slot token counts (LDS atomics), one block-wide exclusive scan
-// of counts and of group counts, group list emission, then each wave copies
+// of counts and of group counts, group list emission (records past the last
+// group, up to the capacity, are empty), then each wave copies
 // the token indices of its rows to the slot's segment.  Row order inside a
 // segment follows LDS atomic order and is not fixed; no consumer depends on
 // it.
@@ -109,6 +110,16 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
         groups[gi] = gr;
       }
     }
+  }
+  // The rest of the capacity holds empty groups (slot 0, length 0), so a
+  // kernel may read any record below group_cap without first reading meta.
+  for (int64_t gi = (int64_t)tg + tid; gi < group_cap; gi += kPlanThreads) {
+    pl_group gr;
+    gr.slot = 0;
+    gr.start = 0;
+    gr.len = 0;
+    gr.reserved = 0;
+    groups[gi] = gr;
   }
   __syncthreads();
   for (int s = tid; s < S; s += kPlanThreads) cnt[s] = 0;  // reused as fill counters

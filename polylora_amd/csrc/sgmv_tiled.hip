@@ -1,55 +1,43 @@
 // Adapter-major tiled SGMV kernels for gfx950 (MFMA 16x16, wave64).
 //
-// Both kernels walk the plan written by pl_plan_build: a list of groups of
-// at most G tokens that share one slot, G = 16 * RT with RT = 1 (short
-// adapter segments, e.g. decode) or RT = 4 (long segments, e.g. prefill).
-// RT is a template parameter so that registers are sized for the group:
-// short segments get more K and more ranks in flight per wave instead of
-// accumulators for rows that do not exist.  A token's result never depends
-// on which other tokens share its group, so the plan's order inside a slot
-// is free.
+// Every kernel walks the plan written by pl_plan_build: a list of groups of
+// at most G tokens that share one slot, G = 16 (decode and small batches) or
+// 64 (large batches of long segments).  A token's result never depends on
+// which other tokens share its group, so the plan's order inside a slot is
+// free.
 //
-// Shrink (replaces sgmv.py:63-138): one workgroup per (group, K split).  Its
-// four waves split the split's K range; per step each lane loads CC 16-byte
-// chunks of one token row of x and of one rank row of A, and the four lanes
-// that share a row read 64 contiguous bytes per load.  16x16 MFMA tiles
-// [tokens x ranks] accumulate in fp32 (16*JT ranks per pass), the four wave
-// partials are summed in LDS in a fixed order, and the block stores its sum
-// with plain stores into its own fp32 plane planes[split][position][rank].
+// Shrink (replaces sgmv.py:63-138).  16-token groups: pl_shrink_short, one
+// workgroup per (group, 32-rank pass, K split, module).  64-token groups:
+// pl_shrink_long, one workgroup per (group, K split, module), each A chunk
+// feeding the group's four row tiles.  In both, the four waves split the
+// split's K range, 16x16 MFMA tiles [tokens x ranks] accumulate in fp32, the
+// four wave partials are summed in LDS in a fixed order, and the workgroup
+// stores its sum with plain stores into its own fp32 plane
+// planes[split][position][rank].
 //
-// Expand (replaces sgmv.py:178-275): one workgroup per (group, column chunk
-// of 256 bf16/f16 or 128 f32 output columns), one 16-token row tile at a
-// time.  The intermediate is the shrink planes summed in split order (four
-// planes' loads in flight together) and rounded once to the model dtype; the
-// MFMA runs on the transposed tile [columns x tokens] so that B (stored
-// [out][rank8], rank contiguous) and the planes (rank contiguous) are both
-// read in contiguous 16-byte rank chunks.  Split-K therefore needs no
-// atomics, no cross-workgroup signalling and no cleared buffers: results are
-// bitwise reproducible and every launch can be recorded in a HIP graph.
-// The scaled, rounded delta goes through LDS to the row-major layout of y,
-// and the fused add-back reads and writes y once with 16-byte accesses (512
-// contiguous bytes per row).  With RT = 1 the y rows are loaded up front, in
-// parallel with B.  Registers stay at or below 128 per lane so that four
-// workgroups share a CU and hide each other's memory latency.
+// Expand (replaces sgmv.py:178-275): pl_expand_short, one workgroup per
+// (group, column chunk of 256 bf16/f16 or 128 f32 output columns, 16-token
+// sub-tile).  The planes of the sub-tile's tokens are summed in split order
+// and rounded once to the model dtype, staged in LDS, and multiplied with B
+// on the transposed tile [columns x tokens], so that B (stored [out][rank8],
+// rank contiguous) is read in contiguous 16-byte rank chunks.  Split-K
+// therefore needs no atomics, no cross-workgroup signalling and no cleared
+// buffers: results are bitwise reproducible and every launch can be recorded
+// in a HIP graph.  The scaled, rounded delta goes through LDS to the
+// row-major layout of y, and the fused add-back reads and writes y once with
+// 16-byte accesses (512 contiguous bytes per row).
+//
+// Latency is what these launches are short of, so every kernel issues a
+// wave's loads together before their first use: guards select an address
+// (masked lanes read a zero page) instead of branching around a load, and
+// scheduling barriers keep the compiler from interleaving the loads with
+// the MFMAs that consume them.
 #include "pl_common.h"
 
 namespace {
 
 constexpr int kWaves = 4;
 constexpr int kYRowsPerPass = 8;  // 256 threads, 32 lanes per tile row
-
-// Shrink shape per row-tile count: CC 16-byte chunks per lane per step and
-// JT 16-rank column tiles per pass.
-template <int RT>
-struct pl_shrink_shape;
-template <>
-struct pl_shrink_shape<1> {
-  enum { CC = 4, JT = 4 };
-};
-template <>
-struct pl_shrink_shape<4> {
-  enum { CC = 2, JT = 2 };
-};
 
 // Modules one shrink launch serves: wrapped Linears fed the same input x.
 constexpr int kMaxJobs = PL_MAX_STACKED_MODULES;
@@ -70,7 +58,9 @@ struct pl_shrink_args {
   const int32_t* meta;
   int32_t ldt;
   int32_t k_splits;
-  int64_t plane;  // floats between split planes
+  int32_t rank_passes;  // 32-rank passes per (group, split)
+  int32_t sub;          // 16-token sub-tiles per plan group (1 or 4)
+  int64_t plane;        // floats between split planes
 };
 
 struct pl_expand_args {
@@ -90,6 +80,7 @@ struct pl_expand_args {
   int32_t N;
   int32_t n_chunks;
   int32_t epilogue;
+  int32_t sub;  // 16-token sub-tiles per plan group (1 or 4)
 };
 
 // Columns of y one expand wave owns: 64 for 2-byte types, 32 for fp32, so
@@ -103,18 +94,157 @@ struct pl_expand_shape {
   enum { kLdsRow = kChunk + kPad };
 };
 
-template <int DT, int RT>
-__global__ __launch_bounds__(256, 4) void pl_shrink_tiled(pl_shrink_args a) {
+// ------------------------------------------------------------ short groups
+// Groups of at most 16 tokens (decode: a handful of rows per adapter) move
+// little data per workgroup, so these kernels are built for latency: every
+// load a wave needs is issued before its first MFMA, one memory round trip
+// per workgroup for ranks up to 64.
+//
+// Shrink: one workgroup per (group, pass of 32 ranks, K split, served
+// module); ranks beyond the slot's rank exit before loading anything.  The
+// four waves split the split's K range (256 per wave for 2-byte types) and
+// their partials are summed in LDS in a fixed order, as in pl_shrink_tiled.
+//
+// Expand: one workgroup per (group, 256-column chunk).  The shrink planes of
+// the group's tokens are summed once per workgroup (all planes' loads in
+// flight together), rounded to T and staged in LDS as [token][rank]; B and
+// the y rows are loaded at the same time.
+constexpr int kShortCC = 8;      // 16-byte chunks per lane per shrink step
+constexpr int kShortJT = 2;      // 16-rank tiles per shrink workgroup
+constexpr int kShortRanks = 16 * kShortJT;
+constexpr int kShortMaxPlanes = 16;
+constexpr int kShortRankBlock = 64;  // ranks staged in LDS per expand pass
+
+template <int DT>
+__global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
   typedef typename pl_traits<DT>::T T;
-  typedef pl_shrink_shape<RT> S;
   constexpr int E = pl_traits<DT>::E;
-  constexpr int kInstr = 4 * E;          // k covered by one wave load (4 lane groups)
-  constexpr int kStep = S::CC * kInstr;  // k covered by one wave step
-  constexpr int kSlots = RT * S::JT;     // 16x16 tiles per pass
+  constexpr int kInstr = 4 * E;
+  constexpr int kStep = kShortCC * kInstr;
+  __shared__ pl_f32x4 red[kWaves][kShortJT][64];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+
+  // block -> (group g, K split c, rank pass rp, served module job); blocks
+  // that read the same x rows are adjacent
+  const int job = blockIdx.x % a.n_jobs;
+  int rest = blockIdx.x / a.n_jobs;
+  const int rp = rest % a.rank_passes;
+  rest /= a.rank_passes;
+  const int c = rest % a.k_splits;
+  const int g = rest / a.k_splits;
+  // the group count and the group record load together (every record below
+  // the capacity is readable); the record is used only for g below the count
+  const int n_groups = a.meta[0];
+  const pl_group grp = a.groups[g];
+  const int len = min(grp.len, 16);  // the host pairs 16-token groups with this kernel
+  if (g >= n_groups || len <= 0) return;
+  const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module[job]];
+  const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
+  const int rb = rp * kShortRanks;
+  if (rb >= rank) return;
+  const int K = a.K;
+  const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
+  const T* __restrict__ A = reinterpret_cast<const T*>(a.arena + e.a_off);
+  float* __restrict__ out = a.planes[job] + (int64_t)c * a.plane;
+
+  // Every load below is unconditional (pl_ld16_or0), so a wave's loads are
+  // all in flight before its first MFMA.  The token index loads first; A,
+  // which does not need it, issues next, and only then x, whose addresses
+  // wait for the index (the load counter retires in order).
+  const bool xok = li < len;
+  const int xt = a.tok[grp.start + min(li, len - 1)];
+  const int k0 = (c * kWaves + wave) * a.kw;
+  const int k1 = min(K, k0 + a.kw);
+
+  pl_f32x4 acc[kShortJT];
+#pragma unroll
+  for (int jt = 0; jt < kShortJT; ++jt) acc[jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto step = [&](int kb) {
+    // chunk cc of lane (li, lg) covers k = kb + cc*kInstr + lg*E .. +E
+    pl_u32x4 xf[kShortCC];
+    pl_u32x4 af[kShortJT][kShortCC];
+#pragma unroll
+    for (int jt = 0; jt < kShortJT; ++jt) {
+      const int j = rb + jt * 16 + li;
+      const T* arow = A + (int64_t)j * K + lg * E;
+#pragma unroll
+      for (int cc = 0; cc < kShortCC; ++cc) {
+        const int k = kb + cc * kInstr;
+        af[jt][cc] = pl_ld16_or0(arow + k, j < rank && k + lg * E < k1);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const T* xrow = x + (int64_t)xt * a.ldx + lg * E;
+#pragma unroll
+    for (int cc = 0; cc < kShortCC; ++cc) {
+      const int k = kb + cc * kInstr;
+      xf[cc] = pl_ld16_or0(xrow + k, xok && k + lg * E < k1);
+    }
+    // keep the scheduler from interleaving the loads above with the MFMAs
+    // below (it would wait on each load in turn)
+    __builtin_amdgcn_sched_barrier(0);
+    // no rank guard here: a guard would let the compiler sink the second
+    // tile's loads behind the first tile's MFMAs; a tile past the rank
+    // multiplies zeros
+#pragma unroll
+    for (int jt = 0; jt < kShortJT; ++jt)
+#pragma unroll
+      for (int cc = 0; cc < kShortCC; ++cc)
+        acc[jt] = pl_mfma_chunk<DT>(xf[cc], af[jt][cc], acc[jt]);
+  };
+  // The first step is peeled and unguarded (a wave with no K range reads
+  // only zeros), so nothing that needs the index can be placed ahead of the
+  // first A loads.
+  step(k0);
+  for (int kb = k0 + kStep; kb < k1; kb += kStep) step(kb);
+
+  // Sum the four wave partials of each tile in a fixed order; acc[jt][v]
+  // holds tile element (token 4*lg+v, rank rb + jt*16 + li).
+#pragma unroll
+  for (int jt = 0; jt < kShortJT; ++jt) red[wave][jt][lane] = acc[jt];
+  __syncthreads();
+  if (tid < kShortJT * 64) {
+    const int jt = tid >> 6;
+    const int l = tid & 63;
+    const pl_f32x4 s = red[0][jt][l] + red[1][jt][l] + red[2][jt][l] + red[3][jt][l];
+    const int j = rb + jt * 16 + (l & 15);
+    if (j < rank) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int prow = (l >> 4) * 4 + v;
+        if (prow < len) out[(int64_t)(grp.start + prow) * a.ldt + j] = s[v];
+      }
+    }
+  }
+}
+
+// Long-group shrink (64-token groups, e.g. prefill): one workgroup per
+// (group, K split, served module).  Each wave takes a quarter of the split's
+// K range for all four 16-token row tiles, so every A chunk it loads feeds
+// four MFMAs; the four wave partials are summed in LDS in a fixed order.
+// The K loop is double-buffered: the loads of step s+1 are in flight while
+// step s runs on the MFMA.
+constexpr int kLongCC = 2;  // 16-byte chunks per lane per step
+constexpr int kLongJT = 2;  // 16-rank tiles per pass
+constexpr int kLongRT = 4;  // 16-token row tiles per group
+
+template <int DT>
+__global__ __launch_bounds__(256, 2) void pl_shrink_long(pl_shrink_args a) {
+  typedef typename pl_traits<DT>::T T;
+  constexpr int E = pl_traits<DT>::E;
+  constexpr int kInstr = 4 * E;
+  constexpr int kStep = kLongCC * kInstr;
+  constexpr int kTiles = kLongRT * kLongJT;
   __shared__ pl_f32x4 red[kWaves][kWaves][64];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;
@@ -125,95 +255,104 @@ __global__ __launch_bounds__(256, 4) void pl_shrink_tiled(pl_shrink_args a) {
   const int gc = blockIdx.x / a.n_jobs;
   const int g = gc / a.k_splits;
   const int c = gc - g * a.k_splits;
-  if (g >= a.meta[0]) return;
+  const int n_groups = a.meta[0];
   const pl_group grp = a.groups[g];
+  const int len = min(grp.len, 16 * kLongRT);  // the host pairs 64-token groups with this kernel
+  if (g >= n_groups || len <= 0) return;
   const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module[job]];
   const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
   if (rank <= 0) return;
-  const int len = min(grp.len, 16 * RT);  // the host pairs the plan's group size with RT
   const int nrt = (len + 15) >> 4;
   const int K = a.K;
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
   const T* __restrict__ A = reinterpret_cast<const T*>(a.arena + e.a_off);
   float* __restrict__ out = a.planes[job] + (int64_t)c * a.plane;
 
-  const T* xrow[RT];
-  bool xok[RT];
+  bool xok[kLongRT];
+  int xt[kLongRT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int p = rt * 16 + li;
-    xok[rt] = p < len;
-    const int t = xok[rt] ? a.tok[grp.start + p] : 0;
-    xrow[rt] = x + (int64_t)t * a.ldx + lg * E;
+  for (int rt = 0; rt < kLongRT; ++rt) {
+    xok[rt] = rt * 16 + li < len;
+    xt[rt] = a.tok[grp.start + min(rt * 16 + li, len - 1)];
   }
   const int k0 = (c * kWaves + wave) * a.kw;
   const int k1 = min(K, k0 + a.kw);
 
-  for (int rb = 0; rb < rank; rb += 16 * S::JT) {
-    pl_f32x4 acc[RT][S::JT];
+  for (int rb = 0; rb < rank; rb += 16 * kLongJT) {
+    pl_f32x4 acc[kLongRT][kLongJT];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
+    for (int rt = 0; rt < kLongRT; ++rt)
 #pragma unroll
-      for (int jt = 0; jt < S::JT; ++jt) acc[rt][jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int jt = 0; jt < kLongJT; ++jt) acc[rt][jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int kb = k0; kb < k1; kb += kStep) {
-      // chunk cc of lane (li, lg) covers k = kb + cc*kInstr + lg*E .. +E
-      pl_u32x4 xf[RT][S::CC];
+    // chunk cc of lane (li, lg) covers k = kb + cc*kInstr + lg*E .. +E
+    auto load = [&](pl_u32x4 (&xf)[kLongRT][kLongCC], pl_u32x4 (&af)[kLongJT][kLongCC], int kb) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
+      for (int jt = 0; jt < kLongJT; ++jt) {
+        const int j = rb + jt * 16 + li;
+        const T* arow = A + (int64_t)j * K + lg * E;
 #pragma unroll
-        for (int cc = 0; cc < S::CC; ++cc) {
+        for (int cc = 0; cc < kLongCC; ++cc) {
           const int k = kb + cc * kInstr;
-          pl_u32x4 v = {0u, 0u, 0u, 0u};
-          if (xok[rt] && k + lg * E < k1) v = pl_ld16(xrow[rt] + k);
-          xf[rt][cc] = v;
-        }
-#pragma unroll
-      for (int jt = 0; jt < S::JT; ++jt) {
-        if (rb + jt * 16 < rank) {
-          const int j = rb + jt * 16 + li;
-          const T* arow = A + (int64_t)j * K + lg * E;
-          pl_u32x4 af[S::CC];
-#pragma unroll
-          for (int cc = 0; cc < S::CC; ++cc) {
-            const int k = kb + cc * kInstr;
-            pl_u32x4 v = {0u, 0u, 0u, 0u};
-            if (j < rank && k + lg * E < k1) v = pl_ld16(arow + k);
-            af[cc] = v;
-          }
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt)
-            if (rt < nrt)
-#pragma unroll
-              for (int cc = 0; cc < S::CC; ++cc)
-                acc[rt][jt] = pl_mfma_chunk<DT>(xf[rt][cc], af[cc], acc[rt][jt]);
+          af[jt][cc] = pl_ld16_or0(arow + k, j < rank && k + lg * E < k1);
         }
       }
+#pragma unroll
+      for (int rt = 0; rt < kLongRT; ++rt) {
+        const T* xrow = x + (int64_t)xt[rt] * a.ldx + lg * E;
+#pragma unroll
+        for (int cc = 0; cc < kLongCC; ++cc) {
+          const int k = kb + cc * kInstr;
+          xf[rt][cc] = pl_ld16_or0(xrow + k, xok[rt] && k + lg * E < k1);
+        }
+      }
+    };
+    auto mfma = [&](const pl_u32x4 (&xf)[kLongRT][kLongCC], const pl_u32x4 (&af)[kLongJT][kLongCC]) {
+#pragma unroll
+      for (int rt = 0; rt < kLongRT; ++rt)
+#pragma unroll
+        for (int jt = 0; jt < kLongJT; ++jt)
+#pragma unroll
+          for (int cc = 0; cc < kLongCC; ++cc)
+            acc[rt][jt] = pl_mfma_chunk<DT>(xf[rt][cc], af[jt][cc], acc[rt][jt]);
+    };
+    // steps past k1 load only zeros; no guard, so no branch splits the
+    // loads of a step from each other
+    pl_u32x4 xa[kLongRT][kLongCC], aa[kLongJT][kLongCC];
+    pl_u32x4 xb[kLongRT][kLongCC], ab[kLongJT][kLongCC];
+    load(xa, aa, k0);
+    for (int kb = k0; kb < k1; kb += 2 * kStep) {
+      load(xb, ab, kb + kStep);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(xa, aa);
+      load(xa, aa, kb + 2 * kStep);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(xb, ab);
     }
 
     // Sum the four wave partials of each tile in a fixed order, four tiles
     // (one per finishing wave) at a time.  acc[rt][jt][v] holds tile element
     // (row 4*lg+v, column li); tile index = rt*JT + jt.
 #pragma unroll
-    for (int t0 = 0; t0 < kSlots; t0 += kWaves) {
-      if (t0 / S::JT < nrt) {
+    for (int t0 = 0; t0 < kTiles; t0 += kWaves) {
+      if (t0 / kLongJT < nrt) {
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < kWaves; ++q) {
           const int t = t0 + q;
-          red[wave][q][lane] = acc[t / S::JT][t % S::JT];
+          red[wave][q][lane] = acc[t / kLongJT][t % kLongJT];
         }
         __syncthreads();
         const int t = t0 + wave;  // tile this wave finishes
-        const int rt = t / S::JT;
-        const int j = rb + (t % S::JT) * 16 + li;
-        const pl_f32x4 s = red[0][wave][lane] + red[1][wave][lane] + red[2][wave][lane] +
-                           red[3][wave][lane];
+        const int rt = t / kLongJT;
+        const int j = rb + (t % kLongJT) * 16 + li;
+        const pl_f32x4 sum = red[0][wave][lane] + red[1][wave][lane] + red[2][wave][lane] +
+                             red[3][wave][lane];
         if (j < rank && rt < nrt) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int prow = rt * 16 + lg * 4 + v;
-            if (prow < len) out[(int64_t)(grp.start + prow) * a.ldt + j] = s[v];
+            if (prow < len) out[(int64_t)(grp.start + prow) * a.ldt + j] = sum[v];
           }
         }
       }
@@ -221,59 +360,19 @@ __global__ __launch_bounds__(256, 4) void pl_shrink_tiled(pl_shrink_args a) {
   }
 }
 
-// Intermediate chunk of one token for an MFMA operand: planes summed in split
-// order, entries at or beyond `rank` zero, rounded once to T.  Four planes'
-// loads are issued before any of them is added.
-template <int DT, int E>
-__device__ __forceinline__ pl_u32x4 pl_sum_planes(const float* __restrict__ src, int64_t plane,
-                                                  int planes, int jl, int rank) {
-  typedef typename pl_traits<DT>::T T;
-  typedef typename pl_traits<DT>::T8 T8;
-  pl_f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
-  int q = 0;
-  for (; q + 4 <= planes; q += 4) {
-    pl_f32x4 l[4], h[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      l[u] = *reinterpret_cast<const pl_f32x4*>(src + (q + u) * plane);
-      if constexpr (E == 8) h[u] = *reinterpret_cast<const pl_f32x4*>(src + (q + u) * plane + 4);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      lo += l[u];
-      if constexpr (E == 8) hi += h[u];
-    }
-  }
-  for (; q < planes; ++q) {
-    lo += *reinterpret_cast<const pl_f32x4*>(src + q * plane);
-    if constexpr (E == 8) hi += *reinterpret_cast<const pl_f32x4*>(src + q * plane + 4);
-  }
-  if constexpr (E == 8) {
-    T8 h8;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      h8[i] = (T)((jl + i < rank) ? lo[i] : 0.f);
-      h8[i + 4] = (T)((jl + i + 4 < rank) ? hi[i] : 0.f);
-    }
-    return __builtin_bit_cast(pl_u32x4, h8);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lo[i] = (jl + i < rank) ? lo[i] : 0.f;
-    return __builtin_bit_cast(pl_u32x4, lo);
-  }
-}
-
-template <int DT, int RT>
-__global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
+template <int DT, int PMAX>
+__global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   typedef typename pl_traits<DT>::T T;
   typedef typename pl_traits<DT>::T4 T4;
   typedef typename pl_traits<DT>::T8 T8;
   typedef pl_expand_shape<DT> S;
   constexpr int E = pl_traits<DT>::E;
-  constexpr int kStep = 4 * E;  // rank slots per MFMA step
-  constexpr int kRows = 16 * RT;
-  constexpr int kYPer = kRows / kYRowsPerPass;  // y rows per thread
-  __shared__ __attribute__((aligned(16))) T delta[kRows * S::kLdsRow];
+  constexpr int kStep = 4 * E;                        // rank slots per MFMA step
+  constexpr int kSteps = kShortRankBlock / kStep;     // MFMA steps per staged rank block
+  constexpr int kTRow = kShortRankBlock + S::kPad;    // LDS row of the staged intermediate
+  constexpr int kYPer = 16 / kYRowsPerPass;           // y rows per thread
+  __shared__ __attribute__((aligned(16))) T tt[16 * kTRow];
+  __shared__ __attribute__((aligned(16))) T delta[16 * S::kLdsRow];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -281,79 +380,129 @@ __global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
   const int li = lane & 15;
   const int lg = lane >> 4;
 
-  const int g = blockIdx.x / a.n_chunks;
-  const int c = blockIdx.x - g * a.n_chunks;
-  if (g >= a.meta[0]) return;
-  const pl_group grp = a.groups[g];
+  // block -> (group g, column chunk c, 16-token sub-tile rt); the sub-tiles
+  // of one chunk, which read the same B rows, are adjacent
+  const int rt = blockIdx.x % a.sub;
+  const int gc = blockIdx.x / a.sub;
+  const int g = gc / a.n_chunks;
+  const int c = gc - g * a.n_chunks;
+  // the group count and the group record load together (every record below
+  // the capacity is readable); the record is used only for g below the count
+  const int n_groups = a.meta[0];
+  pl_group grp = a.groups[g];
+  grp.start += rt * 16;
+  const int len = min(grp.len - rt * 16, 16);
+  if (g >= n_groups || len <= 0) return;
   const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module];
   const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
   if (rank <= 0) return;
   const int r8 = e.rank8;
   const int N = a.N;
   const int n_base = c * S::kChunk;
-  const int len = min(grp.len, kRows);  // the host pairs the plan's group size with RT
-  const int nrt = (len + 15) >> 4;
   const float scale = e.scale;
   const float scale_t = pl_round<DT>(scale);
   const int n0 = n_base + wave * S::kColsWave;
   const T* __restrict__ Bc = reinterpret_cast<const T*>(a.arena + e.b_off);
 
-  // y tile rows of this thread: rows t/32 + 8*i, columns (t%32)*E .. +E.
+  // Load order: the y rows' token indices, then B and the planes of the
+  // first rank block, then the y rows (their addresses need the indices).
+  // The load counter retires in order, so waiting for the indices does not
+  // wait for B or the planes.
   const int yq = tid & 31;
   const int yr0 = tid >> 5;
   const int ycol = n_base + yq * E;
   T* __restrict__ y = reinterpret_cast<T*>(a.y);
+  int yt[kYPer];
+#pragma unroll
+  for (int i = 0; i < kYPer; ++i) yt[i] = a.tok[grp.start + min(yr0 + kYRowsPerPass * i, len - 1)];
+
+  // planes -> staged intermediate: thread (token sp, ranks rb + sq .. +4)
+  const int sp = tid >> 4;
+  const int sq = (tid & 15) * 4;
+  const float* srow = a.planes + (int64_t)(grp.start + (sp < len ? sp : 0)) * a.ldt;
+
+  pl_u32x4 bf[kSteps][S::kCT];
+  pl_u32x4 pv[PMAX];
+  // B rows n0 + ct*16 + li and the planes of ranks rb .. rb+63
+  auto load_block = [&](int rb) {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const int jl = rb + s * kStep + lg * E;
+#pragma unroll
+      for (int ct = 0; ct < S::kCT; ++ct) {
+        const int n = n0 + ct * 16 + li;
+        bf[s][ct] = pl_ld16_or0(Bc + (int64_t)n * r8 + jl, n < N && jl < r8);
+      }
+    }
+    // PMAX loads per thread, the plane index clamped to the last plane;
+    // only the first k_splits are summed
+    const int jr = rb + sq;
+    const bool sok = sp < len && jr < rank;
+    const float* sbase = srow + jr;
+#pragma unroll
+    for (int q = 0; q < PMAX; ++q)
+      pv[q] = pl_ld16_or0(sbase + (int64_t)min(q, a.k_splits - 1) * a.plane, sok);
+  };
+
+  // delta^T tiles [columns x tokens]: acc[ct][v] = delta(column n0 + ct*16 + 4*lg + v, token li)
+  pl_f32x4 acc[S::kCT];
+#pragma unroll
+  for (int ct = 0; ct < S::kCT; ++ct) acc[ct] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+  // planes summed in split order, masked at the rank, rounded once to T,
+  // staged in LDS and multiplied with B
+  auto use_block = [&](int rb) {
+    const int jr = rb + sq;
+    const bool sok = sp < len && jr < rank;
+    pl_f32x4 sum = __builtin_bit_cast(pl_f32x4, pv[0]);
+#pragma unroll
+    for (int q = 1; q < PMAX; ++q)
+      if (q < a.k_splits) sum += __builtin_bit_cast(pl_f32x4, pv[q]);
+    T4 tv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tv[i] = (T)((sok && jr + i < rank) ? sum[i] : 0.f);
+    if (rb > 0) __syncthreads();  // the previous rank block's MFMA reads are done
+    *reinterpret_cast<T4*>(tt + sp * kTRow + sq) = tv;
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      if (rb + s * kStep < r8) {
+        const pl_u32x4 tf = *reinterpret_cast<const pl_u32x4*>(tt + li * kTRow + s * kStep + lg * E);
+#pragma unroll
+        for (int ct = 0; ct < S::kCT; ++ct) acc[ct] = pl_mfma_chunk<DT>(bf[s][ct], tf, acc[ct]);
+      }
+    }
+  };
+
+  load_block(0);
+  __builtin_amdgcn_sched_barrier(0);  // B and plane loads issue before the y loads
   pl_u32x4 yv[kYPer];
   T* yptr[kYPer];
 #pragma unroll
   for (int i = 0; i < kYPer; ++i) {
     const int r = yr0 + kYRowsPerPass * i;
-    yptr[i] = (r < len && ycol < N) ? y + (int64_t)a.tok[grp.start + r] * a.ldy + ycol : nullptr;
-    yv[i] = pl_u32x4{0u, 0u, 0u, 0u};
-    if (RT == 1 && yptr[i] != nullptr) yv[i] = pl_ld16(yptr[i]);  // short tiles: load y early
+    yptr[i] = (r < len && ycol < N) ? y + (int64_t)yt[i] * a.ldy + ycol : nullptr;
+    yv[i] = pl_ld16_or0(yptr[i], yptr[i] != nullptr);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first use
+  use_block(0);
+  for (int rb = kShortRankBlock; rb < r8; rb += kShortRankBlock) {
+    load_block(rb);
+    __builtin_amdgcn_sched_barrier(0);
+    use_block(rb);
   }
 
-  // 1. delta^T tiles [columns x tokens] on the MFMA, one 16-token row tile at
-  // a time; acc[ct][v] = delta(column n0 + ct*16 + 4*lg + v, token rt*16 + li).
-  for (int rt = 0; rt < nrt; ++rt) {
-    const int p = rt * 16 + li;
-    const bool tok_ok = p < len;
-    const float* prow = a.planes + (int64_t)(grp.start + (tok_ok ? p : 0)) * a.ldt;
-    pl_f32x4 acc[S::kCT];
+  // scale and round in the epilogue's order, stage in LDS as [token][column]
+  T* drow = delta + li * S::kLdsRow + wave * S::kColsWave;
 #pragma unroll
-    for (int ct = 0; ct < S::kCT; ++ct) acc[ct] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < r8; j0 += kStep) {
-      const int jl = j0 + lg * E;
-      pl_u32x4 bf[S::kCT];
+  for (int ct = 0; ct < S::kCT; ++ct) {
+    T4 d;
 #pragma unroll
-      for (int ct = 0; ct < S::kCT; ++ct) {
-        const int n = n0 + ct * 16 + li;
-        bf[ct] = pl_u32x4{0u, 0u, 0u, 0u};
-        if (n < N && jl < r8) bf[ct] = pl_ld16(Bc + (int64_t)n * r8 + jl);
-      }
-      pl_u32x4 tf = {0u, 0u, 0u, 0u};
-      if (tok_ok && jl < rank) tf = pl_sum_planes<DT, E>(prow + jl, a.plane, a.k_splits, jl, rank);
-#pragma unroll
-      for (int ct = 0; ct < S::kCT; ++ct) acc[ct] = pl_mfma_chunk<DT>(bf[ct], tf, acc[ct]);
-    }
-    // 2. scale and round in the epilogue's order, stage in LDS as [token][column]
-    T* drow = delta + p * S::kLdsRow + wave * S::kColsWave;
-#pragma unroll
-    for (int ct = 0; ct < S::kCT; ++ct) {
-      T4 d;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) d[v] = (T)pl_delta<DT>(acc[ct][v], scale, scale_t, a.epilogue);
-      *reinterpret_cast<T4*>(drow + ct * 16 + lg * 4) = d;
-    }
+    for (int v = 0; v < 4; ++v) d[v] = (T)pl_delta<DT>(acc[ct][v], scale, scale_t, a.epilogue);
+    *reinterpret_cast<T4*>(drow + ct * 16 + lg * 4) = d;
   }
   __syncthreads();
 
-  // 3. y = T(y + delta) with full-width stores.
-  if (RT != 1) {
-#pragma unroll
-    for (int i = 0; i < kYPer; ++i)
-      if (yptr[i] != nullptr) yv[i] = pl_ld16(yptr[i]);
-  }
+  // y = T(y + delta) with full-width stores
 #pragma unroll
   for (int i = 0; i < kYPer; ++i) {
     if (yptr[i] != nullptr) {
@@ -374,19 +523,31 @@ __global__ __launch_bounds__(256, 4) void pl_expand_tiled(pl_expand_args a) {
   }
 }
 
-template <int DT, int RT>
+template <int DT>
 int launch_shrink(const pl_shrink_args& a, int64_t group_cap, hipStream_t stream) {
-  const int64_t grid = group_cap * a.k_splits * a.n_jobs;
-  if (grid <= 0) return PL_OK;
-  hipLaunchKernelGGL((pl_shrink_tiled<DT, RT>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  if (a.sub == 1) {
+    const int64_t grid = group_cap * a.k_splits * a.rank_passes * a.n_jobs;
+    if (grid <= 0) return PL_OK;
+    hipLaunchKernelGGL((pl_shrink_short<DT>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  } else {
+    const int64_t grid = group_cap * a.k_splits * a.n_jobs;
+    if (grid <= 0) return PL_OK;
+    hipLaunchKernelGGL((pl_shrink_long<DT>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  }
   return pl_launch_status("pl_sgmv_shrink");
 }
 
-template <int DT, int RT>
+template <int DT>
 int launch_expand(const pl_expand_args& a, int64_t group_cap, hipStream_t stream) {
-  const int64_t grid = group_cap * a.n_chunks;
+  const int64_t grid = group_cap * a.n_chunks * a.sub;
   if (grid <= 0) return PL_OK;
-  hipLaunchKernelGGL((pl_expand_tiled<DT, RT>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  if (a.k_splits <= 4)
+    hipLaunchKernelGGL((pl_expand_short<DT, 4>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  else if (a.k_splits <= 8)
+    hipLaunchKernelGGL((pl_expand_short<DT, 8>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((pl_expand_short<DT, kShortMaxPlanes>), dim3((unsigned)grid), dim3(256),
+                       0, stream, a);
   return pl_launch_status("pl_sgmv_expand");
 }
 
@@ -423,9 +584,12 @@ int check_common(int32_t dtype, const void* arena, const pl_slot_entry* table,
   return PL_OK;
 }
 
-// K per wave for a requested split count: a multiple of the wave step.
+// K per wave for a requested split count: a multiple of the wave step.  The
+// short-group expand sums at most kShortMaxPlanes planes, so 16-token groups
+// take at most that many splits.
 int64_t shrink_kw(int32_t dtype, int32_t K, int32_t k_splits, int32_t group_tokens) {
-  const int cc = group_tokens == 16 ? pl_shrink_shape<1>::CC : pl_shrink_shape<4>::CC;
+  const int cc = group_tokens == 16 ? kShortCC : kLongCC;
+  k_splits = k_splits < kShortMaxPlanes ? k_splits : kShortMaxPlanes;
   const int64_t step = (int64_t)cc * 4 * pl_chunk_elems(dtype);
   const int64_t per_split = (K + (int64_t)k_splits - 1) / k_splits;
   const int64_t kw = (per_split + kWaves - 1) / kWaves;
@@ -495,7 +659,9 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
     return PL_ERR_ALIGN;
   }
   const int32_t planes = shrink_planes(dtype, K, k_splits, group_tokens);
-  if (group_cap * planes * n_jobs > 0x7fffffffLL) {
+  const int32_t rank_passes = (ldt + kShortRanks - 1) / kShortRanks;
+  const int32_t sub = group_tokens / 16;
+  if (group_cap * planes * rank_passes * sub * n_jobs > 0x7fffffffLL) {
     pl_set_error("shrink grid too large");
     return PL_ERR_LIMIT;
   }
@@ -521,6 +687,8 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
   a.meta = meta;
   a.ldt = ldt;
   a.k_splits = planes;
+  a.rank_passes = rank_passes;
+  a.sub = sub;
   a.plane = tmp_rows * ldt;
   return PL_OK;
 }
@@ -545,6 +713,10 @@ int prepare_expand(pl_expand_args& a, int32_t dtype, const void* ws, int32_t ldt
     pl_set_error("bad expand sizes N=%d ldy=%lld planes=%d", N, (long long)ldy, planes);
     return PL_ERR_ARG;
   }
+  if (planes > kShortMaxPlanes) {
+    pl_set_error("the expand sums at most %d shrink planes (got %d)", kShortMaxPlanes, planes);
+    return PL_ERR_ARG;
+  }
   if (epilogue != PL_EPI_FALLBACK && epilogue != PL_EPI_TRITON) {
     pl_set_error("bad epilogue mode %d", epilogue);
     return PL_ERR_ARG;
@@ -555,7 +727,7 @@ int prepare_expand(pl_expand_args& a, int32_t dtype, const void* ws, int32_t ldt
   }
   const int chunk = 4 * (dtype == PL_F32 ? 32 : 64);
   const int64_t n_chunks = (N + chunk - 1) / chunk;
-  if (group_cap * n_chunks > 0x7fffffffLL) {
+  if (group_cap * n_chunks * (group_tokens / 16) > 0x7fffffffLL) {
     pl_set_error("expand grid too large");
     return PL_ERR_LIMIT;
   }
@@ -575,39 +747,24 @@ int prepare_expand(pl_expand_args& a, int32_t dtype, const void* ws, int32_t ldt
   a.N = N;
   a.n_chunks = (int32_t)n_chunks;
   a.epilogue = epilogue;
+  a.sub = group_tokens / 16;
   return PL_OK;
 }
 
-template <int RT>
-int dispatch_shrink_rt(int32_t dtype, const pl_shrink_args& a, int64_t group_cap,
-                       hipStream_t s) {
+int dispatch_shrink(int32_t dtype, const pl_shrink_args& a, int64_t group_cap, hipStream_t s) {
   switch (dtype) {
-    case PL_BF16: return launch_shrink<PL_BF16, RT>(a, group_cap, s);
-    case PL_F16: return launch_shrink<PL_F16, RT>(a, group_cap, s);
-    default: return launch_shrink<PL_F32, RT>(a, group_cap, s);
+    case PL_BF16: return launch_shrink<PL_BF16>(a, group_cap, s);
+    case PL_F16: return launch_shrink<PL_F16>(a, group_cap, s);
+    default: return launch_shrink<PL_F32>(a, group_cap, s);
   }
 }
 
-template <int RT>
-int dispatch_expand_rt(int32_t dtype, const pl_expand_args& a, int64_t group_cap,
-                       hipStream_t s) {
+int dispatch_expand(int32_t dtype, const pl_expand_args& a, int64_t group_cap, hipStream_t s) {
   switch (dtype) {
-    case PL_BF16: return launch_expand<PL_BF16, RT>(a, group_cap, s);
-    case PL_F16: return launch_expand<PL_F16, RT>(a, group_cap, s);
-    default: return launch_expand<PL_F32, RT>(a, group_cap, s);
+    case PL_BF16: return launch_expand<PL_BF16>(a, group_cap, s);
+    case PL_F16: return launch_expand<PL_F16>(a, group_cap, s);
+    default: return launch_expand<PL_F32>(a, group_cap, s);
   }
-}
-
-int dispatch_shrink(int32_t dtype, int32_t group_tokens, const pl_shrink_args& a,
-                    int64_t group_cap, hipStream_t s) {
-  return group_tokens == 16 ? dispatch_shrink_rt<1>(dtype, a, group_cap, s)
-                            : dispatch_shrink_rt<4>(dtype, a, group_cap, s);
-}
-
-int dispatch_expand(int32_t dtype, int32_t group_tokens, const pl_expand_args& a,
-                    int64_t group_cap, hipStream_t s) {
-  return group_tokens == 16 ? dispatch_expand_rt<1>(dtype, a, group_cap, s)
-                            : dispatch_expand_rt<4>(dtype, a, group_cap, s);
 }
 
 }  // namespace
@@ -651,7 +808,7 @@ extern "C" int pl_sgmv_shrink_stacked(int32_t dtype, const void* x, int64_t ldx,
                           tok, groups, meta, group_cap, group_tokens, ws_bytes, ldt, tmp_rows,
                           k_splits);
   if (st) return st;
-  return dispatch_shrink(dtype, group_tokens, a, group_cap, reinterpret_cast<hipStream_t>(stream));
+  return dispatch_shrink(dtype, a, group_cap, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int pl_sgmv_expand(int32_t dtype, const void* ws, int32_t ldt, int64_t tmp_rows,
@@ -664,7 +821,7 @@ extern "C" int pl_sgmv_expand(int32_t dtype, const void* ws, int32_t ldt, int64_
   int st = prepare_expand(a, dtype, ws, ldt, tmp_rows, planes, arena, table, num_modules, module,
                           tok, groups, meta, group_cap, group_tokens, y, ldy, N, epilogue);
   if (st) return st;
-  return dispatch_expand(dtype, group_tokens, a, group_cap, reinterpret_cast<hipStream_t>(stream));
+  return dispatch_expand(dtype, a, group_cap, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
@@ -683,7 +840,7 @@ extern "C" int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t 
                       module, tok, groups, meta, group_cap, group_tokens, y, ldy, N, epilogue);
   if (st) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  st = dispatch_shrink(dtype, group_tokens, sa, group_cap, s);
+  st = dispatch_shrink(dtype, sa, group_cap, s);
   if (st) return st;
-  return dispatch_expand(dtype, group_tokens, ea, group_cap, s);
+  return dispatch_expand(dtype, ea, group_cap, s);
 }

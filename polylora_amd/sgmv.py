@@ -41,13 +41,19 @@ def _i32(t: torch.Tensor) -> torch.Tensor:
     return t.to(torch.int32).contiguous()
 
 
-def choose_group_tokens(tokens: int, distinct_slots: int | None) -> int:
-    """Plan group size: 16-token groups when adapter segments average at most 32 tokens (decode).
+_LONG_GROUP_MIN_TOKENS = 8192
 
-    Short groups let the kernels keep one 16-row tile per workgroup; long
-    segments use 64-token groups so each adapter's weights are read once per
-    64 tokens.
+
+def choose_group_tokens(tokens: int, distinct_slots: int | None) -> int:
+    """Plan group size: 64-token groups only for large batches of long adapter segments.
+
+    16-token groups give one workgroup per 16-row tile, the most parallel
+    launch; 64-token groups let the shrink read each adapter's A once per 64
+    tokens, which pays once a batch has enough tokens (prefill) to fill the
+    GPU with 64-token groups anyway.
     """
+    if tokens < _LONG_GROUP_MIN_TOKENS:
+        return _native.PL_GROUP_TOKENS_SHORT
     if distinct_slots is not None and tokens <= 32 * max(1, distinct_slots):
         return _native.PL_GROUP_TOKENS_SHORT
     return _native.PL_GROUP_TOKENS_LONG

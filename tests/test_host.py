@@ -350,11 +350,16 @@ def test_library_host_side_errors_without_gpu():
     assert lib.pl_plan_group_capacity(256, 1, 65, 64) == 4 + 64
     assert lib.pl_plan_group_capacity(256, 1, 65, 16) == 16 + 64
     assert lib.pl_plan_group_capacity(32, 1024, 9, 64) == 512 + 8
-    # split planes: whole block steps (bf16: 256 elements with 64-token groups,
-    # 512 with 16-token groups), at most the requested count
+    # split planes: whole wave steps (16-token groups: 256 elements of a
+    # 2-byte type per wave, 128 of fp32; 64-token groups: 64 and 32), four
+    # waves per split, at most the requested count and at most 16
     assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 8, 64) == 8
     assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 100, 64) == 16
-    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 100, 16) == 8
+    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 100, 16) == 4
+    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 2, 16) == 2
+    assert lib.pl_shrink_planes(_native.PL_BF16, 14336, 100, 16) == 14
+    assert lib.pl_shrink_planes(_native.PL_BF16, 65536, 100, 16) == 16
+    assert lib.pl_shrink_planes(_native.PL_F32, 4096, 100, 16) == 8
     assert lib.pl_shrink_planes(_native.PL_BF16, 14336, 16, 64) == 14
     assert lib.pl_shrink_planes(_native.PL_F32, 768, 4, 64) == 3
     assert lib.pl_shrink_planes(_native.PL_BF16, 32, 1, 16) == 1
@@ -378,3 +383,16 @@ def test_no_cpu_fallback_in_product_ops():
     x = torch.randn(2, 3, 4)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         sgmv.sgmv_lora_a_fwd(x, torch.randn(2, 4, 2), torch.tensor([3, 3]), torch.tensor([0, 1]), torch.tensor([0, 2]))
+
+
+def test_group_size_choice():
+    from polylora_amd import sgmv
+
+    short, long_ = _native.PL_GROUP_TOKENS_SHORT, _native.PL_GROUP_TOKENS_LONG
+    assert sgmv.choose_group_tokens(256, 47) == short  # decode: a few rows per adapter
+    assert sgmv.choose_group_tokens(4096, 16) == short  # below the long-group batch size
+    assert sgmv.choose_group_tokens(32 * 1024, 8) == long_  # prefill: long segments
+    assert sgmv.choose_group_tokens(32 * 1024, None) == long_
+    assert sgmv.choose_group_tokens(32 * 1024, 2048) == short  # many adapters, short segments
+    assert sgmv.choose_k_splits(80, 4096, torch.bfloat16) == 4
+    assert sgmv.choose_k_splits(4096, 4096, torch.bfloat16) == 1  # groups alone fill the GPU

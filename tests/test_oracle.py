@@ -308,6 +308,12 @@ def test_check_plan_accepts_valid_and_rejects_planted():
     bad_meta[1] += 1
     with pytest.raises(AssertionError):
         plan.check_plan(tok, groups, bad_meta, row_slot, seq_lens, 70, 7)
+    # capacity past the last group holds empty records
+    padded = np.concatenate([groups, np.zeros((3, 4), dtype=groups.dtype)])
+    plan.check_plan(tok, padded, meta, row_slot, seq_lens, 70, 7)
+    padded[-1] = (1, 0, 1, 0)  # a stale record past the end
+    with pytest.raises(AssertionError):
+        plan.check_plan(tok, padded, meta, row_slot, seq_lens, 70, 7)
 
 
 # --------------------------------------------------------------------------- slot bookkeeping
