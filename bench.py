@@ -377,6 +377,45 @@ class SgmvLaunch:
         self.n.check(self.lib.pl_sgmv_expand(*self.expand_args), "pl_sgmv_expand")
 
 
+class StackedLaunch:
+    """One shrink launch for sibling Linears fed the same x (pl_sgmv_shrink_stacked) and their expands."""
+
+    def __init__(self, x, ys, cache, modules, plan, k_splits=None):
+        import ctypes
+
+        from polylora_amd import _native, sgmv
+
+        self.lib, self.n = _native.load(), _native
+        self.stream = torch.cuda.current_stream()
+        dt = _native.dtype_code(x.dtype)
+        K = int(x.shape[1])
+        splits = k_splits if k_splits is not None else sgmv.choose_k_splits(plan.group_cap, K, x.dtype)
+        rows = max(1, plan.tokens_cap)
+        ldt = cache.rank8_cap
+        gt = plan.group_tokens
+        nbytes = int(self.lib.pl_shrink_workspace_bytes(dt, K, splits, gt, rows, ldt))
+        planes = int(self.lib.pl_shrink_planes(dt, K, splits, gt))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=x.device) for _ in modules]
+        n_mod = len(cache.module_index)
+        s = self.stream.cuda_stream
+        self.mods = (ctypes.c_int32 * len(modules))(*(cache.module_index[m] for m in modules))
+        self.ptrs = (ctypes.c_void_p * len(modules))(*(b.data_ptr() for b in bufs))
+        self.shrink_args = (dt, x.data_ptr(), x.stride(0), K, cache.arena.data_ptr(), cache.table.data_ptr(), n_mod,
+                            len(modules), self.mods, self.ptrs, plan.tok.data_ptr(), plan.groups.data_ptr(),
+                            plan.meta.data_ptr(), max(1, plan.group_cap), gt, nbytes, ldt, rows, splits, s)
+        self.expand_args = [(dt, b.data_ptr(), ldt, rows, planes, cache.arena.data_ptr(), cache.table.data_ptr(), n_mod,
+                             cache.module_index[m], plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(),
+                             max(1, plan.group_cap), gt, y.data_ptr(), y.stride(0), int(y.shape[1]),
+                             _native.PL_EPI_FALLBACK, s) for b, y, m in zip(bufs, ys, modules)]
+        self.keep = (x, ys, bufs, plan)
+
+    def shrink(self):
+        self.n.check(self.lib.pl_sgmv_shrink_stacked(*self.shrink_args), "pl_sgmv_shrink_stacked")
+
+    def expands(self):
+        return [lambda a=a: self.n.check(self.lib.pl_sgmv_expand(*a), "pl_sgmv_expand") for a in self.expand_args]
+
+
 def time_launches(fns: list, reps: int, warmup: int = 2) -> float:
     """Milliseconds per pass over `fns`, launched back to back on the current stream between two events."""
     stream = torch.cuda.current_stream()
@@ -596,17 +635,30 @@ def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Te
     xs = {k: torch.randn(T, k, generator=gen, device=device, dtype=torch.bfloat16) for k, _ in shapes}
     ys = {n: torch.randn(T, n, generator=gen, device=device, dtype=torch.bfloat16) for _, n in shapes}
     launches = [SgmvLaunch(xs[s.in_features], ys[s.out_features], cache, s.name, plan) for s in pm.module_specs]
-    pairs = [f for l in launches for f in (l.shrink, l.expand)]
-    total_ms = time_launches(pairs, reps)
-    sh_ms = time_launches([l.shrink for l in launches], reps)
-    ex_ms = time_launches([l.expand for l in launches], reps)
     per_type = {}
     for key in sorted({s.name.rsplit(".", 1)[-1] for s in pm.module_specs}):
         sel = [l for l, s in zip(launches, pm.module_specs) if s.name.rsplit(".", 1)[-1] == key]
         per_type[key] = [round(1e3 * time_launches([l.shrink for l in sel], reps) / len(sel), 2),
                          round(1e3 * time_launches([l.expand for l in sel], reps) / len(sel), 2)]
+    # The forward's own launch sequence: sibling Linears that read the same
+    # input (q/k/v, gate/up) share one stacked shrink, as MultiLoraLinear
+    # does once it has seen a forward; every Linear has its own expand.
+    by_name = {s.name: s for s in pm.module_specs}
+    stacks = []
+    for s in pm.module_specs:
+        parent, leaf = s.name.rsplit(".", 1)
+        if leaf in ("k_proj", "v_proj", "up_proj"):
+            continue
+        group = {"q_proj": ("q_proj", "k_proj", "v_proj"), "gate_proj": ("gate_proj", "up_proj")}.get(leaf, (leaf,))
+        names = [f"{parent}.{g}" for g in group if f"{parent}.{g}" in by_name]
+        k = by_name[names[0]].in_features
+        stacks.append(StackedLaunch(xs[k], [ys[by_name[n].out_features] for n in names], cache, names, plan))
+    seq = [f for st in stacks for f in (st.shrink, *st.expands())]
+    total_ms = time_launches(seq, reps)
+    sh_ms = time_launches([st.shrink for st in stacks], reps)
+    ex_ms = time_launches([f for st in stacks for f in st.expands()], reps)
     return {"pairs_ms": total_ms, "shrink_ms": sh_ms, "expand_ms": ex_ms, "per_type_us": per_type,
-            "group_tokens": plan.group_tokens}
+            "group_tokens": plan.group_tokens, "launches": len(seq)}
 
 
 def _graph_ms(fn, reps: int) -> float:
@@ -677,6 +729,9 @@ def run_decode(args) -> dict:
         out["lora_kernels_shrink_ms"] = round(kt["shrink_ms"], 4)
         out["lora_kernels_expand_ms"] = round(kt["expand_ms"], 4)
         out["per_op_us_shrink_expand"] = kt["per_type_us"]
+        out["lora_kernel_launches_per_step"] = kt["launches"]
+        out["lora_kernels_timing"] = ("the forward's launch sequence (stacked q/k/v and gate/up shrinks, one expand "
+                                      "per Linear) back to back without the base model")
         _log(f"decode: kernels {out['lora_kernels_gbs']} GB/s")
         e_base = _eager_ms(base_step, args.decode_steps)
         e_lora = _eager_ms(lora_step, args.decode_steps)
