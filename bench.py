@@ -661,6 +661,61 @@ def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Te
             "group_tokens": plan.group_tokens, "launches": len(seq)}
 
 
+def cpu_baseline_decode_layer(pm, adapter_ids: list, budget_s: float) -> dict:
+    """The reference fallback (oracle restatement of layers.py:112-134) for one decoder layer's 7 LoRA ops.
+
+    Same adapters, slots and row -> slot map as the GPU step; x and the base
+    outputs are random bf16 of the decode shapes ([256, 1, in] and
+    [256, 1, out]).  A full 8B forward on the host is out of reach, so the
+    LoRA ops of one layer are timed and the per-step figure scales them by
+    the layer count.
+    """
+    from oracle.lora import dense_slot_tensors, reference_forward
+
+    cache = pm.adapter_cache
+    base_id = pm.config.base_adapter_id
+    rows = len(adapter_ids)
+    widx = torch.tensor([0 if a == base_id else cache.adapter_to_slot[a] for a in adapter_ids])
+    seq = torch.ones(rows, dtype=torch.int32)
+    layer0 = [s for s in pm.module_specs if ".0." in f".{s.name}."][:7]
+    gen = torch.Generator().manual_seed(1003)
+    ops = []
+    for spec in layer0:
+        per_slot = [None] * cache.num_slots
+        for slot, aid in enumerate(cache.slot_to_adapter):
+            if slot == 0 or aid is None:
+                continue
+            w = pm.adapter_store.adapters[aid].layers.get(spec.name)
+            if w is not None:  # stored A [in, r], B [r, out] -> PEFT lora_A [r, in], lora_B [out, r], alpha
+                per_slot[slot] = (w.A.t(), w.B.t(), float(w.scale) * int(w.rank))
+        A, B, ranks, scales = dense_slot_tensors(per_slot, spec.in_features, spec.out_features,
+                                                 pm.config.max_rank, torch.bfloat16)
+        x = torch.randn(rows, 1, spec.in_features, generator=gen).to(torch.bfloat16)
+        base = torch.randn(rows, 1, spec.out_features, generator=gen).to(torch.bfloat16)
+        ops.append((x, base, A, B, ranks, scales))
+    threads = torch.get_num_threads()
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        for x, base, A, B, ranks, scales in ops:
+            reference_forward(x, base, seq, widx, A, B, ranks, scales)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 20:
+            break
+    per_layer = el / reps
+    layers = pm.base_model.config.num_hidden_layers
+    return {
+        "value": round(rows / (per_layer * layers), 3),
+        "unit": "tokens/s (LoRA ops only)",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{reps} passes over one layer's 7 LoRA ops (256 rows, {int((widx > 0).sum())} with an adapter) "
+                  f"of the fallback loop, {per_layer * 1e3:.1f} ms each, scaled by {layers} layers; "
+                  f"torch {threads} threads, {platform.processor() or platform.machine()}",
+    }
+
+
 def _graph_ms(fn, reps: int) -> float:
     """Capture fn() in a HIP graph (after eager warm-up) and time replays."""
     s = torch.cuda.Stream()
@@ -732,6 +787,8 @@ def run_decode(args) -> dict:
         out["lora_kernel_launches_per_step"] = kt["launches"]
         out["lora_kernels_timing"] = ("the forward's launch sequence (stacked q/k/v and gate/up shrinks, one expand "
                                       "per Linear) back to back without the base model")
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline_decode_layer(pm, wl.adapter_ids, args.cpu_seconds)
         _log(f"decode: kernels {out['lora_kernels_gbs']} GB/s")
         e_base = _eager_ms(base_step, args.decode_steps)
         e_lora = _eager_ms(lora_step, args.decode_steps)
@@ -835,16 +892,21 @@ def run_prefill(args, pm) -> dict:
 def run_churn(args) -> dict:
     """Adapter churn: 1024 rank-16 adapters on all 7 targets, 32 GPU slots, batch 128, Zipf(0.9) ids.
 
-    Each step's rows are split, in row order, into sub-batches of at most 32
-    distinct adapters (the reference raises beyond its slot count,
-    cache.py:65-66).  Every sub-batch is one forward of one new token per row
-    (no KV cache), preceded by the loads its adapters need; loads go to the
-    side stream and overlap the previous sub-batch's compute.  The catalog
+    Each step's rows are split, in row order, into sub-batches of at most
+    `--churn-sub-distinct` distinct adapters (default 32, the slot count; the
+    reference raises beyond it, cache.py:65-66).  Every sub-batch is one
+    forward of one new token per row (empty KV cache), preceded by the loads
+    its adapters need.  Loads go to the side stream and a slot is rewritten
+    only after the forwards that read it; the host never waits for the GPU,
+    so it queues the next sub-batch's loads and forward while the device is
+    still copying and computing.  The catalog
     aliases 64 distinct random weight images (adapter i uses image i % 64) so
     that the pinned host catalog is 5.4 GB instead of 86 GB; every load still
     copies the full 84 MB image.  Compared with the same rows restricted to 32
     resident adapters (no loads).
     """
+    from transformers import DynamicCache
+
     from polylora_amd import PolyLoraConfig, PolyLoraModel
     from polylora_amd.store import CpuAdapter
 
@@ -864,12 +926,15 @@ def run_churn(args) -> dict:
     w = 1.0 / np.arange(1, 1025) ** 0.9
     w /= w.sum()
     B = 128
-    steps = [[catalog[int(i)] for i in rng.choice(1024, size=B, p=w)] for _ in range(args.churn_steps)]
+    draws = [rng.choice(1024, size=B, p=w) for _ in range(args.churn_steps + 2)]
+    steps = [[catalog[int(i)] for i in d] for d in draws]
+
+    limit = args.churn_sub_distinct
 
     def sub_batches(ids):
         out, cur, seen = [], [], set()
         for a in ids:
-            if a not in seen and len(seen) == 32:
+            if a not in seen and len(seen) == limit:
                 out.append(cur)
                 cur, seen = [], set()
             cur.append(a)
@@ -877,32 +942,49 @@ def run_churn(args) -> dict:
         out.append(cur)
         return out
 
+    hot = catalog[:32]
+
+    def resident(sub):
+        """The same sub-batch with its distinct adapters renamed to resident ones (no loads)."""
+        names = {}
+        for a in sub:
+            if a not in names:
+                names[a] = hot[len(names)]
+        return [names[a] for a in sub]
+
     vocab = pm.base_model.config.vocab_size
     gen = torch.Generator(device=device).manual_seed(1005)
 
-    def run(all_steps):
+    def run(batches):
         n_tok = 0
         loads0 = pm.adapter_cache.loads
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         with torch.inference_mode():
-            for ids in all_steps:
-                for sub in sub_batches(ids):
-                    x = torch.randint(0, vocab, (len(sub), 1), generator=gen, device=device)
-                    pm(input_ids=x, adapter_ids=sub, use_cache=False)
-                    n_tok += len(sub)
+            for sub in batches:
+                x = torch.randint(0, vocab, (len(sub), 1), generator=gen, device=device)
+                # a (fresh) KV cache, as in decoding; without one, transformers
+                # checks position_ids for packed sequences, which waits for the
+                # GPU every forward
+                pm(input_ids=x, adapter_ids=sub, past_key_values=DynamicCache(config=pm.base_model.config),
+                   use_cache=True)
+                n_tok += len(sub)
         torch.cuda.synchronize()
         return time.perf_counter() - t0, n_tok, pm.adapter_cache.loads - loads0
 
     # pack every image once and touch the pinned copies before timing
     for n in range(64):
         pm.adapter_cache._packed(store.adapters[catalog[n]])
-    run(steps[:2])
-    churn_s, n_tok, loads = run(steps)
-    hot = catalog[:32]
-    hot_steps = [[hot[int(i) % 32] for i in rng.choice(1024, size=B, p=w)] for _ in range(args.churn_steps)]
+    churn_batches = [sub for ids in steps[2:] for sub in sub_batches(ids)]
+    run([sub for ids in steps[:2] for sub in sub_batches(ids)])
+    churn_s, n_tok, loads = run(churn_batches)
+    # compute alone: the same sub-batches, every adapter resident
+    run([resident(sub) for ids in steps[:2] for sub in sub_batches(ids)])
+    comp_s, _, comp_loads = run([resident(sub) for sub in churn_batches])
+    # the all-resident hot set: the same rows with ids folded onto 32 adapters, whole 128-row steps
+    hot_steps = [[hot[int(i) % 32] for i in d] for d in draws]
     run(hot_steps[:2])
-    hot_s, hot_tok, hot_loads = run(hot_steps)
+    hot_s, hot_tok, hot_loads = run(hot_steps[2:])
     image_bytes = int(pm.adapter_cache._packed(store.adapters[catalog[0]]).image.numel())
     # pinned host -> device bandwidth of one adapter image
     img = pm.adapter_cache._packed(store.adapters[catalog[0]]).image
@@ -916,15 +998,19 @@ def run_churn(args) -> dict:
     torch.cuda.synchronize()
     h2d_gbs = 10 * image_bytes / (time.perf_counter() - t0) / 1e9
     copy_s = loads * image_bytes / (h2d_gbs * 1e9)
-    overlap = (copy_s + hot_s - churn_s) / max(1e-9, min(copy_s, hot_s))
+    overlap = (copy_s + comp_s - churn_s) / max(1e-9, min(copy_s, comp_s))
     out = {"steps": args.churn_steps, "batch": B, "slots": 32, "catalog": 1024, "distinct_images": 64,
-           "slot_loads": loads, "loads_per_step": round(loads / args.churn_steps, 1), "adapter_image_bytes": image_bytes,
-           "h2d_bytes_per_step": round(loads * image_bytes / args.churn_steps), "pinned_h2d_gbs": round(h2d_gbs, 1),
+           "sub_batch_max_distinct": limit, "sub_batches": len(churn_batches), "slot_loads": loads, "loads_per_step": round(loads / args.churn_steps, 1),
+           "adapter_image_bytes": image_bytes, "h2d_bytes_per_step": round(loads * image_bytes / args.churn_steps),
+           "pinned_h2d_gbs": round(h2d_gbs, 1),
            "tokens_per_s_churn": round(n_tok / churn_s, 1), "tokens_per_s_hot_set": round(hot_tok / hot_s, 1),
            "ratio_churn_to_hot": round(hot_s / churn_s * n_tok / hot_tok, 4),
-           "copy_s_at_measured_h2d": round(copy_s, 3), "compute_s_hot": round(hot_s, 3), "wall_s_churn": round(churn_s, 3),
+           "wall_s_churn": round(churn_s, 3), "copy_s_at_measured_h2d": round(copy_s, 3),
+           "compute_s_same_sub_batches_resident": round(comp_s, 3), "resident_run_loads": comp_loads,
            "overlap_efficiency": round(overlap, 3), "hot_set_loads": hot_loads,
-           "timing": "eager wall clock; one new token per row, no KV cache"}
+           "overlap_definition": "(copy + compute - wall) / min(copy, compute); compute = the same sub-batches "
+                                 "with every adapter resident",
+           "timing": "eager wall clock; one new token per row on an empty KV cache"}
     _log(f"churn: {out['tokens_per_s_churn']} tok/s vs hot {out['tokens_per_s_hot_set']}, overlap {out['overlap_efficiency']}")
     del pm, model
     torch.cuda.empty_cache()
@@ -946,6 +1032,8 @@ def main(argv=None) -> int:
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-churn", action="store_true")
     p.add_argument("--churn-steps", type=int, default=10, help="decode steps of the churn workload (200 in the full config)")
+    p.add_argument("--churn-sub-distinct", type=int, default=32, choices=range(1, 33), metavar="1..32",
+                   help="most distinct adapters per churn sub-batch (the cache has 32 slots)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                    help="only copy a BYTES-sized device buffer 5 times (calibrates HBM byte counters) and exit")
     args = p.parse_args(argv)
