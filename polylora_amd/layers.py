@@ -34,10 +34,9 @@ OVERLAP_MIN_TOKENS = 2048
 
 def _version_of(x: torch.Tensor):
     """In-place modification counter of x, or None for inference tensors (they keep none)."""
-    try:
-        return x._version
-    except RuntimeError:
+    if x.is_inference():
         return None
+    return x._version
 
 
 class MultiLoraLinear(nn.Module):
@@ -89,17 +88,18 @@ class MultiLoraLinear(nn.Module):
             side = sgmv.side_stream(x.device)
             side.wait_stream(main)  # x is ready, and every earlier expand has read the side workspaces
             with torch.cuda.stream(side):
-                shrunk = self._shrink(x, x2, plan, lora_ctx)
+                shrunk = self._shrink(x, x2, plan, lora_ctx, side.cuda_stream)
             base = self.base_layer(x)
             main.wait_stream(side)
         else:
-            shrunk = self._shrink(x, x2, plan, lora_ctx)
+            shrunk = self._shrink(x, x2, plan, lora_ctx, main.cuda_stream)
             base = self.base_layer(x)
         base_3d = reshape(base)
-        sgmv.lora_expand(shrunk, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name)
+        sgmv.lora_expand(shrunk, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name,
+                         stream=main.cuda_stream)
         return base_3d.reshape(base.shape)
 
-    def _shrink(self, x: torch.Tensor, x2: torch.Tensor, plan, lora_ctx: LoraBatchContext):
+    def _shrink(self, x: torch.Tensor, x2: torch.Tensor, plan, lora_ctx: LoraBatchContext, stream: int):
         """This module's shrink result: computed ahead by a sibling, stacked with siblings, or alone.
 
         Siblings are wrapped Linears that the model calls back to back on the
@@ -114,33 +114,34 @@ class MultiLoraLinear(nn.Module):
         stack = lora_ctx.stack
         shared = stack.setdefault("shared", {})
         hit = shared.pop(self.module_name, None)
-        self._observe_call(x, stack)
+        version = _version_of(x)
+        self._observe_call(x, version, stack)
         if hit is not None:
-            hx, version, res = hit
-            if hx is x and version == _version_of(x) and res.plan is plan and res.valid:
+            hx, hversion, res = hit
+            if hx is x and hversion == version and res.plan is plan and res.valid:
                 return res
         run = self.cache.stacked_runs.get((self.module_name, tuple(x.shape)))
         if run is not None and len(run) > 1:
-            results = sgmv.lora_shrink_stacked(x2, self.cache, list(run), plan)
+            results = sgmv.lora_shrink_stacked(x2, self.cache, list(run), plan, stream=stream)
             for name, res in zip(run[1:], results[1:]):
-                shared[name] = (x, _version_of(x), res)
+                shared[name] = (x, version, res)
             return results[0]
-        return sgmv.lora_shrink(x2, self.cache, self.module_name, plan)
+        return sgmv.lora_shrink(x2, self.cache, self.module_name, plan, stream=stream)
 
-    def _observe_call(self, x: torch.Tensor, stack: dict) -> None:
+    def _observe_call(self, x: torch.Tensor, version, stack: dict) -> None:
         """Extend the current run of calls on one input tensor, recording it as a sibling set."""
         run = stack.get("run")
         if (
             run is not None
             and stack.get("run_x") is x
-            and stack.get("run_version") == _version_of(x)
+            and stack.get("run_version") == version
             and self.module_name not in run
             and len(run) < sgmv.MAX_STACKED_MODULES
         ):
             run.append(self.module_name)
             self.cache.stacked_runs[(run[0], tuple(x.shape))] = tuple(run)
         else:
-            stack["run"], stack["run_x"], stack["run_version"] = [self.module_name], x, _version_of(x)
+            stack["run"], stack["run_x"], stack["run_version"] = [self.module_name], x, version
 
     def _plan(self, lora_ctx: LoraBatchContext, rows: int, row_len: int, seq_lens, weight_indices):
         key = (rows, row_len)

@@ -229,10 +229,9 @@ def lora_apply(
     N = int(y.shape[1])
     ldt = cache.rank8_cap
     stream = _stream(x.device)
-    splits = k_splits if k_splits is not None else choose_k_splits(plan.group_cap, K, x.dtype)
     rows = max(1, plan.tokens_cap)
     group_cap = max(1, plan.group_cap)
-    nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, plan.group_tokens, rows, ldt))
+    splits, _, nbytes = _shrink_geometry(lib, dt, K, x.dtype, plan, rows, ldt, k_splits)
     ws = _workspace(x.device, stream)
     buf = ws.get(nbytes)
     ws.owner = None  # planes of an earlier separate shrink on this workspace are gone
@@ -310,16 +309,34 @@ def tiled_shapes_ok(x: torch.Tensor, out_features: int) -> bool:
     )
 
 
-def lora_shrink(x: torch.Tensor, cache, module_name: str, plan: SgmvPlan, *, k_splits: int | None = None) -> ShrinkResult:
+_GEOMETRY: dict[tuple, tuple[int, int, int]] = {}
+
+
+def _shrink_geometry(lib, dt: int, K: int, dtype: torch.dtype, plan: SgmvPlan, rows: int, ldt: int,
+                     k_splits: int | None) -> tuple[int, int, int]:
+    """(k_splits, planes, workspace bytes) of a shrink, computed once per shape."""
+    key = (dt, K, plan.group_cap, plan.group_tokens, rows, ldt, k_splits)
+    geo = _GEOMETRY.get(key)
+    if geo is None:
+        splits = k_splits if k_splits is not None else choose_k_splits(plan.group_cap, K, dtype)
+        planes = int(lib.pl_shrink_planes(dt, K, splits, plan.group_tokens))
+        nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, plan.group_tokens, rows, ldt))
+        geo = _GEOMETRY[key] = (splits, planes, nbytes)
+    return geo
+
+
+def lora_shrink(x: torch.Tensor, cache, module_name: str, plan: SgmvPlan, *, k_splits: int | None = None,
+                stream: int | None = None) -> ShrinkResult:
     """Launch the shrink of one wrapped Linear on the current stream; the expand reads the result later."""
-    return lora_shrink_stacked(x, cache, [module_name], plan, k_splits=k_splits)[0]
+    return lora_shrink_stacked(x, cache, [module_name], plan, k_splits=k_splits, stream=stream)[0]
 
 
 def lora_shrink_stacked(x: torch.Tensor, cache, module_names: list, plan: SgmvPlan, *,
-                        k_splits: int | None = None) -> list:
+                        k_splits: int | None = None, stream: int | None = None) -> list:
     """One shrink launch for wrapped Linears that read the same x (pl_sgmv_shrink_stacked).
 
     Module i's partial sums go to workspace position i of the current stream.
+    `stream` is that stream's handle when the caller already has it.
     """
     _require_gpu(x, "lora_shrink")
     n = len(module_names)
@@ -339,11 +356,10 @@ def lora_shrink_stacked(x: torch.Tensor, cache, module_names: list, plan: SgmvPl
     lib = _native.load()
     dt = _native.dtype_code(x.dtype)
     ldt = cache.rank8_cap
-    stream = _stream(x.device)
-    splits = k_splits if k_splits is not None else choose_k_splits(plan.group_cap, K, x.dtype)
+    if stream is None:
+        stream = _stream(x.device)
     rows = max(1, plan.tokens_cap)
-    planes = int(lib.pl_shrink_planes(dt, K, splits, plan.group_tokens))
-    nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, plan.group_tokens, rows, ldt))
+    splits, planes, nbytes = _shrink_geometry(lib, dt, K, x.dtype, plan, rows, ldt, k_splits)
     wss = [_workspace(x.device, stream, i) for i in range(n)]
     bufs = [ws.get(nbytes) for ws in wss]
     modules = (ctypes.c_int32 * n)(*(cache.module_index[name] for name in module_names))
@@ -360,8 +376,8 @@ def lora_shrink_stacked(x: torch.Tensor, cache, module_names: list, plan: SgmvPl
 
 
 def lora_expand(res: ShrinkResult, y: torch.Tensor, cache, module_name: str, *,
-                epilogue: int = _native.PL_EPI_FALLBACK) -> torch.Tensor:
-    """Launch the expand on the current stream, which must already be ordered after the shrink."""
+                epilogue: int = _native.PL_EPI_FALLBACK, stream: int | None = None) -> torch.Tensor:
+    """Launch the expand on the current stream (handle `stream` if given), ordered after the shrink."""
     _require_gpu(y, "lora_expand")
     spec = cache.module_specs[module_name]
     plan = res.plan
@@ -377,7 +393,7 @@ def lora_expand(res: ShrinkResult, y: torch.Tensor, cache, module_name: str, *,
             _native.dtype_code(y.dtype), res.buf.data_ptr(), res.ldt, res.rows, res.planes, cache.arena.data_ptr(),
             cache.table.data_ptr(), len(cache.module_index), cache.module_index[module_name], plan.tok.data_ptr(),
             plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap), plan.group_tokens, y.data_ptr(),
-            y.stride(0), int(y.shape[1]), epilogue, _stream(y.device),
+            y.stride(0), int(y.shape[1]), epilogue, _stream(y.device) if stream is None else stream,
         ),
         "pl_sgmv_expand",
     )
