@@ -416,6 +416,25 @@ class StackedLaunch:
         return [lambda a=a: self.n.check(self.lib.pl_sgmv_expand(*a), "pl_sgmv_expand") for a in self.expand_args]
 
 
+class FusedLaunch:
+    """One wrapped Linear's fused shrink+expand (pl_lora_fused) with its arguments bound once."""
+
+    def __init__(self, x, y, cache, module, plan, slices=None):
+        from polylora_amd import _native, sgmv
+
+        self.lib, self.n = _native.load(), _native
+        n_slices = slices if slices is not None else sgmv.choose_slices(plan, int(y.shape[1]))
+        self.args = (_native.dtype_code(x.dtype), x.data_ptr(), x.stride(0), int(x.shape[1]), y.data_ptr(),
+                     y.stride(0), int(y.shape[1]), cache.arena.data_ptr(), cache.table.data_ptr(),
+                     len(cache.module_index), cache.module_index[module], cache.rank8_cap, plan.tok.data_ptr(),
+                     plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap), plan.group_tokens, n_slices,
+                     _native.PL_EPI_FALLBACK, torch.cuda.current_stream().cuda_stream)
+        self.keep = (x, y, plan)
+
+    def __call__(self):
+        self.n.check(self.lib.pl_lora_fused(*self.args), "pl_lora_fused")
+
+
 def time_launches(fns: list, reps: int, warmup: int = 2) -> float:
     """Milliseconds per pass over `fns`, launched back to back on the current stream between two events."""
     stream = torch.cuda.current_stream()
@@ -433,13 +452,14 @@ def time_launches(fns: list, reps: int, warmup: int = 2) -> float:
     return t0.elapsed_time(t1) / reps
 
 
-def _profiled_traffic():
-    """HBM bytes per expand launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs, or None."""
+def _profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs, or None."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "sgmv_isolated_traffic.json")
     try:
         with open(path, encoding="utf-8") as fh:
-            return int(json.load(fh)["traffic_bytes_per_launch"])
-    except (OSError, ValueError, KeyError):
+            data = json.load(fh)
+        return int(data["kernels"][kernel]["traffic_bytes_per_launch"])
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
@@ -475,13 +495,21 @@ def run_isolated(args) -> dict:
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
 
-    launches = [SgmvLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets]
     reps = max(10, args.steps // n_sets)
+    # the split shrink + expand, for comparison (and the kernels a plan with
+    # few tokens per adapter would use)
+    launches = [SgmvLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets]
     sh_ms = time_launches([l.shrink for l in launches], reps) / n_sets
     ex_ms = time_launches([l.expand for l in launches], reps) / n_sets
+    fused = sgmv.fused_ok(base_set.plan, base_set.cache, K)
     value = nb["total"] / (ms * 1e-3) / 1e9
-    kern_gbs = nb["total"] / ((sh_ms + ex_ms) * 1e-3) / 1e9
-    exp_gbs = nb["expand"] / (ex_ms * 1e-3) / 1e9
+    if fused:
+        # lora_apply runs the fused kernel: one launch carries all of the op's bytes
+        f_ms = time_launches([FusedLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets], reps) / n_sets
+        kernel, k_bytes, k_ms = "pl_lora_fused_tile<bf16>", nb["total"], f_ms
+    else:
+        kernel, k_bytes, k_ms = "pl_expand_short<bf16>", nb["expand"], ex_ms
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
     out = {
         "value": round(value, 2),
         "ms_per_step": round(ms, 5),
@@ -494,21 +522,21 @@ def run_isolated(args) -> dict:
             "input_sets_rotated": n_sets,
             "timing": "lora_apply calls back to back, device events around the timed steps",
             "plan_group_tokens": base_set.plan.group_tokens,
-            "shrink_ms": round(sh_ms, 5),
-            "expand_ms": round(ex_ms, 5),
-            "shrink_plus_expand_kernel_gbs": round(kern_gbs, 1),
-            "shrink_gbs": round(nb["shrink"] / (sh_ms * 1e-3) / 1e9, 1),
+            "lora_apply_kernels": "pl_lora_fused (one launch)" if fused else "pl_sgmv_shrink + pl_sgmv_expand",
+            "split_shrink_ms": round(sh_ms, 5),
+            "split_expand_ms": round(ex_ms, 5),
+            "split_pair_gbs": round(nb["total"] / ((sh_ms + ex_ms) * 1e-3) / 1e9, 1),
         },
         "roofline": {
-            "kernel": "pl_expand_short<bf16>",
+            "kernel": kernel,
             "bound": "hbm",
-            "achieved": round(exp_gbs, 2),
+            "achieved": round(k_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(exp_gbs / HBM_PEAK_GBS, 4),
-            "traffic": _profiled_traffic(),
-            "algorithmic_bytes_per_launch": nb["expand"],
-            "avg_launch_ms": round(ex_ms, 5),
+            "frac": round(k_gbs / HBM_PEAK_GBS, 4),
+            "traffic": _profiled_traffic(kernel.split("<")[0]),
+            "algorithmic_bytes_per_launch": k_bytes,
+            "avg_launch_ms": round(k_ms, 5),
         },
     }
     if not args.no_cpu_baseline:
@@ -643,22 +671,31 @@ def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Te
     # The forward's own launch sequence: sibling Linears that read the same
     # input (q/k/v, gate/up) share one stacked shrink, as MultiLoraLinear
     # does once it has seen a forward; every Linear has its own expand.
+    # Modules whose plan suits the fused kernel take one pl_lora_fused launch
+    # each (MultiLoraLinear does the same).
     by_name = {s.name: s for s in pm.module_specs}
-    stacks = []
+    stacks, fused, seq = [], [], []
     for s in pm.module_specs:
+        if sgmv.fused_ok(plan, cache, s.in_features):
+            f = FusedLaunch(xs[s.in_features], ys[s.out_features], cache, s.name, plan)
+            fused.append(f)
+            seq.append(f)
+            continue
         parent, leaf = s.name.rsplit(".", 1)
         if leaf in ("k_proj", "v_proj", "up_proj"):
             continue
         group = {"q_proj": ("q_proj", "k_proj", "v_proj"), "gate_proj": ("gate_proj", "up_proj")}.get(leaf, (leaf,))
         names = [f"{parent}.{g}" for g in group if f"{parent}.{g}" in by_name]
         k = by_name[names[0]].in_features
-        stacks.append(StackedLaunch(xs[k], [ys[by_name[n].out_features] for n in names], cache, names, plan))
-    seq = [f for st in stacks for f in (st.shrink, *st.expands())]
+        st = StackedLaunch(xs[k], [ys[by_name[n].out_features] for n in names], cache, names, plan)
+        stacks.append(st)
+        seq.extend((st.shrink, *st.expands()))
     total_ms = time_launches(seq, reps)
-    sh_ms = time_launches([st.shrink for st in stacks], reps)
-    ex_ms = time_launches([f for st in stacks for f in st.expands()], reps)
-    return {"pairs_ms": total_ms, "shrink_ms": sh_ms, "expand_ms": ex_ms, "per_type_us": per_type,
-            "group_tokens": plan.group_tokens, "launches": len(seq)}
+    sh_ms = time_launches([st.shrink for st in stacks], reps) if stacks else 0.0
+    ex_ms = time_launches([f for st in stacks for f in st.expands()], reps) if stacks else 0.0
+    fu_ms = time_launches(fused, reps) if fused else 0.0
+    return {"pairs_ms": total_ms, "shrink_ms": sh_ms, "expand_ms": ex_ms, "fused_ms": fu_ms, "per_type_us": per_type,
+            "group_tokens": plan.group_tokens, "launches": len(seq), "fused_launches": len(fused)}
 
 
 def cpu_baseline_decode_layer(pm, adapter_ids: list, budget_s: float) -> dict:
@@ -871,6 +908,9 @@ def run_prefill(args, pm) -> dict:
         out["lora_kernels_pct_mfma_bf16"] = round(100 * nb["flops"] / (kern_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 3)
         out["lora_kernels_shrink_ms"] = round(kt["shrink_ms"], 3)
         out["lora_kernels_expand_ms"] = round(kt["expand_ms"], 3)
+        out["lora_kernels_fused_ms"] = round(kt["fused_ms"], 3)
+        out["lora_kernel_launches"] = kt["launches"]
+        out["lora_fused_launches"] = kt["fused_launches"]
 
         def base_fwd():
             return pm.base_model(input_ids=ids, use_cache=False).last_hidden_state

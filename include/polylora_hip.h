@@ -20,6 +20,8 @@
  *   pl_sgmv_expand      <- src/polylora/sgmv.py:178-275  _sgmv_lora_b_kernel
  *   pl_lora_apply       <- src/polylora/layers.py:42-53  (shrink then expand,
  *                          the LoRA half of MultiLoraLinear.forward)
+ *   pl_lora_fused       <- src/polylora/sgmv.py:63-138 and :178-275 in one
+ *                          launch (both Triton kernels of layers.py:45-53)
  *   pl_slot_upload      <- src/polylora/cache.py:119-150 _load_adapter_into_slot
  *                          (host->device copy of one adapter into a slot)
  *   pl_check_right_padded <- src/polylora/context.py:37-45 assert_right_padded
@@ -180,6 +182,23 @@ int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
                   const pl_group* groups, const int32_t* meta, int64_t group_cap,
                   int32_t group_tokens, void* ws, int64_t ws_bytes, int32_t ldt,
                   int64_t tmp_rows, int32_t k_splits, int32_t epilogue, void* stream);
+
+/* Fused shrink + expand in one launch for long adapter segments: one
+ * workgroup per (16-token tile of a plan group, column slice) computes
+ * t = T(x·Aᵀ) over all of K and then y[tok[p]][n] = T(y + d) over its
+ * columns, d rounded in the order of `epilogue`.  No workspace.  Takes slot
+ * ranks up to 64 (ldt, the table's rank capacity, must be <= 64), 1..8
+ * column slices per tile (each slice recomputes the tile's shrink; more
+ * slices, more workgroups), the alignment rules of the tiled path, and a
+ * plan of 16- or 64-token groups.  Pays off when groups are full (many
+ * tokens per adapter); for a few tokens per adapter (decode) use
+ * pl_sgmv_shrink + pl_sgmv_expand, which split K and N over many
+ * workgroups. */
+int pl_lora_fused(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y, int64_t ldy,
+                  int32_t N, const void* arena, const pl_slot_entry* table, int32_t num_modules,
+                  int32_t module, int32_t ldt, const int32_t* tok, const pl_group* groups,
+                  const int32_t* meta, int64_t group_cap, int32_t group_tokens, int32_t slices,
+                  int32_t epilogue, void* stream);
 
 /* Row-based LoRA on the slot arena for shapes the tiled path rejects
  * (any K, N, strides, alignment).  Writes y[b*row_len+m] for m < seq_len[b].

@@ -63,6 +63,28 @@ __device__ __forceinline__ pl_u32x4 pl_ld16(const void* p) {
   return *reinterpret_cast<const pl_u32x4*>(p);
 }
 
+// Workgroups go to the GPU's 8 XCDs round-robin by block index, and each XCD
+// has its own L2.  pl_xcd_map gives every work item of one plan group to the
+// same XCD, so the group's rereads (x rows, A and B) hit that XCD's L2, and
+// deals the groups to the XCDs in turn (group g to XCD g % 8), so the live
+// groups, which come first in the plan, spread over all of them.  The grid
+// is 8 * ceil(group_cap / 8) * per_group blocks; a block whose group is past
+// group_cap does nothing.
+constexpr int kXcds = 8;
+struct pl_xcd_slot {
+  int g;  // plan group
+  int j;  // work item within the group, 0 .. per_group-1
+};
+__device__ __forceinline__ pl_xcd_slot pl_xcd_map(int per_group) {
+  const int x = (int)(blockIdx.x % kXcds);
+  const int s = (int)(blockIdx.x / kXcds);
+  const int gq = s / per_group;
+  return {gq * kXcds + x, s - gq * per_group};
+}
+static inline int64_t pl_xcd_grid(int64_t group_cap, int64_t per_group) {
+  return (group_cap + kXcds - 1) / kXcds * kXcds * per_group;
+}
+
 // Sixteen zero bytes in device memory: the source of every masked-off lane.
 static __device__ __attribute__((aligned(16))) uint32_t pl_zero16[4];
 

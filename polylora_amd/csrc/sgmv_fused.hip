@@ -1,0 +1,393 @@
+// Fused shrink + expand for long adapter segments (prefill, large batches of
+// few adapters), gfx950.
+//
+// One workgroup per (16-token tile of a plan group, slice of the output
+// columns).  Its four waves split K and accumulate x·Aᵀ for the tile in
+// 16x16 MFMA tiles (fp32), the four partials are summed in LDS in a fixed
+// order and rounded once to the model dtype (the reference's
+// t = T(x @ A[:, :r]), layers.py:127), and then each wave streams its share
+// of the slice's columns: B rows and y rows for the next 64 columns are in
+// flight while the MFMA, the epilogue (the expand's rounding order) and the
+// 16-byte read-modify-write of y run on the current ones.  The intermediate
+// never leaves the workgroup, so there is one launch per wrapped Linear, no
+// workspace and no split-K partial sums; results are bitwise reproducible.
+//
+// A tile's slices (column ranges) all recompute the same shrink; they run on
+// one XCD (workgroups are dealt to the 8 XCDs round-robin by index), so x and
+// A are fetched from HBM once and reread from that XCD's L2.
+//
+// Ranks up to 64 (4 tiles of 16) are held in registers; the kernel is
+// instantiated for at most 1, 2 or 4 rank tiles and each group runs the
+// narrowest body that covers its slot's rank.
+#include "pl_common.h"
+
+namespace {
+
+constexpr int kFWaves = 4;
+constexpr int kFThreads = 64 * kFWaves;
+constexpr int kFCC = 4;         // 16-byte chunks per lane per shrink step
+constexpr int kFColsMax = 128;  // output columns per wave per expand step (at most)
+constexpr int kFStages = 3;     // expand steps in flight per wave
+constexpr int kFRankMax = 64;   // largest rank the fused kernel takes
+
+// Columns per wave per expand step: as wide as the registers allow for the
+// rank tiles in play (B's rank chunks and y's rows of kFStages steps are
+// held at once).
+template <int DT, int JT>
+constexpr int pl_fused_cols() {
+  return (JT >= 4 || (DT == PL_F32 && JT >= 2)) ? 64 : kFColsMax;
+}
+constexpr int kFSliceMax = 8;   // column slices per tile
+
+struct pl_fused_args {
+  const void* x;
+  int64_t ldx;
+  int32_t K;
+  int32_t kw;  // K per wave, a multiple of the shrink step
+  void* y;
+  int64_t ldy;
+  int32_t N;
+  int32_t nw;  // columns per wave, a multiple of kFColsMax
+  const char* arena;
+  const pl_slot_entry* table;
+  int32_t num_modules;
+  int32_t module;
+  const int32_t* tok;
+  const pl_group* groups;
+  const int32_t* meta;
+  int32_t group_cap;
+  int32_t sub;     // 16-token tiles per plan group (1 or 4)
+  int32_t slices;  // column slices per tile
+  int32_t epilogue;
+};
+
+template <int DT>
+struct pl_fused_lds {
+  typedef typename pl_traits<DT>::T T;
+  enum { kPad = DT == PL_F32 ? 4 : 8 };  // 16 bytes of row padding
+  enum { kTRow = kFRankMax + kPad };     // staged intermediate [token][rank]
+  enum { kDRow = kFColsMax + kPad };     // per-wave delta tile [token][column]
+};
+
+template <int DT, int JT>
+__device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_group& grp, int len,
+                                              const pl_slot_entry& e, int rank, int slice,
+                                              pl_f32x4 (*red)[4][64],
+                                              typename pl_traits<DT>::T* tt,
+                                              typename pl_traits<DT>::T* dbuf) {
+  typedef typename pl_traits<DT>::T T;
+  typedef typename pl_traits<DT>::T4 T4;
+  typedef typename pl_traits<DT>::T8 T8;
+  typedef pl_fused_lds<DT> L;
+  constexpr int E = pl_traits<DT>::E;
+  constexpr int kInstr = 4 * E;              // K covered by one wave load
+  constexpr int kStep = kFCC * kInstr;       // K covered by one shrink step
+  constexpr int kRStep = 4 * E;              // ranks per expand MFMA step
+  constexpr int kRSteps = (16 * JT + kRStep - 1) / kRStep;
+  constexpr int kCols = pl_fused_cols<DT, JT>();
+  constexpr int kCT = kCols / 16;            // 16-column MFMA tiles per expand step
+  constexpr int kYLanes = kCols * (int)sizeof(T) / 16;  // lanes per y row of a step
+  constexpr int kYRows = 64 / kYLanes;       // y rows one wave load covers
+  constexpr int kYLoads = 16 / kYRows;       // loads per lane for the 16 rows
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int K = a.K;
+  const int N = a.N;
+
+  // ---- shrink: t[token][j] = sum_k x[token][k] * A[j][k] over this wave's K quarter
+  const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
+  const T* __restrict__ A = reinterpret_cast<const T*>(a.arena + e.a_off);
+  const bool xok = li < len;
+  const int xt = a.tok[grp.start + min(li, len - 1)];
+  const T* xrow = x + (int64_t)xt * a.ldx + lg * E;
+  const int k0 = wave * a.kw;
+  const int k1 = min(K, k0 + a.kw);
+
+  pl_f32x4 acc[JT];
+#pragma unroll
+  for (int jt = 0; jt < JT; ++jt) acc[jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+  auto load_k = [&](pl_u32x4 (&xf)[kFCC], pl_u32x4 (&af)[JT][kFCC], int kb) {
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) {
+      const int j = jt * 16 + li;
+      const T* arow = A + (int64_t)j * K + lg * E;
+#pragma unroll
+      for (int cc = 0; cc < kFCC; ++cc) {
+        const int k = kb + cc * kInstr;
+        af[jt][cc] = pl_ld16_or0(arow + k, j < rank && k + lg * E < k1);
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < kFCC; ++cc) {
+      const int k = kb + cc * kInstr;
+      xf[cc] = pl_ld16_or0(xrow + k, xok && k + lg * E < k1);
+    }
+  };
+  auto mfma_k = [&](const pl_u32x4 (&xf)[kFCC], const pl_u32x4 (&af)[JT][kFCC]) {
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+      for (int cc = 0; cc < kFCC; ++cc) acc[jt] = pl_mfma_chunk<DT>(xf[cc], af[jt][cc], acc[jt]);
+  };
+  {
+    // double-buffered K loop; steps past k1 load only zeros
+    pl_u32x4 xa[kFCC], aa[JT][kFCC], xb[kFCC], ab[JT][kFCC];
+    load_k(xa, aa, k0);
+    for (int kb = k0; kb < k1; kb += 2 * kStep) {
+      load_k(xb, ab, kb + kStep);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_k(xa, aa);
+      load_k(xa, aa, kb + 2 * kStep);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_k(xb, ab);
+    }
+  }
+  // the four wave partials summed in a fixed order, rounded once to T;
+  // acc[jt][v] holds (token 4*lg+v, rank jt*16+li)
+#pragma unroll
+  for (int jt = 0; jt < JT; ++jt) red[wave][jt][lane] = acc[jt];
+  __syncthreads();
+  if (tid < JT * 64) {
+    const int jt = tid >> 6;
+    const int l = tid & 63;
+    pl_f32x4 s = red[0][jt][l];
+#pragma unroll
+    for (int w = 1; w < kFWaves; ++w) s += red[w][jt][l];
+    const int j = jt * 16 + (l & 15);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tt[((l >> 4) * 4 + v) * L::kTRow + j] = (T)(j < rank ? s[v] : 0.f);
+  }
+  __syncthreads();
+
+  // ---- expand over this wave's columns
+  const int c0 = (slice * kFWaves + wave) * a.nw;
+  const int c1 = min(N, c0 + a.nw);
+  const int r8 = e.rank8;
+  const float scale = e.scale;
+  const float scale_t = pl_round<DT>(scale);
+  const T* __restrict__ Bc = reinterpret_cast<const T*>(a.arena + e.b_off);
+  T* __restrict__ y = reinterpret_cast<T*>(a.y);
+  T* __restrict__ dw = dbuf + wave * 16 * L::kDRow;
+
+  pl_u32x4 tf[kRSteps];  // MFMA operand: (token li, ranks s*kRStep + lg*E ..)
+#pragma unroll
+  for (int s = 0; s < kRSteps; ++s)
+    tf[s] = *reinterpret_cast<const pl_u32x4*>(tt + li * L::kTRow + s * kRStep + lg * E);
+
+  const int yq = lane % kYLanes;
+  const int yr0 = lane / kYLanes;
+  T* yrow[kYLoads];
+  bool yok[kYLoads];
+#pragma unroll
+  for (int i = 0; i < kYLoads; ++i) {
+    const int r = yr0 + kYRows * i;
+    yok[i] = r < len;
+    yrow[i] = y + (int64_t)a.tok[grp.start + min(r, len - 1)] * a.ldy + yq * E;
+  }
+
+  auto load_n = [&](pl_u32x4 (&bf)[kRSteps][kCT], pl_u32x4 (&yv)[kYLoads], int cb) {
+#pragma unroll
+    for (int s = 0; s < kRSteps; ++s) {
+      const int jl = s * kRStep + lg * E;
+#pragma unroll
+      for (int ct = 0; ct < kCT; ++ct) {
+        const int n = cb + ct * 16 + li;
+        bf[s][ct] = pl_ld16_or0(Bc + (int64_t)n * r8 + jl, n < c1 && jl < r8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kYLoads; ++i) yv[i] = pl_ld16_or0(yrow[i] + cb, yok[i] && cb + yq * E < c1);
+  };
+  auto apply_n = [&](const pl_u32x4 (&bf)[kRSteps][kCT], const pl_u32x4 (&yv)[kYLoads], int cb) {
+    pl_f32x4 d[kCT];
+#pragma unroll
+    for (int ct = 0; ct < kCT; ++ct) d[ct] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kRSteps; ++s)
+#pragma unroll
+      for (int ct = 0; ct < kCT; ++ct) d[ct] = pl_mfma_chunk<DT>(bf[s][ct], tf[s], d[ct]);
+    // d[ct][v] = delta(column cb + ct*16 + 4*lg + v, token li): scale and round,
+    // then through this wave's LDS tile to the row-major layout of y
+#pragma unroll
+    for (int ct = 0; ct < kCT; ++ct) {
+      T4 dd;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dd[v] = (T)pl_delta<DT>(d[ct][v], scale, scale_t, a.epilogue);
+      *reinterpret_cast<T4*>(dw + li * L::kDRow + ct * 16 + lg * 4) = dd;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+    for (int i = 0; i < kYLoads; ++i) {
+      const int r = yr0 + kYRows * i;
+      const pl_u32x4 dv = *reinterpret_cast<const pl_u32x4*>(dw + r * L::kDRow + yq * E);
+      if (yok[i] && cb + yq * E < c1) {
+        if constexpr (E == 8) {
+          T8 yy = __builtin_bit_cast(T8, yv[i]);
+          const T8 dd = __builtin_bit_cast(T8, dv);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) yy[q] = (T)((float)yy[q] + (float)dd[q]);
+          *reinterpret_cast<pl_u32x4*>(yrow[i] + cb) = __builtin_bit_cast(pl_u32x4, yy);
+        } else {
+          pl_f32x4 yy = __builtin_bit_cast(pl_f32x4, yv[i]);
+          yy += __builtin_bit_cast(pl_f32x4, dv);
+          *reinterpret_cast<pl_f32x4*>(yrow[i] + cb) = yy;
+        }
+      }
+    }
+    // the next step rewrites the tile only after these reads (in-order LDS)
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  };
+  // a ring of kFStages steps: the loads of the next kFStages-1 steps are in
+  // flight while one is applied; steps past c1 load only zeros
+  pl_u32x4 bring[kFStages][kRSteps][kCT], yring[kFStages][kYLoads];
+#pragma unroll
+  for (int st = 0; st < kFStages - 1; ++st) load_n(bring[st], yring[st], c0 + st * kCols);
+  for (int cb = c0; cb < c1; cb += kFStages * kCols) {
+#pragma unroll
+    for (int st = 0; st < kFStages; ++st) {
+      constexpr int kAhead = kFStages - 1;
+      const int nx = (st + kAhead) % kFStages;
+      load_n(bring[nx], yring[nx], cb + (st + kAhead) * kCols);
+      __builtin_amdgcn_sched_barrier(0);
+      apply_n(bring[st], yring[st], cb + st * kCols);
+    }
+  }
+}
+
+template <int DT, int JTMAX>
+__global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args a) {
+  typedef typename pl_traits<DT>::T T;
+  typedef pl_fused_lds<DT> L;
+  __shared__ pl_f32x4 red[kFWaves][4][64];
+  __shared__ __attribute__((aligned(16))) T tt[16 * L::kTRow];
+  __shared__ __attribute__((aligned(16))) T dbuf[kFWaves * 16 * L::kDRow];
+
+  // block -> (group g, 16-token tile rt, column slice); a tile's slices go
+  // to one XCD, and the groups are dealt to the XCDs in turn
+  const pl_xcd_slot ws = pl_xcd_map(a.sub * a.slices);
+  const int g = ws.g;
+  if (g >= a.group_cap) return;
+  const int rt = ws.j / a.slices;
+  const int slice = ws.j - rt * a.slices;
+  const int n_groups = a.meta[0];
+  pl_group grp = a.groups[g];
+  grp.start += rt * 16;
+  const int len = min(grp.len - rt * 16, 16);
+  if (g >= n_groups || len <= 0) return;
+  const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module];
+  const int rank = min(e.rank, kFRankMax);  // the host guarantees rank <= kFRankMax
+  if (rank <= 0) return;
+
+  // the staged intermediate's unused ranks must read as zeros
+  for (int i = threadIdx.x; i < 16 * L::kTRow; i += kFThreads) tt[i] = (T)0.f;
+
+  const int jt = (rank + 15) >> 4;
+  if (JTMAX == 1 || jt == 1)
+    pl_fused_body<DT, 1>(a, grp, len, e, rank, slice, red, tt, dbuf);
+  else if (JTMAX == 2 || jt == 2)
+    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX>(a, grp, len, e, rank, slice, red, tt, dbuf);
+  else
+    pl_fused_body<DT, JTMAX>(a, grp, len, e, rank, slice, red, tt, dbuf);
+}
+
+template <int DT>
+int launch_fused(const pl_fused_args& a, int jtmax, hipStream_t stream) {
+  const dim3 grid((unsigned)pl_xcd_grid(a.group_cap, (int64_t)a.sub * a.slices));
+  if (jtmax <= 1)
+    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 1>), grid, dim3(kFThreads), 0, stream, a);
+  else if (jtmax == 2)
+    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 2>), grid, dim3(kFThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 4>), grid, dim3(kFThreads), 0, stream, a);
+  return pl_launch_status("pl_lora_fused");
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int pl_lora_fused(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
+                             int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
+                             int32_t num_modules, int32_t module, int32_t ldt, const int32_t* tok,
+                             const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                             int32_t group_tokens, int32_t slices, int32_t epilogue, void* stream) {
+  if (dtype != PL_F32 && dtype != PL_BF16 && dtype != PL_F16) {
+    pl_set_error("unsupported dtype code %d", dtype);
+    return PL_ERR_ARG;
+  }
+  if (!x || !y || !arena || !table || !tok || !groups || !meta) {
+    pl_set_error("pl_lora_fused: null pointer");
+    return PL_ERR_ARG;
+  }
+  if (num_modules <= 0 || module < 0 || module >= num_modules) {
+    pl_set_error("module index %d out of range [0, %d)", module, num_modules);
+    return PL_ERR_ARG;
+  }
+  if (group_tokens != PL_GROUP_TOKENS_SHORT && group_tokens != PL_GROUP_TOKENS_LONG) {
+    pl_set_error("group_tokens must be 16 or 64 (got %d)", group_tokens);
+    return PL_ERR_ARG;
+  }
+  if (ldt <= 0 || ldt > kFRankMax) {
+    pl_set_error("pl_lora_fused takes ranks up to %d (slot rank capacity %d)", kFRankMax, ldt);
+    return PL_ERR_LIMIT;
+  }
+  if (slices < 1 || slices > kFSliceMax) {
+    pl_set_error("pl_lora_fused: slices must be in [1, %d] (got %d)", kFSliceMax, slices);
+    return PL_ERR_ARG;
+  }
+  if (epilogue != PL_EPI_FALLBACK && epilogue != PL_EPI_TRITON) {
+    pl_set_error("bad epilogue mode %d", epilogue);
+    return PL_ERR_ARG;
+  }
+  const int E = dtype == PL_F32 ? 4 : 8;
+  const int es = dtype == PL_F32 ? 4 : 2;
+  if (K <= 0 || N <= 0 || ldx < K || ldy < N) {
+    pl_set_error("bad fused sizes K=%d N=%d ldx=%lld ldy=%lld", K, N, (long long)ldx,
+                 (long long)ldy);
+    return PL_ERR_ARG;
+  }
+  if (K % E != 0 || N % E != 0 || (ldx * es) % 16 != 0 || (ldy * es) % 16 != 0 || !aligned16(x) ||
+      !aligned16(y) || !aligned16(arena)) {
+    pl_set_error("pl_lora_fused needs K, N multiples of %d and 16-byte aligned rows", E);
+    return PL_ERR_ALIGN;
+  }
+  if (group_cap < 0 || group_cap > (int64_t)1 << 24) {
+    pl_set_error("group capacity %lld out of range", (long long)group_cap);
+    return PL_ERR_LIMIT;
+  }
+  if (group_cap == 0) return PL_OK;
+  pl_fused_args a;
+  a.x = x;
+  a.ldx = ldx;
+  a.K = K;
+  const int64_t step = (int64_t)kFCC * 4 * E;
+  const int64_t kq = (K + kFWaves - 1) / kFWaves;
+  a.kw = (int32_t)((kq + step - 1) / step * step);
+  a.y = y;
+  a.ldy = ldy;
+  a.N = N;
+  const int64_t per_wave = ((int64_t)N + (int64_t)slices * kFWaves - 1) / ((int64_t)slices * kFWaves);
+  a.nw = (int32_t)((per_wave + kFColsMax - 1) / kFColsMax * kFColsMax);
+  a.arena = reinterpret_cast<const char*>(arena);
+  a.table = table;
+  a.num_modules = num_modules;
+  a.module = module;
+  a.tok = tok;
+  a.groups = groups;
+  a.meta = meta;
+  a.group_cap = (int32_t)group_cap;
+  a.sub = group_tokens / 16;
+  a.slices = slices;
+  a.epilogue = epilogue;
+  const int jtmax = (ldt + 15) / 16;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case PL_BF16: return launch_fused<PL_BF16>(a, jtmax, s);
+    case PL_F16: return launch_fused<PL_F16>(a, jtmax, s);
+    default: return launch_fused<PL_F32>(a, jtmax, s);
+  }
+}

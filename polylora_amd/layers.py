@@ -84,6 +84,14 @@ class MultiLoraLinear(nn.Module):
             return None
         plan = self._plan(lora_ctx, rows, row_len, seq_lens, weight_indices)
         main = torch.cuda.current_stream(x.device)
+        if sgmv.fused_ok(plan, cache, in_features):
+            # long adapter segments: base GEMM, then one fused shrink+expand launch
+            self._observe_call(x, _version_of(x), lora_ctx.stack)
+            base = self.base_layer(x)
+            base_3d = reshape(base)
+            sgmv.lora_fused(x2, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name, plan,
+                            stream=main.cuda_stream)
+            return base_3d.reshape(base.shape)
         if rows * row_len >= OVERLAP_MIN_TOKENS:
             side = sgmv.side_stream(x.device)
             side.wait_stream(main)  # x is ready, and every earlier expand has read the side workspaces

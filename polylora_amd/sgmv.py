@@ -22,7 +22,8 @@ import torch
 from . import _native
 
 __all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "lora_shrink", "lora_expand", "sgmv_lora_a_fwd",
-           "sgmv_lora_b_fwd", "choose_k_splits", "choose_group_tokens", "side_stream", "lora_shrink_stacked"]
+           "sgmv_lora_b_fwd", "choose_k_splits", "choose_group_tokens", "side_stream", "lora_shrink_stacked",
+           "lora_fused", "fused_ok", "choose_slices"]
 
 
 def _stream(device: torch.device) -> int:
@@ -72,7 +73,7 @@ class SgmvPlan:
     """
 
     __slots__ = ("rows", "row_len", "num_slots", "group_tokens", "tokens_cap", "group_cap", "tok", "groups", "meta",
-                 "row_slot", "seq_lens")
+                 "row_slot", "seq_lens", "distinct_slots")
 
     def __init__(self, row_slot: torch.Tensor, seq_lens: torch.Tensor, row_len: int, num_slots: int,
                  distinct_slots: int | None = None, group_tokens: int | None = None) -> None:
@@ -85,6 +86,7 @@ class SgmvPlan:
             raise ValueError("row_slot and seq_lens must have the same length")
         self.rows, self.row_len, self.num_slots = rows, int(row_len), int(num_slots)
         self.tokens_cap = rows * self.row_len
+        self.distinct_slots = distinct_slots
         if group_tokens is None:
             group_tokens = choose_group_tokens(self.tokens_cap, distinct_slots)
         if group_tokens not in (_native.PL_GROUP_TOKENS_SHORT, _native.PL_GROUP_TOKENS_LONG):
@@ -216,13 +218,17 @@ def lora_apply(
     """y[t] += scale * (x[t] @ A^T) @ B^T for every planned token t, in place.
 
     x: [rows*row_len, in_features], y: [rows*row_len, out_features], both of
-    the cache's dtype, on the cache's device.  Falls back to the row-based HIP
-    kernels when x / y do not meet the tiled path's alignment.
+    the cache's dtype, on the cache's device.  Long adapter segments go to
+    the fused kernel (lora_fused) unless k_splits asks for the split pair;
+    x / y that do not meet the tiled path's alignment go to the row-based HIP
+    kernels.
     """
     _require_gpu(x, "lora_apply")
     _check_operands(x, y, cache, module_name, plan.tokens_cap)
     if not _tiled_ok(x, y):
         return lora_apply_rows(x, y, cache, module_name, plan.row_slot, plan.seq_lens, plan.row_len, epilogue=epilogue)
+    if k_splits is None and fused_ok(plan, cache, int(x.shape[1])):
+        return lora_fused(x, y, cache, module_name, plan, epilogue=epilogue)
     lib = _native.load()
     dt = _native.dtype_code(x.dtype)
     K = int(x.shape[1])
@@ -396,6 +402,80 @@ def lora_expand(res: ShrinkResult, y: torch.Tensor, cache, module_name: str, *,
             y.stride(0), int(y.shape[1]), epilogue, _stream(y.device) if stream is None else stream,
         ),
         "pl_sgmv_expand",
+    )
+    return y
+
+
+FUSED_MAX_RANK = 64
+
+
+def choose_slices(plan: SgmvPlan, out_features: int) -> int:
+    """Column slices per 16-token tile of the fused kernel.
+
+    Every slice recomputes its tile's shrink, which costs more than the extra
+    workgroups gain as soon as the tiles alone give about one workgroup per
+    CU (measured on MI355X at 256 and 2048 tiles: one slice is fastest), so
+    slices are added only below 128 tiles, and never below 1024 columns each.
+    """
+    tiles = max(1, plan.tokens_cap // 16)
+    want = max(1, 256 // tiles)
+    most = max(1, out_features // 1024)
+    return max(1, min(want, most, 4))
+
+
+# Largest in_features the fused kernel takes on the forward path: its shrink
+# streams x at a lower rate than the split shrink, so for long reductions
+# (down_proj, K = 14336) the split pair is faster (measured on MI355X).
+FUSED_MAX_K = 8192
+
+
+def fused_ok(plan: SgmvPlan, cache, in_features: int) -> bool:
+    """Whether the fused kernel suits a plan and module: ranks within its limit, full 16-token tiles.
+
+    The fused kernel reads each adapter's A and B once per 16-token tile, so it
+    wants tiles that are full (long adapter segments, known from the plan's
+    distinct-adapter count); with a few tokens per adapter (decode) the split
+    shrink/expand spreads the weights over many more workgroups.
+    """
+    distinct = plan.distinct_slots
+    if cache.rank8_cap > FUSED_MAX_RANK or distinct is None or in_features > FUSED_MAX_K:
+        return False
+    return plan.tokens_cap >= 64 * max(1, distinct) and plan.tokens_cap >= 1024
+
+
+def lora_fused(
+    x: torch.Tensor,
+    y: torch.Tensor,
+    cache,
+    module_name: str,
+    plan: SgmvPlan,
+    *,
+    epilogue: int = _native.PL_EPI_FALLBACK,
+    slices: int | None = None,
+    stream: int | None = None,
+) -> torch.Tensor:
+    """y[t] += scale * (x[t] @ A^T) @ B^T for every planned token t, in place, in one launch (pl_lora_fused).
+
+    Same operands as lora_apply; needs the tiled path's alignment and slot
+    ranks up to FUSED_MAX_RANK.
+    """
+    _require_gpu(x, "lora_fused")
+    _check_operands(x, y, cache, module_name, plan.tokens_cap)
+    if not _tiled_ok(x, y):
+        raise ValueError("lora_fused needs 16-byte aligned rows and K, N multiples of 16 bytes")
+    if cache.rank8_cap > FUSED_MAX_RANK:
+        raise ValueError(f"lora_fused takes ranks up to {FUSED_MAX_RANK}; the cache holds up to {cache.rank8_cap}")
+    lib = _native.load()
+    N = int(y.shape[1])
+    n_slices = slices if slices is not None else choose_slices(plan, N)
+    _native.check(
+        lib.pl_lora_fused(
+            _native.dtype_code(x.dtype), x.data_ptr(), x.stride(0), int(x.shape[1]), y.data_ptr(), y.stride(0), N,
+            cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), cache.module_index[module_name],
+            cache.rank8_cap, plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap),
+            plan.group_tokens, n_slices, epilogue, _stream(x.device) if stream is None else stream,
+        ),
+        "pl_lora_fused",
     )
     return y
 
