@@ -27,7 +27,7 @@ constexpr int kFWaves = 4;
 constexpr int kFThreads = 64 * kFWaves;
 constexpr int kFCC = 4;         // 16-byte chunks per lane per shrink step
 constexpr int kFColsMax = 128;  // output columns per wave per expand step (at most)
-constexpr int kFStages = 3;     // expand steps in flight per wave
+constexpr int kFStages = 2;     // expand steps in flight per wave
 constexpr int kFRankMax = 64;   // largest rank the fused kernel takes
 
 // Columns per wave per expand step: as wide as the registers allow for the
