@@ -18,6 +18,9 @@
  *   pl_shrink_planes, pl_shrink_workspace_bytes
  *                          (sizes of the shrink -> expand workspace)
  *   pl_sgmv_expand      <- src/polylora/sgmv.py:178-275  _sgmv_lora_b_kernel
+ *   pl_sgmv_shrink_stacked, pl_sgmv_expand_stacked
+ *                       <- the same for sibling Linears in one launch each
+ *                          (sgmv.py:141-175 stack_num reads x once)
  *   pl_lora_apply       <- src/polylora/layers.py:42-53  (shrink then expand,
  *                          the LoRA half of MultiLoraLinear.forward)
  *   pl_lora_fused       <- src/polylora/sgmv.py:63-138 and :178-275 in one
@@ -174,6 +177,18 @@ int pl_sgmv_expand(int32_t dtype, const void* ws, int32_t ldt, int64_t tmp_rows,
                    int32_t module, const int32_t* tok, const pl_group* groups,
                    const int32_t* meta, int64_t group_cap, int32_t group_tokens, void* y,
                    int64_t ldy, int32_t N, int32_t epilogue, void* stream);
+
+/* Expand for up to PL_MAX_STACKED_MODULES modules in one launch: module i
+ * reads the planes in ws[i] (left by a shrink of the same plan, K split and
+ * ldt, e.g. pl_sgmv_shrink_stacked) and adds its delta into y[i] [*, ldy[i]]
+ * of N[i] columns, each as pl_sgmv_expand would.  For sibling Linears whose
+ * base outputs all exist before any of them is read (q/k/v, gate/up). */
+int pl_sgmv_expand_stacked(int32_t dtype, void* const* ws, int32_t ldt, int64_t tmp_rows,
+                           int32_t planes, const void* arena, const pl_slot_entry* table,
+                           int32_t num_modules, int32_t n_modules, const int32_t* modules,
+                           const int32_t* tok, const pl_group* groups, const int32_t* meta,
+                           int64_t group_cap, int32_t group_tokens, void* const* y,
+                           const int64_t* ldy, const int32_t* N, int32_t epilogue, void* stream);
 
 /* Shrink followed by expand on one stream (one call per wrapped Linear). */
 int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y, int64_t ldy,

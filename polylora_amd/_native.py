@@ -54,6 +54,10 @@ _SIGNATURES: dict[str, tuple] = {
         c_int32, c_void_p, c_int32, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
         c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_int32, c_void_p,
     ),
+    "pl_sgmv_expand_stacked": (
+        c_int32, c_void_p, c_int32, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
+        c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
+    ),
     "pl_lora_apply": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
         c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_int64,

@@ -164,6 +164,9 @@ class GpuAdapterCache:
         # (first module, input shape) -> modules called back to back on that
         # same input tensor; learned by MultiLoraLinear, used to stack shrinks
         self.stacked_runs: dict[tuple, tuple[str, ...]] = {}
+        # module name -> its MultiLoraLinear, so the first Linear of a run can
+        # compute its siblings' outputs
+        self.wrapped: dict[str, object] = {}
         self.loads = 0  # adapters copied into a slot since construction
         self._allocate()
 

@@ -64,23 +64,25 @@ struct pl_shrink_args {
 };
 
 struct pl_expand_args {
-  const float* planes;
   int32_t ldt;
   int32_t k_splits;
   int64_t plane;
   const char* arena;
   const pl_slot_entry* table;
   int32_t num_modules;
-  int32_t module;
   const int32_t* tok;
   const pl_group* groups;
   const int32_t* meta;
-  void* y;
-  int64_t ldy;
-  int32_t N;
-  int32_t n_chunks;
   int32_t epilogue;
-  int32_t sub;  // 16-token sub-tiles per plan group (1 or 4)
+  int32_t sub;                    // 16-token sub-tiles per plan group (1 or 4)
+  int32_t n_jobs;                 // modules written, 1..kMaxJobs
+  int32_t n_chunks;               // column chunks of all jobs together
+  int32_t chunk0[kMaxJobs];       // first chunk of each job
+  int32_t module[kMaxJobs];       // table column of each job's module
+  const float* planes[kMaxJobs];  // its shrink planes
+  void* y[kMaxJobs];              // its output
+  int64_t ldy[kMaxJobs];
+  int32_t N[kMaxJobs];
 };
 
 // Columns of y one expand wave owns: 64 for 2-byte types, 32 for fp32, so
@@ -380,12 +382,17 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   const int li = lane & 15;
   const int lg = lane >> 4;
 
-  // block -> (group g, column chunk c, 16-token sub-tile rt); the sub-tiles
-  // of one chunk, which read the same B rows, are adjacent
+  // block -> (group g, column chunk c of module job, 16-token sub-tile rt);
+  // the sub-tiles of one chunk, which read the same B rows, are adjacent
   const int rt = blockIdx.x % a.sub;
   const int gc = blockIdx.x / a.sub;
   const int g = gc / a.n_chunks;
-  const int c = gc - g * a.n_chunks;
+  const int cg = gc - g * a.n_chunks;
+  int job = 0;
+#pragma unroll
+  for (int j = 1; j < kMaxJobs; ++j)
+    if (j < a.n_jobs && cg >= a.chunk0[j]) job = j;
+  const int c = cg - a.chunk0[job];
   // the group count and the group record load together (every record below
   // the capacity is readable); the record is used only for g below the count
   const int n_groups = a.meta[0];
@@ -393,11 +400,11 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   grp.start += rt * 16;
   const int len = min(grp.len - rt * 16, 16);
   if (g >= n_groups || len <= 0) return;
-  const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module];
+  const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module[job]];
   const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
   if (rank <= 0) return;
   const int r8 = e.rank8;
-  const int N = a.N;
+  const int N = a.N[job];
   const int n_base = c * S::kChunk;
   const float scale = e.scale;
   const float scale_t = pl_round<DT>(scale);
@@ -411,7 +418,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   const int yq = tid & 31;
   const int yr0 = tid >> 5;
   const int ycol = n_base + yq * E;
-  T* __restrict__ y = reinterpret_cast<T*>(a.y);
+  T* __restrict__ y = reinterpret_cast<T*>(a.y[job]);
   int yt[kYPer];
 #pragma unroll
   for (int i = 0; i < kYPer; ++i) yt[i] = a.tok[grp.start + min(yr0 + kYRowsPerPass * i, len - 1)];
@@ -419,7 +426,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   // planes -> staged intermediate: thread (token sp, ranks rb + sq .. +4)
   const int sp = tid >> 4;
   const int sq = (tid & 15) * 4;
-  const float* srow = a.planes + (int64_t)(grp.start + (sp < len ? sp : 0)) * a.ldt;
+  const float* srow = a.planes[job] + (int64_t)(grp.start + (sp < len ? sp : 0)) * a.ldt;
 
   pl_u32x4 bf[kSteps][S::kCT];
   pl_u32x4 pv[PMAX];
@@ -480,7 +487,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
 #pragma unroll
   for (int i = 0; i < kYPer; ++i) {
     const int r = yr0 + kYRowsPerPass * i;
-    yptr[i] = (r < len && ycol < N) ? y + (int64_t)yt[i] * a.ldy + ycol : nullptr;
+    yptr[i] = (r < len && ycol < N) ? y + (int64_t)yt[i] * a.ldy[job] + ycol : nullptr;
     yv[i] = pl_ld16_or0(yptr[i], yptr[i] != nullptr);
   }
   __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first use
@@ -693,61 +700,75 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
   return PL_OK;
 }
 
-int prepare_expand(pl_expand_args& a, int32_t dtype, const void* ws, int32_t ldt,
+int prepare_expand(pl_expand_args& a, int32_t dtype, void* const* ws, int32_t ldt,
                    int64_t tmp_rows, int32_t planes, const void* arena,
-                   const pl_slot_entry* table, int32_t num_modules, int32_t module,
-                   const int32_t* tok, const pl_group* groups, const int32_t* meta,
-                   int64_t group_cap, int32_t group_tokens, void* y, int64_t ldy, int32_t N,
-                   int32_t epilogue) {
-  int st = check_common(dtype, arena, table, num_modules, module, tok, groups, meta, group_cap,
-                        group_tokens);
-  if (st) return st;
-  if ((st = check_ws(ws, ldt, tmp_rows))) return st;
+                   const pl_slot_entry* table, int32_t num_modules, int32_t n_jobs,
+                   const int32_t* modules, const int32_t* tok, const pl_group* groups,
+                   const int32_t* meta, int64_t group_cap, int32_t group_tokens, void* const* y,
+                   const int64_t* ldy, const int32_t* N, int32_t epilogue) {
+  if (n_jobs < 1 || n_jobs > kMaxJobs || !modules || !ws || !y || !ldy || !N) {
+    pl_set_error("expand serves 1..%d modules (got %d), each with its workspace, y, ldy and N",
+                 kMaxJobs, n_jobs);
+    return PL_ERR_ARG;
+  }
   const int E = pl_chunk_elems(dtype);
   const int es = pl_elem_size(dtype);
-  if (!y) {
-    pl_set_error("null y pointer");
-    return PL_ERR_ARG;
+  const int chunk = 4 * (dtype == PL_F32 ? 32 : 64);
+  int64_t n_chunks = 0;
+  for (int j = 0; j < n_jobs; ++j) {
+    int st = check_common(dtype, arena, table, num_modules, modules[j], tok, groups, meta,
+                          group_cap, group_tokens);
+    if (st) return st;
+    if ((st = check_ws(ws[j], ldt, tmp_rows))) return st;
+    if (!y[j]) {
+      pl_set_error("null y pointer");
+      return PL_ERR_ARG;
+    }
+    if (N[j] <= 0 || ldy[j] < N[j]) {
+      pl_set_error("bad expand sizes N=%d ldy=%lld", N[j], (long long)ldy[j]);
+      return PL_ERR_ARG;
+    }
+    if (N[j] % E != 0 || (ldy[j] * es) % 16 != 0 || !aligned16(y[j])) {
+      pl_set_error("expand needs N %% %d == 0 and 16-byte aligned y rows", E);
+      return PL_ERR_ALIGN;
+    }
+    a.chunk0[j] = (int32_t)n_chunks;
+    n_chunks += (N[j] + chunk - 1) / chunk;
   }
-  if (N <= 0 || ldy < N || planes < 1 || planes > 4096) {
-    pl_set_error("bad expand sizes N=%d ldy=%lld planes=%d", N, (long long)ldy, planes);
-    return PL_ERR_ARG;
-  }
-  if (planes > kShortMaxPlanes) {
-    pl_set_error("the expand sums at most %d shrink planes (got %d)", kShortMaxPlanes, planes);
+  if (planes < 1 || planes > kShortMaxPlanes) {
+    pl_set_error("the expand sums 1..%d shrink planes (got %d)", kShortMaxPlanes, planes);
     return PL_ERR_ARG;
   }
   if (epilogue != PL_EPI_FALLBACK && epilogue != PL_EPI_TRITON) {
     pl_set_error("bad epilogue mode %d", epilogue);
     return PL_ERR_ARG;
   }
-  if (N % E != 0 || (ldy * es) % 16 != 0 || !aligned16(y)) {
-    pl_set_error("expand needs N %% %d == 0 and 16-byte aligned y rows", E);
-    return PL_ERR_ALIGN;
-  }
-  const int chunk = 4 * (dtype == PL_F32 ? 32 : 64);
-  const int64_t n_chunks = (N + chunk - 1) / chunk;
   if (group_cap * n_chunks * (group_tokens / 16) > 0x7fffffffLL) {
     pl_set_error("expand grid too large");
     return PL_ERR_LIMIT;
   }
-  a.planes = reinterpret_cast<const float*>(ws);
   a.ldt = ldt;
   a.k_splits = planes;
   a.plane = tmp_rows * ldt;
   a.arena = reinterpret_cast<const char*>(arena);
   a.table = table;
   a.num_modules = num_modules;
-  a.module = module;
   a.tok = tok;
   a.groups = groups;
   a.meta = meta;
-  a.y = y;
-  a.ldy = ldy;
-  a.N = N;
-  a.n_chunks = (int32_t)n_chunks;
   a.epilogue = epilogue;
   a.sub = group_tokens / 16;
+  a.n_jobs = n_jobs;
+  a.n_chunks = (int32_t)n_chunks;
+  for (int j = 0; j < kMaxJobs; ++j) {
+    const bool on = j < n_jobs;
+    if (!on) a.chunk0[j] = (int32_t)n_chunks;
+    a.module[j] = on ? modules[j] : 0;
+    a.planes[j] = on ? reinterpret_cast<const float*>(ws[j]) : nullptr;
+    a.y[j] = on ? y[j] : nullptr;
+    a.ldy[j] = on ? ldy[j] : 0;
+    a.N[j] = on ? N[j] : 0;
+  }
   return PL_OK;
 }
 
@@ -817,9 +838,24 @@ extern "C" int pl_sgmv_expand(int32_t dtype, const void* ws, int32_t ldt, int64_
                               const pl_group* groups, const int32_t* meta, int64_t group_cap,
                               int32_t group_tokens, void* y, int64_t ldy, int32_t N,
                               int32_t epilogue, void* stream) {
+  void* wsp = const_cast<void*>(ws);
+  return pl_sgmv_expand_stacked(dtype, &wsp, ldt, tmp_rows, planes, arena, table, num_modules, 1,
+                                &module, tok, groups, meta, group_cap, group_tokens, &y, &ldy, &N,
+                                epilogue, stream);
+}
+
+extern "C" int pl_sgmv_expand_stacked(int32_t dtype, void* const* ws, int32_t ldt,
+                                      int64_t tmp_rows, int32_t planes, const void* arena,
+                                      const pl_slot_entry* table, int32_t num_modules,
+                                      int32_t n_modules, const int32_t* modules,
+                                      const int32_t* tok, const pl_group* groups,
+                                      const int32_t* meta, int64_t group_cap,
+                                      int32_t group_tokens, void* const* y, const int64_t* ldy,
+                                      const int32_t* N, int32_t epilogue, void* stream) {
   pl_expand_args a;
-  int st = prepare_expand(a, dtype, ws, ldt, tmp_rows, planes, arena, table, num_modules, module,
-                          tok, groups, meta, group_cap, group_tokens, y, ldy, N, epilogue);
+  int st = prepare_expand(a, dtype, ws, ldt, tmp_rows, planes, arena, table, num_modules,
+                          n_modules, modules, tok, groups, meta, group_cap, group_tokens, y, ldy, N,
+                          epilogue);
   if (st) return st;
   return dispatch_expand(dtype, a, group_cap, reinterpret_cast<hipStream_t>(stream));
 }
@@ -836,8 +872,8 @@ extern "C" int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t 
   int st = prepare_shrink(sa, dtype, x, ldx, K, arena, table, num_modules, 1, &module, &ws, tok,
                           groups, meta, group_cap, group_tokens, ws_bytes, ldt, tmp_rows, k_splits);
   if (st) return st;
-  st = prepare_expand(ea, dtype, ws, ldt, tmp_rows, sa.k_splits, arena, table, num_modules,
-                      module, tok, groups, meta, group_cap, group_tokens, y, ldy, N, epilogue);
+  st = prepare_expand(ea, dtype, &ws, ldt, tmp_rows, sa.k_splits, arena, table, num_modules, 1,
+                      &module, tok, groups, meta, group_cap, group_tokens, &y, &ldy, &N, epilogue);
   if (st) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   st = dispatch_shrink(dtype, sa, group_cap, s);

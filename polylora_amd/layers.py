@@ -45,6 +45,7 @@ class MultiLoraLinear(nn.Module):
         self.base_layer = base_layer
         self.module_name = module_name
         self.cache = cache
+        cache.wrapped[module_name] = self
 
     @property
     def in_features(self) -> int:
@@ -92,6 +93,9 @@ class MultiLoraLinear(nn.Module):
             sgmv.lora_fused(x2, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name, plan,
                             stream=main.cuda_stream)
             return base_3d.reshape(base.shape)
+        run_out = self._run_forward(x, x2, plan, lora_ctx, reshape, main)
+        if run_out is not None:
+            return run_out
         if rows * row_len >= OVERLAP_MIN_TOKENS:
             side = sgmv.side_stream(x.device)
             side.wait_stream(main)  # x is ready, and every earlier expand has read the side workspaces
@@ -106,6 +110,59 @@ class MultiLoraLinear(nn.Module):
         sgmv.lora_expand(shrunk, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name,
                          stream=main.cuda_stream)
         return base_3d.reshape(base.shape)
+
+    def _run_forward(self, x, x2, plan, lora_ctx: LoraBatchContext, reshape, main):
+        """Whole outputs for a run of sibling Linears, or None to take the single-module path.
+
+        Siblings are wrapped Linears that the model calls back to back on the
+        very same input tensor (q/k/v, gate/up), learned from the call order of
+        a forward.  The first of a run computes every sibling's base output,
+        one stacked shrink and one stacked expand, and keeps the siblings'
+        finished outputs; a sibling then returns its kept output when its own
+        call brings the same input tensor, unmodified (same version counter;
+        inference-mode tensors keep none, so for them object identity alone),
+        for the same plan.  A base output is a function of x and the weights
+        only, so computing it at the first sibling's call gives the value the
+        sibling's own call would.  Only without autograd: the LoRA path is for
+        inference.
+        """
+        if torch.is_grad_enabled() and (x.requires_grad or self.base_layer.weight.requires_grad):
+            return None
+        stack = lora_ctx.stack
+        outputs = stack.setdefault("outputs", {})
+        version = _version_of(x)
+        kept = outputs.pop(self.module_name, None)
+        if kept is not None:
+            kx, kversion, kplan, out = kept
+            if kx is x and kversion == version and kplan is plan:
+                self._observe_call(x, version, stack)
+                return out
+        cache = self.cache
+        run = cache.stacked_runs.get((self.module_name, tuple(x.shape)))
+        if run is None or len(run) < 2:
+            return None
+        siblings = [cache.wrapped.get(name) for name in run]
+        if any(m is None for m in siblings) or not all(sgmv.tiled_shapes_ok(x2, m.out_features) for m in siblings):
+            return None
+        self._observe_call(x, version, stack)
+        tokens = x2.shape[0]
+        if tokens >= OVERLAP_MIN_TOKENS:
+            side = sgmv.side_stream(x.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                results = sgmv.lora_shrink_stacked(x2, cache, list(run), plan, stream=side.cuda_stream)
+            bases = [m.base_layer(x) for m in siblings]
+            main.wait_stream(side)
+        else:
+            results = sgmv.lora_shrink_stacked(x2, cache, list(run), plan, stream=main.cuda_stream)
+            bases = [m.base_layer(x) for m in siblings]
+        outs = [reshape(b) for b in bases]
+        sgmv.lora_expand_stacked(results, [o.view(tokens, o.shape[-1]) for o in outs], cache, list(run),
+                                 stream=main.cuda_stream)
+        finished = [o.reshape(b.shape) for o, b in zip(outs, bases)]
+        for name, out in zip(run[1:], finished[1:]):
+            outputs[name] = (x, version, plan, out)
+        return finished[0]
 
     def _shrink(self, x: torch.Tensor, x2: torch.Tensor, plan, lora_ctx: LoraBatchContext, stream: int):
         """This module's shrink result: computed ahead by a sibling, stacked with siblings, or alone.

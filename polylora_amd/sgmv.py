@@ -23,7 +23,7 @@ from . import _native
 
 __all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "lora_shrink", "lora_expand", "sgmv_lora_a_fwd",
            "sgmv_lora_b_fwd", "choose_k_splits", "choose_group_tokens", "side_stream", "lora_shrink_stacked",
-           "lora_fused", "fused_ok", "choose_slices"]
+           "lora_fused", "fused_ok", "choose_slices", "lora_expand_stacked"]
 
 
 def _stream(device: torch.device) -> int:
@@ -478,6 +478,48 @@ def lora_fused(
         "pl_lora_fused",
     )
     return y
+
+
+def lora_expand_stacked(results: list, ys: list, cache, module_names: list, *,
+                        epilogue: int = _native.PL_EPI_FALLBACK, stream: int | None = None) -> list:
+    """One expand launch for sibling Linears (pl_sgmv_expand_stacked): results[i] -> ys[i] in place.
+
+    results are the ShrinkResults of one stacked shrink (same plan, K split
+    and workspace geometry); the stream must be ordered after that shrink and
+    after every ys[i]'s producer.
+    """
+    n = len(module_names)
+    if not 1 <= n <= _native.PL_MAX_STACKED_MODULES or len(results) != n or len(ys) != n:
+        raise ValueError(f"an expand serves 1..{_native.PL_MAX_STACKED_MODULES} modules with one result and one y each")
+    plan = results[0].plan
+    for res, y, name in zip(results, ys, module_names):
+        _require_gpu(y, "lora_expand_stacked")
+        spec = cache.module_specs[name]
+        if res.plan is not plan or res.planes != results[0].planes or res.rows != results[0].rows:
+            raise ValueError("stacked expand results must come from one stacked shrink")
+        if y.dim() != 2 or y.shape[0] != plan.tokens_cap or y.shape[1] != spec.out_features:
+            raise ValueError(f"y must be [{plan.tokens_cap}, {spec.out_features}], got {list(y.shape)}")
+        if y.dtype != cache.dtype or y.device != cache.device:
+            raise TypeError(f"y {y.dtype} on {y.device} must match the adapter cache ({cache.dtype} on {cache.device})")
+        if not res.valid:
+            raise RuntimeError("the shrink result was overwritten by a later shrink on the same workspace")
+    lib = _native.load()
+    r0 = results[0]
+    ws = (ctypes.c_void_p * n)(*(r.buf.data_ptr() for r in results))
+    mods = (ctypes.c_int32 * n)(*(cache.module_index[m] for m in module_names))
+    yp = (ctypes.c_void_p * n)(*(y.data_ptr() for y in ys))
+    ldy = (ctypes.c_int64 * n)(*(y.stride(0) for y in ys))
+    nn_ = (ctypes.c_int32 * n)(*(int(y.shape[1]) for y in ys))
+    _native.check(
+        lib.pl_sgmv_expand_stacked(
+            _native.dtype_code(ys[0].dtype), ws, r0.ldt, r0.rows, r0.planes, cache.arena.data_ptr(),
+            cache.table.data_ptr(), len(cache.module_index), n, mods, plan.tok.data_ptr(), plan.groups.data_ptr(),
+            plan.meta.data_ptr(), max(1, plan.group_cap), plan.group_tokens, yp, ldy, nn_, epilogue,
+            _stream(ys[0].device) if stream is None else stream,
+        ),
+        "pl_sgmv_expand_stacked",
+    )
+    return ys
 
 
 def lora_apply_rows(

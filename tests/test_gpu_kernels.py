@@ -360,6 +360,16 @@ def test_stacked_shrink_equals_separate(gpu, group_tokens):
         y = base[m].clone()
         sgmv.lora_expand(res, y, cache, m)
         assert torch.equal(y, sep[m]), m
+    # one stacked expand over all three modules
+    ys = [base[m].clone() for m in shapes]
+    sgmv.lora_expand_stacked(results, ys, cache, list(shapes))
+    for m, y in zip(shapes, ys):
+        assert torch.equal(y, sep[m]), m
+    # results of two different shrinks cannot share one expand (position 0 is
+    # rewritten by the second shrink, so pair it with position 1's result)
+    other = sgmv.lora_shrink(x, cache, "k", sgmv.SgmvPlan(row_slot, seq, 1, cache.num_slots, group_tokens=group_tokens))
+    with pytest.raises(ValueError, match="one stacked shrink"):
+        sgmv.lora_expand_stacked([results[1], other], [ys[1], ys[1].clone()], cache, ["k", "k"])
     # a later shrink on position 0 invalidates the first stacked result only
     sgmv.lora_shrink(x, cache, "q", plan)
     assert not results[0].valid and results[1].valid and results[2].valid

@@ -18,6 +18,7 @@ import pytest
 import torch
 
 from oracle import model as oracle_model
+from polylora_amd import sgmv
 from polylora_amd import PolyLoraConfig, PolyLoraModel
 from tests import _peft
 
@@ -502,7 +503,20 @@ def test_sibling_shrinks_are_stacked(gpu):
             p = f"layers.{layer}."
             assert (p + "self_attn.q_proj", p + "self_attn.k_proj", p + "self_attn.v_proj") in runs
             assert (p + "mlp.gate_proj", p + "mlp.up_proj") in runs
-        second = pm(input_ids=ids, adapter_ids=adapter_ids).last_hidden_state
+        calls = []
+        stacked_expand = sgmv.lora_expand_stacked
+
+        def counting(*a, **k):
+            calls.append(tuple(a[3]))
+            return stacked_expand(*a, **k)
+
+        sgmv.lora_expand_stacked = counting
+        try:
+            second = pm(input_ids=ids, adapter_ids=adapter_ids).last_hidden_state
+        finally:
+            sgmv.lora_expand_stacked = stacked_expand
+        # every run was computed whole by its first Linear: one stacked expand each
+        assert sorted(calls) == sorted(runs), (calls, runs)
         om, bank = _oracle(base, LLAMA_TARGETS, ads, 32, torch.bfloat16, gpu)
         want = oracle_model.run(om, bank, adapter_ids, input_ids=ids).last_hidden_state
     assert torch.equal(first, second)
