@@ -378,7 +378,7 @@ class SgmvLaunch:
 
 
 class StackedLaunch:
-    """One shrink launch for sibling Linears fed the same x (pl_sgmv_shrink_stacked) and their expands."""
+    """Sibling Linears fed the same x: one stacked shrink launch and one stacked expand launch."""
 
     def __init__(self, x, ys, cache, modules, plan, k_splits=None):
         import ctypes
@@ -403,17 +403,19 @@ class StackedLaunch:
         self.shrink_args = (dt, x.data_ptr(), x.stride(0), K, cache.arena.data_ptr(), cache.table.data_ptr(), n_mod,
                             len(modules), self.mods, self.ptrs, plan.tok.data_ptr(), plan.groups.data_ptr(),
                             plan.meta.data_ptr(), max(1, plan.group_cap), gt, nbytes, ldt, rows, splits, s)
-        self.expand_args = [(dt, b.data_ptr(), ldt, rows, planes, cache.arena.data_ptr(), cache.table.data_ptr(), n_mod,
-                             cache.module_index[m], plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(),
-                             max(1, plan.group_cap), gt, y.data_ptr(), y.stride(0), int(y.shape[1]),
-                             _native.PL_EPI_FALLBACK, s) for b, y, m in zip(bufs, ys, modules)]
+        self.yptrs = (ctypes.c_void_p * len(modules))(*(y.data_ptr() for y in ys))
+        self.ldys = (ctypes.c_int64 * len(modules))(*(y.stride(0) for y in ys))
+        self.Ns = (ctypes.c_int32 * len(modules))(*(int(y.shape[1]) for y in ys))
+        self.expand_args = (dt, self.ptrs, ldt, rows, planes, cache.arena.data_ptr(), cache.table.data_ptr(), n_mod,
+                            len(modules), self.mods, plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(),
+                            max(1, plan.group_cap), gt, self.yptrs, self.ldys, self.Ns, _native.PL_EPI_FALLBACK, s)
         self.keep = (x, ys, bufs, plan)
 
     def shrink(self):
         self.n.check(self.lib.pl_sgmv_shrink_stacked(*self.shrink_args), "pl_sgmv_shrink_stacked")
 
-    def expands(self):
-        return [lambda a=a: self.n.check(self.lib.pl_sgmv_expand(*a), "pl_sgmv_expand") for a in self.expand_args]
+    def expand(self):
+        self.n.check(self.lib.pl_sgmv_expand_stacked(*self.expand_args), "pl_sgmv_expand_stacked")
 
 
 class FusedLaunch:
@@ -669,8 +671,8 @@ def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Te
         per_type[key] = [round(1e3 * time_launches([l.shrink for l in sel], reps) / len(sel), 2),
                          round(1e3 * time_launches([l.expand for l in sel], reps) / len(sel), 2)]
     # The forward's own launch sequence: sibling Linears that read the same
-    # input (q/k/v, gate/up) share one stacked shrink, as MultiLoraLinear
-    # does once it has seen a forward; every Linear has its own expand.
+    # input (q/k/v, gate/up) share one stacked shrink and one stacked expand,
+    # as MultiLoraLinear does once it has seen a forward.
     # Modules whose plan suits the fused kernel take one pl_lora_fused launch
     # each (MultiLoraLinear does the same).
     by_name = {s.name: s for s in pm.module_specs}
@@ -689,10 +691,10 @@ def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Te
         k = by_name[names[0]].in_features
         st = StackedLaunch(xs[k], [ys[by_name[n].out_features] for n in names], cache, names, plan)
         stacks.append(st)
-        seq.extend((st.shrink, *st.expands()))
+        seq.extend((st.shrink, st.expand))
     total_ms = time_launches(seq, reps)
     sh_ms = time_launches([st.shrink for st in stacks], reps) if stacks else 0.0
-    ex_ms = time_launches([f for st in stacks for f in st.expands()], reps) if stacks else 0.0
+    ex_ms = time_launches([st.expand for st in stacks], reps) if stacks else 0.0
     fu_ms = time_launches(fused, reps) if fused else 0.0
     return {"pairs_ms": total_ms, "shrink_ms": sh_ms, "expand_ms": ex_ms, "fused_ms": fu_ms, "per_type_us": per_type,
             "group_tokens": plan.group_tokens, "launches": len(seq), "fused_launches": len(fused)}
@@ -822,8 +824,9 @@ def run_decode(args) -> dict:
         out["lora_kernels_expand_ms"] = round(kt["expand_ms"], 4)
         out["per_op_us_shrink_expand"] = kt["per_type_us"]
         out["lora_kernel_launches_per_step"] = kt["launches"]
-        out["lora_kernels_timing"] = ("the forward's launch sequence (stacked q/k/v and gate/up shrinks, one expand "
-                                      "per Linear) back to back without the base model")
+        out["lora_kernels_timing"] = ("the forward's launch sequence (one stacked shrink and one stacked expand for "
+                                      "q/k/v and for gate/up, a shrink and an expand for o and down) back to back "
+                                      "without the base model")
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_decode_layer(pm, wl.adapter_ids, args.cpu_seconds)
         _log(f"decode: kernels {out['lora_kernels_gbs']} GB/s")
