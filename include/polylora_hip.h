@@ -61,9 +61,17 @@ enum pl_status {
 /* One entry per (slot, module) of the slot table, 32 bytes.  The table is a
  * device array laid out [num_slots][num_modules].  Slot 0 is the base
  * adapter and always has rank 0.  `a_off` points (bytes from the arena base)
- * at the adapter's A for this module, stored [rank][in_features] row-major;
- * `b_off` points at B stored [out_features][rank8] row-major where
- * rank8 = rank rounded up to a multiple of 8 and columns rank..rank8-1 are 0.
+ * at the adapter's A for this module, an [rank][in_features] matrix; `b_off`
+ * points at B, an [out_features][rank8] matrix where rank8 = rank rounded up
+ * to a multiple of 8 and columns rank..rank8-1 are 0.  Both are stored in
+ * MFMA blocks: an [R][C] matrix is cut into tiles of 16 rows (the last tile
+ * has rt = min(16, R - 16t) rows), and each tile is stored as its column
+ * blocks of W = 64 bytes (32 bf16/f16 or 16 f32 elements; the last block is
+ * wb = min(W, C - sW) wide), one after the other, each row-major:
+ *   element (i, c) at 16*t*C + s*rt*W + (i % 16)*wb + (c - s*W),
+ *   t = i / 16, s = c / W.
+ * A 16-row x 64-byte MFMA operand load then reads contiguous memory.  For
+ * C <= W (e.g. B of ranks up to 32 in bf16) this is plain row-major.
  * Replaces the per-module A/B/ranks/scales tensors of cache.py:37-58. */
 typedef struct pl_slot_entry {
   int32_t rank;

@@ -9,7 +9,10 @@ Here every slot s >= 1 owns one contiguous region of ``slot_bytes`` in a
 single device arena.  An adapter is packed once on the host (pinned, model
 dtype) into a compact image: for each module it has weights for, A as
 ``[rank][in]`` (= PEFT lora_A) then B as ``[out][rank8]`` (= PEFT lora_B,
-rank padded to a multiple of 8 with zeros), each part 256-byte aligned.
+rank padded to a multiple of 8 with zeros), each part 256-byte aligned and
+stored in MFMA blocks (``tile_rows``): the first dimension cut into tiles of
+16 rows, each tile stored as consecutive 64-byte column blocks, so that a
+kernel's 16-row x 64-byte operand load reads contiguous memory.
 Loading is one host->device copy of that image plus one copy of the slot's
 table row (32 bytes per module: rank, scale, rank8, A and B offsets), both
 on a side stream that first waits for the last forward that read the slot;
@@ -54,6 +57,50 @@ def _align(n: int) -> int:
 
 def _round8(r: int) -> int:
     return (r + 7) // 8 * 8
+
+
+_TILE_ROWS = 16
+_BLOCK_BYTES = 64
+
+
+def tile_rows(m: torch.Tensor) -> torch.Tensor:
+    """``[R][C]`` -> the arena's block layout, flattened (same element count).
+
+    Rows are cut into tiles of 16 (the last may be shorter, ``rt`` rows); a
+    tile is stored as its column blocks of ``W = 64 bytes`` one after the
+    other, each block row-major (the last block may be narrower, ``wb``
+    columns).  Element (i, c) lands at
+    ``16*t*C + s*rt*W + (i % 16)*wb + (c - s*W)`` with ``t = i // 16`` and
+    ``s = c // W``.  For ``C <= W`` this is the plain row-major layout.
+    """
+    R, C = m.shape
+    w = _BLOCK_BYTES // m.element_size()
+    out = torch.empty(R * C, dtype=m.dtype)
+    full = C // w
+    for t0 in range(0, R, _TILE_ROWS):
+        tile = m[t0 : t0 + _TILE_ROWS]
+        rt = tile.shape[0]
+        base = t0 * C
+        if full:
+            out[base : base + rt * full * w] = tile[:, : full * w].reshape(rt, full, w).transpose(0, 1).reshape(-1)
+        if C > full * w:
+            out[base + rt * full * w : base + rt * C] = tile[:, full * w :].reshape(-1)
+    return out
+
+
+def untile_rows(flat: torch.Tensor, R: int, C: int) -> torch.Tensor:
+    """Inverse of ``tile_rows``: the block layout back to ``[R][C]``."""
+    w = _BLOCK_BYTES // flat.element_size()
+    out = torch.empty((R, C), dtype=flat.dtype, device=flat.device)
+    full = C // w
+    for t0 in range(0, R, _TILE_ROWS):
+        rt = min(_TILE_ROWS, R - t0)
+        base = t0 * C
+        if full:
+            out[t0 : t0 + rt, : full * w] = flat[base : base + rt * full * w].view(full, rt, w).transpose(0, 1).reshape(rt, full * w)
+        if C > full * w:
+            out[t0 : t0 + rt, full * w :] = flat[base + rt * full * w : base + rt * C].view(rt, C - full * w)
+    return out
 
 
 class SlotLayout:
@@ -114,10 +161,12 @@ def pack_adapter(adapter: CpuAdapter, layout: SlotLayout) -> PackedAdapter:
     image = torch.zeros(max(cursor, 1), dtype=torch.uint8)
     for weights, spec, r, r8, a_off, b_off in parts:
         a_bytes = r * spec.in_features * es
-        image[a_off : a_off + a_bytes].view(layout.dtype).view(r, spec.in_features).copy_(weights.A.t())
+        a_rows = weights.A.t().to(layout.dtype)
+        image[a_off : a_off + a_bytes].view(layout.dtype).copy_(tile_rows(a_rows))
         b_bytes = spec.out_features * r8 * es
-        b_view = image[b_off : b_off + b_bytes].view(layout.dtype).view(spec.out_features, r8)
-        b_view[:, :r].copy_(weights.B.t())
+        b_rows = torch.zeros(spec.out_features, r8, dtype=layout.dtype)
+        b_rows[:, :r].copy_(weights.B.t())
+        image[b_off : b_off + b_bytes].view(layout.dtype).copy_(tile_rows(b_rows))
     if torch.cuda.is_available():
         image = image.pin_memory()
     return PackedAdapter(image=image, rows=rows)
@@ -218,11 +267,11 @@ class GpuAdapterCache:
             offs = entry.view(np.int64)
             if side == "A":
                 a = self.arena[int(offs[2]) : int(offs[2]) + r * spec.in_features * es]
-                out[slot, :, :r] = a.view(self.dtype).view(r, spec.in_features).t()
+                out[slot, :, :r] = untile_rows(a.view(self.dtype), r, spec.in_features).t()
             else:
                 r8 = int(entry[2])
                 b = self.arena[int(offs[3]) : int(offs[3]) + spec.out_features * r8 * es]
-                out[slot, :r, :] = b.view(self.dtype).view(spec.out_features, r8)[:, :r].t()
+                out[slot, :r, :] = untile_rows(b.view(self.dtype), spec.out_features, r8)[:, :r].t()
         return out
 
     # ------------------------------------------------------------- residency

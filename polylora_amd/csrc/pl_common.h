@@ -85,6 +85,24 @@ static inline int64_t pl_xcd_grid(int64_t group_cap, int64_t per_group) {
   return (group_cap + kXcds - 1) / kXcds * kXcds * per_group;
 }
 
+// Slot arena layout of a module's A ([rank][K]) and B ([N][rank8]): MFMA
+// blocks.  An [R][C] matrix is cut into tiles of 16 rows (rt = min(16,
+// R - 16t) in tile t) and each tile is stored as its column blocks of W =
+// 64 bytes (wb = min(W, C - sW) wide), one after the other, row-major:
+//   element (i, c) at 16*t*C + s*rt*W + (i % 16)*wb + (c - s*W),
+// t = i / 16, s = c / W.  A wave's 16-row x 64-byte operand load (lane
+// (li, lg): row 16t + li, columns sW + lg*E .. +E) reads rt*wb contiguous
+// elements.  With c0 = sW the block of tile t starts at 16*t*C + c0*rt.
+template <int DT>
+__device__ __forceinline__ int64_t pl_tile_off(int i, int c, int R, int C) {
+  constexpr int W = 4 * pl_traits<DT>::E;
+  const int t = i >> 4;
+  const int rt = min(16, R - (t << 4));
+  const int c0 = c - c % W;
+  const int wb = min(W, C - c0);
+  return (int64_t)(t << 4) * C + (int64_t)c0 * rt + (i & 15) * wb + (c - c0);
+}
+
 // Sixteen zero bytes in device memory: the source of every masked-off lane.
 static __device__ __attribute__((aligned(16))) uint32_t pl_zero16[4];
 

@@ -113,12 +113,16 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   auto load_k = [&](pl_u32x4 (&xf)[kFCC], pl_u32x4 (&af)[JT][kFCC], int kb) {
 #pragma unroll
     for (int jt = 0; jt < JT; ++jt) {
-      const int j = jt * 16 + li;
-      const T* arow = A + (int64_t)j * K + lg * E;
+      // rank tile of A's MFMA blocks (rt rows): the block of columns k
+      // starts at t0*K + k*rt and is wb wide
+      const int t0 = jt * 16;
+      const int rt = min(16, rank - t0);
 #pragma unroll
       for (int cc = 0; cc < kFCC; ++cc) {
         const int k = kb + cc * kInstr;
-        af[jt][cc] = pl_ld16_or0(arow + k, j < rank && k + lg * E < k1);
+        const int wb = min(kInstr, K - k);
+        af[jt][cc] = pl_ld16_or0(A + (int64_t)t0 * K + (int64_t)k * rt + li * wb + lg * E,
+                                 li < rt && k + lg * E < k1);
       }
     }
 #pragma unroll
@@ -192,11 +196,16 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   auto load_n = [&](pl_u32x4 (&bf)[kRSteps][kCT], pl_u32x4 (&yv)[kYLoads], int cb) {
 #pragma unroll
     for (int s = 0; s < kRSteps; ++s) {
-      const int jl = s * kRStep + lg * E;
+      // B's MFMA blocks: the 16-column tile at nb (nt columns), rank block
+      // j0 (wb wide) starts at nb*r8 + j0*nt
+      const int j0 = s * kRStep;
+      const int wb = min(kRStep, r8 - j0);
 #pragma unroll
       for (int ct = 0; ct < kCT; ++ct) {
-        const int n = cb + ct * 16 + li;
-        bf[s][ct] = pl_ld16_or0(Bc + (int64_t)n * r8 + jl, n < c1 && jl < r8);
+        const int nb = cb + ct * 16;
+        const int nt = min(16, N - nb);
+        bf[s][ct] = pl_ld16_or0(Bc + (int64_t)nb * r8 + (int64_t)j0 * nt + li * wb + lg * E,
+                                nb + li < c1 && j0 + lg * E < r8);
       }
     }
 #pragma unroll

@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void pl_rows_shrink(pl_rows_args a) {
   for (int j = 0; j < rank; ++j) {
     float acc = 0.f;
     for (int k = lane; k < a.K; k += 64)
-      acc += pl_ld<DT>(a.x, t * a.ldx + k) * pl_ld<DT>(A, (int64_t)j * a.K + k);
+      acc += pl_ld<DT>(a.x, t * a.ldx + k) * pl_ld<DT>(A, pl_tile_off<DT>(j, k, e->rank, a.K));
     acc = pl_wave_sum(acc);
     if (lane == 0) a.tmp[t * a.ldt + j] = acc;
   }
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void pl_rows_expand(pl_rows_args a) {
   const void* Bc = a.arena + e->b_off;
   float acc = 0.f;
   for (int j = 0; j < rank; ++j)
-    acc += pl_round<DT>(a.tmp[t * a.ldt + j]) * pl_ld<DT>(Bc, (int64_t)n * r8 + j);
+    acc += pl_round<DT>(a.tmp[t * a.ldt + j]) * pl_ld<DT>(Bc, pl_tile_off<DT>(n, j, a.N, r8));
   T* o = reinterpret_cast<T*>(a.y) + t * a.ldy + n;
   *o = (T)pl_epilogue<DT>(acc, (float)*o, e->scale, pl_round<DT>(e->scale), a.epilogue);
 }

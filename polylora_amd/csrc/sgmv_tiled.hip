@@ -173,12 +173,16 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
     pl_u32x4 af[kShortJT][kShortCC];
 #pragma unroll
     for (int jt = 0; jt < kShortJT; ++jt) {
-      const int j = rb + jt * 16 + li;
-      const T* arow = A + (int64_t)j * K + lg * E;
+      // rank tile of A's MFMA blocks (rt rows): the block of columns k
+      // starts at t0*K + k*rt and is wb wide
+      const int t0 = rb + jt * 16;
+      const int rt = min(16, rank - t0);
 #pragma unroll
       for (int cc = 0; cc < kShortCC; ++cc) {
         const int k = kb + cc * kInstr;
-        af[jt][cc] = pl_ld16_or0(arow + k, j < rank && k + lg * E < k1);
+        const int wb = min(kInstr, K - k);
+        af[jt][cc] = pl_ld16_or0(A + (int64_t)t0 * K + (int64_t)k * rt + li * wb + lg * E,
+                                 li < rt && k + lg * E < k1);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -291,12 +295,14 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_long(pl_shrink_args a) {
     auto load = [&](pl_u32x4 (&xf)[kLongRT][kLongCC], pl_u32x4 (&af)[kLongJT][kLongCC], int kb) {
 #pragma unroll
       for (int jt = 0; jt < kLongJT; ++jt) {
-        const int j = rb + jt * 16 + li;
-        const T* arow = A + (int64_t)j * K + lg * E;
+        const int t0 = rb + jt * 16;
+        const int rt = min(16, rank - t0);
 #pragma unroll
         for (int cc = 0; cc < kLongCC; ++cc) {
           const int k = kb + cc * kInstr;
-          af[jt][cc] = pl_ld16_or0(arow + k, j < rank && k + lg * E < k1);
+          const int wb = min(kInstr, K - k);
+          af[jt][cc] = pl_ld16_or0(A + (int64_t)t0 * K + (int64_t)k * rt + li * wb + lg * E,
+                                   li < rt && k + lg * E < k1);
         }
       }
 #pragma unroll
@@ -434,11 +440,16 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   auto load_block = [&](int rb) {
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      const int jl = rb + s * kStep + lg * E;
+      // B's MFMA blocks: the 16-column tile at nb (nt columns), rank block
+      // j0 (wb wide) starts at nb*r8 + j0*nt
+      const int j0 = rb + s * kStep;
+      const int wb = min(kStep, r8 - j0);
 #pragma unroll
       for (int ct = 0; ct < S::kCT; ++ct) {
-        const int n = n0 + ct * 16 + li;
-        bf[s][ct] = pl_ld16_or0(Bc + (int64_t)n * r8 + jl, n < N && jl < r8);
+        const int nb = n0 + ct * 16;
+        const int nt = min(16, N - nb);
+        bf[s][ct] = pl_ld16_or0(Bc + (int64_t)nb * r8 + (int64_t)j0 * nt + li * wb + lg * E,
+                                li < nt && j0 + lg * E < r8);
       }
     }
     // PMAX loads per thread, the plane index clamped to the last plane;

@@ -21,7 +21,7 @@ import torch
 from oracle.lora import dense_slot_tensors
 from oracle.slots import SlotCacheModel
 from polylora_amd import PolyLoraConfig, PolyLoraModel, _native
-from polylora_amd.cache import GpuAdapterCache, ModuleSpec, SlotLayout, pack_adapter
+from polylora_amd.cache import GpuAdapterCache, ModuleSpec, SlotLayout, pack_adapter, tile_rows, untile_rows
 from polylora_amd.context import LoraBatchContext, assert_right_padded, get_lora_context, use_lora_context
 from polylora_amd.store import CpuAdapterStore, CpuLayerWeights, DiskAdapterCache
 from tests import _peft
@@ -280,6 +280,55 @@ def test_pack_adapter_layout():
     assert torch.equal(B[:, 3:], torch.zeros(24, 5, dtype=torch.bfloat16))  # rank padding is zero
     assert rows[1].tolist() == [0] * 8  # module without weights: rank 0, scale 0
     assert layout.rank8_cap == 8
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("R,C", [(3, 16), (20, 72), (40, 33 * 8), (16, 64), (1, 1000), (64, 8)])
+def test_tile_rows_block_layout(dtype, R, C):
+    """The arena's MFMA-block layout: a round trip, and the position of every element."""
+    m = torch.randn(R, C).to(dtype)
+    flat = tile_rows(m)
+    assert flat.shape == (R * C,)
+    assert torch.equal(untile_rows(flat, R, C), m)
+    w = 64 // m.element_size()
+    # element (i, c) sits at 16t*C + s*rt*W + (i % 16)*wb + (c - sW): walk the
+    # tiles and blocks in storage order and compare slices of the flat image
+    pos = 0
+    for t in range(0, R, 16):
+        rt = min(16, R - t)
+        for c0 in range(0, C, w):
+            wb = min(w, C - c0)
+            assert torch.equal(flat[pos : pos + rt * wb].view(rt, wb), m[t : t + rt, c0 : c0 + wb]), (t, c0)
+            pos += rt * wb
+    assert pos == R * C
+    if C <= w:
+        assert torch.equal(flat.view(R, C), m)  # narrow matrices stay row-major
+
+
+def test_pack_adapter_block_layout_round_trip():
+    """Packed A and B of ranks and widths that use several tiles and blocks read back exactly."""
+    g = torch.Generator().manual_seed(11)
+    shapes = {"a": (72, 40), "b": (4104, 1000)}
+    store = CpuAdapterStore()
+    ws = {}
+    for name, (fin, fout) in shapes.items():
+        r = 20 if name == "a" else 40
+        A = torch.randn(fin, r, generator=g)
+        B = torch.randn(r, fout, generator=g)
+        ws[name] = (A, B, r)
+    store.add_adapter("p", {n: CpuLayerWeights(A, B, r, 0.5) for n, (A, B, r) in ws.items()})
+    layout = SlotLayout([ModuleSpec(n, i, o) for n, (i, o) in shapes.items()], torch.bfloat16, 40)
+    packed = pack_adapter(store.adapters["p"], layout)
+    for i, (name, (fin, fout)) in enumerate(shapes.items()):
+        A, B, r = ws[name]
+        r8 = (r + 7) // 8 * 8
+        a_off, b_off = int(packed.rows.view(np.int64)[i, 2]), int(packed.rows.view(np.int64)[i, 3])
+        a_img = packed.image[a_off : a_off + r * fin * 2].view(torch.bfloat16)
+        b_img = packed.image[b_off : b_off + fout * r8 * 2].view(torch.bfloat16)
+        assert torch.equal(untile_rows(a_img, r, fin), A.t().bfloat16())
+        b_rows = untile_rows(b_img, fout, r8)
+        assert torch.equal(b_rows[:, :r], B.t().bfloat16())
+        assert not b_rows[:, r:].any()  # rank padding is zero
 
 
 # --------------------------------------------------------------------------- context and model wrapper
