@@ -67,6 +67,7 @@ struct pl_fused_lds {
   enum { kPad = DT == PL_F32 ? 4 : 8 };  // 16 bytes of row padding
   enum { kTRow = kFRankMax + kPad };     // staged intermediate [token][rank]
   enum { kDRow = kFColsMax + kPad };     // per-wave delta tile [token][column]
+  enum { kXRow = 256 / (int)sizeof(T) + kPad };  // per-wave x tile [token][one step's K]
 };
 
 template <int DT, int JT>
@@ -74,7 +75,8 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
                                               const pl_slot_entry& e, int rank, int slice,
                                               pl_f32x4 (*red)[4][64],
                                               typename pl_traits<DT>::T* tt,
-                                              typename pl_traits<DT>::T* dbuf) {
+                                              typename pl_traits<DT>::T* dbuf,
+                                              typename pl_traits<DT>::T* xtile) {
   typedef typename pl_traits<DT>::T T;
   typedef typename pl_traits<DT>::T4 T4;
   typedef typename pl_traits<DT>::T8 T8;
@@ -82,6 +84,8 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   constexpr int E = pl_traits<DT>::E;
   constexpr int kInstr = 4 * E;              // K covered by one wave load
   constexpr int kStep = kFCC * kInstr;       // K covered by one shrink step
+  constexpr int kXLoads = 4;                 // x loads per lane per step (4 rows of 256 bytes each)
+  static_assert(kStep * (int)sizeof(T) == 256, "one shrink step spans 256 bytes of each x row");
   constexpr int kRStep = 4 * E;              // ranks per expand MFMA step
   constexpr int kRSteps = (16 * JT + kRStep - 1) / kRStep;
   constexpr int kCols = pl_fused_cols<DT, JT>();
@@ -101,16 +105,28 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   // ---- shrink: t[token][j] = sum_k x[token][k] * A[j][k] over this wave's K quarter
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
   const T* __restrict__ A = reinterpret_cast<const T*>(a.arena + e.a_off);
-  const bool xok = li < len;
-  const int xt = a.tok[grp.start + min(li, len - 1)];
-  const T* xrow = x + (int64_t)xt * a.ldx + lg * E;
+  // x is loaded in whole 128-byte lines: load i of a step brings rows
+  // 4i .. 4i+3, lane l taking row 4i + l/16 and 16-byte piece l%16 of the
+  // step's 256 bytes; the wave's LDS tile then hands each lane its MFMA
+  // operand chunks (row li, pieces cc*4 + lg)
+  const int xr = lane >> 4;
+  const int xp = lane & 15;
+  const T* xrow[kXLoads];
+  bool xok[kXLoads];
+#pragma unroll
+  for (int i = 0; i < kXLoads; ++i) {
+    const int r = xr + 4 * i;
+    xok[i] = r < len;
+    xrow[i] = x + (int64_t)a.tok[grp.start + min(r, len - 1)] * a.ldx + xp * E;
+  }
+  T* __restrict__ xw = xtile + wave * 16 * L::kXRow;
   const int k0 = wave * a.kw;
   const int k1 = min(K, k0 + a.kw);
 
   pl_f32x4 acc[JT];
 #pragma unroll
   for (int jt = 0; jt < JT; ++jt) acc[jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
-  auto load_k = [&](pl_u32x4 (&xf)[kFCC], pl_u32x4 (&af)[JT][kFCC], int kb) {
+  auto load_k = [&](pl_u32x4 (&xf)[kXLoads], pl_u32x4 (&af)[JT][kFCC], int kb) {
 #pragma unroll
     for (int jt = 0; jt < JT; ++jt) {
       // rank tile of A's MFMA blocks (rt rows): the block of columns k
@@ -126,20 +142,26 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
       }
     }
 #pragma unroll
-    for (int cc = 0; cc < kFCC; ++cc) {
-      const int k = kb + cc * kInstr;
-      xf[cc] = pl_ld16_or0(xrow + k, xok && k + lg * E < k1);
-    }
+    for (int i = 0; i < kXLoads; ++i) xf[i] = pl_ld16_or0(xrow[i] + kb, xok[i] && kb + xp * E < k1);
   };
-  auto mfma_k = [&](const pl_u32x4 (&xf)[kFCC], const pl_u32x4 (&af)[JT][kFCC]) {
+  auto mfma_k = [&](const pl_u32x4 (&xf)[kXLoads], const pl_u32x4 (&af)[JT][kFCC]) {
+    // through the wave's LDS tile into the MFMA layout (one wave writes and
+    // reads it, and LDS accesses of a wave complete in order)
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i)
+      *reinterpret_cast<pl_u32x4*>(xw + (xr + 4 * i) * L::kXRow + xp * E) = xf[i];
+    pl_u32x4 xm[kFCC];
+#pragma unroll
+    for (int cc = 0; cc < kFCC; ++cc)
+      xm[cc] = *reinterpret_cast<const pl_u32x4*>(xw + li * L::kXRow + cc * kInstr + lg * E);
 #pragma unroll
     for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
-      for (int cc = 0; cc < kFCC; ++cc) acc[jt] = pl_mfma_chunk<DT>(xf[cc], af[jt][cc], acc[jt]);
+      for (int cc = 0; cc < kFCC; ++cc) acc[jt] = pl_mfma_chunk<DT>(xm[cc], af[jt][cc], acc[jt]);
   };
   {
     // double-buffered K loop; steps past k1 load only zeros
-    pl_u32x4 xa[kFCC], aa[JT][kFCC], xb[kFCC], ab[JT][kFCC];
+    pl_u32x4 xa[kXLoads], aa[JT][kFCC], xb[kXLoads], ab[JT][kFCC];
     load_k(xa, aa, k0);
     for (int kb = k0; kb < k1; kb += 2 * kStep) {
       load_k(xb, ab, kb + kStep);
@@ -274,6 +296,7 @@ __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args
   __shared__ pl_f32x4 red[kFWaves][4][64];
   __shared__ __attribute__((aligned(16))) T tt[16 * L::kTRow];
   __shared__ __attribute__((aligned(16))) T dbuf[kFWaves * 16 * L::kDRow];
+  __shared__ __attribute__((aligned(16))) T xtile[kFWaves * 16 * L::kXRow];
 
   // block -> (group g, 16-token tile rt, column slice); a tile's slices go
   // to one XCD, and the groups are dealt to the XCDs in turn
@@ -296,11 +319,11 @@ __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args
 
   const int jt = (rank + 15) >> 4;
   if (JTMAX == 1 || jt == 1)
-    pl_fused_body<DT, 1>(a, grp, len, e, rank, slice, red, tt, dbuf);
+    pl_fused_body<DT, 1>(a, grp, len, e, rank, slice, red, tt, dbuf, xtile);
   else if (JTMAX == 2 || jt == 2)
-    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX>(a, grp, len, e, rank, slice, red, tt, dbuf);
+    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX>(a, grp, len, e, rank, slice, red, tt, dbuf, xtile);
   else
-    pl_fused_body<DT, JTMAX>(a, grp, len, e, rank, slice, red, tt, dbuf);
+    pl_fused_body<DT, JTMAX>(a, grp, len, e, rank, slice, red, tt, dbuf, xtile);
 }
 
 template <int DT>
