@@ -423,10 +423,11 @@ def choose_slices(plan: SgmvPlan, out_features: int) -> int:
     return max(1, min(want, most, 4))
 
 
-# Largest in_features the fused kernel takes on the forward path: its shrink
-# streams x at a lower rate than the split shrink, so for long reductions
-# (down_proj, K = 14336) the split pair is faster (measured on MI355X).
-FUSED_MAX_K = 8192
+# Largest in_features the fused kernel takes on the forward path.  Measured
+# on MI355X (Llama-3-8B prefill shapes): at K = 14336 (down_proj) one fused
+# launch per layer beats the split shrink/expand pair in the forward's launch
+# sequence; longer reductions are untried and keep the split pair.
+FUSED_MAX_K = 16384
 
 
 def fused_ok(plan: SgmvPlan, cache, in_features: int) -> bool:
