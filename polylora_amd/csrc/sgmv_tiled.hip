@@ -383,7 +383,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   __shared__ __attribute__((aligned(16))) T delta[16 * S::kLdsRow];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;
