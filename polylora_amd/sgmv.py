@@ -156,14 +156,18 @@ def _workspace(device: torch.device, stream: int, position: int = 0) -> _Workspa
 # K elements per shrink split, and the active shrink workgroups to aim for.
 # Measured on MI355X (bf16, K=4096/14336): more splits feed the shrink more
 # workgroups, but every expand workgroup re-reads every split's partial sums,
-# so about one split per 1024 of K balances the two kernels.
+# so about one split per 1024 of K balances the two kernels.  At most 8
+# splits: the expand holds one register set per split, and with 9..16 it runs
+# half as many waves per SIMD (decode down_proj, K = 14336: 14 splits 22.7 us
+# for the pair, 8 splits 21.9 us).
 _K_PER_SPLIT = 1024
 _TARGET_SHRINK_BLOCKS = 2048
+_MAX_K_SPLITS = 8
 
 
 def choose_k_splits(group_cap: int, K: int, dtype: torch.dtype) -> int:
-    """K splits of the shrink: about one per 1024 of K, fewer when the group count alone fills the GPU."""
-    by_k = max(1, -(-K // _K_PER_SPLIT))
+    """K splits of the shrink: about one per 1024 of K (at most 8), fewer when the group count alone fills the GPU."""
+    by_k = min(_MAX_K_SPLITS, max(1, -(-K // _K_PER_SPLIT)))
     by_groups = max(1, -(-_TARGET_SHRINK_BLOCKS // max(1, group_cap)))
     return min(by_k, by_groups)
 
