@@ -161,12 +161,15 @@ def test_lora_fused_bitwise_reproducible_and_triton_order(gpu):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_rows_kernels_match_oracle(gpu, dtype):
-    _announce(test="rows", dtype=dtype)
+@pytest.mark.parametrize("K,N,ranks", [(37, 30, [1, 3, 5]), (101, 75, [17, 40, 33])])
+def test_rows_kernels_match_oracle(gpu, dtype, K, N, ranks):
+    """K, N not multiples of the 16-byte chunk; the second shape spans several
+    16-row tiles and 64-byte blocks of the arena's A and B."""
+    _announce(test="rows", dtype=dtype, K=K, N=N, ranks=ranks)
     g = torch.Generator().manual_seed(30)
-    rows, M, K, N = 5, 9, 37, 30  # K, N not multiples of the 16-byte chunk
-    adapters = _adapters(g, [1, 3, 5], K, N)
-    cache = make_cache(adapters, {"m": (K, N)}, 3, 5, gpu, dtype, tiled=False)
+    rows, M = 5, 9
+    adapters = _adapters(g, ranks, K, N)
+    cache = make_cache(adapters, {"m": (K, N)}, 3, max(ranks), gpu, dtype, tiled=False)
     ids = ["a000", "__base__", "a001", "a002", "a001"]
     row_slot = cache.ensure_resident(ids)
     seq_lens = torch.tensor([9, 9, 0, 4, 11], dtype=torch.int32)
