@@ -142,4 +142,5 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def current_stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)

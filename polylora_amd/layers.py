@@ -84,34 +84,35 @@ class MultiLoraLinear(nn.Module):
         if not sgmv.tiled_shapes_ok(x2, self.out_features):
             return None
         plan = self._plan(lora_ctx, rows, row_len, seq_lens, weight_indices)
-        main = torch.cuda.current_stream(x.device)
+        main = sgmv._stream(x.device)  # handle of the caller's stream
         if sgmv.fused_ok(plan, cache, in_features):
             # long adapter segments: base GEMM, then one fused shrink+expand launch
             self._observe_call(x, _version_of(x), lora_ctx.stack)
             base = self.base_layer(x)
             base_3d = reshape(base)
             sgmv.lora_fused(x2, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name, plan,
-                            stream=main.cuda_stream)
+                            stream=main)
             return base_3d.reshape(base.shape)
         run_out = self._run_forward(x, x2, plan, lora_ctx, reshape, main)
         if run_out is not None:
             return run_out
         if rows * row_len >= OVERLAP_MIN_TOKENS:
+            main_s = torch.cuda.current_stream(x.device)
             side = sgmv.side_stream(x.device)
-            side.wait_stream(main)  # x is ready, and every earlier expand has read the side workspaces
+            side.wait_stream(main_s)  # x is ready, and every earlier expand has read the side workspaces
             with torch.cuda.stream(side):
                 shrunk = self._shrink(x, x2, plan, lora_ctx, side.cuda_stream)
             base = self.base_layer(x)
-            main.wait_stream(side)
+            main_s.wait_stream(side)
         else:
-            shrunk = self._shrink(x, x2, plan, lora_ctx, main.cuda_stream)
+            shrunk = self._shrink(x, x2, plan, lora_ctx, main)
             base = self.base_layer(x)
         base_3d = reshape(base)
         sgmv.lora_expand(shrunk, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name,
-                         stream=main.cuda_stream)
+                         stream=main)
         return base_3d.reshape(base.shape)
 
-    def _run_forward(self, x, x2, plan, lora_ctx: LoraBatchContext, reshape, main):
+    def _run_forward(self, x, x2, plan, lora_ctx: LoraBatchContext, reshape, main: int):
         """Whole outputs for a run of sibling Linears, or None to take the single-module path.
 
         Siblings are wrapped Linears that the model calls back to back on the
@@ -147,18 +148,19 @@ class MultiLoraLinear(nn.Module):
         self._observe_call(x, version, stack)
         tokens = x2.shape[0]
         if tokens >= OVERLAP_MIN_TOKENS:
+            main_s = torch.cuda.current_stream(x.device)
             side = sgmv.side_stream(x.device)
-            side.wait_stream(main)
+            side.wait_stream(main_s)
             with torch.cuda.stream(side):
                 results = sgmv.lora_shrink_stacked(x2, cache, list(run), plan, stream=side.cuda_stream)
             bases = [m.base_layer(x) for m in siblings]
-            main.wait_stream(side)
+            main_s.wait_stream(side)
         else:
-            results = sgmv.lora_shrink_stacked(x2, cache, list(run), plan, stream=main.cuda_stream)
+            results = sgmv.lora_shrink_stacked(x2, cache, list(run), plan, stream=main)
             bases = [m.base_layer(x) for m in siblings]
         outs = [reshape(b) for b in bases]
         sgmv.lora_expand_stacked(results, [o.view(tokens, o.shape[-1]) for o in outs], cache, list(run),
-                                 stream=main.cuda_stream)
+                                 stream=main)
         finished = [o.reshape(b.shape) for o, b in zip(outs, bases)]
         for name, out in zip(run[1:], finished[1:]):
             outputs[name] = (x, version, plan, out)

@@ -27,7 +27,9 @@ __all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "lora_shrink", "lora_exp
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """Handle of the current stream of `device` (one C call, no Stream object)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def _require_gpu(t: torch.Tensor, what: str) -> None:
@@ -278,12 +280,16 @@ class ShrinkResult:
     """Where a shrink left its partial sums: a workspace of the stream it ran on.
 
     ``valid`` turns False once a later shrink has reused that workspace.
+    ``batch`` is the list of results of the stacked shrink this one came from,
+    and ``ptrs`` their workspace pointers as the shrink passed them.
     """
 
-    __slots__ = ("ws", "buf", "planes", "rows", "ldt", "plan", "K")
+    __slots__ = ("ws", "buf", "planes", "rows", "ldt", "plan", "K", "batch", "ptrs")
 
     def __init__(self, ws, buf, planes, rows, ldt, plan, K) -> None:
         self.ws, self.buf, self.planes, self.rows, self.ldt, self.plan, self.K = ws, buf, planes, rows, ldt, plan, K
+        self.batch = None
+        self.ptrs = None
         ws.owner = self
 
     @property
@@ -341,6 +347,45 @@ def lora_shrink(x: torch.Tensor, cache, module_name: str, plan: SgmvPlan, *, k_s
     return lora_shrink_stacked(x, cache, [module_name], plan, k_splits=k_splits, stream=stream)[0]
 
 
+_MODULE_SETS: dict = {}
+
+
+def _module_set(cache, module_names) -> tuple:
+    """(specs, ctypes int32 array of table columns) of a module list, built once per cache and list."""
+    key = (id(cache), tuple(module_names))
+    hit = _MODULE_SETS.get(key)
+    if hit is not None and hit[0] is cache:
+        return hit[1], hit[2]
+    specs = []
+    for name in module_names:
+        spec = cache.module_specs.get(name)
+        if spec is None:
+            raise KeyError(f"module {name!r} is not in the adapter cache")
+        specs.append(spec)
+    cols = (ctypes.c_int32 * len(specs))(*(cache.module_index[name] for name in module_names))
+    _MODULE_SETS[key] = (cache, specs, cols)
+    return specs, cols
+
+
+_WS_SETS: dict = {}
+
+
+def _workspace_set(device: torch.device, stream: int, n: int, nbytes: int) -> tuple:
+    """(workspaces, buffers, ctypes pointer array) of positions 0..n-1 of (device, stream)."""
+    key = (device.index, stream, n)
+    hit = _WS_SETS.get(key)
+    if hit is None:
+        wss = [_workspace(device, stream, i) for i in range(n)]
+        hit = [wss, None, None]
+        _WS_SETS[key] = hit
+    wss = hit[0]
+    bufs = [ws.get(nbytes) for ws in wss]
+    if hit[1] is None or any(b is not c for b, c in zip(bufs, hit[1])):
+        hit[1] = bufs
+        hit[2] = (ctypes.c_void_p * n)(*(b.data_ptr() for b in bufs))
+    return wss, hit[1], hit[2]
+
+
 def lora_shrink_stacked(x: torch.Tensor, cache, module_names: list, plan: SgmvPlan, *,
                         k_splits: int | None = None, stream: int | None = None) -> list:
     """One shrink launch for wrapped Linears that read the same x (pl_sgmv_shrink_stacked).
@@ -352,12 +397,7 @@ def lora_shrink_stacked(x: torch.Tensor, cache, module_names: list, plan: SgmvPl
     n = len(module_names)
     if not 1 <= n <= _native.PL_MAX_STACKED_MODULES:
         raise ValueError(f"a shrink serves 1..{_native.PL_MAX_STACKED_MODULES} modules, got {n}")
-    specs = []
-    for name in module_names:
-        spec = cache.module_specs.get(name)
-        if spec is None:
-            raise KeyError(f"module {name!r} is not in the adapter cache")
-        specs.append(spec)
+    specs, modules = _module_set(cache, module_names)
     K = int(x.shape[1]) if x.dim() == 2 else -1
     if x.dim() != 2 or x.shape[0] != plan.tokens_cap or any(sp.in_features != K for sp in specs):
         raise ValueError(f"x must be [{plan.tokens_cap}, in_features] for every module, got {list(x.shape)}")
@@ -370,10 +410,7 @@ def lora_shrink_stacked(x: torch.Tensor, cache, module_names: list, plan: SgmvPl
         stream = _stream(x.device)
     rows = max(1, plan.tokens_cap)
     splits, planes, nbytes = _shrink_geometry(lib, dt, K, x.dtype, plan, rows, ldt, k_splits)
-    wss = [_workspace(x.device, stream, i) for i in range(n)]
-    bufs = [ws.get(nbytes) for ws in wss]
-    modules = (ctypes.c_int32 * n)(*(cache.module_index[name] for name in module_names))
-    ptrs = (ctypes.c_void_p * n)(*(b.data_ptr() for b in bufs))
+    wss, bufs, ptrs = _workspace_set(x.device, stream, n, nbytes)
     _native.check(
         lib.pl_sgmv_shrink_stacked(
             dt, x.data_ptr(), x.stride(0), K, cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index),
@@ -382,7 +419,11 @@ def lora_shrink_stacked(x: torch.Tensor, cache, module_names: list, plan: SgmvPl
         ),
         "pl_sgmv_shrink_stacked",
     )
-    return [ShrinkResult(ws, b, planes, rows, ldt, plan, K) for ws, b in zip(wss, bufs)]
+    results = [ShrinkResult(ws, b, planes, rows, ldt, plan, K) for ws, b in zip(wss, bufs)]
+    for r in results:
+        r.batch = results
+        r.ptrs = ptrs
+    return results
 
 
 def lora_expand(res: ShrinkResult, y: torch.Tensor, cache, module_name: str, *,
@@ -510,8 +551,11 @@ def lora_expand_stacked(results: list, ys: list, cache, module_names: list, *,
             raise RuntimeError("the shrink result was overwritten by a later shrink on the same workspace")
     lib = _native.load()
     r0 = results[0]
-    ws = (ctypes.c_void_p * n)(*(r.buf.data_ptr() for r in results))
-    mods = (ctypes.c_int32 * n)(*(cache.module_index[m] for m in module_names))
+    if r0.batch is not None and len(r0.batch) == n and all(a is b for a, b in zip(r0.batch, results)):
+        ws = r0.ptrs  # the shrink's own pointer array, in the same order
+    else:
+        ws = (ctypes.c_void_p * n)(*(r.buf.data_ptr() for r in results))
+    _, mods = _module_set(cache, module_names)
     yp = (ctypes.c_void_p * n)(*(y.data_ptr() for y in ys))
     ldy = (ctypes.c_int64 * n)(*(y.stride(0) for y in ys))
     nn_ = (ctypes.c_int32 * n)(*(int(y.shape[1]) for y in ys))
