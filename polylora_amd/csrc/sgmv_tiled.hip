@@ -98,20 +98,25 @@ struct pl_expand_shape {
 
 // ------------------------------------------------------------ short groups
 // Groups of at most 16 tokens (decode: a handful of rows per adapter) move
-// little data per workgroup, so these kernels are built for latency: every
-// load a wave needs is issued before its first MFMA, one memory round trip
-// per workgroup for ranks up to 64.
+// little data per workgroup, so these kernels are built for latency: all of
+// a step's loads are issued before its first MFMA.
 //
 // Shrink: one workgroup per (group, pass of 32 ranks, K split, served
 // module); ranks beyond the slot's rank exit before loading anything.  The
 // four waves split the split's K range (256 per wave for 2-byte types) and
 // their partials are summed in LDS in a fixed order, as in pl_shrink_tiled.
+// A step is 2 chunks (64 K per lane group) of both rank tiles, so a wave
+// walks its K range in a few short steps with 48 VGPRs; eight waves per SIMD
+// then hide each other's latency better than fewer waves holding their whole
+// K range in flight (measured on MI355X, decode shapes: 8 chunks per step,
+// 120 VGPRs, 4 waves per SIMD: q_proj 5.9 us, down_proj 14.2 us; 2 chunks:
+// 5.5 and 13.5 us).
 //
 // Expand: one workgroup per (group, 256-column chunk).  The shrink planes of
 // the group's tokens are summed once per workgroup (all planes' loads in
 // flight together), rounded to T and staged in LDS as [token][rank]; B and
 // the y rows are loaded at the same time.
-constexpr int kShortCC = 8;      // 16-byte chunks per lane per shrink step
+constexpr int kShortCC = 2;      // 16-byte chunks per lane per shrink step
 constexpr int kShortJT = 2;      // 16-rank tiles per shrink workgroup
 constexpr int kShortRanks = 16 * kShortJT;
 constexpr int kShortMaxPlanes = 16;

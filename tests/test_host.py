@@ -399,16 +399,18 @@ def test_library_host_side_errors_without_gpu():
     assert lib.pl_plan_group_capacity(256, 1, 65, 64) == 4 + 64
     assert lib.pl_plan_group_capacity(256, 1, 65, 16) == 16 + 64
     assert lib.pl_plan_group_capacity(32, 1024, 9, 64) == 512 + 8
-    # split planes: whole wave steps (16-token groups: 256 elements of a
-    # 2-byte type per wave, 128 of fp32; 64-token groups: 64 and 32), four
+    # split planes: whole wave steps (16-token groups: 64 elements of a
+    # 2-byte type per wave step, 32 of fp32; 64-token groups: 64 and 32), four
     # waves per split, at most the requested count and at most 16
     assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 8, 64) == 8
     assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 100, 64) == 16
-    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 100, 16) == 4
+    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 100, 16) == 16  # capped at 16 planes
+    assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 4, 16) == 4
     assert lib.pl_shrink_planes(_native.PL_BF16, 4096, 2, 16) == 2
     assert lib.pl_shrink_planes(_native.PL_BF16, 14336, 100, 16) == 14
     assert lib.pl_shrink_planes(_native.PL_BF16, 65536, 100, 16) == 16
-    assert lib.pl_shrink_planes(_native.PL_F32, 4096, 100, 16) == 8
+    assert lib.pl_shrink_planes(_native.PL_F32, 4096, 100, 16) == 16
+    assert lib.pl_shrink_planes(_native.PL_BF16, 100, 16, 16) == 1  # one 64-element step covers a split
     assert lib.pl_shrink_planes(_native.PL_BF16, 14336, 16, 64) == 14
     assert lib.pl_shrink_planes(_native.PL_F32, 768, 4, 64) == 3
     assert lib.pl_shrink_planes(_native.PL_BF16, 32, 1, 16) == 1
