@@ -37,7 +37,6 @@
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kYRowsPerPass = 8;  // 256 threads, 32 lanes per tile row
 
 // Modules one shrink launch serves: wrapped Linears fed the same input x.
 constexpr int kMaxJobs = PL_MAX_STACKED_MODULES;
@@ -85,15 +84,21 @@ struct pl_expand_args {
   int32_t N[kMaxJobs];
 };
 
-// Columns of y one expand wave owns: 64 for 2-byte types, 32 for fp32, so
-// that a block's tile row is always 512 bytes.
+// Columns of y one expand wave owns: 128 bytes of each row (64 for 2-byte
+// types, 32 for fp32), so that a workgroup's tile row is 512 bytes; the 256
+// threads read and write the tile's y rows 16 bytes at a time, kYLanes
+// lanes per row.
+constexpr int kExpandWaveBytes = 128;
 template <int DT>
 struct pl_expand_shape {
-  enum { kColsWave = DT == PL_F32 ? 32 : 64 };
+  typedef typename pl_traits<DT>::T T;
+  enum { kColsWave = kExpandWaveBytes / (int)sizeof(T) };
   enum { kCT = kColsWave / 16 };
   enum { kChunk = kWaves * kColsWave };
-  enum { kPad = DT == PL_F32 ? 4 : 8 };  // 16 bytes of LDS row padding
+  enum { kPad = 16 / (int)sizeof(T) };  // 16 bytes of LDS row padding
   enum { kLdsRow = kChunk + kPad };
+  enum { kYLanes = kChunk * (int)sizeof(T) / 16 };  // lanes per y row
+  enum { kYRowsPerPass = 256 / kYLanes };          // y rows per pass of the workgroup
 };
 
 // ------------------------------------------------------------ short groups
@@ -383,7 +388,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   constexpr int kStep = 4 * E;                        // rank slots per MFMA step
   constexpr int kSteps = kShortRankBlock / kStep;     // MFMA steps per staged rank block
   constexpr int kTRow = kShortRankBlock + S::kPad;    // LDS row of the staged intermediate
-  constexpr int kYPer = 16 / kYRowsPerPass;           // y rows per thread
+  constexpr int kYPer = 16 / S::kYRowsPerPass;        // y rows per thread
   __shared__ __attribute__((aligned(16))) T tt[16 * kTRow];
   __shared__ __attribute__((aligned(16))) T delta[16 * S::kLdsRow];
 
@@ -426,13 +431,13 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   // first rank block, then the y rows (their addresses need the indices).
   // The load counter retires in order, so waiting for the indices does not
   // wait for B or the planes.
-  const int yq = tid & 31;
-  const int yr0 = tid >> 5;
+  const int yq = tid % S::kYLanes;
+  const int yr0 = tid / S::kYLanes;
   const int ycol = n_base + yq * E;
   T* __restrict__ y = reinterpret_cast<T*>(a.y[job]);
   int yt[kYPer];
 #pragma unroll
-  for (int i = 0; i < kYPer; ++i) yt[i] = a.tok[grp.start + min(yr0 + kYRowsPerPass * i, len - 1)];
+  for (int i = 0; i < kYPer; ++i) yt[i] = a.tok[grp.start + min(yr0 + S::kYRowsPerPass * i, len - 1)];
 
   // planes -> staged intermediate: thread (token sp, ranks rb + sq .. +4)
   const int sp = tid >> 4;
@@ -502,7 +507,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   T* yptr[kYPer];
 #pragma unroll
   for (int i = 0; i < kYPer; ++i) {
-    const int r = yr0 + kYRowsPerPass * i;
+    const int r = yr0 + S::kYRowsPerPass * i;
     yptr[i] = (r < len && ycol < N) ? y + (int64_t)yt[i] * a.ldy[job] + ycol : nullptr;
     yv[i] = pl_ld16_or0(yptr[i], yptr[i] != nullptr);
   }
@@ -529,7 +534,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
 #pragma unroll
   for (int i = 0; i < kYPer; ++i) {
     if (yptr[i] != nullptr) {
-      const int r = yr0 + kYRowsPerPass * i;
+      const int r = yr0 + S::kYRowsPerPass * i;
       const pl_u32x4 dv = *reinterpret_cast<const pl_u32x4*>(delta + r * S::kLdsRow + yq * E);
       if constexpr (E == 8) {
         T8 yy = __builtin_bit_cast(T8, yv[i]);
@@ -729,7 +734,8 @@ int prepare_expand(pl_expand_args& a, int32_t dtype, void* const* ws, int32_t ld
   }
   const int E = pl_chunk_elems(dtype);
   const int es = pl_elem_size(dtype);
-  const int chunk = 4 * (dtype == PL_F32 ? 32 : 64);
+  const int chunk = dtype == PL_F32 ? (int)pl_expand_shape<PL_F32>::kChunk
+                                    : (int)pl_expand_shape<PL_BF16>::kChunk;
   int64_t n_chunks = 0;
   for (int j = 0; j < n_jobs; ++j) {
     int st = check_common(dtype, arena, table, num_modules, modules[j], tok, groups, meta,
