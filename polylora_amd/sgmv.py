@@ -280,21 +280,29 @@ class ShrinkResult:
     """Where a shrink left its partial sums: a workspace of the stream it ran on.
 
     ``valid`` turns False once a later shrink has reused that workspace.
-    ``batch`` is the list of results of the stacked shrink this one came from,
-    and ``ptrs`` their workspace pointers as the shrink passed them.
+    ``batch`` identifies the stacked shrink this result came from (its
+    workspace pointer array) and ``index`` its position in it.
     """
 
-    __slots__ = ("ws", "buf", "planes", "rows", "ldt", "plan", "K", "batch", "ptrs")
+    __slots__ = ("ws", "buf", "planes", "rows", "ldt", "plan", "K", "batch", "index")
 
-    def __init__(self, ws, buf, planes, rows, ldt, plan, K) -> None:
+    def __init__(self, ws, buf, planes, rows, ldt, plan, K, batch=None, index=0) -> None:
         self.ws, self.buf, self.planes, self.rows, self.ldt, self.plan, self.K = ws, buf, planes, rows, ldt, plan, K
-        self.batch = None
-        self.ptrs = None
+        self.batch, self.index = batch, index
         ws.owner = self
 
     @property
     def valid(self) -> bool:
         return self.ws.owner is self
+
+
+class _ShrinkBatch:
+    """The modules of one stacked shrink: their count and workspace pointers as passed to the kernel."""
+
+    __slots__ = ("n", "ptrs")
+
+    def __init__(self, n: int, ptrs) -> None:
+        self.n, self.ptrs = n, ptrs
 
 
 MAX_STACKED_MODULES = _native.PL_MAX_STACKED_MODULES
@@ -347,15 +355,13 @@ def lora_shrink(x: torch.Tensor, cache, module_name: str, plan: SgmvPlan, *, k_s
     return lora_shrink_stacked(x, cache, [module_name], plan, k_splits=k_splits, stream=stream)[0]
 
 
-_MODULE_SETS: dict = {}
-
-
 def _module_set(cache, module_names) -> tuple:
     """(specs, ctypes int32 array of table columns) of a module list, built once per cache and list."""
-    key = (id(cache), tuple(module_names))
-    hit = _MODULE_SETS.get(key)
-    if hit is not None and hit[0] is cache:
-        return hit[1], hit[2]
+    sets = cache.__dict__.setdefault("_module_sets", {})
+    key = tuple(module_names)
+    hit = sets.get(key)
+    if hit is not None:
+        return hit
     specs = []
     for name in module_names:
         spec = cache.module_specs.get(name)
@@ -363,7 +369,7 @@ def _module_set(cache, module_names) -> tuple:
             raise KeyError(f"module {name!r} is not in the adapter cache")
         specs.append(spec)
     cols = (ctypes.c_int32 * len(specs))(*(cache.module_index[name] for name in module_names))
-    _MODULE_SETS[key] = (cache, specs, cols)
+    sets[key] = (specs, cols)
     return specs, cols
 
 
@@ -372,7 +378,7 @@ _WS_SETS: dict = {}
 
 def _workspace_set(device: torch.device, stream: int, n: int, nbytes: int) -> tuple:
     """(workspaces, buffers, ctypes pointer array) of positions 0..n-1 of (device, stream)."""
-    key = (device.index, stream, n)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream, n)
     hit = _WS_SETS.get(key)
     if hit is None:
         wss = [_workspace(device, stream, i) for i in range(n)]
@@ -419,11 +425,8 @@ def lora_shrink_stacked(x: torch.Tensor, cache, module_names: list, plan: SgmvPl
         ),
         "pl_sgmv_shrink_stacked",
     )
-    results = [ShrinkResult(ws, b, planes, rows, ldt, plan, K) for ws, b in zip(wss, bufs)]
-    for r in results:
-        r.batch = results
-        r.ptrs = ptrs
-    return results
+    batch = _ShrinkBatch(n, ptrs)
+    return [ShrinkResult(ws, b, planes, rows, ldt, plan, K, batch, i) for i, (ws, b) in enumerate(zip(wss, bufs))]
 
 
 def lora_expand(res: ShrinkResult, y: torch.Tensor, cache, module_name: str, *,
@@ -551,8 +554,9 @@ def lora_expand_stacked(results: list, ys: list, cache, module_names: list, *,
             raise RuntimeError("the shrink result was overwritten by a later shrink on the same workspace")
     lib = _native.load()
     r0 = results[0]
-    if r0.batch is not None and len(r0.batch) == n and all(a is b for a, b in zip(r0.batch, results)):
-        ws = r0.ptrs  # the shrink's own pointer array, in the same order
+    batch = r0.batch
+    if batch is not None and batch.n == n and all(r.batch is batch and r.index == i for i, r in enumerate(results)):
+        ws = batch.ptrs  # the shrink's own pointer array, in the same order
     else:
         ws = (ctypes.c_void_p * n)(*(r.buf.data_ptr() for r in results))
     _, mods = _module_set(cache, module_names)

@@ -331,6 +331,22 @@ def test_pack_adapter_block_layout_round_trip():
         assert not b_rows[:, r:].any()  # rank padding is zero
 
 
+def test_shrink_result_ownership():
+    """A shrink result stays valid until a later shrink takes over its workspace."""
+    from polylora_amd import sgmv
+
+    class _Ws:
+        owner = None
+
+    ws0, ws1 = _Ws(), _Ws()
+    batch = sgmv._ShrinkBatch(2, None)
+    a = sgmv.ShrinkResult(ws0, None, 4, 16, 8, None, 64, batch, 0)
+    b = sgmv.ShrinkResult(ws1, None, 4, 16, 8, None, 64, batch, 1)
+    assert a.valid and b.valid and a.batch is b.batch and (a.index, b.index) == (0, 1)
+    c = sgmv.ShrinkResult(ws0, None, 4, 16, 8, None, 64)
+    assert c.valid and not a.valid and b.valid and c.batch is None
+
+
 # --------------------------------------------------------------------------- context and model wrapper
 
 
