@@ -108,7 +108,7 @@ struct pl_expand_shape {
 //
 // Shrink: one workgroup per (group, pass of 32 ranks, K split, served
 // module); ranks beyond the slot's rank exit before loading anything.  The
-// four waves split the split's K range (256 per wave for 2-byte types) and
+// four waves split the split's K range (256 each for a split of 1024) and
 // their partials are summed in LDS in a fixed order, as in pl_shrink_tiled.
 // A step is 2 chunks (64 K per lane group) of both rank tiles, so a wave
 // walks its K range in a few short steps with 48 VGPRs; eight waves per SIMD
