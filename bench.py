@@ -437,6 +437,32 @@ class FusedLaunch:
         self.n.check(self.lib.pl_lora_fused(*self.args), "pl_lora_fused")
 
 
+class StackedFusedLaunch:
+    """Sibling Linears fed the same x: one fused shrink+expand launch for all (pl_lora_fused_stacked)."""
+
+    def __init__(self, x, ys, cache, modules, plan, slices=None):
+        import ctypes
+
+        from polylora_amd import _native, sgmv
+
+        self.lib, self.n = _native.load(), _native
+        n = len(modules)
+        n_slices = slices if slices is not None else sgmv.choose_slices(plan, min(int(y.shape[1]) for y in ys))
+        self.mods = (ctypes.c_int32 * n)(*(cache.module_index[m] for m in modules))
+        self.yptrs = (ctypes.c_void_p * n)(*(y.data_ptr() for y in ys))
+        self.ldys = (ctypes.c_int64 * n)(*(y.stride(0) for y in ys))
+        self.Ns = (ctypes.c_int32 * n)(*(int(y.shape[1]) for y in ys))
+        self.args = (_native.dtype_code(x.dtype), x.data_ptr(), x.stride(0), int(x.shape[1]), n, self.mods,
+                     self.yptrs, self.ldys, self.Ns, cache.arena.data_ptr(), cache.table.data_ptr(),
+                     len(cache.module_index), cache.rank8_cap, plan.tok.data_ptr(), plan.groups.data_ptr(),
+                     plan.meta.data_ptr(), max(1, plan.group_cap), plan.group_tokens, n_slices,
+                     _native.PL_EPI_FALLBACK, torch.cuda.current_stream().cuda_stream)
+        self.keep = (x, ys, plan)
+
+    def __call__(self):
+        self.n.check(self.lib.pl_lora_fused_stacked(*self.args), "pl_lora_fused_stacked")
+
+
 def time_launches(fns: list, reps: int, warmup: int = 2) -> float:
     """Milliseconds per pass over `fns`, launched back to back on the current stream between two events."""
     stream = torch.cuda.current_stream()
@@ -673,23 +699,32 @@ def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Te
     # The forward's own launch sequence: sibling Linears that read the same
     # input (q/k/v, gate/up) share one stacked shrink and one stacked expand,
     # as MultiLoraLinear does once it has seen a forward.
-    # Modules whose plan suits the fused kernel take one pl_lora_fused launch
-    # each (MultiLoraLinear does the same).
+    # Where the plan suits the fused kernel the siblings share one
+    # pl_lora_fused_stacked launch and the other modules take one pl_lora_fused
+    # launch each (MultiLoraLinear does the same).  Every module type writes its
+    # own y, so siblings in one launch never share an output.
     by_name = {s.name: s for s in pm.module_specs}
+    leaf_ys = {}
+    for s in pm.module_specs:
+        leaf = s.name.rsplit(".", 1)[-1]
+        if leaf not in leaf_ys:
+            leaf_ys[leaf] = torch.randn(T, s.out_features, generator=gen, device=device, dtype=torch.bfloat16)
     stacks, fused, seq = [], [], []
     for s in pm.module_specs:
-        if sgmv.fused_ok(plan, cache, s.in_features):
-            f = FusedLaunch(xs[s.in_features], ys[s.out_features], cache, s.name, plan)
-            fused.append(f)
-            seq.append(f)
-            continue
         parent, leaf = s.name.rsplit(".", 1)
         if leaf in ("k_proj", "v_proj", "up_proj"):
             continue
         group = {"q_proj": ("q_proj", "k_proj", "v_proj"), "gate_proj": ("gate_proj", "up_proj")}.get(leaf, (leaf,))
         names = [f"{parent}.{g}" for g in group if f"{parent}.{g}" in by_name]
         k = by_name[names[0]].in_features
-        st = StackedLaunch(xs[k], [ys[by_name[n].out_features] for n in names], cache, names, plan)
+        outs = [leaf_ys[n.rsplit(".", 1)[-1]] for n in names]
+        if sgmv.fused_ok(plan, cache, k):
+            f = (FusedLaunch(xs[k], outs[0], cache, names[0], plan) if len(names) == 1
+                 else StackedFusedLaunch(xs[k], outs, cache, names, plan))
+            fused.append(f)
+            seq.append(f)
+            continue
+        st = StackedLaunch(xs[k], outs, cache, names, plan)
         stacks.append(st)
         seq.extend((st.shrink, st.expand))
     total_ms = time_launches(seq, reps)
@@ -862,19 +897,26 @@ def run_decode(args) -> dict:
 
 
 def prefill_bytes(pm, adapter_ids: list, lens: list) -> dict:
-    """Algorithmic bytes and flops of one prefill forward's 224 shrink+expand pairs over the valid tokens."""
+    """Algorithmic bytes and flops of one prefill forward's 224 shrink+expand pairs over the valid tokens.
+
+    "total" reads x once per module; "shared_x" reads it once per set of
+    sibling Linears fed the same input (q/k/v, gate/up), as one stacked launch
+    does.
+    """
     es = 2
-    xy = ab = flops = 0
+    xy = ab = flops = repeat_x = 0
     uniq = sorted(set(adapter_ids))
     for spec in pm.module_specs:
+        sibling = spec.name.rsplit(".", 1)[-1] in ("k_proj", "v_proj", "up_proj")
         for aid, n in zip(adapter_ids, lens):
             w = pm.adapter_store.adapters[aid].layers[spec.name]
             xy += es * n * spec.in_features + 2 * es * n * spec.out_features
+            repeat_x += es * n * spec.in_features if sibling else 0
             flops += 2 * n * w.rank * (spec.in_features + spec.out_features)
         for aid in uniq:
             w = pm.adapter_store.adapters[aid].layers[spec.name]
             ab += es * w.rank * (spec.in_features + spec.out_features)
-    return {"total": xy + ab, "flops": flops}
+    return {"total": xy + ab, "shared_x": xy + ab - repeat_x, "flops": flops}
 
 
 def run_prefill(args, pm) -> dict:
@@ -899,7 +941,7 @@ def run_prefill(args, pm) -> dict:
     ctx = pm.prepare_lora_context(adapter_ids, mask, B, S, device)
     nb = prefill_bytes(pm, adapter_ids, [int(v) for v in lens])
     out = {"rows": B, "seq": S, "valid_tokens": int(lens.sum()), "lora_bytes_per_forward": nb["total"],
-           "lora_flops_per_forward": nb["flops"]}
+           "lora_bytes_per_forward_shared_x": nb["shared_x"], "lora_flops_per_forward": nb["flops"]}
     with torch.inference_mode():
         kt = time_lora_ops(pm, adapter_ids, S, torch.as_tensor(lens, dtype=torch.int32, device=device), reps=2)
         kern_ms = kt["pairs_ms"]
@@ -907,6 +949,7 @@ def run_prefill(args, pm) -> dict:
         out["lora_kernels_ms"] = round(kern_ms, 3)
         out["lora_kernels_gbs"] = round(nb["total"] / (kern_ms * 1e-3) / 1e9, 1)
         out["lora_kernels_pct_hbm"] = round(100 * nb["total"] / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
+        out["lora_kernels_gbs_shared_x"] = round(nb["shared_x"] / (kern_ms * 1e-3) / 1e9, 1)
         out["lora_kernels_mfma_tflops"] = round(nb["flops"] / (kern_ms * 1e-3) / 1e12, 2)
         out["lora_kernels_pct_mfma_bf16"] = round(100 * nb["flops"] / (kern_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 3)
         out["lora_kernels_shrink_ms"] = round(kt["shrink_ms"], 3)

@@ -25,6 +25,8 @@
  *                          the LoRA half of MultiLoraLinear.forward)
  *   pl_lora_fused       <- src/polylora/sgmv.py:63-138 and :178-275 in one
  *                          launch (both Triton kernels of layers.py:45-53)
+ *   pl_lora_fused_stacked <- the same for sibling Linears in one launch
+ *                          (sgmv.py:141-175 stack_num reads x once)
  *   pl_slot_upload      <- src/polylora/cache.py:119-150 _load_adapter_into_slot
  *                          (host->device copy of one adapter into a slot)
  *   pl_check_right_padded <- src/polylora/context.py:37-45 assert_right_padded
@@ -222,6 +224,19 @@ int pl_lora_fused(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
                   int32_t module, int32_t ldt, const int32_t* tok, const pl_group* groups,
                   const int32_t* meta, int64_t group_cap, int32_t group_tokens, int32_t slices,
                   int32_t epilogue, void* stream);
+
+/* pl_lora_fused for 1..PL_MAX_STACKED_MODULES sibling Linears fed the same
+ * x [*, ldx] (K columns): module modules[i] adds into y[i] [*, ldy[i]] of
+ * N[i] columns.  A tile's modules run side by side on one XCD, so its x rows
+ * come from HBM once and from that XCD's L2 for the other modules.  modules,
+ * y, ldy and N are host arrays of n_modules entries; every other argument
+ * is as for pl_lora_fused. */
+int pl_lora_fused_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K, int32_t n_modules,
+                          const int32_t* modules, void* const* y, const int64_t* ldy,
+                          const int32_t* N, const void* arena, const pl_slot_entry* table,
+                          int32_t num_modules, int32_t ldt, const int32_t* tok,
+                          const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                          int32_t group_tokens, int32_t slices, int32_t epilogue, void* stream);
 
 /* Row-based LoRA on the slot arena for shapes the tiled path rejects
  * (any K, N, strides, alignment).  Writes y[b*row_len+m] for m < seq_len[b].

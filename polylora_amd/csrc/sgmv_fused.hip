@@ -38,20 +38,16 @@ constexpr int pl_fused_cols() {
   return (JT >= 4 || (DT == PL_F32 && JT >= 2)) ? 64 : kFColsMax;
 }
 constexpr int kFSliceMax = 8;   // column slices per tile
+constexpr int kFJobs = PL_MAX_STACKED_MODULES;  // sibling modules one launch serves
 
 struct pl_fused_args {
   const void* x;
   int64_t ldx;
   int32_t K;
   int32_t kw;  // K per wave, a multiple of the shrink step
-  void* y;
-  int64_t ldy;
-  int32_t N;
-  int32_t nw;  // columns per wave, a multiple of kFColsMax
   const char* arena;
   const pl_slot_entry* table;
   int32_t num_modules;
-  int32_t module;
   const int32_t* tok;
   const pl_group* groups;
   const int32_t* meta;
@@ -59,6 +55,12 @@ struct pl_fused_args {
   int32_t sub;     // 16-token tiles per plan group (1 or 4)
   int32_t slices;  // column slices per tile
   int32_t epilogue;
+  int32_t n_jobs;  // modules served, 1..kFJobs, all fed the same x
+  int32_t module[kFJobs];  // table column of each served module
+  void* y[kFJobs];
+  int64_t ldy[kFJobs];
+  int32_t N[kFJobs];
+  int32_t nw[kFJobs];  // columns per wave, a multiple of kFColsMax
 };
 
 template <int DT>
@@ -72,7 +74,7 @@ struct pl_fused_lds {
 
 template <int DT, int JT>
 __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_group& grp, int len,
-                                              const pl_slot_entry& e, int rank, int slice,
+                                              const pl_slot_entry& e, int rank, int job, int slice,
                                               pl_f32x4 (*red)[4][64],
                                               typename pl_traits<DT>::T* tt,
                                               typename pl_traits<DT>::T* dbuf,
@@ -100,7 +102,7 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   const int li = lane & 15;
   const int lg = lane >> 4;
   const int K = a.K;
-  const int N = a.N;
+  const int N = a.N[job];
 
   // ---- shrink: t[token][j] = sum_k x[token][k] * A[j][k] over this wave's K quarter
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
@@ -190,13 +192,14 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   __syncthreads();
 
   // ---- expand over this wave's columns
-  const int c0 = (slice * kFWaves + wave) * a.nw;
-  const int c1 = min(N, c0 + a.nw);
+  const int c0 = (slice * kFWaves + wave) * a.nw[job];
+  const int c1 = min(N, c0 + a.nw[job]);
   const int r8 = e.rank8;
   const float scale = e.scale;
   const float scale_t = pl_round<DT>(scale);
   const T* __restrict__ Bc = reinterpret_cast<const T*>(a.arena + e.b_off);
-  T* __restrict__ y = reinterpret_cast<T*>(a.y);
+  T* __restrict__ y = reinterpret_cast<T*>(a.y[job]);
+  const int64_t ldy = a.ldy[job];
   T* __restrict__ dw = dbuf + wave * 16 * L::kDRow;
 
   pl_u32x4 tf[kRSteps];  // MFMA operand: (token li, ranks s*kRStep + lg*E ..)
@@ -212,7 +215,7 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   for (int i = 0; i < kYLoads; ++i) {
     const int r = yr0 + kYRows * i;
     yok[i] = r < len;
-    yrow[i] = y + (int64_t)a.tok[grp.start + min(r, len - 1)] * a.ldy + yq * E;
+    yrow[i] = y + (int64_t)a.tok[grp.start + min(r, len - 1)] * ldy + yq * E;
   }
 
   auto load_n = [&](pl_u32x4 (&bf)[kRSteps][kCT], pl_u32x4 (&yv)[kYLoads], int cb) {
@@ -298,19 +301,23 @@ __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args
   __shared__ __attribute__((aligned(16))) T dbuf[kFWaves * 16 * L::kDRow];
   __shared__ __attribute__((aligned(16))) T xtile[kFWaves * 16 * L::kXRow];
 
-  // block -> (group g, 16-token tile rt, column slice); a tile's slices go
-  // to one XCD, and the groups are dealt to the XCDs in turn
-  const pl_xcd_slot ws = pl_xcd_map(a.sub * a.slices);
+  // block -> (group g, 16-token tile rt, column slice, served module job); a
+  // group's work items go to one XCD, the modules of one tile and slice are
+  // adjacent (they read the same x rows, which the later ones find in that
+  // XCD's L2), and the groups are dealt to the XCDs in turn
+  const pl_xcd_slot ws = pl_xcd_map(a.n_jobs * a.sub * a.slices);
   const int g = ws.g;
   if (g >= a.group_cap) return;
-  const int rt = ws.j / a.slices;
-  const int slice = ws.j - rt * a.slices;
+  const int job = ws.j % a.n_jobs;
+  const int ts = ws.j / a.n_jobs;
+  const int rt = ts / a.slices;
+  const int slice = ts - rt * a.slices;
   const int n_groups = a.meta[0];
   pl_group grp = a.groups[g];
   grp.start += rt * 16;
   const int len = min(grp.len - rt * 16, 16);
   if (g >= n_groups || len <= 0) return;
-  const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module];
+  const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module[job]];
   const int rank = min(e.rank, kFRankMax);  // the host guarantees rank <= kFRankMax
   if (rank <= 0) return;
 
@@ -319,16 +326,16 @@ __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args
 
   const int jt = (rank + 15) >> 4;
   if (JTMAX == 1 || jt == 1)
-    pl_fused_body<DT, 1>(a, grp, len, e, rank, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, 1>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
   else if (JTMAX == 2 || jt == 2)
-    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX>(a, grp, len, e, rank, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
   else
-    pl_fused_body<DT, JTMAX>(a, grp, len, e, rank, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, JTMAX>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
 }
 
 template <int DT>
 int launch_fused(const pl_fused_args& a, int jtmax, hipStream_t stream) {
-  const dim3 grid((unsigned)pl_xcd_grid(a.group_cap, (int64_t)a.sub * a.slices));
+  const dim3 grid((unsigned)pl_xcd_grid(a.group_cap, (int64_t)a.n_jobs * a.sub * a.slices));
   if (jtmax <= 1)
     hipLaunchKernelGGL((pl_lora_fused_tile<DT, 1>), grid, dim3(kFThreads), 0, stream, a);
   else if (jtmax == 2)
@@ -342,21 +349,23 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
-extern "C" int pl_lora_fused(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
-                             int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
-                             int32_t num_modules, int32_t module, int32_t ldt, const int32_t* tok,
-                             const pl_group* groups, const int32_t* meta, int64_t group_cap,
-                             int32_t group_tokens, int32_t slices, int32_t epilogue, void* stream) {
+extern "C" int pl_lora_fused_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K,
+                                     int32_t n_modules, const int32_t* modules, void* const* y,
+                                     const int64_t* ldy, const int32_t* N, const void* arena,
+                                     const pl_slot_entry* table, int32_t num_modules, int32_t ldt,
+                                     const int32_t* tok, const pl_group* groups,
+                                     const int32_t* meta, int64_t group_cap, int32_t group_tokens,
+                                     int32_t slices, int32_t epilogue, void* stream) {
   if (dtype != PL_F32 && dtype != PL_BF16 && dtype != PL_F16) {
     pl_set_error("unsupported dtype code %d", dtype);
     return PL_ERR_ARG;
   }
-  if (!x || !y || !arena || !table || !tok || !groups || !meta) {
+  if (!x || !arena || !table || !tok || !groups || !meta || !modules || !y || !ldy || !N) {
     pl_set_error("pl_lora_fused: null pointer");
     return PL_ERR_ARG;
   }
-  if (num_modules <= 0 || module < 0 || module >= num_modules) {
-    pl_set_error("module index %d out of range [0, %d)", module, num_modules);
+  if (n_modules < 1 || n_modules > kFJobs) {
+    pl_set_error("pl_lora_fused serves 1..%d modules (got %d)", kFJobs, n_modules);
     return PL_ERR_ARG;
   }
   if (group_tokens != PL_GROUP_TOKENS_SHORT && group_tokens != PL_GROUP_TOKENS_LONG) {
@@ -377,37 +386,52 @@ extern "C" int pl_lora_fused(int32_t dtype, const void* x, int64_t ldx, int32_t 
   }
   const int E = dtype == PL_F32 ? 4 : 8;
   const int es = dtype == PL_F32 ? 4 : 2;
-  if (K <= 0 || N <= 0 || ldx < K || ldy < N) {
-    pl_set_error("bad fused sizes K=%d N=%d ldx=%lld ldy=%lld", K, N, (long long)ldx,
-                 (long long)ldy);
-    return PL_ERR_ARG;
-  }
-  if (K % E != 0 || N % E != 0 || (ldx * es) % 16 != 0 || (ldy * es) % 16 != 0 || !aligned16(x) ||
-      !aligned16(y) || !aligned16(arena)) {
-    pl_set_error("pl_lora_fused needs K, N multiples of %d and 16-byte aligned rows", E);
+  if (K <= 0 || ldx < K || K % E != 0 || (ldx * es) % 16 != 0 || !aligned16(x) ||
+      !aligned16(arena)) {
+    pl_set_error("pl_lora_fused needs K > 0, a multiple of %d, and 16-byte aligned x rows "
+                 "(K=%d ldx=%lld)", E, K, (long long)ldx);
     return PL_ERR_ALIGN;
   }
   if (group_cap < 0 || group_cap > (int64_t)1 << 24) {
     pl_set_error("group capacity %lld out of range", (long long)group_cap);
     return PL_ERR_LIMIT;
   }
-  if (group_cap == 0) return PL_OK;
   pl_fused_args a;
+  for (int j = 0; j < n_modules; ++j) {
+    if (num_modules <= 0 || modules[j] < 0 || modules[j] >= num_modules) {
+      pl_set_error("module index %d out of range [0, %d)", modules[j], num_modules);
+      return PL_ERR_ARG;
+    }
+    if (!y[j] || N[j] <= 0 || ldy[j] < N[j]) {
+      pl_set_error("bad fused output %d: N=%d ldy=%lld", j, N[j], (long long)ldy[j]);
+      return PL_ERR_ARG;
+    }
+    if (N[j] % E != 0 || (ldy[j] * es) % 16 != 0 || !aligned16(y[j])) {
+      pl_set_error("pl_lora_fused needs N a multiple of %d and 16-byte aligned y rows", E);
+      return PL_ERR_ALIGN;
+    }
+    a.module[j] = modules[j];
+    a.y[j] = y[j];
+    a.ldy[j] = ldy[j];
+    a.N[j] = N[j];
+    const int64_t per_wave =
+        ((int64_t)N[j] + (int64_t)slices * kFWaves - 1) / ((int64_t)slices * kFWaves);
+    a.nw[j] = (int32_t)((per_wave + kFColsMax - 1) / kFColsMax * kFColsMax);
+  }
+  if (pl_xcd_grid(group_cap, (int64_t)n_modules * (group_tokens / 16) * slices) > 0x7fffffffLL) {
+    pl_set_error("pl_lora_fused: grid of %lld groups too large", (long long)group_cap);
+    return PL_ERR_LIMIT;
+  }
+  if (group_cap == 0) return PL_OK;
   a.x = x;
   a.ldx = ldx;
   a.K = K;
   const int64_t step = (int64_t)kFCC * 4 * E;
   const int64_t kq = (K + kFWaves - 1) / kFWaves;
   a.kw = (int32_t)((kq + step - 1) / step * step);
-  a.y = y;
-  a.ldy = ldy;
-  a.N = N;
-  const int64_t per_wave = ((int64_t)N + (int64_t)slices * kFWaves - 1) / ((int64_t)slices * kFWaves);
-  a.nw = (int32_t)((per_wave + kFColsMax - 1) / kFColsMax * kFColsMax);
   a.arena = reinterpret_cast<const char*>(arena);
   a.table = table;
   a.num_modules = num_modules;
-  a.module = module;
   a.tok = tok;
   a.groups = groups;
   a.meta = meta;
@@ -415,6 +439,7 @@ extern "C" int pl_lora_fused(int32_t dtype, const void* x, int64_t ldx, int32_t 
   a.sub = group_tokens / 16;
   a.slices = slices;
   a.epilogue = epilogue;
+  a.n_jobs = n_modules;
   const int jtmax = (ldt + 15) / 16;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
@@ -422,4 +447,14 @@ extern "C" int pl_lora_fused(int32_t dtype, const void* x, int64_t ldx, int32_t 
     case PL_F16: return launch_fused<PL_F16>(a, jtmax, s);
     default: return launch_fused<PL_F32>(a, jtmax, s);
   }
+}
+
+extern "C" int pl_lora_fused(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
+                             int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
+                             int32_t num_modules, int32_t module, int32_t ldt, const int32_t* tok,
+                             const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                             int32_t group_tokens, int32_t slices, int32_t epilogue, void* stream) {
+  return pl_lora_fused_stacked(dtype, x, ldx, K, 1, &module, &y, &ldy, &N, arena, table,
+                               num_modules, ldt, tok, groups, meta, group_cap, group_tokens, slices,
+                               epilogue, stream);
 }

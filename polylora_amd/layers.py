@@ -85,7 +85,11 @@ class MultiLoraLinear(nn.Module):
             return None
         plan = self._plan(lora_ctx, rows, row_len, seq_lens, weight_indices)
         main = sgmv._stream(x.device)  # handle of the caller's stream
-        if sgmv.fused_ok(plan, cache, in_features):
+        fused = sgmv.fused_ok(plan, cache, in_features)
+        run_out = self._run_forward(x, x2, plan, lora_ctx, reshape, main, fused)
+        if run_out is not None:
+            return run_out
+        if fused:
             # long adapter segments: base GEMM, then one fused shrink+expand launch
             self._observe_call(x, _version_of(x), lora_ctx.stack)
             base = self.base_layer(x)
@@ -93,9 +97,6 @@ class MultiLoraLinear(nn.Module):
             sgmv.lora_fused(x2, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name, plan,
                             stream=main)
             return base_3d.reshape(base.shape)
-        run_out = self._run_forward(x, x2, plan, lora_ctx, reshape, main)
-        if run_out is not None:
-            return run_out
         if rows * row_len >= OVERLAP_MIN_TOKENS:
             main_s = torch.cuda.current_stream(x.device)
             side = sgmv.side_stream(x.device)
@@ -112,7 +113,7 @@ class MultiLoraLinear(nn.Module):
                          stream=main)
         return base_3d.reshape(base.shape)
 
-    def _run_forward(self, x, x2, plan, lora_ctx: LoraBatchContext, reshape, main: int):
+    def _run_forward(self, x, x2, plan, lora_ctx: LoraBatchContext, reshape, main: int, fused: bool):
         """Whole outputs for a run of sibling Linears, or None to take the single-module path.
 
         Siblings are wrapped Linears that the model calls back to back on the
@@ -147,7 +148,14 @@ class MultiLoraLinear(nn.Module):
             return None
         self._observe_call(x, version, stack)
         tokens = x2.shape[0]
-        if tokens >= OVERLAP_MIN_TOKENS:
+        if fused:
+            # long adapter segments: every sibling's base GEMM, then one fused
+            # launch for all of them
+            bases = [m.base_layer(x) for m in siblings]
+            outs = [reshape(b) for b in bases]
+            sgmv.lora_fused_stacked(x2, [o.view(tokens, o.shape[-1]) for o in outs], cache, list(run), plan,
+                                    stream=main)
+        elif tokens >= OVERLAP_MIN_TOKENS:
             main_s = torch.cuda.current_stream(x.device)
             side = sgmv.side_stream(x.device)
             side.wait_stream(main_s)
@@ -158,9 +166,10 @@ class MultiLoraLinear(nn.Module):
         else:
             results = sgmv.lora_shrink_stacked(x2, cache, list(run), plan, stream=main)
             bases = [m.base_layer(x) for m in siblings]
-        outs = [reshape(b) for b in bases]
-        sgmv.lora_expand_stacked(results, [o.view(tokens, o.shape[-1]) for o in outs], cache, list(run),
-                                 stream=main)
+        if not fused:
+            outs = [reshape(b) for b in bases]
+            sgmv.lora_expand_stacked(results, [o.view(tokens, o.shape[-1]) for o in outs], cache, list(run),
+                                     stream=main)
         finished = [o.reshape(b.shape) for o, b in zip(outs, bases)]
         for name, out in zip(run[1:], finished[1:]):
             outputs[name] = (x, version, plan, out)

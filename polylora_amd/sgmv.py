@@ -529,6 +529,49 @@ def lora_fused(
     return y
 
 
+def lora_fused_stacked(
+    x: torch.Tensor,
+    ys: list,
+    cache,
+    module_names: list,
+    plan: SgmvPlan,
+    *,
+    epilogue: int = _native.PL_EPI_FALLBACK,
+    slices: int | None = None,
+    stream: int | None = None,
+) -> list:
+    """lora_fused for sibling Linears fed the same x, in one launch (pl_lora_fused_stacked): ys[i] in place.
+
+    A tile's modules run side by side on one XCD, so x comes from HBM once.
+    """
+    _require_gpu(x, "lora_fused_stacked")
+    n = len(module_names)
+    if not 1 <= n <= _native.PL_MAX_STACKED_MODULES or len(ys) != n:
+        raise ValueError(f"a fused launch serves 1..{_native.PL_MAX_STACKED_MODULES} modules with one y each")
+    for y, name in zip(ys, module_names):
+        _check_operands(x, y, cache, name, plan.tokens_cap)
+        if not _tiled_ok(x, y):
+            raise ValueError("lora_fused needs 16-byte aligned rows and K, N multiples of 16 bytes")
+    if cache.rank8_cap > FUSED_MAX_RANK:
+        raise ValueError(f"lora_fused takes ranks up to {FUSED_MAX_RANK}; the cache holds up to {cache.rank8_cap}")
+    lib = _native.load()
+    _, mods = _module_set(cache, module_names)
+    yp = (ctypes.c_void_p * n)(*(y.data_ptr() for y in ys))
+    ldy = (ctypes.c_int64 * n)(*(y.stride(0) for y in ys))
+    nn_ = (ctypes.c_int32 * n)(*(int(y.shape[1]) for y in ys))
+    n_slices = slices if slices is not None else choose_slices(plan, min(int(y.shape[1]) for y in ys))
+    _native.check(
+        lib.pl_lora_fused_stacked(
+            _native.dtype_code(x.dtype), x.data_ptr(), x.stride(0), int(x.shape[1]), n, mods, yp, ldy, nn_,
+            cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), cache.rank8_cap,
+            plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap),
+            plan.group_tokens, n_slices, epilogue, _stream(x.device) if stream is None else stream,
+        ),
+        "pl_lora_fused_stacked",
+    )
+    return ys
+
+
 def lora_expand_stacked(results: list, ys: list, cache, module_names: list, *,
                         epilogue: int = _native.PL_EPI_FALLBACK, stream: int | None = None) -> list:
     """One expand launch for sibling Linears (pl_sgmv_expand_stacked): results[i] -> ys[i] in place.

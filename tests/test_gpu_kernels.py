@@ -160,6 +160,42 @@ def test_lora_fused_bitwise_reproducible_and_triton_order(gpu):
     torch.testing.assert_close(y3.float(), y1.float(), rtol=2e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("dtype,group_tokens", [(torch.bfloat16, 16), (torch.bfloat16, 64), (torch.float32, 64)])
+def test_stacked_fused_equals_separate(gpu, dtype, group_tokens):
+    """pl_lora_fused_stacked over q/k/v-like modules == one pl_lora_fused per module, bit for bit, and the oracle."""
+    _announce(test="stacked_fused", dtype=dtype, group_tokens=group_tokens)
+    g = torch.Generator().manual_seed(61)
+    K, rows, M = 1024, 6, 90
+    shapes = {"q": (K, 1024), "k": (K, 256), "v": (K, 136)}
+    adapters = {}
+    for i, r in enumerate([8, 24, 64]):
+        adapters[f"s{i}"] = {m: peft_layer(g, fi, fo, r, 2.0 * r) for m, (fi, fo) in shapes.items() if not (i == 1 and m == "k")}
+    cache = make_cache(adapters, shapes, 3, 64, gpu, dtype)
+    ids = list(adapters) + ["__base__"]
+    row_slot = cache.ensure_resident([ids[i % 4] for i in range(rows)])
+    seq_lens = torch.tensor([90, 17, 64, 0, 33, 81], dtype=torch.int32)
+    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), M, cache.num_slots, group_tokens=group_tokens)
+    x = torch.randn(rows, M, K, generator=g).to(dtype)
+    base = {m: torch.randn(rows, M, fo, generator=g).to(dtype) for m, (fi, fo) in shapes.items()}
+    xg = x.to(gpu).view(-1, K)
+    for slices in (None, 1, 3):
+        sep = {}
+        for m in shapes:
+            y = base[m].to(gpu).view(rows * M, -1)
+            sgmv.lora_fused(xg, y, cache, m, plan, slices=slices)
+            sep[m] = y
+        ys = [base[m].to(gpu).view(rows * M, -1) for m in shapes]
+        sgmv.lora_fused_stacked(xg, ys, cache, list(shapes), plan, slices=slices)
+        for m, y in zip(shapes, ys):
+            assert torch.equal(y, sep[m]), (m, slices)
+    for m in shapes:
+        A, B, rk, sc = oracle_slot_tensors(cache, adapters, m, dtype)
+        expect = reference_forward(x, base[m], seq_lens, row_slot.cpu(), A, B, rk, sc)
+        torch.testing.assert_close(sep[m].cpu().view(rows, M, -1), expect, **tol_for(dtype))
+    with pytest.raises(ValueError, match="modules with one y each"):
+        sgmv.lora_fused_stacked(xg, ys[:2], cache, list(shapes), plan)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("K,N,ranks", [(37, 30, [1, 3, 5]), (101, 75, [17, 40, 33])])
 def test_rows_kernels_match_oracle(gpu, dtype, K, N, ranks):

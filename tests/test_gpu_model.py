@@ -401,6 +401,25 @@ def test_llama_prefill_right_padded_bf16(gpu):
     valid = mask.bool()
     diff = (got[valid].float() - want[valid].float()).norm() / want[valid].float().norm()
     assert float(diff) < 1e-2, float(diff)
+    # the first forward learned q/k/v and gate/up as siblings; the second runs each
+    # run in one stacked fused launch and gives the same output bit for bit
+    runs = set(pm.adapter_cache.stacked_runs.values())
+    assert len(runs) == 2 * cfg.num_hidden_layers, runs
+    calls = []
+    stacked_fused = sgmv.lora_fused_stacked
+
+    def counting(*a, **k):
+        calls.append(tuple(a[3]))
+        return stacked_fused(*a, **k)
+
+    sgmv.lora_fused_stacked = counting
+    try:
+        with torch.inference_mode():
+            again = pm(input_ids=ids, attention_mask=mask, adapter_ids=adapter_ids).last_hidden_state
+    finally:
+        sgmv.lora_fused_stacked = stacked_fused
+    assert sorted(calls) == sorted(runs), (calls, runs)
+    assert torch.equal(again, got)
 
 
 def test_adapter_churn_matches_fallback(gpu):
