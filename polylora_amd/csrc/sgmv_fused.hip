@@ -122,6 +122,20 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
     xrow[i] = x + (int64_t)a.tok[grp.start + min(r, len - 1)] * a.ldx + xp * E;
   }
   T* __restrict__ xw = xtile + wave * 16 * L::kXRow;
+  // y rows of the expand, addressed now so that their token indices are not
+  // a round trip between the two phases
+  T* __restrict__ y = reinterpret_cast<T*>(a.y[job]);
+  const int64_t ldy = a.ldy[job];
+  const int yq = lane % kYLanes;
+  const int yr0 = lane / kYLanes;
+  T* yrow[kYLoads];
+  bool yok[kYLoads];
+#pragma unroll
+  for (int i = 0; i < kYLoads; ++i) {
+    const int r = yr0 + kYRows * i;
+    yok[i] = r < len;
+    yrow[i] = y + (int64_t)a.tok[grp.start + min(r, len - 1)] * ldy + yq * E;
+  }
   const int k0 = wave * a.kw;
   const int k1 = min(K, k0 + a.kw);
 
@@ -162,10 +176,13 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
       for (int cc = 0; cc < kFCC; ++cc) acc[jt] = pl_mfma_chunk<DT>(xm[cc], af[jt][cc], acc[jt]);
   };
   {
-    // double-buffered K loop; steps past k1 load only zeros
+    // double-buffered K loop over pairs of steps; the last pair is peeled
+    // so that no loads past k1 are left in flight when the shrink ends (its
+    // second step may lie past k1 and then loads only zeros)
     pl_u32x4 xa[kXLoads], aa[JT][kFCC], xb[kXLoads], ab[JT][kFCC];
     load_k(xa, aa, k0);
-    for (int kb = k0; kb < k1; kb += 2 * kStep) {
+    int kb = k0;
+    for (; kb + 2 * kStep < k1; kb += 2 * kStep) {
       load_k(xb, ab, kb + kStep);
       __builtin_amdgcn_sched_barrier(0);
       mfma_k(xa, aa);
@@ -173,51 +190,22 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
       __builtin_amdgcn_sched_barrier(0);
       mfma_k(xb, ab);
     }
+    if (kb < k1) {
+      load_k(xb, ab, kb + kStep);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_k(xa, aa);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_k(xb, ab);
+    }
   }
-  // the four wave partials summed in a fixed order, rounded once to T;
-  // acc[jt][v] holds (token 4*lg+v, rank jt*16+li)
-#pragma unroll
-  for (int jt = 0; jt < JT; ++jt) red[wave][jt][lane] = acc[jt];
-  __syncthreads();
-  if (tid < JT * 64) {
-    const int jt = tid >> 6;
-    const int l = tid & 63;
-    pl_f32x4 s = red[0][jt][l];
-#pragma unroll
-    for (int w = 1; w < kFWaves; ++w) s += red[w][jt][l];
-    const int j = jt * 16 + (l & 15);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) tt[((l >> 4) * 4 + v) * L::kTRow + j] = (T)(j < rank ? s[v] : 0.f);
-  }
-  __syncthreads();
 
-  // ---- expand over this wave's columns
+  // ---- expand set-up; its first steps' loads need nothing from the shrink
+  // and are issued before the partials are reduced
   const int c0 = (slice * kFWaves + wave) * a.nw[job];
   const int c1 = min(N, c0 + a.nw[job]);
   const int r8 = e.rank8;
-  const float scale = e.scale;
-  const float scale_t = pl_round<DT>(scale);
   const T* __restrict__ Bc = reinterpret_cast<const T*>(a.arena + e.b_off);
-  T* __restrict__ y = reinterpret_cast<T*>(a.y[job]);
-  const int64_t ldy = a.ldy[job];
   T* __restrict__ dw = dbuf + wave * 16 * L::kDRow;
-
-  pl_u32x4 tf[kRSteps];  // MFMA operand: (token li, ranks s*kRStep + lg*E ..)
-#pragma unroll
-  for (int s = 0; s < kRSteps; ++s)
-    tf[s] = *reinterpret_cast<const pl_u32x4*>(tt + li * L::kTRow + s * kRStep + lg * E);
-
-  const int yq = lane % kYLanes;
-  const int yr0 = lane / kYLanes;
-  T* yrow[kYLoads];
-  bool yok[kYLoads];
-#pragma unroll
-  for (int i = 0; i < kYLoads; ++i) {
-    const int r = yr0 + kYRows * i;
-    yok[i] = r < len;
-    yrow[i] = y + (int64_t)a.tok[grp.start + min(r, len - 1)] * ldy + yq * E;
-  }
-
   auto load_n = [&](pl_u32x4 (&bf)[kRSteps][kCT], pl_u32x4 (&yv)[kYLoads], int cb) {
 #pragma unroll
     for (int s = 0; s < kRSteps; ++s) {
@@ -236,6 +224,38 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
 #pragma unroll
     for (int i = 0; i < kYLoads; ++i) yv[i] = pl_ld16_or0(yrow[i] + cb, yok[i] && cb + yq * E < c1);
   };
+  // a ring of kFStages steps: the loads of the next kFStages-1 steps are in
+  // flight while one is applied; steps past c1 load only zeros
+  pl_u32x4 bring[kFStages][kRSteps][kCT], yring[kFStages][kYLoads];
+#pragma unroll
+  for (int st = 0; st < kFStages - 1; ++st) load_n(bring[st], yring[st], c0 + st * kCols);
+
+  // the four wave partials summed in a fixed order, rounded once to T;
+  // acc[jt][v] holds (token 4*lg+v, rank jt*16+li)
+#pragma unroll
+  for (int jt = 0; jt < JT; ++jt) red[wave][jt][lane] = acc[jt];
+  __syncthreads();
+  if (tid < JT * 64) {
+    const int jt = tid >> 6;
+    const int l = tid & 63;
+    pl_f32x4 s = red[0][jt][l];
+#pragma unroll
+    for (int w = 1; w < kFWaves; ++w) s += red[w][jt][l];
+    const int j = jt * 16 + (l & 15);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tt[((l >> 4) * 4 + v) * L::kTRow + j] = (T)(j < rank ? s[v] : 0.f);
+  }
+  __syncthreads();
+
+  // ---- expand over this wave's columns
+  const float scale = e.scale;
+  const float scale_t = pl_round<DT>(scale);
+
+  pl_u32x4 tf[kRSteps];  // MFMA operand: (token li, ranks s*kRStep + lg*E ..)
+#pragma unroll
+  for (int s = 0; s < kRSteps; ++s)
+    tf[s] = *reinterpret_cast<const pl_u32x4*>(tt + li * L::kTRow + s * kRStep + lg * E);
+
   auto apply_n = [&](const pl_u32x4 (&bf)[kRSteps][kCT], const pl_u32x4 (&yv)[kYLoads], int cb) {
     pl_f32x4 d[kCT];
 #pragma unroll
@@ -275,11 +295,6 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
     // the next step rewrites the tile only after these reads (in-order LDS)
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   };
-  // a ring of kFStages steps: the loads of the next kFStages-1 steps are in
-  // flight while one is applied; steps past c1 load only zeros
-  pl_u32x4 bring[kFStages][kRSteps][kCT], yring[kFStages][kYLoads];
-#pragma unroll
-  for (int st = 0; st < kFStages - 1; ++st) load_n(bring[st], yring[st], c0 + st * kCols);
   for (int cb = c0; cb < c1; cb += kFStages * kCols) {
 #pragma unroll
     for (int st = 0; st < kFStages; ++st) {
