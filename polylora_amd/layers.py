@@ -39,6 +39,20 @@ def _version_of(x: torch.Tensor):
     return x._version
 
 
+def _siblings(cache: GpuAdapterCache, run: tuple, element_size: int):
+    """The wrapped Linears of a sibling run, or None when one is missing or has an output width
+    that is not whole 16-byte chunks (x itself is checked by the caller); memoized per cache."""
+    memo = cache.__dict__.setdefault("_run_siblings", {})
+    key = (run, element_size, len(cache.wrapped))
+    hit = memo.get(key, False)
+    if hit is False:
+        mods = [cache.wrapped.get(name) for name in run]
+        chunk = 16 // element_size
+        ok = all(m is not None and m.out_features % chunk == 0 for m in mods)
+        hit = memo[key] = mods if ok else None
+    return hit
+
+
 class MultiLoraLinear(nn.Module):
     def __init__(self, base_layer: nn.Linear, module_name: str, cache: GpuAdapterCache) -> None:
         super().__init__()
@@ -143,8 +157,8 @@ class MultiLoraLinear(nn.Module):
         run = cache.stacked_runs.get((self.module_name, tuple(x.shape)))
         if run is None or len(run) < 2:
             return None
-        siblings = [cache.wrapped.get(name) for name in run]
-        if any(m is None for m in siblings) or not all(sgmv.tiled_shapes_ok(x2, m.out_features) for m in siblings):
+        siblings = _siblings(cache, run, x2.element_size())
+        if siblings is None:
             return None
         self._observe_call(x, version, stack)
         tokens = x2.shape[0]

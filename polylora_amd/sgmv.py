@@ -75,7 +75,7 @@ class SgmvPlan:
     """
 
     __slots__ = ("rows", "row_len", "num_slots", "group_tokens", "tokens_cap", "group_cap", "tok", "groups", "meta",
-                 "row_slot", "seq_lens", "distinct_slots")
+                 "row_slot", "seq_lens", "distinct_slots", "launch_args")
 
     def __init__(self, row_slot: torch.Tensor, seq_lens: torch.Tensor, row_len: int, num_slots: int,
                  distinct_slots: int | None = None, group_tokens: int | None = None) -> None:
@@ -99,6 +99,9 @@ class SgmvPlan:
         self.tok = torch.empty(max(1, self.tokens_cap), dtype=torch.int32, device=dev)
         self.groups = torch.empty((max(1, self.group_cap), 4), dtype=torch.int32, device=dev)
         self.meta = torch.empty(4, dtype=torch.int32, device=dev)
+        # the plan's arguments of the fused entry points, in their order
+        self.launch_args = (self.tok.data_ptr(), self.groups.data_ptr(), self.meta.data_ptr(), max(1, self.group_cap),
+                            self.group_tokens)
         self.row_slot, self.seq_lens = row_slot, seq_lens
         _native.check(
             lib.pl_plan_build(
@@ -175,19 +178,14 @@ def choose_k_splits(group_cap: int, K: int, dtype: torch.dtype) -> int:
 
 
 def _tiled_ok(x: torch.Tensor, y: torch.Tensor) -> bool:
-    chunk = 4 if x.dtype == torch.float32 else 8
-    K = x.shape[1]
-    N = y.shape[1]
-    es = x.element_size()
+    """Unit column stride, 16-byte aligned base pointers, and K, N and both row strides whole 16-byte chunks."""
+    xs, ys = x.stride(), y.stride()
+    chunk = 16 // x.element_size()  # elements per 16 bytes
     return (
-        x.stride(1) == 1
-        and y.stride(1) == 1
-        and K % chunk == 0
-        and N % chunk == 0
-        and (x.stride(0) * es) % 16 == 0
-        and (y.stride(0) * es) % 16 == 0
-        and x.data_ptr() % 16 == 0
-        and y.data_ptr() % 16 == 0
+        xs[1] == 1
+        and ys[1] == 1
+        and (x.shape[1] | y.shape[1] | xs[0] | ys[0]) % chunk == 0
+        and (x.data_ptr() | y.data_ptr()) % 16 == 0
     )
 
 
@@ -196,11 +194,12 @@ def _check_operands(x: torch.Tensor, y: torch.Tensor, cache, module_name: str, t
     spec = cache.module_specs.get(module_name)
     if spec is None:
         raise KeyError(f"module {module_name!r} is not in the adapter cache")
-    if x.dim() != 2 or y.dim() != 2:
+    xs, ys = x.shape, y.shape
+    if len(xs) != 2 or len(ys) != 2:
         raise ValueError("x and y must be 2-D [tokens, features]")
-    if x.shape[0] != tokens or y.shape[0] != tokens:
-        raise ValueError(f"x / y have {x.shape[0]} / {y.shape[0]} token rows; the plan covers {tokens}")
-    if x.shape[1] != spec.in_features or y.shape[1] != spec.out_features:
+    if xs[0] != tokens or ys[0] != tokens:
+        raise ValueError(f"x / y have {xs[0]} / {ys[0]} token rows; the plan covers {tokens}")
+    if xs[1] != spec.in_features or ys[1] != spec.out_features:
         raise ValueError(
             f"module {module_name!r} is {spec.in_features} -> {spec.out_features}, "
             f"got x [.., {x.shape[1]}] and y [.., {y.shape[1]}]"
@@ -234,7 +233,9 @@ def lora_apply(
     if not _tiled_ok(x, y):
         return lora_apply_rows(x, y, cache, module_name, plan.row_slot, plan.seq_lens, plan.row_len, epilogue=epilogue)
     if k_splits is None and fused_ok(plan, cache, int(x.shape[1])):
-        return lora_fused(x, y, cache, module_name, plan, epilogue=epilogue)
+        # operands checked above; fused_ok guarantees the rank limit
+        _fused_launch(x, y, cache, module_name, plan, epilogue, None, _stream(x.device))
+        return y
     lib = _native.load()
     dt = _native.dtype_code(x.dtype)
     K = int(x.shape[1])
@@ -371,6 +372,23 @@ def _module_set(cache, module_names) -> tuple:
     cols = (ctypes.c_int32 * len(specs))(*(cache.module_index[name] for name in module_names))
     sets[key] = (specs, cols)
     return specs, cols
+
+
+def _fused_set(cache, module_names) -> tuple:
+    """_module_set plus the output-pointer, row-stride and column-count arrays of one stacked fused launch.
+
+    The arrays are reused call after call (the pointers and strides are
+    rewritten before each launch; a launch reads them when it is enqueued).
+    """
+    sets = cache.__dict__.setdefault("_fused_sets", {})
+    key = tuple(module_names)
+    hit = sets.get(key)
+    if hit is None:
+        specs, cols = _module_set(cache, module_names)
+        n = len(specs)
+        cnt = (ctypes.c_int32 * n)(*(spec.out_features for spec in specs))
+        hit = sets[key] = (specs, cols, ((ctypes.c_void_p * n)(), (ctypes.c_int64 * n)(), cnt))
+    return hit
 
 
 _WS_SETS: dict = {}
@@ -514,19 +532,35 @@ def lora_fused(
         raise ValueError("lora_fused needs 16-byte aligned rows and K, N multiples of 16 bytes")
     if cache.rank8_cap > FUSED_MAX_RANK:
         raise ValueError(f"lora_fused takes ranks up to {FUSED_MAX_RANK}; the cache holds up to {cache.rank8_cap}")
-    lib = _native.load()
-    N = int(y.shape[1])
-    n_slices = slices if slices is not None else choose_slices(plan, N)
+    _fused_launch(x, y, cache, module_name, plan, epilogue, slices, _stream(x.device) if stream is None else stream)
+    return y
+
+
+def _cache_args(cache, module_name: str) -> tuple:
+    """(arena, table, module count, table column, rank capacity) of a module as pl_lora_fused takes them.
+
+    The arena and table are allocated once with the cache, so the tuple is
+    built once per cache and module.
+    """
+    args = cache.__dict__.setdefault("_launch_args", {})
+    hit = args.get(module_name)
+    if hit is None:
+        hit = args[module_name] = (cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index),
+                                   cache.module_index[module_name], cache.rank8_cap)
+    return hit
+
+
+def _fused_launch(x, y, cache, module_name: str, plan: SgmvPlan, epilogue: int, slices, stream: int) -> None:
+    """pl_lora_fused on operands the caller has checked."""
+    N = y.shape[1]
     _native.check(
-        lib.pl_lora_fused(
-            _native.dtype_code(x.dtype), x.data_ptr(), x.stride(0), int(x.shape[1]), y.data_ptr(), y.stride(0), N,
-            cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), cache.module_index[module_name],
-            cache.rank8_cap, plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap),
-            plan.group_tokens, n_slices, epilogue, _stream(x.device) if stream is None else stream,
+        _native.load().pl_lora_fused(
+            _native.dtype_code(x.dtype), x.data_ptr(), x.stride(0), x.shape[1], y.data_ptr(), y.stride(0), N,
+            *_cache_args(cache, module_name), *plan.launch_args,
+            choose_slices(plan, N) if slices is None else slices, epilogue, stream,
         ),
         "pl_lora_fused",
     )
-    return y
 
 
 def lora_fused_stacked(
@@ -548,24 +582,35 @@ def lora_fused_stacked(
     n = len(module_names)
     if not 1 <= n <= _native.PL_MAX_STACKED_MODULES or len(ys) != n:
         raise ValueError(f"a fused launch serves 1..{_native.PL_MAX_STACKED_MODULES} modules with one y each")
-    for y, name in zip(ys, module_names):
-        _check_operands(x, y, cache, name, plan.tokens_cap)
-        if not _tiled_ok(x, y):
+    # x and the first output in full, the others against the first
+    _check_operands(x, ys[0], cache, module_names[0], plan.tokens_cap)
+    if not _tiled_ok(x, ys[0]):
+        raise ValueError("lora_fused needs 16-byte aligned rows and K, N multiples of 16 bytes")
+    specs, mods, arrays = _fused_set(cache, module_names)
+    chunk = 16 // x.element_size()
+    for y, spec in zip(ys[1:], specs[1:]):
+        if spec.in_features != x.shape[1]:
+            raise ValueError(f"module {spec.name!r} takes {spec.in_features} inputs; x has {x.shape[1]}")
+        shape, st = y.shape, y.stride()
+        if len(shape) != 2 or shape[0] != plan.tokens_cap or shape[1] != spec.out_features:
+            raise ValueError(f"y of {spec.name!r} must be [{plan.tokens_cap}, {spec.out_features}], got {list(shape)}")
+        if y.dtype != cache.dtype or y.device != cache.device:
+            raise TypeError(f"y {y.dtype} on {y.device} must match the adapter cache ({cache.dtype} on {cache.device})")
+        if st[1] != 1 or (shape[1] | st[0]) % chunk or y.data_ptr() % 16:
             raise ValueError("lora_fused needs 16-byte aligned rows and K, N multiples of 16 bytes")
     if cache.rank8_cap > FUSED_MAX_RANK:
         raise ValueError(f"lora_fused takes ranks up to {FUSED_MAX_RANK}; the cache holds up to {cache.rank8_cap}")
-    lib = _native.load()
-    _, mods = _module_set(cache, module_names)
-    yp = (ctypes.c_void_p * n)(*(y.data_ptr() for y in ys))
-    ldy = (ctypes.c_int64 * n)(*(y.stride(0) for y in ys))
-    nn_ = (ctypes.c_int32 * n)(*(int(y.shape[1]) for y in ys))
-    n_slices = slices if slices is not None else choose_slices(plan, min(int(y.shape[1]) for y in ys))
+    yp, ldy, nn_ = arrays
+    for i, y in enumerate(ys):
+        yp[i] = y.data_ptr()
+        ldy[i] = y.stride(0)
+    n_slices = slices if slices is not None else choose_slices(plan, min(spec.out_features for spec in specs))
+    arena, table, n_mod, _, ldt = _cache_args(cache, module_names[0])
     _native.check(
-        lib.pl_lora_fused_stacked(
-            _native.dtype_code(x.dtype), x.data_ptr(), x.stride(0), int(x.shape[1]), n, mods, yp, ldy, nn_,
-            cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), cache.rank8_cap,
-            plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), max(1, plan.group_cap),
-            plan.group_tokens, n_slices, epilogue, _stream(x.device) if stream is None else stream,
+        _native.load().pl_lora_fused_stacked(
+            _native.dtype_code(x.dtype), x.data_ptr(), x.stride(0), x.shape[1], n, mods, yp, ldy, nn_,
+            arena, table, n_mod, ldt, *plan.launch_args, n_slices, epilogue,
+            _stream(x.device) if stream is None else stream,
         ),
         "pl_lora_fused_stacked",
     )
