@@ -509,6 +509,18 @@ def run_isolated(args) -> dict:
     def apply(wl):
         sgmv.lora_apply(wl.x, wl.y, wl.cache, "op", wl.plan)
 
+    # Per-kernel timings first (they also bring the GPU to its working clocks
+    # before the timed steps): the split shrink + expand, for comparison (the
+    # kernels a plan with few tokens per adapter would use), and the fused
+    # kernel alone with its arguments bound once.
+    reps = max(10, args.steps // n_sets)
+    launches = [SgmvLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets]
+    sh_ms = time_launches([l.shrink for l in launches], reps) / n_sets
+    ex_ms = time_launches([l.expand for l in launches], reps) / n_sets
+    fused = sgmv.fused_ok(base_set.plan, base_set.cache, K)
+    if fused:
+        f_ms = time_launches([FusedLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets], reps) / n_sets
+
     # a step is one lora_apply call through the Python host API (plan already
     # built, inputs resident); the calls queue back to back, so the device,
     # not the host, sets the pace
@@ -522,18 +534,9 @@ def run_isolated(args) -> dict:
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
-
-    reps = max(10, args.steps // n_sets)
-    # the split shrink + expand, for comparison (and the kernels a plan with
-    # few tokens per adapter would use)
-    launches = [SgmvLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets]
-    sh_ms = time_launches([l.shrink for l in launches], reps) / n_sets
-    ex_ms = time_launches([l.expand for l in launches], reps) / n_sets
-    fused = sgmv.fused_ok(base_set.plan, base_set.cache, K)
     value = nb["total"] / (ms * 1e-3) / 1e9
     if fused:
         # lora_apply runs the fused kernel: one launch carries all of the op's bytes
-        f_ms = time_launches([FusedLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets], reps) / n_sets
         kernel, k_bytes, k_ms = "pl_lora_fused_tile<bf16>", nb["total"], f_ms
     else:
         kernel, k_bytes, k_ms = "pl_expand_short<bf16>", nb["expand"], ex_ms
