@@ -16,6 +16,7 @@ There is no CPU path: CPU tensors raise.
 from __future__ import annotations
 
 import ctypes
+import threading
 
 import torch
 
@@ -377,11 +378,13 @@ def _module_set(cache, module_names) -> tuple:
 def _fused_set(cache, module_names) -> tuple:
     """_module_set plus the output-pointer, row-stride and column-count arrays of one stacked fused launch.
 
-    The arrays are reused call after call (the pointers and strides are
-    rewritten before each launch; a launch reads them when it is enqueued).
+    The arrays are reused call after call by the calling thread (the pointers
+    and strides are rewritten before each launch, which reads them when it is
+    enqueued); another thread gets its own, since the library call runs
+    without the GIL.
     """
     sets = cache.__dict__.setdefault("_fused_sets", {})
-    key = tuple(module_names)
+    key = (tuple(module_names), threading.get_ident())
     hit = sets.get(key)
     if hit is None:
         specs, cols = _module_set(cache, module_names)

@@ -160,13 +160,15 @@ def test_lora_fused_bitwise_reproducible_and_triton_order(gpu):
     torch.testing.assert_close(y3.float(), y1.float(), rtol=2e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("dtype,group_tokens", [(torch.bfloat16, 16), (torch.bfloat16, 64), (torch.float32, 64)])
-def test_stacked_fused_equals_separate(gpu, dtype, group_tokens):
+@pytest.mark.parametrize("dtype,group_tokens,n_mod", [(torch.bfloat16, 16, 3), (torch.bfloat16, 64, 3),
+                                                     (torch.float32, 64, 3), (torch.float16, 16, 4)])
+def test_stacked_fused_equals_separate(gpu, dtype, group_tokens, n_mod):
     """pl_lora_fused_stacked over q/k/v-like modules == one pl_lora_fused per module, bit for bit, and the oracle."""
-    _announce(test="stacked_fused", dtype=dtype, group_tokens=group_tokens)
+    _announce(test="stacked_fused", dtype=dtype, group_tokens=group_tokens, n_mod=n_mod)
     g = torch.Generator().manual_seed(61)
     K, rows, M = 1024, 6, 90
-    shapes = {"q": (K, 1024), "k": (K, 256), "v": (K, 136)}
+    shapes = {"q": (K, 1024), "k": (K, 256), "v": (K, 136), "u": (K, 2056)}
+    shapes = dict(list(shapes.items())[:n_mod])
     adapters = {}
     for i, r in enumerate([8, 24, 64]):
         adapters[f"s{i}"] = {m: peft_layer(g, fi, fo, r, 2.0 * r) for m, (fi, fo) in shapes.items() if not (i == 1 and m == "k")}
@@ -194,6 +196,8 @@ def test_stacked_fused_equals_separate(gpu, dtype, group_tokens):
         torch.testing.assert_close(sep[m].cpu().view(rows, M, -1), expect, **tol_for(dtype))
     with pytest.raises(ValueError, match="modules with one y each"):
         sgmv.lora_fused_stacked(xg, ys[:2], cache, list(shapes), plan)
+    with pytest.raises(ValueError, match="must be"):  # a later module's output of the wrong width
+        sgmv.lora_fused_stacked(xg, [ys[0], ys[1][:, :8].contiguous(), *ys[2:]], cache, list(shapes), plan)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
