@@ -125,7 +125,15 @@ constexpr int kShortCC = 2;      // 16-byte chunks per lane per shrink step
 constexpr int kShortJT = 2;      // 16-rank tiles per shrink workgroup
 constexpr int kShortRanks = 16 * kShortJT;
 constexpr int kShortMaxPlanes = 16;
-constexpr int kShortRankBlock = 64;  // ranks staged in LDS per expand pass
+// Ranks staged in LDS per expand pass: 32 when the shrink left at most 4
+// planes, else 64.  Measured on MI355X (decode, Llama-8B shapes, 4 planes):
+// the narrower block frees B registers, and the q/k/v expand went from 7.3
+// to 6.3 us, gate/up from 21.7 to 20.0 us; with 8 planes (down_proj) the
+// 64-rank block stays faster (5.9 against 6.6 us).
+template <int PMAX>
+constexpr int pl_expand_rank_block() {
+  return PMAX <= 4 ? 32 : 64;
+}
 
 template <int DT>
 __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
@@ -386,8 +394,9 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   typedef pl_expand_shape<DT> S;
   constexpr int E = pl_traits<DT>::E;
   constexpr int kStep = 4 * E;                        // rank slots per MFMA step
-  constexpr int kSteps = kShortRankBlock / kStep;     // MFMA steps per staged rank block
-  constexpr int kTRow = kShortRankBlock + S::kPad;    // LDS row of the staged intermediate
+  constexpr int kRB = pl_expand_rank_block<PMAX>();  // ranks per staged block
+  constexpr int kSteps = kRB / kStep;                 // MFMA steps per staged rank block
+  constexpr int kTRow = kRB + S::kPad;                // LDS row of the staged intermediate
   constexpr int kYPer = 16 / S::kYRowsPerPass;        // y rows per thread
   __shared__ __attribute__((aligned(16))) T tt[16 * kTRow];
   __shared__ __attribute__((aligned(16))) T delta[16 * S::kLdsRow];
@@ -439,9 +448,14 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
 #pragma unroll
   for (int i = 0; i < kYPer; ++i) yt[i] = a.tok[grp.start + min(yr0 + S::kYRowsPerPass * i, len - 1)];
 
-  // planes -> staged intermediate: thread (token sp, ranks rb + sq .. +4)
-  const int sp = tid >> 4;
-  const int sq = (tid & 15) * 4;
+  // planes -> staged intermediate: thread (token sp, ranks rb + sq .. +4);
+  // the waves past the 16 tokens' rows stage nothing and load no planes
+  constexpr int kStageLanes = kRB / 4;  // threads per token row
+  constexpr int kStageThreads = 16 * kStageLanes;
+  static_assert(kStageThreads <= 256 && kStageThreads % 64 == 0, "whole waves stage a rank block");
+  const bool stager = kStageThreads == 256 || wave * 64 < kStageThreads;  // wave-uniform
+  const int sp = tid / kStageLanes;
+  const int sq = (tid % kStageLanes) * 4;
   const float* srow = a.planes[job] + (int64_t)(grp.start + (sp < len ? sp : 0)) * a.ldt;
 
   pl_u32x4 bf[kSteps][S::kCT];
@@ -464,12 +478,14 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
     }
     // PMAX loads per thread, the plane index clamped to the last plane;
     // only the first k_splits are summed
-    const int jr = rb + sq;
-    const bool sok = sp < len && jr < rank;
-    const float* sbase = srow + jr;
+    if (stager) {
+      const int jr = rb + sq;
+      const bool sok = sp < len && jr < rank;
+      const float* sbase = srow + jr;
 #pragma unroll
-    for (int q = 0; q < PMAX; ++q)
-      pv[q] = pl_ld16_or0(sbase + (int64_t)min(q, a.k_splits - 1) * a.plane, sok);
+      for (int q = 0; q < PMAX; ++q)
+        pv[q] = pl_ld16_or0(sbase + (int64_t)min(q, a.k_splits - 1) * a.plane, sok);
+    }
   };
 
   // delta^T tiles [columns x tokens]: acc[ct][v] = delta(column n0 + ct*16 + 4*lg + v, token li)
@@ -479,17 +495,19 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   // planes summed in split order, masked at the rank, rounded once to T,
   // staged in LDS and multiplied with B
   auto use_block = [&](int rb) {
-    const int jr = rb + sq;
-    const bool sok = sp < len && jr < rank;
-    pl_f32x4 sum = __builtin_bit_cast(pl_f32x4, pv[0]);
-#pragma unroll
-    for (int q = 1; q < PMAX; ++q)
-      if (q < a.k_splits) sum += __builtin_bit_cast(pl_f32x4, pv[q]);
-    T4 tv;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) tv[i] = (T)((sok && jr + i < rank) ? sum[i] : 0.f);
     if (rb > 0) __syncthreads();  // the previous rank block's MFMA reads are done
-    *reinterpret_cast<T4*>(tt + sp * kTRow + sq) = tv;
+    if (stager) {
+      const int jr = rb + sq;
+      const bool sok = sp < len && jr < rank;
+      pl_f32x4 sum = __builtin_bit_cast(pl_f32x4, pv[0]);
+#pragma unroll
+      for (int q = 1; q < PMAX; ++q)
+        if (q < a.k_splits) sum += __builtin_bit_cast(pl_f32x4, pv[q]);
+      T4 tv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tv[i] = (T)((sok && jr + i < rank) ? sum[i] : 0.f);
+      *reinterpret_cast<T4*>(tt + sp * kTRow + sq) = tv;
+    }
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
@@ -513,7 +531,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   }
   __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first use
   use_block(0);
-  for (int rb = kShortRankBlock; rb < r8; rb += kShortRankBlock) {
+  for (int rb = kRB; rb < r8; rb += kRB) {
     load_block(rb);
     __builtin_amdgcn_sched_barrier(0);
     use_block(rb);
