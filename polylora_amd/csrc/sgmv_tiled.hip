@@ -7,7 +7,7 @@
 // free.
 //
 // Shrink (replaces sgmv.py:63-138).  16-token groups: pl_shrink_short, one
-// workgroup per (group, 32-rank pass, K split, module).  64-token groups:
+// workgroup per (group, 64-rank pass, K split, module).  64-token groups:
 // pl_shrink_long, one workgroup per (group, K split, module), each A chunk
 // feeding the group's four row tiles.  In both, the four waves split the
 // split's K range, 16x16 MFMA tiles [tokens x ranks] accumulate in fp32, the
@@ -57,7 +57,7 @@ struct pl_shrink_args {
   const int32_t* meta;
   int32_t ldt;
   int32_t k_splits;
-  int32_t rank_passes;  // 32-rank passes per (group, split)
+  int32_t rank_passes;  // 64-rank passes per (group, split)
   int32_t sub;          // 16-token sub-tiles per plan group (1 or 4)
   int64_t plane;        // floats between split planes
 };
@@ -106,23 +106,26 @@ struct pl_expand_shape {
 // little data per workgroup, so these kernels are built for latency: all of
 // a step's loads are issued before its first MFMA.
 //
-// Shrink: one workgroup per (group, pass of 32 ranks, K split, served
-// module); ranks beyond the slot's rank exit before loading anything.  The
+// Shrink: one workgroup per (group, pass of 64 ranks, K split, served
+// module); passes beyond the slot's rank exit before loading anything.  The
 // four waves split the split's K range (256 each for a split of 1024) and
 // their partials are summed in LDS in a fixed order, as in pl_shrink_tiled.
-// A step is 2 chunks (64 K per lane group) of both rank tiles, so a wave
-// walks its K range in a few short steps with 48 VGPRs; eight waves per SIMD
+// A step is 2 chunks (64 K per lane group) of the four rank tiles, so a wave
+// walks its K range in a few short steps with 70 VGPRs; seven waves per SIMD
 // then hide each other's latency better than fewer waves holding their whole
 // K range in flight (measured on MI355X, decode shapes: 8 chunks per step,
 // 120 VGPRs, 4 waves per SIMD: q_proj 5.9 us, down_proj 14.2 us; 2 chunks:
-// 5.5 and 13.5 us).
+// 5.5 and 13.5 us).  One 64-rank pass reads the group's x rows once for all
+// of a slot's ranks (32-rank passes read them twice for rank 64): decode
+// gate/up shrink 8.1 -> 6.8 us, down_proj 11.8 -> 10.5 us; tiles past the
+// rank multiply zeros.
 //
 // Expand: one workgroup per (group, 256-column chunk).  The shrink planes of
 // the group's tokens are summed once per workgroup (all planes' loads in
 // flight together), rounded to T and staged in LDS as [token][rank]; B and
 // the y rows are loaded at the same time.
 constexpr int kShortCC = 2;      // 16-byte chunks per lane per shrink step
-constexpr int kShortJT = 2;      // 16-rank tiles per shrink workgroup
+constexpr int kShortJT = 4;      // 16-rank tiles per shrink workgroup
 constexpr int kShortRanks = 16 * kShortJT;
 constexpr int kShortMaxPlanes = 16;
 // Ranks staged in LDS per expand pass: 32 when the shrink left at most 4
