@@ -7,7 +7,7 @@
 // free.
 //
 // Shrink (replaces sgmv.py:63-138).  16-token groups: pl_shrink_short, one
-// workgroup per (group, 64-rank pass, K split, module).  64-token groups:
+// workgroup per (group, 64- or 32-rank pass, K split, module).  64-token groups:
 // pl_shrink_long, one workgroup per (group, K split, module), each A chunk
 // feeding the group's four row tiles.  In both, the four waves split the
 // split's K range, 16x16 MFMA tiles [tokens x ranks] accumulate in fp32, the
@@ -57,7 +57,8 @@ struct pl_shrink_args {
   const int32_t* meta;
   int32_t ldt;
   int32_t k_splits;
-  int32_t rank_passes;  // 64-rank passes per (group, split)
+  int32_t rank_passes;  // rank passes per (group, split) of the short shrink
+  int32_t rank_tiles;   // 16-rank tiles per short-shrink pass (2 or 4)
   int32_t sub;          // 16-token sub-tiles per plan group (1 or 4)
   int64_t plane;        // floats between split planes
 };
@@ -106,27 +107,31 @@ struct pl_expand_shape {
 // little data per workgroup, so these kernels are built for latency: all of
 // a step's loads are issued before its first MFMA.
 //
-// Shrink: one workgroup per (group, pass of 64 ranks, K split, served
+// Shrink: one workgroup per (group, pass of 64 or 32 ranks, K split, served
 // module); passes beyond the slot's rank exit before loading anything.  The
 // four waves split the split's K range (256 each for a split of 1024) and
 // their partials are summed in LDS in a fixed order, as in pl_shrink_tiled.
 // A step is 2 chunks (64 K per lane group) of the four rank tiles, so a wave
-// walks its K range in a few short steps with 70 VGPRs; seven waves per SIMD
+// walks its K range in a few short steps with 70 VGPRs (48 for 32-rank
+// passes); seven waves per SIMD
 // then hide each other's latency better than fewer waves holding their whole
 // K range in flight (measured on MI355X, decode shapes: 8 chunks per step,
 // 120 VGPRs, 4 waves per SIMD: q_proj 5.9 us, down_proj 14.2 us; 2 chunks:
 // 5.5 and 13.5 us).  One 64-rank pass reads the group's x rows once for all
 // of a slot's ranks (32-rank passes read them twice for rank 64): decode
 // gate/up shrink 8.1 -> 6.8 us, down_proj 11.8 -> 10.5 us; tiles past the
-// rank multiply zeros.
+// rank multiply zeros.  A launch that would have fewer than
+// kShortWideMinBlocks workgroups at 64 ranks (o_proj in decode: 320) keeps
+// 32-rank passes (6.95 against 7.7 us).
 //
 // Expand: one workgroup per (group, 256-column chunk).  The shrink planes of
 // the group's tokens are summed once per workgroup (all planes' loads in
 // flight together), rounded to T and staged in LDS as [token][rank]; B and
 // the y rows are loaded at the same time.
 constexpr int kShortCC = 2;      // 16-byte chunks per lane per shrink step
-constexpr int kShortJT = 4;      // 16-rank tiles per shrink workgroup
-constexpr int kShortRanks = 16 * kShortJT;
+// Short-shrink passes cover 64 ranks (4 tiles) when the launch still has at
+// least kShortWideMinBlocks workgroups, else 32 (more, smaller workgroups).
+constexpr int kShortWideMinBlocks = 512;
 constexpr int kShortMaxPlanes = 16;
 // Ranks staged in LDS per expand pass: 32 when the shrink left at most 4
 // planes, else 64.  Measured on MI355X (decode, Llama-8B shapes, 4 planes):
@@ -138,13 +143,14 @@ constexpr int pl_expand_rank_block() {
   return PMAX <= 4 ? 32 : 64;
 }
 
-template <int DT>
+template <int DT, int JT>
 __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
   typedef typename pl_traits<DT>::T T;
   constexpr int E = pl_traits<DT>::E;
   constexpr int kInstr = 4 * E;
   constexpr int kStep = kShortCC * kInstr;
-  __shared__ pl_f32x4 red[kWaves][kShortJT][64];
+  constexpr int kShortRanks = 16 * JT;
+  __shared__ pl_f32x4 red[kWaves][JT][64];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -184,16 +190,16 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
   const int k0 = (c * kWaves + wave) * a.kw;
   const int k1 = min(K, k0 + a.kw);
 
-  pl_f32x4 acc[kShortJT];
+  pl_f32x4 acc[JT];
 #pragma unroll
-  for (int jt = 0; jt < kShortJT; ++jt) acc[jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int jt = 0; jt < JT; ++jt) acc[jt] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto step = [&](int kb) {
     // chunk cc of lane (li, lg) covers k = kb + cc*kInstr + lg*E .. +E
     pl_u32x4 xf[kShortCC];
-    pl_u32x4 af[kShortJT][kShortCC];
+    pl_u32x4 af[JT][kShortCC];
 #pragma unroll
-    for (int jt = 0; jt < kShortJT; ++jt) {
+    for (int jt = 0; jt < JT; ++jt) {
       // rank tile of A's MFMA blocks (rt rows): the block of columns k
       // starts at t0*K + k*rt and is wb wide
       const int t0 = rb + jt * 16;
@@ -220,7 +226,7 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
     // tile's loads behind the first tile's MFMAs; a tile past the rank
     // multiplies zeros
 #pragma unroll
-    for (int jt = 0; jt < kShortJT; ++jt)
+    for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
       for (int cc = 0; cc < kShortCC; ++cc)
         acc[jt] = pl_mfma_chunk<DT>(xf[cc], af[jt][cc], acc[jt]);
@@ -234,9 +240,9 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
   // Sum the four wave partials of each tile in a fixed order; acc[jt][v]
   // holds tile element (token 4*lg+v, rank rb + jt*16 + li).
 #pragma unroll
-  for (int jt = 0; jt < kShortJT; ++jt) red[wave][jt][lane] = acc[jt];
+  for (int jt = 0; jt < JT; ++jt) red[wave][jt][lane] = acc[jt];
   __syncthreads();
-  if (tid < kShortJT * 64) {
+  if (tid < JT * 64) {
     const int jt = tid >> 6;
     const int l = tid & 63;
     const pl_f32x4 s = red[0][jt][l] + red[1][jt][l] + red[2][jt][l] + red[3][jt][l];
@@ -577,7 +583,10 @@ int launch_shrink(const pl_shrink_args& a, int64_t group_cap, hipStream_t stream
   if (a.sub == 1) {
     const int64_t grid = group_cap * a.k_splits * a.rank_passes * a.n_jobs;
     if (grid <= 0) return PL_OK;
-    hipLaunchKernelGGL((pl_shrink_short<DT>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    if (a.rank_tiles == 4)
+      hipLaunchKernelGGL((pl_shrink_short<DT, 4>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((pl_shrink_short<DT, 2>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   } else {
     const int64_t grid = group_cap * a.k_splits * a.n_jobs;
     if (grid <= 0) return PL_OK;
@@ -708,7 +717,8 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
     return PL_ERR_ALIGN;
   }
   const int32_t planes = shrink_planes(dtype, K, k_splits, group_tokens);
-  const int32_t rank_passes = (ldt + kShortRanks - 1) / kShortRanks;
+  const int32_t rank_tiles = group_cap * planes * n_jobs >= kShortWideMinBlocks ? 4 : 2;
+  const int32_t rank_passes = (ldt + 16 * rank_tiles - 1) / (16 * rank_tiles);
   const int32_t sub = group_tokens / 16;
   if (group_cap * planes * rank_passes * sub * n_jobs > 0x7fffffffLL) {
     pl_set_error("shrink grid too large");
@@ -737,6 +747,7 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
   a.ldt = ldt;
   a.k_splits = planes;
   a.rank_passes = rank_passes;
+  a.rank_tiles = rank_tiles;
   a.sub = sub;
   a.plane = tmp_rows * ldt;
   return PL_OK;
