@@ -133,15 +133,15 @@ constexpr int kShortCC = 2;      // 16-byte chunks per lane per shrink step
 // least kShortWideMinBlocks workgroups, else 32 (more, smaller workgroups).
 constexpr int kShortWideMinBlocks = 512;
 constexpr int kShortMaxPlanes = 16;
-// Ranks staged in LDS per expand pass: 32 when the shrink left at most 4
-// planes, else 64.  Measured on MI355X (decode, Llama-8B shapes, 4 planes):
-// the narrower block frees B registers, and the q/k/v expand went from 7.3
-// to 6.3 us, gate/up from 21.7 to 20.0 us; with 8 planes (down_proj) the
-// 64-rank block stays faster (5.9 against 6.6 us).
-template <int PMAX>
-constexpr int pl_expand_rank_block() {
-  return PMAX <= 4 ? 32 : 64;
-}
+// Ranks staged in LDS per expand pass (RB): 32 when the shrink left at most
+// 4 planes and the launch has at least kExpandNarrowMinBlocks workgroups,
+// else 64.  Measured on MI355X (decode, Llama-8B shapes, 4 planes): the
+// narrower block frees B registers (90 instead of 104 VGPRs), and the q/k/v
+// expand (1920 workgroups) went from 7.3 to 6.3 us, gate/up (8960) from 21.7
+// to 20.0 us, while o_proj (1280) is faster with one 64-rank pass (5.3
+// against 5.5 us); with 8 planes (down_proj) the 64-rank block stays faster
+// (5.9 against 6.6 us).
+constexpr int kExpandNarrowMinBlocks = 1536;
 
 template <int DT, int JT>
 __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_long(pl_shrink_args a) {
   }
 }
 
-template <int DT, int PMAX>
+template <int DT, int PMAX, int RB>
 __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   typedef typename pl_traits<DT>::T T;
   typedef typename pl_traits<DT>::T4 T4;
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   typedef pl_expand_shape<DT> S;
   constexpr int E = pl_traits<DT>::E;
   constexpr int kStep = 4 * E;                        // rank slots per MFMA step
-  constexpr int kRB = pl_expand_rank_block<PMAX>();  // ranks per staged block
+  constexpr int kRB = RB;                             // ranks per staged block
   constexpr int kSteps = kRB / kStep;                 // MFMA steps per staged rank block
   constexpr int kTRow = kRB + S::kPad;                // LDS row of the staged intermediate
   constexpr int kYPer = 16 / S::kYRowsPerPass;        // y rows per thread
@@ -599,13 +599,15 @@ template <int DT>
 int launch_expand(const pl_expand_args& a, int64_t group_cap, hipStream_t stream) {
   const int64_t grid = group_cap * a.n_chunks * a.sub;
   if (grid <= 0) return PL_OK;
-  if (a.k_splits <= 4)
-    hipLaunchKernelGGL((pl_expand_short<DT, 4>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  if (a.k_splits <= 4 && grid >= kExpandNarrowMinBlocks)
+    hipLaunchKernelGGL((pl_expand_short<DT, 4, 32>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+  else if (a.k_splits <= 4)
+    hipLaunchKernelGGL((pl_expand_short<DT, 4, 64>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   else if (a.k_splits <= 8)
-    hipLaunchKernelGGL((pl_expand_short<DT, 8>), dim3((unsigned)grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((pl_expand_short<DT, 8, 64>), dim3((unsigned)grid), dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((pl_expand_short<DT, kShortMaxPlanes>), dim3((unsigned)grid), dim3(256),
-                       0, stream, a);
+    hipLaunchKernelGGL((pl_expand_short<DT, kShortMaxPlanes, 64>), dim3((unsigned)grid),
+                       dim3(256), 0, stream, a);
   return pl_launch_status("pl_sgmv_expand");
 }
 

@@ -69,8 +69,9 @@ CASES = [
     (torch.float32, 6, 128, 3072, 768, [4, 8, 8, 16, 16], 16, None, 19),
     (torch.bfloat16, 16, 3, 4104, 1000, [80, 128], 128, 2, 20),
     (torch.bfloat16, 300, 1, 256, 256, [16] * 5, 16, 1, 21),
-    # >= 512 shrink workgroups at 64-rank passes: the wide short shrink
-    (torch.bfloat16, 2048, 1, 1024, 512, [8, 16, 32, 64, 8, 16, 32, 64], 64, 4, 22),
+    # >= 512 shrink workgroups at 64-rank passes (the wide short shrink) and
+    # >= 1536 expand workgroups at 4 planes (32-rank staged blocks)
+    (torch.bfloat16, 2048, 1, 1024, 3072, [8, 16, 32, 64, 8, 16, 32, 64], 64, 4, 22),
 ]
 
 
