@@ -2,19 +2,23 @@
 // few adapters), gfx950.
 //
 // One workgroup per (16-token tile of a plan group, slice of the output
-// columns).  Its four waves split K and accumulate x·Aᵀ for the tile in
-// 16x16 MFMA tiles (fp32), the four partials are summed in LDS in a fixed
-// order and rounded once to the model dtype (the reference's
+// columns, served module).  Its four waves split K and accumulate x·Aᵀ for
+// the tile in 16x16 MFMA tiles (fp32), the four partials are summed in LDS
+// in a fixed order and rounded once to the model dtype (the reference's
 // t = T(x @ A[:, :r]), layers.py:127), and then each wave streams its share
-// of the slice's columns: B rows and y rows for the next 64 columns are in
-// flight while the MFMA, the epilogue (the expand's rounding order) and the
-// 16-byte read-modify-write of y run on the current ones.  The intermediate
-// never leaves the workgroup, so there is one launch per wrapped Linear, no
-// workspace and no split-K partial sums; results are bitwise reproducible.
+// of the slice's columns: B rows and y rows of the next step (128 columns,
+// 64 at rank 64 or fp32) are in flight while the MFMA, the epilogue (the
+// expand's rounding order) and the 16-byte read-modify-write of y run on
+// the current ones.  The first step's loads, which need nothing from the
+// shrink, issue before the partials are reduced.  The intermediate never
+// leaves the workgroup, so there is one launch per wrapped Linear (or per
+// set of sibling Linears fed the same x), no workspace and no split-K
+// partial sums; results are bitwise reproducible.
 //
-// A tile's slices (column ranges) all recompute the same shrink; they run on
-// one XCD (workgroups are dealt to the 8 XCDs round-robin by index), so x and
-// A are fetched from HBM once and reread from that XCD's L2.
+// A tile's slices (column ranges) and modules all recompute or share the
+// same x rows; they run on one XCD (workgroups are dealt to the 8 XCDs
+// round-robin by index), so x and A are fetched from HBM once and reread
+// from that XCD's L2.
 //
 // Ranks up to 64 (4 tiles of 16) are held in registers; the kernel is
 // instantiated for at most 1, 2 or 4 rank tiles and each group runs the
