@@ -19,7 +19,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import sgmv
+from . import _native, sgmv
 from .cache import GpuAdapterCache
 from .context import LoraBatchContext, get_lora_context
 
@@ -59,6 +59,7 @@ class MultiLoraLinear(nn.Module):
         self.base_layer = base_layer
         self.module_name = module_name
         self.cache = cache
+        self._n_out = base_layer.out_features  # read on every call; the submodule lookup is slower
         cache.wrapped[module_name] = self
 
     @property
@@ -95,7 +96,7 @@ class MultiLoraLinear(nn.Module):
         if rows * row_len == 0 or x.dtype != cache.dtype:
             return None
         x2 = x_3d.reshape(rows * row_len, in_features)
-        if not sgmv.tiled_shapes_ok(x2, self.out_features):
+        if not sgmv.tiled_shapes_ok(x2, self._n_out):
             return None
         plan = self._plan(lora_ctx, rows, row_len, seq_lens, weight_indices)
         main = sgmv._stream(x.device)  # handle of the caller's stream
@@ -108,8 +109,12 @@ class MultiLoraLinear(nn.Module):
             self._observe_call(x, _version_of(x), lora_ctx.stack)
             base = self.base_layer(x)
             base_3d = reshape(base)
-            sgmv.lora_fused(x2, base_3d.view(rows * row_len, base_3d.shape[-1]), cache, self.module_name, plan,
-                            stream=main)
+            y2 = base_3d.view(rows * row_len, base_3d.shape[-1])
+            if y2.shape[1] == self._n_out and y2.dtype == cache.dtype and y2.data_ptr() % 16 == 0:
+                # x2 passed tiled_shapes_ok and y2 is the fresh contiguous base output
+                sgmv._fused_launch(x2, y2, cache, self.module_name, plan, _native.PL_EPI_FALLBACK, None, main)
+            else:
+                sgmv.lora_fused(x2, y2, cache, self.module_name, plan, stream=main)  # checks and raises
             return base_3d.reshape(base.shape)
         if rows * row_len >= OVERLAP_MIN_TOKENS:
             main_s = torch.cuda.current_stream(x.device)
