@@ -137,9 +137,10 @@ class MultiLoraLinear(nn.Module):
 
         Siblings are wrapped Linears that the model calls back to back on the
         very same input tensor (q/k/v, gate/up), learned from the call order of
-        a forward.  The first of a run computes every sibling's base output,
-        one stacked shrink and one stacked expand, and keeps the siblings'
-        finished outputs; a sibling then returns its kept output when its own
+        a forward.  The first of a run computes every sibling's base output
+        and then the LoRA deltas of all of them, in one stacked fused launch
+        for long adapter segments or else one stacked shrink and one stacked
+        expand, and keeps the siblings' finished outputs; a sibling then returns its kept output when its own
         call brings the same input tensor, unmodified (same version counter;
         inference-mode tensors keep none, so for them object identity alone),
         for the same plan.  A base output is a function of x and the weights
