@@ -269,6 +269,34 @@ def test_isolated_sgmv_config_bf16(gpu):
     np.testing.assert_array_equal(np.bincount(wl.row_slot.cpu().numpy(), minlength=17).sum(), 4096)
 
 
+def test_prefill_config_stacked_fused_bf16(gpu):
+    """Prefill size: 32 rows x 1024, lengths U[512,1024], 8 adapters (4 x r16, 4 x r32), q/k/v of a
+    4096-wide model in one stacked fused launch, every token against the oracle."""
+    _announce(test="prefill_config_stacked_fused")
+    g = torch.Generator().manual_seed(1004)
+    K, B, S = 4096, 32, 1024
+    shapes = {"q": (K, 4096), "k": (K, 1024), "v": (K, 1024)}
+    adapters = {f"p{i}": {m: peft_layer(g, fi, fo, 16 if i < 4 else 32, 2.0 * (16 if i < 4 else 32))
+                          for m, (fi, fo) in shapes.items()} for i in range(8)}
+    cache = make_cache(adapters, shapes, 8, 32, gpu, torch.bfloat16)
+    row_slot = cache.ensure_resident([f"p{i // 4}" for i in range(B)])
+    seq_lens = torch.randint(512, S + 1, (B,), generator=g, dtype=torch.int32)
+    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), S, cache.num_slots, distinct_slots=8)
+    assert plan.group_tokens == 64 and sgmv.fused_ok(plan, cache, K)
+    gg = torch.Generator(device=gpu).manual_seed(1004)
+    x = torch.randn(B * S, K, generator=gg, device=gpu).to(torch.bfloat16)
+    base = {m: torch.randn(B * S, fo, generator=gg, device=gpu).to(torch.bfloat16) for m, (fi, fo) in shapes.items()}
+    ys = [base[m].clone() for m in shapes]
+    sgmv.lora_fused_stacked(x, ys, cache, list(shapes), plan)
+    torch.cuda.synchronize()
+    for m, y in zip(shapes, ys):
+        A, Bm, rk, sc = (t.to(gpu) for t in oracle_slot_tensors(cache, adapters, m, torch.bfloat16))
+        expect = reference_forward(x.view(B, S, K), base[m].view(B, S, -1), seq_lens.to(gpu), row_slot, A, Bm, rk, sc)
+        torch.testing.assert_close(y.view(B, S, -1), expect, rtol=2e-2, atol=1e-2)
+        pad = torch.arange(S)[None, :] >= seq_lens[:, None]  # padding tokens keep the base output
+        assert torch.equal(y.view(B, S, -1)[pad.to(gpu)], base[m].view(B, S, -1)[pad.to(gpu)])
+
+
 def _small_case(gpu, dtype=torch.bfloat16, rows=40, M=3, K=1024, N=512, ranks=(4, 16, 33, 64), seed=50):
     g = torch.Generator().manual_seed(seed)
     adapters = _adapters(g, list(ranks), K, N)
