@@ -297,6 +297,44 @@ def test_prefill_config_stacked_fused_bf16(gpu):
         assert torch.equal(y.view(B, S, -1)[pad.to(gpu)], base[m].view(B, S, -1)[pad.to(gpu)])
 
 
+def test_decode_config_stacked_split_bf16(gpu):
+    """Decode size: 256 rows of one token, 64 adapters of ranks {8,16,32,64}, Zipf(1.1) choice with 10%
+    base rows; q/k/v of a 4096-wide model through one stacked shrink and one stacked expand, and
+    down_proj (K=14336, 8 K splits) alone, every row against the oracle."""
+    _announce(test="decode_config_stacked_split")
+    from bench import zipf_ids
+
+    g = torch.Generator().manual_seed(1003)
+    rng = np.random.default_rng(1003)
+    shapes = {"q": (4096, 4096), "k": (4096, 1024), "v": (4096, 1024), "down": (14336, 4096)}
+    names = [f"d{i:02d}" for i in range(64)]
+    ranks = {n: int(rng.choice([8, 16, 32, 64])) for n in names}
+    adapters = {n: {m: peft_layer(g, fi, fo, ranks[n], 2.0 * ranks[n]) for m, (fi, fo) in shapes.items()} for n in names}
+    cache = make_cache(adapters, shapes, 64, 64, gpu, torch.bfloat16)
+    ids = zipf_ids(rng, 256, 64, 1.1, 0.1, names)
+    row_slot = cache.ensure_resident(ids)
+    distinct = len({a for a in ids if a != "__base__"})
+    seq = torch.ones(256, dtype=torch.int32, device=gpu)
+    plan = sgmv.SgmvPlan(row_slot, seq, 1, cache.num_slots, distinct_slots=distinct)
+    assert plan.group_tokens == 16 and not sgmv.fused_ok(plan, cache, 4096)
+    gg = torch.Generator(device=gpu).manual_seed(1003)
+    xs = {K: torch.randn(256, K, generator=gg, device=gpu).to(torch.bfloat16) for K in (4096, 14336)}
+    base = {m: torch.randn(256, fo, generator=gg, device=gpu).to(torch.bfloat16) for m, (fi, fo) in shapes.items()}
+    qkv = ["q", "k", "v"]
+    ys = {m: base[m].clone() for m in shapes}
+    results = sgmv.lora_shrink_stacked(xs[4096], cache, qkv, plan)
+    sgmv.lora_expand_stacked(results, [ys[m] for m in qkv], cache, qkv)
+    res = sgmv.lora_shrink(xs[14336], cache, "down", plan)
+    sgmv.lora_expand(res, ys["down"], cache, "down")
+    torch.cuda.synchronize()
+    for m, (fi, fo) in shapes.items():
+        A, Bm, rk, sc = (t.to(gpu) for t in oracle_slot_tensors(cache, adapters, m, torch.bfloat16))
+        expect = reference_forward(xs[fi].view(256, 1, fi), base[m].view(256, 1, fo), seq, row_slot, A, Bm, rk, sc)
+        torch.testing.assert_close(ys[m].view(256, 1, fo), expect, rtol=2e-2, atol=1e-2)
+        untouched = (row_slot == 0)
+        assert torch.equal(ys[m][untouched], base[m][untouched])
+
+
 def _small_case(gpu, dtype=torch.bfloat16, rows=40, M=3, K=1024, N=512, ranks=(4, 16, 33, 64), seed=50):
     g = torch.Generator().manual_seed(seed)
     adapters = _adapters(g, list(ranks), K, N)
