@@ -72,6 +72,8 @@ CASES = [
     # >= 512 shrink workgroups at 64-rank passes (the wide short shrink) and
     # >= 1536 expand workgroups at 4 planes (32-rank staged blocks)
     (torch.bfloat16, 2048, 1, 1024, 3072, [8, 16, 32, 64, 8, 16, 32, 64], 64, 4, 22),
+    # the wide short shrink with two 64-rank passes (ranks up to 128)
+    (torch.bfloat16, 2048, 1, 1024, 512, [80, 128, 8, 64, 33], 128, 4, 23),
 ]
 
 
