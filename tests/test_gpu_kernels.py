@@ -74,6 +74,8 @@ CASES = [
     (torch.bfloat16, 2048, 1, 1024, 3072, [8, 16, 32, 64, 8, 16, 32, 64], 64, 4, 22),
     # the wide short shrink with two 64-rank passes (ranks up to 128)
     (torch.bfloat16, 2048, 1, 1024, 512, [80, 128, 8, 64, 33], 128, 4, 23),
+    # 16 K splits: the expand sums 16 planes
+    (torch.bfloat16, 24, 2, 4096, 768, [8, 64, 32], 64, 16, 24),
 ]
 
 
