@@ -213,6 +213,8 @@ class GpuAdapterCache:
         # (first module, input shape) -> modules called back to back on that
         # same input tensor; learned by MultiLoraLinear, used to stack shrinks
         self.stacked_runs: dict[tuple, tuple[str, ...]] = {}
+        # False: every wrapped Linear computes its own LoRA delta (no sibling runs)
+        self.stack_siblings = True
         # module name -> its MultiLoraLinear, so the first Linear of a run can
         # compute its siblings' outputs
         self.wrapped: dict[str, object] = {}
@@ -236,9 +238,15 @@ class GpuAdapterCache:
             self._side_stream = torch.cuda.Stream(self.device)
             # the table's zero fill runs on the compute stream; uploads must follow it
             self._side_stream.wait_stream(torch.cuda.current_stream(self.device))
-        self._slot_last_use: dict[int, torch.cuda.Event] = {}
+        # slot -> the event after the last work known to read it, or None when
+        # the slot was handed out by ensure_resident and no mark_used has
+        # covered that hand-out yet (its readers are then somewhere on the
+        # compute stream, and a rewrite waits for everything queued there)
+        self._slot_last_use: dict[int, torch.cuda.Event | None] = {}
         self._slot_ready: dict[int, torch.cuda.Event] = {}
         self._pending: list[tuple] = []
+        # device pointers kept by the launch helpers belong to this arena and table
+        self.__dict__.pop("_launch_args", None)
 
     @property
     def A(self) -> Mapping:
@@ -299,13 +307,22 @@ class GpuAdapterCache:
             for slot in loaded:
                 compute.wait_event(self._slot_ready[slot])
         slots = [0 if aid == base_id else self.adapter_to_slot[aid] for aid in adapter_ids]
+        for slot in set(slots):
+            if slot > 0:
+                self._slot_last_use[slot] = None  # handed out: readers unknown until mark_used
         host = torch.tensor(slots, dtype=torch.int32)
         if self.device.type == "cuda":
             return host.pin_memory().to(self.device, non_blocking=True)
         return host.to(self.device)
 
     def mark_used(self, slots: set[int]) -> None:
-        """Record that work enqueued so far on the current stream reads these slots."""
+        """Record that every reader of these slots is enqueued on the current stream, up to now.
+
+        A later rewrite of such a slot then waits for this point of the stream
+        only.  A slot handed out by ``ensure_resident`` and not marked since
+        (the ``prepare_lora_context`` + ``use_lora_context`` path) is rewritten
+        only after everything queued on the compute stream at the rewrite.
+        """
         if self.device.type != "cuda" or not slots:
             return
         event = torch.cuda.Event()
@@ -397,9 +414,13 @@ class GpuAdapterCache:
             return
         lib = _native.load()
         side = self._side_stream
-        last = self._slot_last_use.pop(slot, None)
-        if last is not None:
-            side.wait_event(last)  # the previous occupant may still be read
+        if slot in self._slot_last_use:
+            last = self._slot_last_use.pop(slot)
+            if last is None:
+                # readers not marked: they are among the work queued on the compute stream
+                side.wait_stream(torch.cuda.current_stream(self.device))
+            else:
+                side.wait_event(last)  # the previous occupant may still be read
         previous = self._slot_ready.get(slot)
         if previous is not None:
             side.wait_event(previous)

@@ -74,6 +74,8 @@ class MultiLoraLinear(nn.Module):
         lora_ctx = get_lora_context()
         if lora_ctx is None:
             return self.base_layer(x)
+        stack = lora_ctx.stack
+        stack["calls"] = stack.get("calls", 0) + 1  # wrapped calls under this context so far
         if x.is_cuda and self.cache.config.use_triton_kernels:
             out = self._tiled_forward(x, lora_ctx)
             if out is not None:
@@ -143,7 +145,11 @@ class MultiLoraLinear(nn.Module):
         expand, and keeps the siblings' finished outputs; a sibling then returns its kept output when its own
         call brings the same input tensor, unmodified (same version counter;
         inference-mode tensors keep none, so for them object identity alone),
-        for the same plan.  A base output is a function of x and the weights
+        for the same plan, and is the very next wrapped call (the i-th sibling
+        the i-th call after the first); any other call drops what was kept.
+        Under inference mode an in-place edit of x by a plain tensor op between
+        two sibling calls is not seen; models that do that set
+        ``cache.stack_siblings = False``.  A base output is a function of x and the weights
         only, so computing it at the first sibling's call gives the value the
         sibling's own call would.  Only without autograd: the LoRA path is for
         inference.
@@ -155,12 +161,13 @@ class MultiLoraLinear(nn.Module):
         version = _version_of(x)
         kept = outputs.pop(self.module_name, None)
         if kept is not None:
-            kx, kversion, kplan, out = kept
-            if kx is x and kversion == version and kplan is plan:
+            kx, kversion, kplan, kcall, out = kept
+            if kx is x and kversion == version and kplan is plan and kcall == stack["calls"]:
                 self._observe_call(x, version, stack)
                 return out
+        outputs.clear()  # a run interrupted by another call keeps nothing
         cache = self.cache
-        run = cache.stacked_runs.get((self.module_name, tuple(x.shape)))
+        run = cache.stacked_runs.get((self.module_name, tuple(x.shape))) if cache.stack_siblings else None
         if run is None or len(run) < 2:
             return None
         siblings = _siblings(cache, run, x2.element_size())
@@ -191,8 +198,10 @@ class MultiLoraLinear(nn.Module):
             sgmv.lora_expand_stacked(results, [o.view(tokens, o.shape[-1]) for o in outs], cache, list(run),
                                      stream=main)
         finished = [o.reshape(b.shape) for o, b in zip(outs, bases)]
-        for name, out in zip(run[1:], finished[1:]):
-            outputs[name] = (x, version, plan, out)
+        # sibling i is valid only as the i-th wrapped call after this one
+        calls = stack["calls"]
+        for i, (name, out) in enumerate(zip(run[1:], finished[1:]), start=1):
+            outputs[name] = (x, version, plan, calls + i, out)
         return finished[0]
 
     def _shrink(self, x: torch.Tensor, x2: torch.Tensor, plan, lora_ctx: LoraBatchContext, stream: int):
@@ -204,8 +213,8 @@ class MultiLoraLinear(nn.Module):
         all in one launch.  A precomputed result is used only if this call's
         input is that same tensor object, unmodified (same version counter;
         inference-mode tensors keep none, so for them object identity alone),
-        with the same plan, and its workspace still holds it; otherwise the
-        module computes its own.
+        with the same plan, as the very next wrapped call, and its workspace
+        still holds it; otherwise the module computes its own.
         """
         stack = lora_ctx.stack
         shared = stack.setdefault("shared", {})
@@ -213,14 +222,16 @@ class MultiLoraLinear(nn.Module):
         version = _version_of(x)
         self._observe_call(x, version, stack)
         if hit is not None:
-            hx, hversion, res = hit
-            if hx is x and hversion == version and res.plan is plan and res.valid:
+            hx, hversion, hcall, res = hit
+            if hx is x and hversion == version and hcall == stack["calls"] and res.plan is plan and res.valid:
                 return res
-        run = self.cache.stacked_runs.get((self.module_name, tuple(x.shape)))
+        shared.clear()  # a run interrupted by another call keeps nothing
+        run = self.cache.stacked_runs.get((self.module_name, tuple(x.shape))) if self.cache.stack_siblings else None
         if run is not None and len(run) > 1:
             results = sgmv.lora_shrink_stacked(x2, self.cache, list(run), plan, stream=stream)
-            for name, res in zip(run[1:], results[1:]):
-                shared[name] = (x, version, res)
+            calls = stack["calls"]
+            for i, (name, res) in enumerate(zip(run[1:], results[1:]), start=1):
+                shared[name] = (x, version, calls + i, res)
             return results[0]
         return sgmv.lora_shrink(x2, self.cache, self.module_name, plan, stream=stream)
 
