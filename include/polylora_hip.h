@@ -272,6 +272,34 @@ int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32
                        const int32_t* lora_ranks, const float* scalings, void* out,
                        void* stream);
 
+/* Bytes of the static device scratch behind pl_lora_apply_noalloc. */
+#define PL_NOALLOC_SCRATCH_BYTES (32 << 20)
+
+/* pl_plan_build followed by pl_lora_apply in one call that allocates
+ * nothing.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The plan (meta, group records,
+ * token list) and the shrink's fp32 planes live in a static device array of
+ * PL_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; the caller
+ * passes only inputs and outputs: x, y, the slot arena and table, and the
+ * int32 row -> slot map and row lengths of pl_plan_build.  A call needs
+ *   256 + align256(16 * pl_plan_group_capacity(rows, row_len, num_slots,
+ *   group_tokens)) + align256(4 * max(1, rows * row_len))
+ *   + pl_shrink_workspace_bytes(dtype, K, k_splits, group_tokens,
+ *   max(1, rows * row_len), ldt)
+ * bytes of it (align256 rounds up to a multiple of 256); larger calls return
+ * PL_ERR_LIMIT.  Every call on one GPU uses that GPU's one array and leaves
+ * its contents behind (nothing in it needs clearing: each call writes every
+ * byte it reads), so calls that overlap on one GPU (other streams, or other
+ * threads without ordering) race.  Results equal pl_plan_build +
+ * pl_lora_apply with the same group_tokens and k_splits bit for bit. */
+int pl_lora_apply_noalloc(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
+                          int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
+                          int32_t num_modules, int32_t module, const int32_t* row_slot,
+                          const int32_t* seq_lens, int32_t rows, int32_t row_len,
+                          int32_t num_slots, int32_t group_tokens, int32_t ldt,
+                          int32_t k_splits, int32_t epilogue, void* stream);
+
 /* Copy one packed adapter (host, pinned) into its slot region and its table
  * row into the slot table, both asynchronously on `stream`. */
 int pl_slot_upload(void* arena_dst, const void* host_src, int64_t nbytes, void* table_dst,

@@ -20,6 +20,7 @@ PL_EPI_FALLBACK, PL_EPI_TRITON = 0, 1
 PL_MAX_SLOTS = 4096
 PL_GROUP_TOKENS_SHORT, PL_GROUP_TOKENS_LONG = 16, 64
 PL_MAX_STACKED_MODULES = 4
+PL_NOALLOC_SCRATCH_BYTES = 32 << 20
 SLOT_ENTRY_INT32S = 8  # sizeof(pl_slot_entry) / 4
 
 DTYPE_CODES = {torch.float32: PL_F32, torch.bfloat16: PL_BF16, torch.float16: PL_F16}
@@ -83,6 +84,10 @@ _SIGNATURES: dict[str, tuple] = {
     "pl_sgmv_lora_b_ref": (
         c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
         c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+    ),
+    "pl_lora_apply_noalloc": (
+        c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
+        c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p,
     ),
     "pl_slot_upload": (c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p),
     "pl_check_right_padded": (c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p),

@@ -32,6 +32,8 @@
 // (masked lanes read a zero page) instead of branching around a load, and
 // scheduling barriers keep the compiler from interleaving the loads with
 // the MFMAs that consume them.
+#include <mutex>
+
 #include "pl_common.h"
 
 namespace {
@@ -932,6 +934,142 @@ extern "C" int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t 
                       &module, tok, groups, meta, group_cap, group_tokens, &y, &ldy, &N, epilogue);
   if (st) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  st = dispatch_shrink(dtype, sa, group_cap, s);
+  if (st) return st;
+  return dispatch_expand(dtype, ea, group_cap, s);
+}
+
+// ---------------------------------------------------------------------------
+// pl_lora_apply_noalloc: pl_plan_build + pl_lora_apply for callers that
+// cannot allocate device memory.  The plan (meta, groups, token list) and
+// the shrink -> expand planes live in `scratch`, a static device array of
+// PL_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds until the
+// process ends.  Host code never passes `scratch` itself to a kernel: on
+// the host that name is only a stand-in for the symbol, so each device's
+// address is looked up once with hipGetSymbolAddress (with that device
+// current) and that pointer is what the kernels receive.  Nothing in the
+// array needs clearing: every byte a kernel reads was written earlier in
+// the same call (plan records up to the capacity, planes of planned tokens
+// and ranks).  All calls on one GPU share its array, so calls that overlap
+// on one GPU (different streams, or threads without ordering) race.
+static __device__ __align__(256) unsigned char scratch[PL_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchMaxDevices] = {};
+
+int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
+
+// Device address of `scratch` on the device `stream` belongs to.
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t err = hipStreamGetDevice(stream, &dev);
+  if (err != hipSuccess) {
+    pl_set_error("pl_lora_apply_noalloc: hipStreamGetDevice: %s", hipGetErrorString(err));
+    return PL_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= kScratchMaxDevices) {
+    pl_set_error("pl_lora_apply_noalloc: device %d beyond the %d supported", dev,
+                 kScratchMaxDevices);
+    return PL_ERR_LIMIT;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int prev = -1;
+    if ((err = hipGetDevice(&prev)) != hipSuccess || (err = hipSetDevice(dev)) != hipSuccess) {
+      pl_set_error("pl_lora_apply_noalloc: selecting device %d: %s", dev, hipGetErrorString(err));
+      return PL_ERR_LAUNCH;
+    }
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t back = hipSetDevice(prev);
+    if (err != hipSuccess || !p) {
+      pl_set_error("pl_lora_apply_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                   hipGetErrorString(err));
+      return PL_ERR_LAUNCH;
+    }
+    if (back != hipSuccess) {
+      pl_set_error("pl_lora_apply_noalloc: restoring device %d: %s", prev,
+                   hipGetErrorString(back));
+      return PL_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PL_OK;
+}
+
+// Scratch bytes a call needs: meta (256), the group records, the token list
+// and the shrink planes, each part 256-byte aligned; -1 for bad sizes.
+int64_t noalloc_bytes(int32_t dtype, int32_t rows, int32_t row_len, int32_t num_slots,
+                      int32_t group_tokens, int32_t K, int32_t ldt, int32_t k_splits) {
+  if (rows < 0 || row_len < 0 || num_slots < 1 || K <= 0 || ldt <= 0 || k_splits < 1 ||
+      (group_tokens != 16 && group_tokens != 64))
+    return -1;
+  const int64_t tokens = (int64_t)rows * row_len;
+  const int64_t tmp_rows = tokens > 0 ? tokens : 1;
+  const int64_t cap = pl_plan_group_capacity(rows, row_len, num_slots, group_tokens);
+  return 256 + align256((cap > 0 ? cap : 1) * (int64_t)sizeof(pl_group)) +
+         align256(tmp_rows * 4) +
+         workspace_bytes(shrink_planes(dtype, K, k_splits, group_tokens), tmp_rows, ldt);
+}
+
+}  // namespace
+
+extern "C" int pl_lora_apply_noalloc(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
+                                     int64_t ldy, int32_t N, const void* arena,
+                                     const pl_slot_entry* table, int32_t num_modules,
+                                     int32_t module, const int32_t* row_slot,
+                                     const int32_t* seq_lens, int32_t rows, int32_t row_len,
+                                     int32_t num_slots, int32_t group_tokens, int32_t ldt,
+                                     int32_t k_splits, int32_t epilogue, void* stream) {
+  const int64_t need = noalloc_bytes(dtype, rows, row_len, num_slots, group_tokens, K, ldt,
+                                    k_splits);
+  if (need < 0) {
+    pl_set_error("pl_lora_apply_noalloc: bad sizes rows=%d row_len=%d num_slots=%d "
+                 "group_tokens=%d K=%d ldt=%d k_splits=%d",
+                 rows, row_len, num_slots, group_tokens, K, ldt, k_splits);
+    return PL_ERR_ARG;
+  }
+  if (need > (int64_t)PL_NOALLOC_SCRATCH_BYTES) {
+    pl_set_error("pl_lora_apply_noalloc: this call needs %lld bytes of scratch; the library's "
+                 "static scratch holds %lld (use pl_plan_build + pl_lora_apply with caller "
+                 "buffers for larger batches)",
+                 (long long)need, (long long)PL_NOALLOC_SCRATCH_BYTES);
+    return PL_ERR_LIMIT;
+  }
+  if (rows > 0 && (!row_slot || !seq_lens)) {
+    pl_set_error("pl_lora_apply_noalloc: null row_slot / seq_lens");
+    return PL_ERR_ARG;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  void* base = nullptr;
+  int st = scratch_address(s, &base);
+  if (st) return st;
+  const int64_t tokens = (int64_t)rows * row_len;
+  const int64_t tmp_rows = tokens > 0 ? tokens : 1;
+  int64_t group_cap = pl_plan_group_capacity(rows, row_len, num_slots, group_tokens);
+  if (group_cap < 1) group_cap = 1;
+  char* p = reinterpret_cast<char*>(base);
+  int32_t* meta = reinterpret_cast<int32_t*>(p);
+  pl_group* groups = reinterpret_cast<pl_group*>(p + 256);
+  int32_t* tok = reinterpret_cast<int32_t*>(p + 256 + align256(group_cap * sizeof(pl_group)));
+  void* ws = p + 256 + align256(group_cap * sizeof(pl_group)) + align256(tmp_rows * 4);
+  const int64_t ws_bytes = (int64_t)PL_NOALLOC_SCRATCH_BYTES - (reinterpret_cast<char*>(ws) - p);
+  // validate every operand before anything is enqueued
+  pl_shrink_args sa;
+  pl_expand_args ea;
+  st = prepare_shrink(sa, dtype, x, ldx, K, arena, table, num_modules, 1, &module, &ws, tok,
+                      groups, meta, group_cap, group_tokens, ws_bytes, ldt, tmp_rows, k_splits);
+  if (st) return st;
+  st = prepare_expand(ea, dtype, &ws, ldt, tmp_rows, sa.k_splits, arena, table, num_modules, 1,
+                      &module, tok, groups, meta, group_cap, group_tokens, &y, &ldy, &N, epilogue);
+  if (st) return st;
+  st = pl_plan_build(row_slot, seq_lens, rows, row_len, num_slots, group_tokens, tok, groups, meta,
+                     group_cap, stream);
+  if (st) return st;
   st = dispatch_shrink(dtype, sa, group_cap, s);
   if (st) return st;
   return dispatch_expand(dtype, ea, group_cap, s);

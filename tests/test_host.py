@@ -442,6 +442,13 @@ def test_library_host_side_errors_without_gpu():
     assert st == 1 and b"dtype" in lib.pl_last_error()
     with pytest.raises(RuntimeError, match="dtype"):
         _native.check(st, "pl_sgmv_shrink")
+    # the no-alloc entry point refuses a call beyond its static scratch before any HIP call
+    st = lib.pl_lora_apply_noalloc(_native.PL_BF16, fake, 4096, 4096, fake, 4096, 4096, fake, fake, 1, 0, fake,
+                                   fake, 8192, 64, 17, 16, 64, 8, 0, None)
+    assert st == 4 and b"needs" in lib.pl_last_error() and b"static scratch" in lib.pl_last_error()
+    st = lib.pl_lora_apply_noalloc(_native.PL_BF16, fake, 4096, 4096, fake, 4096, 4096, fake, fake, 1, 0, fake,
+                                   fake, 4, 1, 17, 32, 64, 8, 0, None)
+    assert st == 1 and b"bad sizes" in lib.pl_last_error()
 
 
 def test_no_cpu_fallback_in_product_ops():

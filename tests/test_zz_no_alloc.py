@@ -1,0 +1,91 @@
+"""pl_lora_apply_noalloc (plan and shrink planes in the library's static scratch) against the entry points it
+combines, pl_plan_build + pl_lora_apply with caller-allocated buffers, through the C ABI.
+
+Two calls in a row per case, the second on a smaller batch (the scratch keeps the first call's
+contents); each must equal the existing entry points' result bit for bit and match the oracle.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle.lora import reference_forward
+from polylora_amd import _native
+from tests._util import make_cache, oracle_slot_tensors, peft_layer, tol_for
+
+pytestmark = pytest.mark.gpu
+
+K, N = 512, 384
+
+
+def _existing(lib, dt, x, y, cache, row_slot, seq, rows, row_len, group_tokens, k_splits, stream):
+    """pl_plan_build + pl_lora_apply with torch-allocated plan and workspace."""
+    dev = x.device
+    cap = int(lib.pl_plan_group_capacity(rows, row_len, cache.num_slots, group_tokens))
+    T = max(1, rows * row_len)
+    tok = torch.empty(T, dtype=torch.int32, device=dev)
+    groups = torch.empty((max(1, cap), 4), dtype=torch.int32, device=dev)
+    meta = torch.empty(4, dtype=torch.int32, device=dev)
+    _native.check(lib.pl_plan_build(row_slot.data_ptr(), seq.data_ptr(), rows, row_len, cache.num_slots,
+                                    group_tokens, tok.data_ptr(), groups.data_ptr(), meta.data_ptr(), max(1, cap),
+                                    stream), "pl_plan_build")
+    ldt = cache.rank8_cap
+    nbytes = int(lib.pl_shrink_workspace_bytes(dt, K, k_splits, group_tokens, T, ldt))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    _native.check(lib.pl_lora_apply(dt, x.data_ptr(), x.stride(0), K, y.data_ptr(), y.stride(0), N,
+                                    cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), 0,
+                                    tok.data_ptr(), groups.data_ptr(), meta.data_ptr(), max(1, cap), group_tokens,
+                                    ws.data_ptr(), nbytes, ldt, T, k_splits, _native.PL_EPI_FALLBACK, stream),
+                  "pl_lora_apply")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("group_tokens,k_splits", [(16, 4), (64, 2)])
+def test_noalloc_equals_plan_build_plus_lora_apply(gpu, dtype, group_tokens, k_splits):
+    print(f"case: noalloc dtype={dtype} group_tokens={group_tokens} k_splits={k_splits}", flush=True)
+    lib = _native.load()
+    dt = _native.dtype_code(dtype)
+    g = torch.Generator().manual_seed(31)
+    adapters = {f"n{i}": {"m": peft_layer(g, K, N, r, 2.0 * r)} for i, r in enumerate([4, 8, 16, 12])}
+    cache = make_cache(adapters, {"m": (K, N)}, 5, 16, gpu, dtype)
+    ids_pool = ["__base__", *adapters]
+    stream = _native.current_stream_handle(gpu)
+    for rows, row_len in ((40, 16), (9, 5)):  # the second call is smaller
+        ids = [ids_pool[int(i)] for i in torch.randint(0, len(ids_pool), (rows,), generator=g)]
+        row_slot = cache.ensure_resident(ids)
+        seq_cpu = torch.randint(0, row_len + 3, (rows,), generator=g, dtype=torch.int32)
+        seq = seq_cpu.to(gpu)
+        x_cpu = torch.randn(rows * row_len, K, generator=g).to(dtype)
+        base_cpu = torch.randn(rows * row_len, N, generator=g).to(dtype)
+        x = x_cpu.to(gpu)
+        y_new = base_cpu.to(gpu)
+        y_old = base_cpu.to(gpu)
+        torch.cuda.synchronize()
+        st = lib.pl_lora_apply_noalloc(dt, x.data_ptr(), x.stride(0), K, y_new.data_ptr(), y_new.stride(0), N,
+                                       cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), 0,
+                                       row_slot.data_ptr(), seq.data_ptr(), rows, row_len, cache.num_slots,
+                                       group_tokens, cache.rank8_cap, k_splits, _native.PL_EPI_FALLBACK, stream)
+        _native.check(st, "pl_lora_apply_noalloc")
+        torch.cuda.synchronize()
+        _existing(lib, dt, x, y_old, cache, row_slot, seq, rows, row_len, group_tokens, k_splits, stream)
+        assert torch.equal(y_new, y_old), (rows, row_len)
+        A, B, rk, sc = oracle_slot_tensors(cache, adapters, "m", dtype)
+        want = reference_forward(x_cpu.view(rows, row_len, K), base_cpu.view(rows, row_len, N), seq_cpu,
+                                 row_slot.cpu().long(), A, B, rk, sc)
+        torch.testing.assert_close(y_new.cpu().view(rows, row_len, N), want, **tol_for(dtype))
+
+
+def test_noalloc_rejects_a_batch_beyond_its_scratch(gpu):
+    print("case: noalloc limit", flush=True)
+    lib = _native.load()
+    g = torch.Generator().manual_seed(32)
+    cache = make_cache({"z": {"m": peft_layer(g, K, N, 8, 16.0)}}, {"m": (K, N)}, 1, 64, gpu, torch.bfloat16)
+    rows, row_len = 4096, 64  # 262144 tokens: far beyond 32 MiB of planes
+    x = torch.empty(8, K, dtype=torch.bfloat16, device=gpu)  # never read: the size check fails first
+    st = lib.pl_lora_apply_noalloc(_native.PL_BF16, x.data_ptr(), K, K, x.data_ptr(), K, N, cache.arena.data_ptr(),
+                                   cache.table.data_ptr(), 1, 0, x.data_ptr(), x.data_ptr(), rows, row_len,
+                                   cache.num_slots, 64, cache.rank8_cap, 8, 0, _native.current_stream_handle(gpu))
+    assert st == 4  # PL_ERR_LIMIT
+    assert b"static scratch" in lib.pl_last_error()
