@@ -115,9 +115,9 @@ const char* pl_last_error(void);
  * that the caller's allocator and this library share one HIP runtime. */
 int pl_is_device_pointer(const void* ptr);
 
-/* Upper bound on the number of groups pl_plan_build can emit for `rows` rows
- * of `row_len` tokens over `num_slots` slots:
- * ceil(rows*row_len/group_tokens) + num_slots - 1. */
+/* Group records a plan for `rows` rows of `row_len` tokens over `num_slots`
+ * slots needs: at most n = ceil(rows*row_len/group_tokens) + num_slots - 1
+ * groups, placed below 8 * ceil(n / 8). */
 int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t num_slots,
                                int32_t group_tokens);
 
@@ -127,10 +127,16 @@ int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t num_slots,
  *                   min(max(seq_len,0), row_len) tokens (layers.py:127 slicing)
  *   group_tokens    16 or 64: tokens per group at most
  *   tok[rows*row_len]          out: token indices (row*row_len + m), grouped by slot
- *   groups[group_cap]          out: pl_group list
- *   meta[4]                    out: {num_groups, num_tokens, group_tokens, 0}
+ *   groups[group_cap]          out: pl_group records
+ *   meta[4]                    out: {num_groups, num_tokens, group_tokens,
+ *                                    positions = 8 * ceil(num_groups / 8)}
  * Rows with slot 0, slot >= num_slots, slot < 0 or length 0 are skipped.
- * Token order inside one slot is unspecified; every consumer is order-free. */
+ * Token order inside one slot is unspecified; every consumer is order-free.
+ * Placement: the kernels give the work of the record at position p to XCD
+ * p % 8, so the slot-major list of the n groups is cut into 8 contiguous
+ * chunks, chunk x = groups [x*n/8, (x+1)*n/8), and the i-th group of chunk
+ * x is stored at position 8*i + x: an adapter's groups share one or two XCDs'
+ * L2.  Every other record below group_cap is empty (slot 0, length 0). */
 int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,
                   int32_t row_len, int32_t num_slots, int32_t group_tokens, int32_t* tok,
                   pl_group* groups, int32_t* meta, int64_t group_cap, void* stream);

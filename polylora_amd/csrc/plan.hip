@@ -7,16 +7,44 @@
 // b*row_len + m, m < L (the slicing x[b, :seq_len] of layers.py:127).
 //
 // Steps: per-slot token counts (LDS atomics), one block-wide exclusive scan
-// of counts and of group counts, group list emission (records past the last
-// group, up to the capacity, are empty), then each wave copies
-// the token indices of its rows to the slot's segment.  Row order inside a
+// of counts and of group counts, group emission, then the token indices of
+// each row are copied to the slot's segment (one thread per row for rows of
+// up to 16 tokens, one wave per row for longer ones).  Row order inside a
 // segment follows LDS atomic order and is not fixed; no consumer depends on
 // it.
+//
+// Group placement.  Kernels give the work items of the group at position p
+// to XCD p % 8 (workgroups are dealt to the 8 XCDs round-robin).  The plan
+// puts the slot-major group list in 8 contiguous chunks, chunk x = groups
+// [x*n/8, (x+1)*n/8) of the n groups, and the i-th group of chunk x at
+// position 8*i + x, so an adapter's groups share one XCD's L2 (or two, where
+// a chunk boundary splits it) instead of all eight, and its A and B come
+// from HBM about once per launch.  Positions below 8*ceil(n/8) that get no
+// group, and the rest of the capacity, hold empty records (slot 0, length 0).
 #include "pl_common.h"
 
 namespace {
 
 constexpr int kPlanThreads = 1024;
+
+// First slot-major group index of XCD chunk x (x = 0..8) of n groups.
+__device__ __forceinline__ int pl_chunk_lo(int x, int n) { return (int)(((int64_t)x * n) / 8); }
+
+// Position of slot-major group gi among n groups (see "Group placement").
+__device__ __forceinline__ int64_t pl_plan_position(int gi, int n) {
+  int x = 7;
+  while (x > 0 && pl_chunk_lo(x, n) > gi) --x;
+  return (int64_t)(gi - pl_chunk_lo(x, n)) * 8 + x;
+}
+
+__device__ __forceinline__ bool pl_plan_position_used(int64_t p, int n) {
+  const int x = (int)(p & 7);
+  const int64_t i = p >> 3;
+  return pl_chunk_lo(x, n) + i < pl_chunk_lo(x + 1, n);
+}
+
+// Positions a plan of n groups spans: 8 * ceil(n / 8).
+__device__ __forceinline__ int pl_plan_positions(int n) { return (n + 7) / 8 * 8; }
 
 __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     const int32_t* __restrict__ row_slot, const int32_t* __restrict__ seq_lens, int32_t rows,
@@ -92,7 +120,7 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     meta[0] = tg;
     meta[1] = tt;
     meta[2] = group_tokens;
-    meta[3] = 0;
+    meta[3] = pl_plan_positions(tg);
   }
   __syncthreads();
 
@@ -100,41 +128,59 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     const int c = cnt[s];
     const int ng = (c + group_tokens - 1) / group_tokens;
     for (int q = 0; q < ng; ++q) {
-      const int64_t gi = (int64_t)goff[s] + q;
-      if (gi < group_cap) {
+      const int64_t p = pl_plan_position(goff[s] + q, tg);
+      if (p < group_cap) {
         pl_group gr;
         gr.slot = s;
         gr.start = off[s] + q * group_tokens;
         gr.len = min(group_tokens, c - q * group_tokens);
         gr.reserved = 0;
-        groups[gi] = gr;
+        groups[p] = gr;
       }
     }
   }
-  // The rest of the capacity holds empty groups (slot 0, length 0), so a
-  // kernel may read any record below group_cap without first reading meta.
-  for (int64_t gi = (int64_t)tg + tid; gi < group_cap; gi += kPlanThreads) {
-    pl_group gr;
-    gr.slot = 0;
-    gr.start = 0;
-    gr.len = 0;
-    gr.reserved = 0;
-    groups[gi] = gr;
+  // Every other position up to the capacity holds an empty group (slot 0,
+  // length 0), so a kernel may read any record below group_cap without first
+  // reading meta.
+  for (int64_t p = tid; p < group_cap; p += kPlanThreads) {
+    if (!pl_plan_position_used(p, tg)) {
+      pl_group gr;
+      gr.slot = 0;
+      gr.start = 0;
+      gr.len = 0;
+      gr.reserved = 0;
+      groups[p] = gr;
+    }
   }
   __syncthreads();
   for (int s = tid; s < S; s += kPlanThreads) cnt[s] = 0;  // reused as fill counters
   __syncthreads();
 
-  for (int b = wave; b < rows; b += kPlanThreads / 64) {
-    const int s = row_slot[b];
-    int L = seq_lens[b];
-    L = L < 0 ? 0 : (L > row_len ? row_len : L);
-    if (s > 0 && s < S && L > 0) {
-      int p = 0;
-      if (lane == 0) p = off[s] + atomicAdd(&cnt[s], L);
-      p = __shfl(p, 0);
-      const int base = b * row_len;
-      for (int m = lane; m < L; m += 64) tok[p + m] = base + m;
+  if (row_len <= 16) {
+    // short rows (decode, flattened tokens): one thread per row
+    for (int b = tid; b < rows; b += kPlanThreads) {
+      const int s = row_slot[b];
+      int L = seq_lens[b];
+      L = L < 0 ? 0 : (L > row_len ? row_len : L);
+      if (s > 0 && s < S && L > 0) {
+        const int p = off[s] + atomicAdd(&cnt[s], L);
+        const int base = b * row_len;
+        for (int m = 0; m < L; ++m) tok[p + m] = base + m;
+      }
+    }
+  } else {
+    // long rows (prefill): one wave per row
+    for (int b = wave; b < rows; b += kPlanThreads / 64) {
+      const int s = row_slot[b];
+      int L = seq_lens[b];
+      L = L < 0 ? 0 : (L > row_len ? row_len : L);
+      if (s > 0 && s < S && L > 0) {
+        int p = 0;
+        if (lane == 0) p = off[s] + atomicAdd(&cnt[s], L);
+        p = __shfl(p, 0);
+        const int base = b * row_len;
+        for (int m = lane; m < L; m += 64) tok[p + m] = base + m;
+      }
     }
   }
 }
@@ -172,7 +218,9 @@ extern "C" int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t
                                           int32_t group_tokens) {
   if (rows < 0 || row_len < 0 || num_slots < 1 || group_tokens < 1) return 0;
   const int64_t t = (int64_t)rows * row_len;
-  return (t + group_tokens - 1) / group_tokens + (num_slots - 1);
+  // at most ceil(t/G) + num_slots - 1 groups, placed below 8 * ceil(groups / 8)
+  const int64_t n = (t + group_tokens - 1) / group_tokens + (num_slots - 1);
+  return (n + 7) / 8 * 8;
 }
 
 extern "C" int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,

@@ -15,6 +15,11 @@
 // set of sibling Linears fed the same x), no workspace and no split-K
 // partial sums; results are bitwise reproducible.
 //
+// y is streamed with non-temporal loads and stores (each byte is touched once
+// per launch), and so is x when only one workgroup reads each x row (one
+// module, one column slice); A and B, which every tile of a slot rereads, go
+// through the caches normally.
+//
 // A tile's slices (column ranges) and modules all recompute or share the
 // same x rows; they run on one XCD (workgroups are dealt to the 8 XCDs
 // round-robin by index), so x and A are fetched from HBM once and reread
@@ -76,7 +81,7 @@ struct pl_fused_lds {
   enum { kXRow = 256 / (int)sizeof(T) + kPad };  // per-wave x tile [token][one step's K]
 };
 
-template <int DT, int JT>
+template <int DT, int JT, bool XNT>
 __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_group& grp, int len,
                                               const pl_slot_entry& e, int rank, int job, int slice,
                                               pl_f32x4 (*red)[4][64],
@@ -162,7 +167,13 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
       }
     }
 #pragma unroll
-    for (int i = 0; i < kXLoads; ++i) xf[i] = pl_ld16_or0(xrow[i] + kb, xok[i] && kb + xp * E < k1);
+    for (int i = 0; i < kXLoads; ++i) {
+      // streamed when no other workgroup of the launch reads these x rows
+      if constexpr (XNT)
+        xf[i] = pl_ld16_nt_or0(xrow[i] + kb, xok[i] && kb + xp * E < k1);
+      else
+        xf[i] = pl_ld16_or0(xrow[i] + kb, xok[i] && kb + xp * E < k1);
+    }
   };
   auto mfma_k = [&](const pl_u32x4 (&xf)[kXLoads], const pl_u32x4 (&af)[JT][kFCC]) {
     // through the wave's LDS tile into the MFMA layout (one wave writes and
@@ -226,7 +237,8 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
       }
     }
 #pragma unroll
-    for (int i = 0; i < kYLoads; ++i) yv[i] = pl_ld16_or0(yrow[i] + cb, yok[i] && cb + yq * E < c1);
+    for (int i = 0; i < kYLoads; ++i)
+      yv[i] = pl_ld16_nt_or0(yrow[i] + cb, yok[i] && cb + yq * E < c1);
   };
   // a ring of kFStages steps: the loads of the next kFStages-1 steps are in
   // flight while one is applied; steps past c1 load only zeros
@@ -288,11 +300,11 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
           const T8 dd = __builtin_bit_cast(T8, dv);
 #pragma unroll
           for (int q = 0; q < 8; ++q) yy[q] = (T)((float)yy[q] + (float)dd[q]);
-          *reinterpret_cast<pl_u32x4*>(yrow[i] + cb) = __builtin_bit_cast(pl_u32x4, yy);
+          pl_st16_nt(yrow[i] + cb, __builtin_bit_cast(pl_u32x4, yy));
         } else {
           pl_f32x4 yy = __builtin_bit_cast(pl_f32x4, yv[i]);
           yy += __builtin_bit_cast(pl_f32x4, dv);
-          *reinterpret_cast<pl_f32x4*>(yrow[i] + cb) = yy;
+          pl_st16_nt(yrow[i] + cb, __builtin_bit_cast(pl_u32x4, yy));
         }
       }
     }
@@ -311,7 +323,7 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   }
 }
 
-template <int DT, int JTMAX>
+template <int DT, int JTMAX, bool XNT>
 __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args a) {
   typedef typename pl_traits<DT>::T T;
   typedef pl_fused_lds<DT> L;
@@ -331,7 +343,7 @@ __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args
   const int ts = ws.j / a.n_jobs;
   const int rt = ts / a.slices;
   const int slice = ts - rt * a.slices;
-  const int n_groups = a.meta[0];
+  const int n_groups = a.meta[3];  // positions in use (the plan spreads groups over them)
   pl_group grp = a.groups[g];
   grp.start += rt * 16;
   const int len = min(grp.len - rt * 16, 16);
@@ -345,22 +357,34 @@ __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args
 
   const int jt = (rank + 15) >> 4;
   if (JTMAX == 1 || jt == 1)
-    pl_fused_body<DT, 1>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, 1, XNT>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
   else if (JTMAX == 2 || jt == 2)
-    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX, XNT>(a, grp, len, e, rank, job, slice, red, tt, dbuf,
+                                                  xtile);
   else
-    pl_fused_body<DT, JTMAX>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, JTMAX, XNT>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
+}
+
+template <int DT, bool XNT>
+void launch_fused_x(const pl_fused_args& a, int jtmax, dim3 grid, hipStream_t stream) {
+  if (jtmax <= 1)
+    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 1, XNT>), grid, dim3(kFThreads), 0, stream, a);
+  else if (jtmax == 2)
+    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 2, XNT>), grid, dim3(kFThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 4, XNT>), grid, dim3(kFThreads), 0, stream, a);
 }
 
 template <int DT>
 int launch_fused(const pl_fused_args& a, int jtmax, hipStream_t stream) {
   const dim3 grid((unsigned)pl_xcd_grid(a.group_cap, (int64_t)a.n_jobs * a.sub * a.slices));
-  if (jtmax <= 1)
-    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 1>), grid, dim3(kFThreads), 0, stream, a);
-  else if (jtmax == 2)
-    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 2>), grid, dim3(kFThreads), 0, stream, a);
+  // x is streamed (non-temporal) only when each tile's x rows have one reader:
+  // sibling modules and column slices of a tile reread them from L2.  Prefill
+  // (q/k/v and gate/up stacked) lost 2 ms per forward with x streamed.
+  if (a.n_jobs == 1 && a.slices == 1)
+    launch_fused_x<DT, true>(a, jtmax, grid, stream);
   else
-    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 4>), grid, dim3(kFThreads), 0, stream, a);
+    launch_fused_x<DT, false>(a, jtmax, grid, stream);
   return pl_launch_status("pl_lora_fused");
 }
 

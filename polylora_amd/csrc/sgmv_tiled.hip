@@ -27,6 +27,13 @@
 // row-major layout of y, and the fused add-back reads and writes y once with
 // 16-byte accesses (512 contiguous bytes per row).
 //
+// Adapter weights (A in the short shrink, B in the expand) are read with
+// non-temporal loads: a decode launch reads each adapter's A and B about once, and
+// keeping them out of the L2 leaves it to x and the split planes, which many
+// workgroups reread (decode sequence of a Llama-3-8B layer, 47 adapters:
+// 87.4 -> 83.8 us; non-temporal x or plane loads made it slower).  The long
+// shrink keeps A cached: every 64-token group of a slot rereads it.
+//
 // Latency is what these launches are short of, so every kernel issues a
 // wave's loads together before their first use: guards select an address
 // (masked lanes read a zero page) instead of branching around a load, and
@@ -170,7 +177,7 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
   const int g = rest / a.k_splits;
   // the group count and the group record load together (every record below
   // the capacity is readable); the record is used only for g below the count
-  const int n_groups = a.meta[0];
+  const int n_groups = a.meta[3];  // positions in use (the plan spreads groups over them)
   const pl_group grp = a.groups[g];
   const int len = min(grp.len, 16);  // the host pairs 16-token groups with this kernel
   if (g >= n_groups || len <= 0) return;
@@ -210,7 +217,7 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
       for (int cc = 0; cc < kShortCC; ++cc) {
         const int k = kb + cc * kInstr;
         const int wb = min(kInstr, K - k);
-        af[jt][cc] = pl_ld16_or0(A + (int64_t)t0 * K + (int64_t)k * rt + li * wb + lg * E,
+        af[jt][cc] = pl_ld16_nt_or0(A + (int64_t)t0 * K + (int64_t)k * rt + li * wb + lg * E,
                                  li < rt && k + lg * E < k1);
       }
     }
@@ -290,7 +297,7 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_long(pl_shrink_args a) {
   const int gc = blockIdx.x / a.n_jobs;
   const int g = gc / a.k_splits;
   const int c = gc - g * a.k_splits;
-  const int n_groups = a.meta[0];
+  const int n_groups = a.meta[3];  // positions in use (the plan spreads groups over them)
   const pl_group grp = a.groups[g];
   const int len = min(grp.len, 16 * kLongRT);  // the host pairs 64-token groups with this kernel
   if (g >= n_groups || len <= 0) return;
@@ -431,7 +438,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   const int c = cg - a.chunk0[job];
   // the group count and the group record load together (every record below
   // the capacity is readable); the record is used only for g below the count
-  const int n_groups = a.meta[0];
+  const int n_groups = a.meta[3];  // positions in use (the plan spreads groups over them)
   pl_group grp = a.groups[g];
   grp.start += rt * 16;
   const int len = min(grp.len - rt * 16, 16);
@@ -483,7 +490,7 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
       for (int ct = 0; ct < S::kCT; ++ct) {
         const int nb = n0 + ct * 16;
         const int nt = min(16, N - nb);
-        bf[s][ct] = pl_ld16_or0(Bc + (int64_t)nb * r8 + (int64_t)j0 * nt + li * wb + lg * E,
+        bf[s][ct] = pl_ld16_nt_or0(Bc + (int64_t)nb * r8 + (int64_t)j0 * nt + li * wb + lg * E,
                                 li < nt && j0 + lg * E < r8);
       }
     }

@@ -412,9 +412,11 @@ def test_library_host_side_errors_without_gpu():
     """Argument checks run before any HIP call, so they are testable on the CPU."""
     lib = _native.load()
     assert lib.pl_version() >= 100
-    assert lib.pl_plan_group_capacity(256, 1, 65, 64) == 4 + 64
-    assert lib.pl_plan_group_capacity(256, 1, 65, 16) == 16 + 64
-    assert lib.pl_plan_group_capacity(32, 1024, 9, 64) == 512 + 8
+    # at most ceil(tokens / G) + slots - 1 groups, rounded up to whole XCD rounds of 8 positions
+    assert lib.pl_plan_group_capacity(256, 1, 65, 64) == 72  # 4 + 64 = 68 -> 72
+    assert lib.pl_plan_group_capacity(256, 1, 65, 16) == 80  # 16 + 64
+    assert lib.pl_plan_group_capacity(32, 1024, 9, 64) == 520  # 512 + 8
+    assert lib.pl_plan_group_capacity(4096, 1, 17, 16) == 272  # 256 + 16
     # split planes: whole wave steps (16-token groups: 64 elements of a
     # 2-byte type per wave step, 32 of fp32; 64-token groups: 64 and 32), four
     # waves per split, at most the requested count and at most 16

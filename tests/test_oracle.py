@@ -279,8 +279,32 @@ def _plan_from_expected(row_slot, seq_lens, row_len, num_slots):
             chunk = toks[q : q + plan.GROUP_TOKENS]
             groups.append((slot, len(tok), len(chunk), 0))
             tok.extend(chunk)
-    meta = np.array([len(groups), len(tok), plan.GROUP_TOKENS, 0])
-    return np.array(tok, dtype=np.int64), np.array(groups, dtype=np.int64).reshape(-1, 4), meta
+    n = len(groups)
+    placed = np.zeros((plan.positions(n), 4), dtype=np.int64)
+    for gi, rec in enumerate(groups):
+        placed[plan.group_position(gi, n)] = rec
+    meta = np.array([n, len(tok), plan.GROUP_TOKENS, plan.positions(n)])
+    return np.array(tok, dtype=np.int64), placed, meta, np.array(groups, dtype=np.int64).reshape(-1, 4)
+
+
+@pytest.mark.parametrize("n", list(range(0, 70)) + [252, 1001])
+def test_group_position_is_a_balanced_chunked_bijection(n):
+    """Placement of the slot-major groups: chunk x of 8 contiguous, balanced chunks at positions = x mod 8."""
+    pos = [plan.group_position(g, n) for g in range(n)]
+    assert len(set(pos)) == n and all(0 <= p < plan.positions(n) for p in pos)
+    assert plan.positions(n) % 8 == 0 and plan.positions(n) - n < 8
+    sizes = []
+    for x in range(8):
+        members = [g for g, p in enumerate(pos) if p % 8 == x]
+        # the groups one XCD gets are a contiguous run, stored in order at x, x+8, x+16, ...
+        assert members == list(range(members[0], members[0] + len(members))) if members else True
+        assert [pos[g] for g in members] == [x + 8 * i for i in range(len(members))]
+        sizes.append(len(members))
+    assert max(sizes) - min(sizes) <= 1
+    # chunks follow the slot-major order: chunk x ends where chunk x+1 starts
+    starts = [min((g for g, p in enumerate(pos) if p % 8 == x), default=None) for x in range(8)]
+    nonempty = [v for v in starts if v is not None]
+    assert nonempty == sorted(nonempty)
 
 
 def test_expected_tokens_brute_force():
@@ -294,8 +318,11 @@ def test_check_plan_accepts_valid_and_rejects_planted():
     rng = np.random.default_rng(0)
     row_slot = rng.integers(-1, 8, size=40).tolist()
     seq_lens = rng.integers(-1, 80, size=40).tolist()
-    tok, groups, meta = _plan_from_expected(row_slot, seq_lens, 70, 7)
+    tok, groups, meta, slot_major = _plan_from_expected(row_slot, seq_lens, 70, 7)
     plan.check_plan(tok, groups, meta, row_slot, seq_lens, 70, 7)
+    assert int(meta[0]) > 8
+    with pytest.raises(AssertionError):  # the records left in slot-major order, not placed per XCD
+        plan.check_plan(tok, slot_major, meta, row_slot, seq_lens, 70, 7)
     bad_tok = tok.copy()
     bad_tok[3] += 1  # a token moved
     with pytest.raises(AssertionError):
@@ -308,7 +335,7 @@ def test_check_plan_accepts_valid_and_rejects_planted():
     bad_meta[1] += 1
     with pytest.raises(AssertionError):
         plan.check_plan(tok, groups, bad_meta, row_slot, seq_lens, 70, 7)
-    # capacity past the last group holds empty records
+    # capacity past the last position holds empty records
     padded = np.concatenate([groups, np.zeros((3, 4), dtype=groups.dtype)])
     plan.check_plan(tok, padded, meta, row_slot, seq_lens, 70, 7)
     padded[-1] = (1, 0, 1, 0)  # a stale record past the end
