@@ -134,13 +134,18 @@ def register_attention() -> None:
 
 # ----------------------------------------------------------------------------- adapters
 def _lora_pair(gen, fin, fout, rank, std, device):
-    a = (torch.randn(rank, fin, generator=gen, device=device) * std).to(torch.bfloat16).cpu()
-    b = (torch.randn(fout, rank, generator=gen, device=device) * std).to(torch.bfloat16).cpu()
+    """PEFT-layout lora_A [rank, in] and lora_B [out, rank], N(0, std), bf16, generated on `device`."""
+    a = (torch.randn(rank, fin, generator=gen, device=device) * std).to(torch.bfloat16)
+    b = (torch.randn(fout, rank, generator=gen, device=device) * std).to(torch.bfloat16)
     return a, b
 
 
 def add_random_adapters(pm, ranks: dict, std: float = 0.02, seed: int = 0, device="cpu", alpha_per_rank: float = 2.0):
-    """Random PEFT-layout adapters (all target modules) added to pm's CPU store; returns id -> rank."""
+    """Random PEFT-layout adapters (all target modules) added to pm's CPU store; returns id -> rank.
+
+    The store packs each straight into its pinned slot image (its layout is
+    bound by the GPU cache), so the tensors generated here are not kept.
+    """
     from polylora_amd.store import CpuLayerWeights
 
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -148,9 +153,73 @@ def add_random_adapters(pm, ranks: dict, std: float = 0.02, seed: int = 0, devic
         layers = {}
         for spec in pm.module_specs:
             a, b = _lora_pair(gen, spec.in_features, spec.out_features, r, std, device)
-            layers[spec.name] = CpuLayerWeights(A=a.t().contiguous(), B=b.t().contiguous(), rank=r, scale=alpha_per_rank)
+            layers[spec.name] = CpuLayerWeights(A=a.t(), B=b.t(), rank=r, scale=alpha_per_rank)
         pm.adapter_store.add_adapter(aid, layers)
     return ranks
+
+
+def random_image_catalog(pm, n: int, rank: int, seed: int, std: float = 0.02, alpha_per_rank: float = 2.0) -> list:
+    """n adapters of one rank on every target module, each with its own pinned slot image of N(0, std) weights.
+
+    Each image is laid out by ImageBuilder for the cache's slot layout (so its
+    slot-table rows are the ones a PEFT adapter of these ranks gets) and its
+    A and B parts are filled with one draw of random bf16 values generated on
+    the GPU; with i.i.d. weights the order of the values inside a part does
+    not matter, so no per-module packing is needed.  Added with
+    add_adapter_image: one host copy per adapter.
+    """
+    from polylora_amd.slot_image import AdapterImage, ImageBuilder
+
+    layout = pm.adapter_cache.layout
+    device = pm.adapter_cache.device
+    modules = {spec.name: (rank, alpha_per_rank) for spec in pm.module_specs}
+    gen = torch.Generator(device=device).manual_seed(seed)
+    ids = [f"cat{i:04d}" for i in range(n)]
+    progress = _Progress("catalog")
+    data_ranges = None
+    for i, aid in enumerate(ids):
+        progress.tick(f"{i}/{n} images")
+        builder = ImageBuilder(layout, modules, pin=pm.adapter_store.pin_image)
+        data = builder.data
+        if data_ranges is None:  # the A and B parts; the alignment gaps between them stay zero
+            data_ranges = []
+            for name, (r, a_off, b_off) in builder.parts.items():
+                spec = layout.specs[layout.index[name]]
+                data_ranges.append((a_off, a_off + r * spec.in_features * layout.elem))
+                data_ranges.append((b_off, b_off + spec.out_features * ((r + 7) // 8 * 8) * layout.elem))
+            data_ranges.sort()
+            merged = [list(data_ranges[0])]
+            for lo, hi in data_ranges[1:]:
+                if lo == merged[-1][1]:
+                    merged[-1][1] = hi
+                else:
+                    merged.append([lo, hi])
+            data_ranges = merged
+        vals = (torch.randn(data.numel() // 2, generator=gen, device=device) * std).to(torch.bfloat16).view(torch.uint8)
+        for lo, hi in data_ranges:
+            data[lo:hi].copy_(vals[lo:hi])
+        pm.adapter_store.add_adapter_image(aid, AdapterImage(layout, data, builder.rows, builder.pinned))
+    torch.cuda.synchronize()
+    return ids
+
+
+class _Progress:
+    """Log a line from inside a long loop at most every `every` seconds (a profiler run must not look silent)."""
+
+    def __init__(self, what: str, every: float = 20.0) -> None:
+        self.what, self.every = what, every
+        self.t0 = self.last = time.perf_counter()
+
+    def tick(self, where: str) -> None:
+        now = time.perf_counter()
+        if now - self.last >= self.every:
+            self.last = now
+            _log(f"{self.what}: {where} ({now - self.t0:.0f} s)")
+
+
+def _rank_of(pm, adapter_id: str, module: str) -> int:
+    """An adapter's rank in a module (0 where it has no weights), without materializing its weights."""
+    return pm.adapter_store.adapters[adapter_id].module_ranks().get(module, (0, 0.0))[0]
 
 
 # ----------------------------------------------------------------------------- config 1: DeBERTa fp32
@@ -472,7 +541,9 @@ def time_launches(fns: list, reps: int, warmup: int = 2) -> float:
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record(stream)
-    for _ in range(reps):
+    progress = _Progress("timed launches")
+    for i in range(reps):
+        progress.tick(f"pass {i}/{reps} of {len(fns)} launches")
         for f in fns:
             f()
     t1.record(stream)
@@ -668,13 +739,10 @@ def decode_lora_bytes(pm, adapter_ids: list, rows: int) -> dict:
     total = xy = ab = flops = 0
     for spec in pm.module_specs:
         for aid in uniq:
-            w = pm.adapter_store.adapters[aid].layers.get(spec.name)
-            if w is None:
-                continue
-            ab += es * w.rank * (spec.in_features + spec.out_features)
-        t_act = sum(1 for a in active if pm.adapter_store.adapters[a].layers.get(spec.name) is not None)
+            ab += es * _rank_of(pm, aid, spec.name) * (spec.in_features + spec.out_features)
+        t_act = sum(1 for a in active if _rank_of(pm, a, spec.name) > 0)
         xy += es * t_act * spec.in_features + 2 * es * t_act * spec.out_features
-        flops += sum(2 * pm.adapter_store.adapters[a].layers[spec.name].rank * (spec.in_features + spec.out_features) for a in active)
+        flops += sum(2 * _rank_of(pm, a, spec.name) * (spec.in_features + spec.out_features) for a in active)
     total = xy + ab
     return {"total": total, "xy": xy, "ab": ab, "flops": flops, "active_rows": len(active), "distinct": len(uniq)}
 
@@ -811,7 +879,9 @@ def _graph_ms(fn, reps: int) -> float:
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record()
-    for _ in range(reps):
+    progress = _Progress("graph replays")
+    for i in range(reps):
+        progress.tick(f"replay {i}/{reps}")
         g.replay()
     t1.record()
     torch.cuda.synchronize()
@@ -823,7 +893,9 @@ def _eager_ms(fn, reps: int) -> float:
         fn()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(reps):
+    progress = _Progress("eager steps")
+    for i in range(reps):
+        progress.tick(f"step {i}/{reps}")
         fn()
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / reps * 1e3
@@ -912,13 +984,11 @@ def prefill_bytes(pm, adapter_ids: list, lens: list) -> dict:
     for spec in pm.module_specs:
         sibling = spec.name.rsplit(".", 1)[-1] in ("k_proj", "v_proj", "up_proj")
         for aid, n in zip(adapter_ids, lens):
-            w = pm.adapter_store.adapters[aid].layers[spec.name]
             xy += es * n * spec.in_features + 2 * es * n * spec.out_features
             repeat_x += es * n * spec.in_features if sibling else 0
-            flops += 2 * n * w.rank * (spec.in_features + spec.out_features)
+            flops += 2 * n * _rank_of(pm, aid, spec.name) * (spec.in_features + spec.out_features)
         for aid in uniq:
-            w = pm.adapter_store.adapters[aid].layers[spec.name]
-            ab += es * w.rank * (spec.in_features + spec.out_features)
+            ab += es * _rank_of(pm, aid, spec.name) * (spec.in_features + spec.out_features)
     return {"total": xy + ab, "shared_x": xy + ab - repeat_x, "flops": flops}
 
 
@@ -993,34 +1063,32 @@ def run_churn(args) -> dict:
     its adapters need.  Loads go to the side stream and a slot is rewritten
     only after the forwards that read it; the host never waits for the GPU,
     so it queues the next sub-batch's loads and forward while the device is
-    still copying and computing.  The catalog
-    aliases 64 distinct random weight images (adapter i uses image i % 64) so
-    that the pinned host catalog is 5.4 GB instead of 86 GB; every load still
-    copies the full 84 MB image.  Compared with the same rows restricted to 32
-    resident adapters (no loads).
+    still copying and computing.  Every adapter of the catalog is its own
+    84 MB pinned slot image (the store's one host copy of it; 86 GB for 1024
+    adapters).  Compared with the same rows restricted to 32 resident adapters
+    (no loads).
     """
     from transformers import DynamicCache
 
     from polylora_amd import PolyLoraConfig, PolyLoraModel
-    from polylora_amd.store import CpuAdapter
 
     device = torch.device("cuda", 0)
     rng = np.random.default_rng(1005)
     model = build_llama(device, args.decode_layers, seed=1005)
     pm = PolyLoraModel(model, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=32, max_rank=16)).eval()
-    images = [f"img{i:02d}" for i in range(64)]
-    add_random_adapters(pm, {n: 16 for n in images}, seed=1005, device=device)
+    # page-locked host memory is limited per process (about 65 GiB on MI355X hosts measured
+    # so far): the Zipf head of the catalog is pinned, the tail stays pageable (its loads
+    # go through the pinned staging ring)
+    pm.adapter_store.pinned_bytes_limit = int(args.churn_pinned_gib * (1 << 30))
+    n_cat = args.churn_catalog
+    t_cat = time.perf_counter()
+    catalog = random_image_catalog(pm, n_cat, rank=16, seed=1005)
+    t_cat = time.perf_counter() - t_cat
     store = pm.adapter_store
-    catalog = [f"cat{i:04d}" for i in range(1024)]
-    for i, aid in enumerate(catalog):
-        src = store.adapters[images[i % 64]]
-        store.adapters[aid] = CpuAdapter(aid, {}, src.layers, packed=src.packed)
-    for n in images:
-        store.adapters.pop(n)
-    w = 1.0 / np.arange(1, 1025) ** 0.9
+    w = 1.0 / np.arange(1, n_cat + 1) ** 0.9
     w /= w.sum()
     B = 128
-    draws = [rng.choice(1024, size=B, p=w) for _ in range(args.churn_steps + 2)]
+    draws = [rng.choice(n_cat, size=B, p=w) for _ in range(args.churn_steps + 2)]
     steps = [[catalog[int(i)] for i in d] for d in draws]
 
     limit = args.churn_sub_distinct
@@ -1054,8 +1122,10 @@ def run_churn(args) -> dict:
         loads0 = pm.adapter_cache.loads
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        progress = _Progress("churn")
         with torch.inference_mode():
-            for sub in batches:
+            for i, sub in enumerate(batches):
+                progress.tick(f"sub-batch {i + 1}/{len(batches)}")
                 x = torch.randint(0, vocab, (len(sub), 1), generator=gen, device=device)
                 # a (fresh) KV cache, as in decoding; without one, transformers
                 # checks position_ids for packed sequences, which waits for the
@@ -1066,9 +1136,6 @@ def run_churn(args) -> dict:
         torch.cuda.synchronize()
         return time.perf_counter() - t0, n_tok, pm.adapter_cache.loads - loads0
 
-    # pack every image once and touch the pinned copies before timing
-    for n in range(64):
-        pm.adapter_cache._packed(store.adapters[catalog[n]])
     churn_batches = [sub for ids in steps[2:] for sub in sub_batches(ids)]
     run([sub for ids in steps[:2] for sub in sub_batches(ids)])
     churn_s, n_tok, loads = run(churn_batches)
@@ -1079,9 +1146,10 @@ def run_churn(args) -> dict:
     hot_steps = [[hot[int(i) % 32] for i in d] for d in draws]
     run(hot_steps[:2])
     hot_s, hot_tok, hot_loads = run(hot_steps[2:])
-    image_bytes = int(pm.adapter_cache._packed(store.adapters[catalog[0]]).image.numel())
+    img = store.adapters[catalog[0]].image.data
+    image_bytes = int(img.numel())
+    pinned_images = sum(1 for a in catalog if store.adapters[a].image.pinned)
     # pinned host -> device bandwidth of one adapter image
-    img = pm.adapter_cache._packed(store.adapters[catalog[0]]).image
     dst = torch.empty(image_bytes, dtype=torch.uint8, device=device)
     for _ in range(3):
         dst.copy_(img, non_blocking=True)
@@ -1093,7 +1161,12 @@ def run_churn(args) -> dict:
     h2d_gbs = 10 * image_bytes / (time.perf_counter() - t0) / 1e9
     copy_s = loads * image_bytes / (h2d_gbs * 1e9)
     overlap = (copy_s + comp_s - churn_s) / max(1e-9, min(copy_s, comp_s))
-    out = {"steps": args.churn_steps, "batch": B, "slots": 32, "catalog": 1024, "distinct_images": 64,
+    out = {"steps": args.churn_steps, "batch": B, "slots": 32, "catalog": n_cat, "distinct_images": n_cat,
+           "host_copies_per_adapter": 1, "catalog_bytes": n_cat * image_bytes, "pinned_images": pinned_images,
+           "pageable_images": n_cat - pinned_images,
+           "pinned_note": "page-locked memory is limited to about 65 GiB per process on this host; the "
+                          "first (Zipf-hottest) images are pinned, the rest pageable and staged",
+           "catalog_build_s": round(t_cat, 1),
            "sub_batch_max_distinct": limit, "sub_batches": len(churn_batches), "slot_loads": loads, "loads_per_step": round(loads / args.churn_steps, 1),
            "adapter_image_bytes": image_bytes, "h2d_bytes_per_step": round(loads * image_bytes / args.churn_steps),
            "pinned_h2d_gbs": round(h2d_gbs, 1),
@@ -1122,10 +1195,14 @@ def main(argv=None) -> int:
     p.add_argument("--only-isolated", action="store_true", help="skip the model workloads")
     p.add_argument("--decode-layers", type=int, default=32)
     p.add_argument("--decode-steps", type=int, default=20)
+    p.add_argument("--no-decode", action="store_true", help="skip the decode and prefill workloads")
     p.add_argument("--no-deberta", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-churn", action="store_true")
-    p.add_argument("--churn-steps", type=int, default=10, help="decode steps of the churn workload (200 in the full config)")
+    p.add_argument("--churn-steps", type=int, default=200, help="decode steps of the churn workload")
+    p.add_argument("--churn-catalog", type=int, default=1024, help="adapters in the churn catalog, each its own image")
+    p.add_argument("--churn-pinned-gib", type=float, default=56.0,
+                   help="page-locked bytes for churn catalog images; the rest are pageable")
     p.add_argument("--churn-sub-distinct", type=int, default=24, choices=range(1, 33), metavar="1..32",
                    help="most distinct adapters per churn sub-batch (the cache has 32 slots)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -1167,13 +1244,14 @@ def main(argv=None) -> int:
         result["cpu_baseline"] = iso["cpu_baseline"]
     if not args.only_isolated:
         workloads = {}
-        args.keep_model = not args.no_prefill
-        workloads["decode"] = run_decode(args)
-        pm = workloads["decode"].pop("_model", None)
-        if pm is not None:
-            workloads["prefill"] = run_prefill(args, pm)
-            del pm
-            torch.cuda.empty_cache()
+        if not args.no_decode:
+            args.keep_model = not args.no_prefill
+            workloads["decode"] = run_decode(args)
+            pm = workloads["decode"].pop("_model", None)
+            if pm is not None:
+                workloads["prefill"] = run_prefill(args, pm)
+                del pm
+                torch.cuda.empty_cache()
         if not args.no_churn:
             workloads["churn"] = run_churn(args)
         if not args.no_deberta:

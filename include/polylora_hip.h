@@ -306,6 +306,13 @@ int pl_lora_apply_noalloc(int32_t dtype, const void* x, int64_t ldx, int32_t K, 
                           int32_t num_slots, int32_t group_tokens, int32_t ldt,
                           int32_t k_splits, int32_t epilogue, void* stream);
 
+/* Page-locked host memory of exactly nbytes for adapter slot images (host
+ * side of cache.py:119-150's uploads: the source of pl_slot_upload), or NULL
+ * (with pl_last_error set and the runtime's error state cleared) when the
+ * system refuses; pl_host_free releases it. */
+void* pl_host_alloc(int64_t nbytes);
+int pl_host_free(void* ptr);
+
 /* Copy one packed adapter (host, pinned) into its slot region and its table
  * row into the slot table, both asynchronously on `stream`. */
 int pl_slot_upload(void* arena_dst, const void* host_src, int64_t nbytes, void* table_dst,

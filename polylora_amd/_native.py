@@ -89,10 +89,13 @@ _SIGNATURES: dict[str, tuple] = {
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
         c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p,
     ),
+    "pl_host_alloc": (c_int64,),
+    "pl_host_free": (c_void_p,),
     "pl_slot_upload": (c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p),
     "pl_check_right_padded": (c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p),
 }
-_RESTYPES = {"pl_last_error": ctypes.c_char_p, "pl_plan_group_capacity": c_int64, "pl_shrink_workspace_bytes": c_int64}
+_RESTYPES = {"pl_last_error": ctypes.c_char_p, "pl_plan_group_capacity": c_int64, "pl_shrink_workspace_bytes": c_int64,
+             "pl_host_alloc": c_void_p}
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

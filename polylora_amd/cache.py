@@ -6,13 +6,15 @@ adapter load is ~10 small default-stream ops per module and zero-fills the
 whole slot.
 
 Here every slot s >= 1 owns one contiguous region of ``slot_bytes`` in a
-single device arena.  An adapter is packed once on the host (pinned, model
-dtype) into a compact image: for each module it has weights for, A as
-``[rank][in]`` (= PEFT lora_A) then B as ``[out][rank8]`` (= PEFT lora_B,
-rank padded to a multiple of 8 with zeros), each part 256-byte aligned and
-stored in MFMA blocks (``tile_rows``): the first dimension cut into tiles of
-16 rows, each tile stored as consecutive 64-byte column blocks, so that a
-kernel's 16-row x 64-byte operand load reads contiguous memory.
+single device arena.  The store holds each adapter as its slot image
+(``slot_image.AdapterImage``, pinned, model dtype): for each module it has
+weights for, A as ``[rank][in]`` (= PEFT lora_A) then B as ``[out][rank8]``
+(= PEFT lora_B, rank padded to a multiple of 8 with zeros), each part
+256-byte aligned and stored in MFMA blocks (``tile_rows``): the first
+dimension cut into tiles of 16 rows, each tile stored as consecutive 64-byte
+column blocks, so that a kernel's 16-row x 64-byte operand load reads
+contiguous memory.  The cache binds its layout to the store, which packs
+every adapter added afterwards straight into that image.
 Loading is one host->device copy of that image plus one copy of the slot's
 table row (32 bytes per module: rank, scale, rank8, A and B offsets), both
 on a side stream that first waits for the last forward that read the slot;
@@ -31,145 +33,18 @@ from __future__ import annotations
 
 from collections import OrderedDict
 from collections.abc import Mapping
-from dataclasses import dataclass
 
 import numpy as np
 import torch
 
 from . import _native
 from .config import PolyLoraConfig
+from .slot_image import AdapterImage, ModuleSpec, SlotLayout, tile_rows, untile_rows
 from .store import CpuAdapter, CpuAdapterStore
 
-_ALIGN = 256
+__all__ = ["GpuAdapterCache", "ModuleSpec", "SlotLayout", "tile_rows", "untile_rows"]
+
 _ENTRY_INTS = _native.SLOT_ENTRY_INT32S  # int32 words per (slot, module) entry
-
-
-@dataclass(frozen=True)
-class ModuleSpec:
-    name: str
-    in_features: int
-    out_features: int
-
-
-def _align(n: int) -> int:
-    return (n + _ALIGN - 1) // _ALIGN * _ALIGN
-
-
-def _round8(r: int) -> int:
-    return (r + 7) // 8 * 8
-
-
-_TILE_ROWS = 16
-_BLOCK_BYTES = 64
-
-
-def tile_rows(m: torch.Tensor) -> torch.Tensor:
-    """``[R][C]`` -> the arena's block layout, flattened (same element count).
-
-    Rows are cut into tiles of 16 (the last may be shorter, ``rt`` rows); a
-    tile is stored as its column blocks of ``W = 64 bytes`` one after the
-    other, each block row-major (the last block may be narrower, ``wb``
-    columns).  Element (i, c) lands at
-    ``16*t*C + s*rt*W + (i % 16)*wb + (c - s*W)`` with ``t = i // 16`` and
-    ``s = c // W``.  For ``C <= W`` this is the plain row-major layout.
-    """
-    R, C = m.shape
-    w = _BLOCK_BYTES // m.element_size()
-    out = torch.empty(R * C, dtype=m.dtype)
-    full = C // w
-    for t0 in range(0, R, _TILE_ROWS):
-        tile = m[t0 : t0 + _TILE_ROWS]
-        rt = tile.shape[0]
-        base = t0 * C
-        if full:
-            out[base : base + rt * full * w] = tile[:, : full * w].reshape(rt, full, w).transpose(0, 1).reshape(-1)
-        if C > full * w:
-            out[base + rt * full * w : base + rt * C] = tile[:, full * w :].reshape(-1)
-    return out
-
-
-def untile_rows(flat: torch.Tensor, R: int, C: int) -> torch.Tensor:
-    """Inverse of ``tile_rows``: the block layout back to ``[R][C]``."""
-    w = _BLOCK_BYTES // flat.element_size()
-    out = torch.empty((R, C), dtype=flat.dtype, device=flat.device)
-    full = C // w
-    for t0 in range(0, R, _TILE_ROWS):
-        rt = min(_TILE_ROWS, R - t0)
-        base = t0 * C
-        if full:
-            out[t0 : t0 + rt, : full * w] = flat[base : base + rt * full * w].view(full, rt, w).transpose(0, 1).reshape(rt, full * w)
-        if C > full * w:
-            out[t0 : t0 + rt, full * w :] = flat[base + rt * full * w : base + rt * C].view(rt, C - full * w)
-    return out
-
-
-class SlotLayout:
-    """Byte budget of one slot for a module list, an element type and a rank cap."""
-
-    def __init__(self, specs: list[ModuleSpec], dtype: torch.dtype, max_rank: int) -> None:
-        self.specs = list(specs)
-        self.dtype = dtype
-        self.elem = torch.empty((), dtype=dtype).element_size()
-        self.max_rank = int(max_rank)
-        self.rank8_cap = _round8(self.max_rank)
-        self.slot_bytes = sum(
-            _align(self.max_rank * s.in_features * self.elem) + _align(s.out_features * self.rank8_cap * self.elem)
-            for s in self.specs
-        )
-        self.key = (str(dtype), self.max_rank, tuple((s.name, s.in_features, s.out_features) for s in self.specs))
-
-
-@dataclass
-class PackedAdapter:
-    image: torch.Tensor  # uint8 [nbytes], pinned when a GPU is present
-    rows: np.ndarray  # int32 [num_modules, 8]; offsets relative to the slot base
-
-
-def pack_adapter(adapter: CpuAdapter, layout: SlotLayout) -> PackedAdapter:
-    """Pack an adapter into the compact slot image, validating like cache.py:129-136."""
-    n_mod = len(layout.specs)
-    rows = np.zeros((n_mod, _ENTRY_INTS), dtype=np.int32)
-    rows_f = rows.view(np.float32)
-    rows_64 = rows.view(np.int64)  # [n_mod, 4]: int64 word 2 = a_off, word 3 = b_off
-    parts = []
-    cursor = 0
-    es = layout.elem
-    for i, spec in enumerate(layout.specs):
-        weights = adapter.layers.get(spec.name)
-        if weights is None:
-            continue  # missing module: rank 0, scale 0 (cache.py:127-128)
-        r = int(weights.rank)
-        if r > layout.max_rank:
-            raise ValueError(
-                f"Adapter {adapter.adapter_id!r} rank {r} exceeds max_rank {layout.max_rank}"
-            )
-        if tuple(weights.A.shape) != (spec.in_features, r):
-            raise ValueError(f"LoRA A shape mismatch for adapter {adapter.adapter_id!r}, module {spec.name!r}")
-        if tuple(weights.B.shape) != (r, spec.out_features):
-            raise ValueError(f"LoRA B shape mismatch for adapter {adapter.adapter_id!r}, module {spec.name!r}")
-        r8 = _round8(r)
-        a_off = cursor
-        cursor += _align(r * spec.in_features * es)
-        b_off = cursor
-        cursor += _align(spec.out_features * r8 * es)
-        rows[i, 0] = r
-        rows_f[i, 1] = np.float32(weights.scale)
-        rows[i, 2] = r8
-        rows_64[i, 2] = a_off
-        rows_64[i, 3] = b_off
-        parts.append((weights, spec, r, r8, a_off, b_off))
-    image = torch.zeros(max(cursor, 1), dtype=torch.uint8)
-    for weights, spec, r, r8, a_off, b_off in parts:
-        a_bytes = r * spec.in_features * es
-        a_rows = weights.A.t().to(layout.dtype)
-        image[a_off : a_off + a_bytes].view(layout.dtype).copy_(tile_rows(a_rows))
-        b_bytes = spec.out_features * r8 * es
-        b_rows = torch.zeros(spec.out_features, r8, dtype=layout.dtype)
-        b_rows[:, :r].copy_(weights.B.t())
-        image[b_off : b_off + b_bytes].view(layout.dtype).copy_(tile_rows(b_rows))
-    if torch.cuda.is_available():
-        image = image.pin_memory()
-    return PackedAdapter(image=image, rows=rows)
 
 
 class _ReferenceLayoutWeights(Mapping):
@@ -224,6 +99,8 @@ class GpuAdapterCache:
     # ------------------------------------------------------------------ storage
     def _allocate(self) -> None:
         self.layout = SlotLayout(list(self.module_specs.values()), self.dtype, self.config.max_rank)
+        # adapters added from now on are packed straight into this layout's slot images
+        self.store.bind_layout(self.layout)
         n_mod = len(self.module_specs)
         arena_bytes = max(1, (self.num_slots - 1) * self.layout.slot_bytes)
         self.arena = torch.empty(arena_bytes, dtype=torch.uint8, device=self.device)
@@ -385,15 +262,11 @@ class GpuAdapterCache:
         )
 
     # ---------------------------------------------------------------- uploads
-    def _packed(self, adapter: CpuAdapter) -> PackedAdapter:
-        key = self.layout.key
-        packed = adapter.packed.get(key)
-        if packed is None:
-            packed = pack_adapter(adapter, self.layout)
-            adapter.packed[key] = packed
-        return packed
+    def _packed(self, adapter: CpuAdapter) -> AdapterImage:
+        """The adapter's slot image for this cache's layout (validated like cache.py:129-136)."""
+        return self.store.image(adapter, self.layout)
 
-    def _write_slot(self, slot: int, packed: PackedAdapter | None) -> None:
+    def _write_slot(self, slot: int, packed: AdapterImage | None) -> None:
         """Copy an adapter image (or nothing, for a cleared slot) and its table row into `slot`."""
         base = (slot - 1) * self.layout.slot_bytes
         if packed is None:
@@ -405,7 +278,7 @@ class GpuAdapterCache:
             row64 = row.view(np.int64)
             row64[has, 2] += base
             row64[has, 3] += base
-            image, nbytes = packed.image, (int(packed.image.numel()) if has.any() else 0)
+            image, nbytes = packed.data, packed.nbytes
         self.table_host[slot] = row
         if self.device.type != "cuda":
             if nbytes:
@@ -424,6 +297,9 @@ class GpuAdapterCache:
         previous = self._slot_ready.get(slot)
         if previous is not None:
             side.wait_event(previous)
+        ring_slot = None
+        if nbytes and not packed.pinned:
+            image, ring_slot = self._stage(image, nbytes)
         row_pinned = torch.from_numpy(row).pin_memory()
         with torch.cuda.device(self.device):
             _native.check(
@@ -442,6 +318,37 @@ class GpuAdapterCache:
         ready.record(side)
         self._slot_ready[slot] = ready
         self._pending.append((ready, image, row_pinned))
+        if ring_slot is not None:
+            self._staging_busy[ring_slot] = ready  # the buffer is reused once this upload is done
+
+    # Page-locked staging buffers for images held in pageable memory.  The
+    # runtime's own copy from pageable memory blocks the calling thread until
+    # the side stream reaches it, i.e. until the forward that last read the
+    # slot has finished, so the host could no longer queue work ahead of the
+    # GPU.  Instead the host copies the image into the next staging buffer of
+    # a small ring (waiting only if that buffer's previous upload is still in
+    # flight) and the DMA engine copies from there asynchronously.
+    STAGING_BUFFERS = 4
+
+    def _stage(self, image: torch.Tensor, nbytes: int) -> tuple[torch.Tensor, int | None]:
+        """(page-locked copy of the image, its ring index), or (the image, None) without locked memory."""
+        from .slot_image import host_bytes
+
+        ring = self.__dict__.setdefault("_staging", [None] * self.STAGING_BUFFERS)
+        busy = self.__dict__.setdefault("_staging_busy", [None] * self.STAGING_BUFFERS)
+        i = self.__dict__.get("_staging_next", 0) % self.STAGING_BUFFERS
+        if busy[i] is not None:
+            busy[i].synchronize()  # the upload that last used this buffer has read it
+            busy[i] = None
+        buf = ring[i]
+        if buf is None or buf.numel() < nbytes:
+            buf, pinned = host_bytes(nbytes, pin=True)
+            if not pinned:
+                return image, None  # no page-locked memory left: the runtime stages the copy itself
+            ring[i] = buf
+        buf[:nbytes].copy_(image[:nbytes])
+        self._staging_next = i + 1
+        return buf, i
 
     def _reap_pending(self) -> None:
         self._pending = [item for item in self._pending if not item[0].query()]

@@ -39,6 +39,37 @@ extern "C" int pl_is_device_pointer(const void* ptr) {
   return (attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged) ? 1 : 0;
 }
 
+// Page-locked host memory of exactly `nbytes` (the caching host allocators
+// of frameworks round requests up, e.g. to powers of two, which matters when
+// adapter images fill most of the page-lockable memory).  A failed
+// allocation returns null and clears the runtime's error state, so the
+// caller can fall back to pageable memory.
+extern "C" void* pl_host_alloc(int64_t nbytes) {
+  if (nbytes <= 0) {
+    pl_set_error("pl_host_alloc: size must be positive (got %lld)", (long long)nbytes);
+    return nullptr;
+  }
+  void* p = nullptr;
+  const hipError_t err = hipHostMalloc(&p, (size_t)nbytes, hipHostMallocDefault);
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    pl_set_error("pl_host_alloc: %lld bytes: %s", (long long)nbytes, hipGetErrorString(err));
+    return nullptr;
+  }
+  return p;
+}
+
+extern "C" int pl_host_free(void* ptr) {
+  if (!ptr) return PL_OK;
+  const hipError_t err = hipHostFree(ptr);
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    pl_set_error("pl_host_free: %s", hipGetErrorString(err));
+    return PL_ERR_LAUNCH;
+  }
+  return PL_OK;
+}
+
 // cache.py:138-145 copies each module's A and B separately with .to(device)
 // and .copy_(); here one packed adapter image (all modules, compact ranks)
 // moves with one host->device copy, followed by its 32-byte-per-module table

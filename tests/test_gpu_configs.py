@@ -1,0 +1,142 @@
+"""Parity at the benchmark configurations' own shapes, against the oracle (oracle.lora.reference_forward).
+
+* Prefill size (32 rows x 1024, U[512,1024] lengths, 8 adapters of ranks 16
+  and 32): the o launch, the stacked gate/up launch (N = 14336) and the down
+  launch (K = 14336) of the fused kernel, every token.
+* Adapter churn (the Llama-3-8B layer shapes, all 7 targets, 32 GPU slots,
+  rank-16 adapters): a catalog of 96 distinct PEFT adapters added through the
+  store's PEFT path, some held in pageable memory (their loads go through the
+  staging ring), batches of 128 rows drawn Zipf(0.9) and split into
+  sub-batches of at most 24 distinct adapters, every wrapped layer of every
+  sub-batch against the oracle on the inputs it saw.
+* Decode (32 Llama-3-8B layers, 64 slots, ranks {8,16,32,64}, 256 rows over
+  a 512-token KV cache, Zipf(1.1) with 10% base rows): one decode step with
+  all 224 wrapped layers checked.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.lora import reference_forward
+from polylora_amd import PolyLoraConfig, PolyLoraModel, sgmv
+from tests import _peft
+from tests._util import make_cache, oracle_slot_tensors, peft_layer
+from tests.test_gpu_model import BF16, LLAMA_TARGETS, _announce, _per_layer_check
+
+pytestmark = pytest.mark.gpu
+
+
+def test_prefill_config_o_gateup_down_fused_bf16(gpu):
+    """o (4096 -> 4096), gate/up stacked (4096 -> 14336 each) and down (14336 -> 4096) at prefill size."""
+    _announce(test="prefill_config_o_gateup_down")
+    g = torch.Generator().manual_seed(1014)
+    B, S = 32, 1024
+    shapes = {"o": (4096, 4096), "gate": (4096, 14336), "up": (4096, 14336), "down": (14336, 4096)}
+    adapters = {f"p{i}": {m: peft_layer(g, fi, fo, 16 if i < 4 else 32, 2.0 * (16 if i < 4 else 32))
+                          for m, (fi, fo) in shapes.items()} for i in range(8)}
+    cache = make_cache(adapters, shapes, 8, 32, gpu, torch.bfloat16)
+    row_slot = cache.ensure_resident([f"p{i // 4}" for i in range(B)])
+    seq_lens = torch.randint(512, S + 1, (B,), generator=g, dtype=torch.int32)
+    plan = sgmv.SgmvPlan(row_slot, seq_lens.to(gpu), S, cache.num_slots, distinct_slots=8)
+    assert plan.group_tokens == 64 and sgmv.fused_ok(plan, cache, 14336)
+    gg = torch.Generator(device=gpu).manual_seed(1014)
+    xs = {k: torch.randn(B * S, k, generator=gg, device=gpu).to(torch.bfloat16) for k in (4096, 14336)}
+    base = {m: torch.randn(B * S, fo, generator=gg, device=gpu).to(torch.bfloat16) for m, (fi, fo) in shapes.items()}
+    ys = {m: base[m].clone() for m in shapes}
+    sgmv.lora_fused(xs[4096], ys["o"], cache, "o", plan)
+    sgmv.lora_fused_stacked(xs[4096], [ys["gate"], ys["up"]], cache, ["gate", "up"], plan)
+    sgmv.lora_fused(xs[14336], ys["down"], cache, "down", plan)
+    torch.cuda.synchronize()
+    pad = (torch.arange(S)[None, :] >= seq_lens[:, None]).to(gpu)
+    for m, (fi, fo) in shapes.items():
+        A, Bm, rk, sc = (t.to(gpu) for t in oracle_slot_tensors(cache, adapters, m, torch.bfloat16))
+        expect = reference_forward(xs[fi].view(B, S, fi), base[m].view(B, S, fo), seq_lens.to(gpu), row_slot, A, Bm,
+                                   rk, sc)
+        torch.testing.assert_close(ys[m].view(B, S, fo), expect, **BF16)
+        assert torch.equal(ys[m].view(B, S, fo)[pad], base[m].view(B, S, fo)[pad])  # padding keeps the base output
+
+
+def _sub_batches(ids, limit):
+    """Rows in order, cut whenever a new adapter would make `limit + 1` distinct ones (as the churn bench)."""
+    out, cur, seen = [], [], set()
+    for a in ids:
+        if a not in seen and len(seen) == limit:
+            out.append(cur)
+            cur, seen = [], set()
+        cur.append(a)
+        seen.add(a)
+    out.append(cur)
+    return out
+
+
+def test_churn_config_every_layer_against_the_oracle(gpu):
+    """Config 5 shapes on 2 layers: 96 distinct rank-16 adapters (40 pinned, 56 pageable) through 32 slots."""
+    _announce(test="churn_config")
+    from transformers import DynamicCache
+
+    from bench import build_llama
+
+    model = build_llama(gpu, layers=2, seed=1005)
+    pm = PolyLoraModel(model, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=32, max_rank=16)).eval()
+    shapes = {s.name: (s.in_features, s.out_features) for s in pm.module_specs}
+    image_bytes = sum(16 * (fi + fo) * 2 for fi, fo in shapes.values())
+    pm.adapter_store.pinned_bytes_limit = 40 * image_bytes  # the rest stay pageable: loads go through staging
+    g = torch.Generator().manual_seed(1005)
+    ads = {}
+    for i in range(96):
+        w = _peft.make_lora_weights(g, shapes, 16, std=0.02)  # N(0, 0.02), as the configurations specify
+        ads[f"c{i:03d}"] = (w, 32.0)
+        pm.adapter_store.add_adapter_from_peft_state_dict(f"c{i:03d}", _peft.state_dict(w), pm.target_module_names, 32.0)
+    store = pm.adapter_store
+    pinned = sum(1 for a in store.adapters.values() if a.image.pinned)
+    assert pinned == 40, pinned
+    rng = np.random.default_rng(1005)
+    w = 1.0 / np.arange(1, 97) ** 0.9
+    w /= w.sum()
+    names = list(ads)
+    vocab = model.config.vocab_size
+    gen = torch.Generator(device=gpu).manual_seed(1005)
+    loads0, forwards = pm.adapter_cache.loads, 0
+    with torch.inference_mode(), _per_layer_check(pm, ads, torch.bfloat16) as checked:
+        for step in range(3):
+            ids = [names[int(i)] for i in rng.choice(96, size=128, p=w)]
+            for sub in _sub_batches(ids, 24):
+                x = torch.randint(0, vocab, (len(sub), 1), generator=gen, device=gpu)
+                pm(input_ids=x, adapter_ids=sub, past_key_values=DynamicCache(config=model.config), use_cache=True)
+                forwards += 1
+    assert checked.count == len(pm.target_module_names)
+    loads = pm.adapter_cache.loads - loads0
+    assert forwards >= 6 and loads > 32, (forwards, loads)  # slots were reused: evictions and reloads happened
+
+
+class _StoreWeights(dict):
+    """PEFT-layout (lora_A, lora_B) of an adapter, read from the store's image on demand."""
+
+    def __init__(self, adapter) -> None:
+        super().__init__()
+        self.adapter = adapter
+
+    def get(self, module, default=None):
+        got = self.adapter.peft_tensors(module)
+        return default if got is None else (got[0], got[1])
+
+
+def test_decode_config_step_every_layer_against_the_oracle(gpu):
+    """One decode step of the 32-layer decode configuration with all 224 wrapped Linears checked."""
+    _announce(test="decode_config_step")
+    from bench import _reset_kv, decode_workload
+
+    wl = decode_workload(gpu, layers=32)
+    pm = wl.model
+    store = pm.adapter_store
+    # the oracle's weights: the random bf16 adapters as the store holds them (alpha = 2 r)
+    ads = {aid: (_StoreWeights(store.adapters[aid]), 2.0 * r) for aid, r in wl.ranks.items()}
+    _reset_kv(wl)
+    with torch.inference_mode(), _per_layer_check(pm, ads, torch.bfloat16) as checked:
+        out = pm(input_ids=wl.input_ids, past_key_values=wl.cache, cache_position=wl.cache_position, use_cache=True,
+                 adapter_ids=wl.adapter_ids).last_hidden_state
+    assert checked.count == len(pm.target_module_names) == 224
+    assert torch.isfinite(out.float()).all()

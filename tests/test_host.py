@@ -21,7 +21,7 @@ import torch
 from oracle.lora import dense_slot_tensors
 from oracle.slots import SlotCacheModel
 from polylora_amd import PolyLoraConfig, PolyLoraModel, _native
-from polylora_amd.cache import GpuAdapterCache, ModuleSpec, SlotLayout, pack_adapter, tile_rows, untile_rows
+from polylora_amd.cache import GpuAdapterCache, ModuleSpec, SlotLayout, tile_rows, untile_rows
 from polylora_amd.context import LoraBatchContext, assert_right_padded, get_lora_context, use_lora_context
 from polylora_amd.store import CpuAdapterStore, CpuLayerWeights, DiskAdapterCache
 from tests import _peft
@@ -268,12 +268,12 @@ def test_pack_adapter_layout():
     store = CpuAdapterStore()
     store.add_adapter("p", {"x": CpuLayerWeights(a.t().contiguous(), b.t().contiguous(), 3, 1.5)})
     layout = SlotLayout([ModuleSpec(n, i, o) for n, (i, o) in shapes.items()], torch.bfloat16, 6)
-    packed = pack_adapter(store.adapters["p"], layout)
+    packed = store.adapters["p"].image_for(layout)
     rows = packed.rows
     assert rows[0, 0] == 3 and rows[0, 2] == 8 and rows.view(np.float32)[0, 1] == np.float32(1.5)
     a_off, b_off = int(rows.view(np.int64)[0, 2]), int(rows.view(np.int64)[0, 3])
     assert a_off % 256 == 0 and b_off % 256 == 0
-    img = packed.image
+    img = packed.data
     A = img[a_off : a_off + 3 * 16 * 2].view(torch.bfloat16).view(3, 16)
     B = img[b_off : b_off + 24 * 8 * 2].view(torch.bfloat16).view(24, 8)
     assert torch.equal(A, a.bfloat16()) and torch.equal(B[:, :3], b.bfloat16())
@@ -318,13 +318,13 @@ def test_pack_adapter_block_layout_round_trip():
         ws[name] = (A, B, r)
     store.add_adapter("p", {n: CpuLayerWeights(A, B, r, 0.5) for n, (A, B, r) in ws.items()})
     layout = SlotLayout([ModuleSpec(n, i, o) for n, (i, o) in shapes.items()], torch.bfloat16, 40)
-    packed = pack_adapter(store.adapters["p"], layout)
+    packed = store.adapters["p"].image_for(layout)
     for i, (name, (fin, fout)) in enumerate(shapes.items()):
         A, B, r = ws[name]
         r8 = (r + 7) // 8 * 8
         a_off, b_off = int(packed.rows.view(np.int64)[i, 2]), int(packed.rows.view(np.int64)[i, 3])
-        a_img = packed.image[a_off : a_off + r * fin * 2].view(torch.bfloat16)
-        b_img = packed.image[b_off : b_off + fout * r8 * 2].view(torch.bfloat16)
+        a_img = packed.data[a_off : a_off + r * fin * 2].view(torch.bfloat16)
+        b_img = packed.data[b_off : b_off + fout * r8 * 2].view(torch.bfloat16)
         assert torch.equal(untile_rows(a_img, r, fin), A.t().bfloat16())
         b_rows = untile_rows(b_img, fout, r8)
         assert torch.equal(b_rows[:, :r], B.t().bfloat16())

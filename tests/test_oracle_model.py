@@ -260,3 +260,21 @@ def test_closed_form_catches_planted_oracle_mistakes(monkeypatch, mutant, name):
     mutant(monkeypatch)
     got, want, _, _ = _outputs(case)
     assert not torch.allclose(got, want, **FP32), (mutant.__name__, name)
+
+
+def test_sum_bound_accepts_an_operand_ulp_and_rejects_wrong_deltas():
+    """The per-layer GPU check's bound: an ulp of the operands at a cancellation passes, mistakes fail."""
+    from tests.test_gpu_model import BF16, assert_close_sum
+
+    g = torch.Generator().manual_seed(7)
+    base = (torch.randn(64, 256, generator=g) * 2).bfloat16()
+    delta = (torch.randn(64, 256, generator=g) * 2).bfloat16()
+    want = (base.float() + delta.float()).bfloat16()
+    delta[0, 0] = -base[0, 0]  # exact cancellation: want 0, got one ulp of |base|
+    want[0, 0] = 0
+    got = want.clone()
+    got[0, 0] = torch.finfo(torch.bfloat16).eps * base[0, 0].abs().float()
+    assert_close_sum(got, want, base, BF16)
+    for wrong in (base.float() + 2 * delta.float(), base.float(), base.float() - delta.float()):
+        with pytest.raises(AssertionError):
+            assert_close_sum(wrong.bfloat16(), want, base, BF16)
