@@ -53,6 +53,24 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo (platform.processor() is often empty on Linux)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _cpu_record(value: float, unit: str, threads: int, sample: str) -> dict:
+    """A cpu_baseline object: the oracle's restatement of the fallback timed on the host cores."""
+    return {"value": value, "unit": unit, "cores": threads, "kind": "port", "cpu_model": cpu_model(),
+            "host_logical_cpus": os.cpu_count(), "sample": sample}
+
+
 # ----------------------------------------------------------------------------- base-model attention
 def _safe_fp32_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
     """Attention in fp32 with contiguous operands (no bf16 batched product on a transposed view)."""
@@ -149,7 +167,9 @@ def add_random_adapters(pm, ranks: dict, std: float = 0.02, seed: int = 0, devic
     from polylora_amd.store import CpuLayerWeights
 
     gen = torch.Generator(device=device).manual_seed(seed)
-    for aid, r in ranks.items():
+    progress = _Progress("random adapters")
+    for i, (aid, r) in enumerate(ranks.items()):
+        progress.tick(f"adapter {i + 1}/{len(ranks)}")
         layers = {}
         for spec in pm.module_specs:
             a, b = _lora_pair(gen, spec.in_features, spec.out_features, r, std, device)
@@ -270,7 +290,43 @@ def deberta_workload(device, seed: int = 1001, layers: int = 12) -> DebertaWorkl
     return DebertaWorkload(pm, base, inputs, ids, adapters)
 
 
-def run_deberta(device, reps: int = 20) -> dict:
+def cpu_baseline_deberta(wl: DebertaWorkload, budget_s: float) -> dict:
+    """The whole 12-layer fp32 forward on the host through the reference fallback.
+
+    The base weights are a CPU copy of the GPU model's; every target Linear
+    adds the oracle's restatement of layers.py:112-134 (oracle.model), on
+    the same batch, mask and adapters.
+    """
+    import copy
+
+    from oracle import model as oracle_model
+
+    m = copy.deepcopy(wl.base).cpu().eval()
+    names = oracle_model.wrap_model(m, DEBERTA_TARGETS, None)
+    shapes = {n: (m.get_submodule(n).base_layer.in_features, m.get_submodule(n).base_layer.out_features) for n in names}
+    bank = oracle_model.OracleBank({aid: {mod: (a, b, alpha) for mod, (a, b) in w.items()}
+                                    for aid, (w, alpha) in wl.adapters.items()}, shapes, 16, torch.float32, "cpu")
+    for n in names:
+        m.get_submodule(n).bank = bank
+    inputs = {k: v.cpu() for k, v in wl.inputs.items()}
+    valid = int(inputs["attention_mask"].sum())
+    threads = torch.get_num_threads()
+    with torch.inference_mode():
+        oracle_model.run(m, bank, wl.adapter_ids, **inputs)  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            oracle_model.run(m, bank, wl.adapter_ids, **inputs)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or reps >= 50:
+                break
+    per = el / reps
+    return _cpu_record(round(valid / per, 1), "tokens/s", threads,
+                       f"{reps} full 12-layer fp32 forwards (8 rows x 128, {valid} valid tokens, 72 wrapped Linears) "
+                       f"through the fallback, {per * 1e3:.1f} ms each; torch {threads} threads")
+
+
+def run_deberta(device, reps: int = 20, cpu_budget_s: float | None = None) -> dict:
     wl = deberta_workload(device)
     valid = int(wl.inputs["attention_mask"].sum())
     with torch.inference_mode():
@@ -288,8 +344,12 @@ def run_deberta(device, reps: int = 20) -> dict:
             wl.model(**wl.inputs)
         torch.cuda.synchronize()
         base_s = (time.perf_counter() - t0) / reps
-    return {"dtype": "f32", "valid_tokens": valid, "lora_tokens_per_s": round(valid / lora_s, 1),
-            "base_tokens_per_s": round(valid / base_s, 1), "ratio": round(base_s / lora_s, 4), "timing": "eager wall clock"}
+    out = {"dtype": "f32", "valid_tokens": valid, "lora_tokens_per_s": round(valid / lora_s, 1),
+           "base_tokens_per_s": round(valid / base_s, 1), "ratio": round(base_s / lora_s, 4), "timing": "eager wall clock"}
+    if cpu_budget_s is not None:
+        _log("deberta: CPU baseline (full fp32 forward through the fallback)")
+        out["cpu_baseline"] = cpu_baseline_deberta(wl, cpu_budget_s)
+    return out
 
 
 # ----------------------------------------------------------------------------- config 2: isolated SGMV
@@ -402,14 +462,9 @@ def cpu_baseline_isolated(wl: IsolatedSgmv, nbytes: int, budget_s: float) -> dic
         if el >= budget_s or reps >= 50:
             break
     per = el / reps
-    return {
-        "value": round(nbytes / per / 1e9, 4),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{reps} full ops (17 segment rows, {int(wl.seg_lens.sum())} tokens) of the fallback loop, "
-                  f"{per * 1e3:.1f} ms each, torch {threads} threads, {platform.processor() or platform.machine()}",
-    }
+    return _cpu_record(round(nbytes / per / 1e9, 4), "GB/s", threads,
+                       f"{reps} full ops (17 segment rows, {int(wl.seg_lens.sum())} tokens) of the fallback loop, "
+                       f"{per * 1e3:.1f} ms each, torch {threads} threads")
 
 
 class SgmvLaunch:
@@ -551,15 +606,35 @@ def time_launches(fns: list, reps: int, warmup: int = 2) -> float:
     return t0.elapsed_time(t1) / reps
 
 
-def _profiled_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs, or None."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "sgmv_isolated_traffic.json")
+def _profiled(workload: str, *keys):
+    """A figure of the committed launch profile of `workload` (profiles/sgmv_<workload>_traffic.json), or None.
+
+    Those files are --reduce-profile's JSON of rocprofv3 kernel-trace,
+    FETCH_SIZE and WRITE_SIZE runs of --launch-profile <workload>.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"sgmv_{workload}_traffic.json")
     try:
         with open(path, encoding="utf-8") as fh:
             data = json.load(fh)
-        return int(data["kernels"][kernel]["traffic_bytes_per_launch"])
+        for k in keys:
+            data = data[k]
+        return int(round(float(data)))
     except (OSError, ValueError, KeyError, TypeError):
         return None
+
+
+def _profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` in the isolated op's profile, or None."""
+    return _profiled("isolated", "kernels", kernel, "traffic_bytes_per_launch")
+
+
+def sequence_roofline(what: str, nbytes: int, ms: float, launches: int, workload: str) -> dict:
+    """Roofline block of a launch sequence: algorithmic bytes over the sequence's back-to-back time."""
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"kernel": what, "bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": _profiled(workload, "pass_traffic_bytes"),
+            "algorithmic_bytes_per_sequence": nbytes, "launches": launches, "sequence_ms": round(ms, 4),
+            "traffic_note": f"HBM bytes of one sequence from profiles/sgmv_{workload}_traffic.json"}
 
 
 def run_isolated(args) -> dict:
@@ -694,7 +769,7 @@ class DecodeWorkload:
 
 
 def decode_workload(device, layers: int = 32, batch: int = 256, past: int = 512, slots: int = 64, seed: int = 1003,
-                    attn: str = "pl_fused_sdpa") -> DecodeWorkload:
+                    attn: str = "pl_fused_sdpa", kv_cache: bool = True) -> DecodeWorkload:
     from transformers import StaticCache
 
     from polylora_amd import PolyLoraConfig, PolyLoraModel
@@ -708,8 +783,10 @@ def decode_workload(device, layers: int = 32, batch: int = 256, past: int = 512,
     add_random_adapters(pm, ranks, seed=seed, device=device)
     ids = zipf_ids(rng, batch, slots, 1.1, 0.10, names)
     cfg = model.config
-    kv = StaticCache(config=cfg, max_cache_len=past + 1)
     gen = torch.Generator(device=device).manual_seed(seed)
+    if not kv_cache:  # the LoRA launches alone (launch profiles): no KV cache, no inputs
+        return DecodeWorkload(pm, None, None, None, ids, ranks, past)
+    kv = StaticCache(config=cfg, max_cache_len=past + 1)
     for layer in range(cfg.num_hidden_layers):
         k = torch.randn(batch, cfg.num_key_value_heads, past, cfg.head_dim, generator=gen, device=device, dtype=torch.bfloat16)
         v = torch.randn(batch, cfg.num_key_value_heads, past, cfg.head_dim, generator=gen, device=device, dtype=torch.bfloat16)
@@ -747,6 +824,86 @@ def decode_lora_bytes(pm, adapter_ids: list, rows: int) -> dict:
     return {"total": total, "xy": xy, "ab": ab, "flops": flops, "active_rows": len(active), "distinct": len(uniq)}
 
 
+@dataclass
+class LaunchEntry:
+    """One launch of a forward's LoRA sequence: what it serves and how to issue it."""
+
+    label: str  # launch type, e.g. "q/k/v stacked shrink"
+    part: str  # "shrink", "expand" or "fused"
+    modules: list  # wrapped Linear names served
+    fn: object  # issues the launch
+    owner: object  # the launch object (shared by a shrink and its expand)
+
+
+_SIBLINGS = {"q_proj": ("q_proj", "k_proj", "v_proj"), "gate_proj": ("gate_proj", "up_proj")}
+
+
+def forward_launch_sequence(pm, plan, xs: dict, T: int, gen) -> list:
+    """The LoRA launches of one forward, in MultiLoraLinear's order, without the base model.
+
+    Sibling Linears that read the same input (q/k/v, gate/up) share one
+    stacked launch, as MultiLoraLinear does once it has seen a forward.  Where
+    the plan suits the fused kernel each set takes one pl_lora_fused(_stacked)
+    launch; otherwise one stacked shrink and one stacked expand.  Every module
+    type writes its own y, so siblings in one launch never share an output.
+    """
+    from polylora_amd import sgmv
+
+    cache = pm.adapter_cache
+    device = cache.device
+    by_name = {s.name: s for s in pm.module_specs}
+    leaf_ys = {}
+    for s in pm.module_specs:
+        leaf = s.name.rsplit(".", 1)[-1]
+        if leaf not in leaf_ys:
+            leaf_ys[leaf] = torch.randn(T, s.out_features, generator=gen, device=device, dtype=torch.bfloat16)
+    out = []
+    for s in pm.module_specs:
+        parent, leaf = s.name.rsplit(".", 1)
+        if leaf in ("k_proj", "v_proj", "up_proj"):
+            continue
+        group = _SIBLINGS.get(leaf, (leaf,))
+        names = [f"{parent}.{g}" for g in group if f"{parent}.{g}" in by_name]
+        tag = "/".join(n.rsplit(".", 1)[-1].replace("_proj", "") for n in names)
+        tag += " stacked" if len(names) > 1 else ""
+        k = by_name[names[0]].in_features
+        outs = [leaf_ys[n.rsplit(".", 1)[-1]] for n in names]
+        if sgmv.fused_ok(plan, cache, k):
+            f = (FusedLaunch(xs[k], outs[0], cache, names[0], plan) if len(names) == 1
+                 else StackedFusedLaunch(xs[k], outs, cache, names, plan))
+            out.append(LaunchEntry(f"{tag} fused", "fused", names, f, f))
+            continue
+        st = StackedLaunch(xs[k], outs, cache, names, plan)
+        out.append(LaunchEntry(f"{tag} shrink", "shrink", names, st.shrink, st))
+        out.append(LaunchEntry(f"{tag} expand", "expand", names, st.expand, st))
+    return out
+
+
+def launch_bytes(pm, modules: list, part: str, adapter_ids: list, lens: list) -> int:
+    """Algorithmic HBM bytes of one launch serving `modules` over a batch (bf16).
+
+    shrink: x once for the tokens of rows whose adapter has a rank for one of
+    the modules, plus each distinct adapter's A once per module; expand: y
+    read and written for the tokens the module adapts, plus each distinct
+    adapter's B once per module; fused: both.
+    """
+    base_id = pm.config.base_adapter_id
+    specs = {s.name: s for s in pm.module_specs}
+    rows = [(a, int(n)) for a, n in zip(adapter_ids, lens) if a != base_id and int(n) > 0]
+    uniq = sorted({a for a, _ in rows})
+    k = specs[modules[0]].in_features
+    total = 0
+    if part in ("shrink", "fused"):
+        total += 2 * k * sum(n for a, n in rows if any(_rank_of(pm, a, m) > 0 for m in modules))
+        total += sum(2 * _rank_of(pm, a, m) * k for m in modules for a in uniq)
+    if part in ("expand", "fused"):
+        for m in modules:
+            nout = specs[m].out_features
+            total += 4 * nout * sum(n for a, n in rows if _rank_of(pm, a, m) > 0)
+            total += sum(2 * _rank_of(pm, a, m) * nout for a in uniq)
+    return total
+
+
 def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Tensor, reps: int, seed: int = 0) -> dict:
     """Every wrapped Linear's shrink+expand over one batch, launched back to back without the base model."""
     from polylora_amd import sgmv
@@ -767,53 +924,30 @@ def time_lora_ops(pm, adapter_ids: list, tokens_per_row: int, seq_lens: torch.Te
         sel = [l for l, s in zip(launches, pm.module_specs) if s.name.rsplit(".", 1)[-1] == key]
         per_type[key] = [round(1e3 * time_launches([l.shrink for l in sel], reps) / len(sel), 2),
                          round(1e3 * time_launches([l.expand for l in sel], reps) / len(sel), 2)]
-    # The forward's own launch sequence: sibling Linears that read the same
-    # input (q/k/v, gate/up) share one stacked shrink and one stacked expand,
-    # as MultiLoraLinear does once it has seen a forward.
-    # Where the plan suits the fused kernel the siblings share one
-    # pl_lora_fused_stacked launch and the other modules take one pl_lora_fused
-    # launch each (MultiLoraLinear does the same).  Every module type writes its
-    # own y, so siblings in one launch never share an output.
-    by_name = {s.name: s for s in pm.module_specs}
-    leaf_ys = {}
-    for s in pm.module_specs:
-        leaf = s.name.rsplit(".", 1)[-1]
-        if leaf not in leaf_ys:
-            leaf_ys[leaf] = torch.randn(T, s.out_features, generator=gen, device=device, dtype=torch.bfloat16)
-    stacks, fused, seq = [], [], []
-    for s in pm.module_specs:
-        parent, leaf = s.name.rsplit(".", 1)
-        if leaf in ("k_proj", "v_proj", "up_proj"):
-            continue
-        group = {"q_proj": ("q_proj", "k_proj", "v_proj"), "gate_proj": ("gate_proj", "up_proj")}.get(leaf, (leaf,))
-        names = [f"{parent}.{g}" for g in group if f"{parent}.{g}" in by_name]
-        k = by_name[names[0]].in_features
-        outs = [leaf_ys[n.rsplit(".", 1)[-1]] for n in names]
-        if sgmv.fused_ok(plan, cache, k):
-            f = (FusedLaunch(xs[k], outs[0], cache, names[0], plan) if len(names) == 1
-                 else StackedFusedLaunch(xs[k], outs, cache, names, plan))
-            fused.append(f)
-            seq.append(f)
-            continue
-        st = StackedLaunch(xs[k], outs, cache, names, plan)
-        stacks.append(st)
-        seq.extend((st.shrink, st.expand))
+    entries = forward_launch_sequence(pm, plan, xs, T, gen)
+    lens = [min(int(v), tokens_per_row) for v in seq_lens.cpu().tolist()]
+    seq_bytes = sum(launch_bytes(pm, e.modules, e.part, adapter_ids, lens) for e in entries)
+    seq = [e.fn for e in entries]
+    stacks = list({id(e.owner): e.owner for e in entries if e.part != "fused"}.values())
+    fused = [e.fn for e in entries if e.part == "fused"]
     total_ms = time_launches(seq, reps)
     sh_ms = time_launches([st.shrink for st in stacks], reps) if stacks else 0.0
     ex_ms = time_launches([st.expand for st in stacks], reps) if stacks else 0.0
     fu_ms = time_launches(fused, reps) if fused else 0.0
     return {"pairs_ms": total_ms, "shrink_ms": sh_ms, "expand_ms": ex_ms, "fused_ms": fu_ms, "per_type_us": per_type,
-            "group_tokens": plan.group_tokens, "launches": len(seq), "fused_launches": len(fused)}
+            "group_tokens": plan.group_tokens, "launches": len(seq), "fused_launches": len(fused), "bytes": seq_bytes}
 
 
-def cpu_baseline_decode_layer(pm, adapter_ids: list, budget_s: float) -> dict:
+def cpu_baseline_layer(pm, adapter_ids: list, budget_s: float, lens: list | None = None, seq: int = 1,
+                       seed: int = 1003) -> dict:
     """The reference fallback (oracle restatement of layers.py:112-134) for one decoder layer's 7 LoRA ops.
 
-    Same adapters, slots and row -> slot map as the GPU step; x and the base
-    outputs are random bf16 of the decode shapes ([256, 1, in] and
-    [256, 1, out]).  A full 8B forward on the host is out of reach, so the
-    LoRA ops of one layer are timed and the per-step figure scales them by
-    the layer count.
+    Same adapters, slots and row -> slot map as the GPU run; x and the base
+    outputs are random bf16 of the run's shapes ([rows, seq, in] and
+    [rows, seq, out]) with the run's valid lengths (`lens`, default: all
+    `seq` tokens).  A full 8B forward on the host is out of reach, so the
+    LoRA ops of one layer are timed and the per-forward figure scales them
+    by the layer count.
     """
     from oracle.lora import dense_slot_tensors, reference_forward
 
@@ -821,10 +955,11 @@ def cpu_baseline_decode_layer(pm, adapter_ids: list, budget_s: float) -> dict:
     base_id = pm.config.base_adapter_id
     rows = len(adapter_ids)
     widx = torch.tensor([0 if a == base_id else cache.adapter_to_slot[a] for a in adapter_ids])
-    seq = torch.ones(rows, dtype=torch.int32)
+    lens = [seq] * rows if lens is None else [int(v) for v in lens]
+    seq_lens = torch.tensor(lens, dtype=torch.int32)
     layer0 = [s for s in pm.module_specs if ".0." in f".{s.name}."][:7]
-    gen = torch.Generator().manual_seed(1003)
-    ops = []
+    gen = torch.Generator().manual_seed(seed)
+    ops, xs = [], {}
     for spec in layer0:
         per_slot = [None] * cache.num_slots
         for slot, aid in enumerate(cache.slot_to_adapter):
@@ -835,30 +970,27 @@ def cpu_baseline_decode_layer(pm, adapter_ids: list, budget_s: float) -> dict:
                 per_slot[slot] = (w.A.t(), w.B.t(), float(w.scale) * int(w.rank))
         A, B, ranks, scales = dense_slot_tensors(per_slot, spec.in_features, spec.out_features,
                                                  pm.config.max_rank, torch.bfloat16)
-        x = torch.randn(rows, 1, spec.in_features, generator=gen).to(torch.bfloat16)
-        base = torch.randn(rows, 1, spec.out_features, generator=gen).to(torch.bfloat16)
-        ops.append((x, base, A, B, ranks, scales))
+        if spec.in_features not in xs:  # one input per width, as the layer's siblings share theirs
+            xs[spec.in_features] = torch.randn(rows, seq, spec.in_features, generator=gen, dtype=torch.bfloat16)
+        base = torch.randn(rows, seq, spec.out_features, generator=gen, dtype=torch.bfloat16)
+        ops.append((xs[spec.in_features], base, A, B, ranks, scales))
     threads = torch.get_num_threads()
     reps = 0
     t0 = time.perf_counter()
     while True:
         for x, base, A, B, ranks, scales in ops:
-            reference_forward(x, base, seq, widx, A, B, ranks, scales)
+            reference_forward(x, base, seq_lens, widx, A, B, ranks, scales)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s or reps >= 20:
             break
     per_layer = el / reps
     layers = pm.base_model.config.num_hidden_layers
-    return {
-        "value": round(rows / (per_layer * layers), 3),
-        "unit": "tokens/s (LoRA ops only)",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{reps} passes over one layer's 7 LoRA ops (256 rows, {int((widx > 0).sum())} with an adapter) "
-                  f"of the fallback loop, {per_layer * 1e3:.1f} ms each, scaled by {layers} layers; "
-                  f"torch {threads} threads, {platform.processor() or platform.machine()}",
-    }
+    valid = sum(min(n, seq) for n in lens)
+    return _cpu_record(round(valid / (per_layer * layers), 3), "tokens/s (LoRA ops only)", threads,
+                       f"{reps} passes over one layer's 7 LoRA ops ({rows} rows x {seq} positions, {valid} valid "
+                       f"tokens, {int((widx > 0).sum())} rows with an adapter) of the fallback loop, "
+                       f"{per_layer * 1e3:.1f} ms each, scaled by {layers} layers; torch {threads} threads")
 
 
 def _graph_ms(fn, reps: int) -> float:
@@ -926,10 +1058,14 @@ def run_decode(args) -> dict:
     with torch.inference_mode():
         kt = time_lora_ops(pm, wl.adapter_ids, 1, torch.ones(B, dtype=torch.int32, device=device), reps=5)
         kern_ms = kt["pairs_ms"]
+        out["lora_bytes_per_step"] = kt["bytes"]  # x read once per stacked launch, as the launches do
+        out["lora_bytes_per_step_x_per_module"] = nb["total"]
         out["plan_group_tokens"] = kt["group_tokens"]
         out["lora_kernels_ms"] = round(kern_ms, 4)
-        out["lora_kernels_gbs"] = round(nb["total"] / (kern_ms * 1e-3) / 1e9, 1)
-        out["lora_kernels_pct_hbm"] = round(100 * nb["total"] / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
+        out["lora_kernels_gbs"] = round(kt["bytes"] / (kern_ms * 1e-3) / 1e9, 1)
+        out["lora_kernels_pct_hbm"] = round(100 * kt["bytes"] / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
+        out["roofline"] = sequence_roofline("one decode step's LoRA launches (pl_shrink_short, pl_expand_short)",
+                                            kt["bytes"], kern_ms, kt["launches"], "decode")
         out["lora_kernels_shrink_ms"] = round(kt["shrink_ms"], 4)
         out["lora_kernels_expand_ms"] = round(kt["expand_ms"], 4)
         out["per_op_us_shrink_expand"] = kt["per_type_us"]
@@ -938,7 +1074,7 @@ def run_decode(args) -> dict:
                                       "q/k/v and for gate/up, a shrink and an expand for o and down) back to back "
                                       "without the base model")
         if not args.no_cpu_baseline:
-            out["cpu_baseline"] = cpu_baseline_decode_layer(pm, wl.adapter_ids, args.cpu_seconds)
+            out["cpu_baseline"] = cpu_baseline_layer(pm, wl.adapter_ids, args.cpu_seconds)
         _log(f"decode: kernels {out['lora_kernels_gbs']} GB/s")
         e_base = _eager_ms(base_step, args.decode_steps)
         e_lora = _eager_ms(lora_step, args.decode_steps)
@@ -955,6 +1091,16 @@ def run_decode(args) -> dict:
             out["tokens_per_s_lora"] = round(B / g_lora * 1e3, 1)
             out["tokens_per_s_base"] = round(B / g_base * 1e3, 1)
             out["ratio_lora_to_base"] = round(g_base / g_lora, 4)
+            # the base step is far from its own floor (attention over the 512-token cache
+            # dominates it), which flatters the ratio: also state it against that floor
+            cfg = pm.base_model.config
+            layer_bytes = 2 * sum(p.numel() for n, p in pm.base_model.named_parameters() if "embed" not in n)
+            kv_bytes = 2 * cfg.num_hidden_layers * 2 * B * cfg.num_key_value_heads * (wl.past + 1) * cfg.head_dim
+            floor_ms = (layer_bytes + kv_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3
+            out["base_step_floor_ms"] = round(floor_ms, 3)
+            out["ratio_at_base_floor"] = round(floor_ms / (floor_ms + g_lora - g_base), 4)
+            out["ratio_note"] = ("the base step runs far above its floor (its weights and KV cache read once at 8 TB/s); "
+                                 "ratio_at_base_floor adds the measured LoRA time to that floor instead")
             out["timing"] = "HIP graph replay of one decode step"
             out["attention"] = "torch SDPA fused kernel, " + ("native GQA" if _GQA_NATIVE["ok"] else "K/V expanded to 32 heads")
             _log(f"decode: graph base {g_base:.2f} ms, lora {g_lora:.2f} ms")
@@ -1026,6 +1172,8 @@ def run_prefill(args, pm) -> dict:
         out["lora_kernels_gbs_x_per_module"] = round(nb["total"] / (kern_ms * 1e-3) / 1e9, 1)
         out["lora_kernels_mfma_tflops"] = round(nb["flops"] / (kern_ms * 1e-3) / 1e12, 2)
         out["lora_kernels_pct_mfma_bf16"] = round(100 * nb["flops"] / (kern_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 3)
+        out["roofline"] = sequence_roofline("one prefill forward's LoRA launches (pl_lora_fused_tile)",
+                                            nb["shared_x"], kern_ms, kt["launches"], "prefill")
         out["lora_kernels_shrink_ms"] = round(kt["shrink_ms"], 3)
         out["lora_kernels_expand_ms"] = round(kt["expand_ms"], 3)
         out["lora_kernels_fused_ms"] = round(kt["fused_ms"], 3)
@@ -1045,6 +1193,9 @@ def run_prefill(args, pm) -> dict:
         out["tokens_per_s_lora"] = round(int(lens.sum()) / out["ms_lora"] * 1e3, 1)
         out["ratio_lora_to_base"] = round(out["ms_base"] / out["ms_lora"], 4)
         out["timing"] = "eager wall clock of one forward (valid tokens per second)"
+    if not args.no_cpu_baseline:
+        _log("prefill: CPU baseline (one layer's LoRA ops at the prefill shapes)")
+        out["cpu_baseline"] = cpu_baseline_layer(pm, adapter_ids, args.cpu_seconds, lens=lens, seq=S, seed=1004)
     _log(f"prefill: kernels {out['lora_kernels_gbs']} GB/s, base {out['ms_base']} ms, lora {out['ms_lora']} ms")
     return out
 
@@ -1185,6 +1336,248 @@ def run_churn(args) -> dict:
 
 
 # ----------------------------------------------------------------------------- main
+# ----------------------------------------------------------------------------- launch profiles
+SEQUENCE_KERNELS = ("pl_shrink", "pl_expand", "pl_lora_fused")
+PLAN_KERNEL = "pl_plan_kernel"
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+
+
+def launch_profile(args) -> int:
+    """Issue one workload's LoRA launches in fixed passes, for rocprofv3, and write the manifest.
+
+    After `--profile-plans` device plan builds, the launch sequence (a
+    forward's launches for decode and prefill; the fused launch and the split
+    shrink + expand for the isolated op, over rotated input sets) is issued
+    `--profile-warmup` + `--profile-passes` times back to back.  The manifest
+    lists one pass's launches (label, part, algorithmic bytes) in issue
+    order, so `--reduce-profile` labels the profiler's dispatches by their
+    position in the pass.
+    """
+    from polylora_amd import sgmv
+
+    device = torch.device("cuda", 0)
+    kind = args.launch_profile
+    gen = torch.Generator(device=device).manual_seed(7)
+    t_build = time.perf_counter()
+    if kind == "isolated":
+        base_set = isolated_sgmv_workload(device)
+        nb = isolated_sgmv_bytes(base_set, 4096, 4096)
+        sets = [base_set] + [IsolatedSgmv(base_set.cache, base_set.adapters, base_set.ranks,
+                                          torch.randn_like(base_set.x), base_set.base, torch.randn_like(base_set.y),
+                                          base_set.row_slot, base_set.seq_lens, base_set.plan, base_set.seg_lens)
+                             for _ in range(8)]
+        seq = []
+        for wl in sets:
+            seq.append(("fused op", "fused", FusedLaunch(wl.x, wl.y, wl.cache, "op", wl.plan), nb["total"]))
+        for wl in sets:
+            sp = SgmvLaunch(wl.x, wl.y, wl.cache, "op", wl.plan)
+            seq += [("split shrink", "shrink", sp.shrink, nb["shrink"]), ("split expand", "expand", sp.expand, nb["expand"])]
+        cache, row_slot, seq_lens, tpr, distinct = base_set.cache, base_set.row_slot, base_set.seq_lens, 1, 16
+        desc = ("isolated SGMV bf16, T=4096 tokens, K=N=4096, 16 slots + base, ranks {0,4,8,16}, 9 rotated input "
+                "sets: the fused launch on each set, then the split shrink + expand on each")
+    else:
+        if kind == "decode":
+            wl = decode_workload(device, layers=args.decode_layers, kv_cache=False)
+            pm, ids, tpr, lens = wl.model, wl.adapter_ids, 1, [1] * len(wl.adapter_ids)
+            desc = (f"Llama-3-8B-shaped decode, {args.decode_layers} layers, 256 rows x 1 token, 64 slots, ranks "
+                    "{8,16,32,64}, Zipf(1.1) with 10% base rows: one forward's LoRA launches")
+        else:
+            from polylora_amd import PolyLoraConfig, PolyLoraModel
+
+            model = build_llama(device, args.decode_layers, seed=1003)
+            pm = PolyLoraModel(model, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=64,
+                                                     max_rank=64)).eval()
+            names = [f"pf{i}" for i in range(8)]
+            add_random_adapters(pm, {n: (16 if i < 4 else 32) for i, n in enumerate(names)}, seed=1004, device=device)
+            rng = np.random.default_rng(1004)
+            tpr = 1024
+            lens = [int(v) for v in rng.integers(512, tpr + 1, size=32)]
+            ids = [names[i // 4] for i in range(32)]
+            desc = (f"Llama-3-8B-shaped prefill, {args.decode_layers} layers, 32 rows x 1024 positions, lengths "
+                    f"U[512,1024] ({sum(lens)} valid tokens), 8 adapters (4 x r16, 4 x r32): one forward's LoRA launches")
+        cache = pm.adapter_cache
+        row_slot = cache.ensure_resident(ids)
+        seq_lens = torch.tensor(lens, dtype=torch.int32, device=device)
+        distinct = len({a for a in ids if a != pm.config.base_adapter_id})
+        plan = sgmv.SgmvPlan(row_slot, seq_lens, tpr, cache.num_slots, distinct_slots=distinct)
+        T = len(ids) * tpr
+        xs = {k: torch.randn(T, k, generator=gen, device=device, dtype=torch.bfloat16)
+              for k in sorted({s.in_features for s in pm.module_specs})}
+        seq = [(e.label, e.part, e.fn, launch_bytes(pm, e.modules, e.part, ids, lens))
+               for e in forward_launch_sequence(pm, plan, xs, T, gen)]
+    torch.cuda.synchronize()
+    _log(f"profile {kind}: {len(seq)} launches per pass, built in {time.perf_counter() - t_build:.1f}s")
+    for _ in range(args.profile_plans):
+        sgmv.SgmvPlan(row_slot, seq_lens, tpr, cache.num_slots, distinct_slots=distinct)
+    torch.cuda.synchronize()
+    progress = _Progress(f"profile {kind}")
+    stream = torch.cuda.current_stream()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for p in range(args.profile_warmup + args.profile_passes):
+        if p == args.profile_warmup:
+            t0.record(stream)
+        progress.tick(f"pass {p + 1}/{args.profile_warmup + args.profile_passes}")
+        for _, _, fn, _ in seq:
+            fn()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    manifest = {"workload": desc, "kind": kind, "warmup": args.profile_warmup, "passes": args.profile_passes,
+                "plan_builds": args.profile_plans, "event_ms_per_pass": t0.elapsed_time(t1) / args.profile_passes,
+                "sequence": [{"label": l, "part": part, "bytes": int(b)} for l, part, _, b in seq]}
+    with open(args.manifest, "w", encoding="utf-8") as fh:
+        json.dump(manifest, fh, indent=1)
+    _log(f"profile {kind}: {manifest['event_ms_per_pass']:.4f} ms per pass; manifest {args.manifest}")
+    return 0
+
+
+def kernel_base_name(name: str) -> str:
+    """'void pl_expand_short<__hip_bfloat16, 2>(args...)' -> 'pl_expand_short'."""
+    n = name.strip().strip('"')
+    if n.startswith("void "):
+        n = n[5:]
+    for ch in "<(":
+        i = n.find(ch)
+        if i >= 0:
+            n = n[:i]
+    return n.strip()
+
+
+def read_dispatches(path: str, counter: str | None = None) -> list:
+    """[(dispatch id, kernel, value, workgroups)] in dispatch order from a rocprofv3 CSV.
+
+    value: duration in ns (kernel trace, counter None) or the counter's value
+    summed over its rows for the dispatch (counter collection).
+    """
+    import csv
+
+    def workgroups(row):
+        if "Grid_Size_X" in row:
+            g = [int(row.get(f"Grid_Size_{a}") or 1) for a in "XYZ"]
+            w = [int(row.get(f"Workgroup_Size_{a}") or 1) for a in "XYZ"]
+            return (g[0] * g[1] * g[2]) // max(1, w[0] * w[1] * w[2])
+        return int(row.get("Grid_Size") or 0) // max(1, int(row.get("Workgroup_Size") or 1))
+
+    out = {}
+    with open(path, newline="", encoding="utf-8") as fh:
+        for row in csv.DictReader(fh):
+            if counter is not None and row.get("Counter_Name") != counter:
+                continue
+            did = int(row["Dispatch_Id"])
+            if counter is None:
+                val = float(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+            else:
+                val = float(row["Counter_Value"])
+            if did in out:
+                out[did][2] += val
+            else:
+                out[did] = [did, kernel_base_name(row["Kernel_Name"]), val, workgroups(row)]
+    return [tuple(v) for _, v in sorted(out.items())]
+
+
+def label_dispatches(dispatches: list, manifest: dict) -> dict:
+    """label -> [(kernel, value, workgroups, algorithmic bytes)] of the timed passes.
+
+    The sequence kernels' dispatches are taken in order; the last
+    (warmup + passes) x len(sequence) of them are the profiled passes, of
+    which the warm-up passes are dropped.  Every pass must dispatch the same
+    kernel at the same position, or the labels would be wrong.
+    """
+    seq = manifest["sequence"]
+    n = len(seq)
+    run = [d for d in dispatches if d[1].startswith(SEQUENCE_KERNELS)]
+    need = (manifest["warmup"] + manifest["passes"]) * n
+    if len(run) < need:
+        raise ValueError(f"{len(run)} sequence dispatches in the profile, the manifest needs {need}")
+    run = run[len(run) - need:][manifest["warmup"] * n:]
+    out = {}
+    for i, (_, kernel, val, wgs) in enumerate(run):
+        if kernel != run[i % n][1]:
+            raise ValueError(f"dispatch {i}: {kernel} where the first pass had {run[i % n][1]}")
+        e = seq[i % n]
+        out.setdefault(e["label"], []).append((kernel, val, wgs, e["bytes"]))
+    return out
+
+
+def _calibration(path: str | None, counter: str, copy_bytes: int) -> float:
+    """Scale for `counter` so that a plain copy of `copy_bytes` reads (or writes) exactly that many bytes."""
+    if not path:
+        return 1.0
+    vals = [v for _, k, v, _ in read_dispatches(path, counter) if k == COPY_KERNEL]
+    if not vals:
+        raise ValueError(f"no {COPY_KERNEL} dispatch in {path}")
+    return (copy_bytes / 1024.0) / (sum(vals) / len(vals))
+
+
+def reduce_profile(args) -> int:
+    """Print the markdown tables of a launch profile (and write its JSON) from rocprofv3 CSVs."""
+    with open(args.manifest, encoding="utf-8") as fh:
+        manifest = json.load(fh)
+    trace = read_dispatches(args.trace)
+    timed = label_dispatches(trace, manifest)
+    fetch = label_dispatches(read_dispatches(args.fetch, "FETCH_SIZE"), manifest) if args.fetch else None
+    write = label_dispatches(read_dispatches(args.write, "WRITE_SIZE"), manifest) if args.write else None
+    fs = _calibration(args.copy_fetch, "FETCH_SIZE", args.copy_bytes)
+    ws = _calibration(args.copy_write, "WRITE_SIZE", args.copy_bytes)
+    per_pass = {}
+    for e in manifest["sequence"]:
+        per_pass[e["label"]] = per_pass.get(e["label"], 0) + 1
+    lines = [f"Workload: {manifest['workload']}.", "",
+             f"{manifest['passes']} profiled passes after {manifest['warmup']} warm-up passes; "
+             f"bench HIP-event time {manifest['event_ms_per_pass'] * 1e3:.1f} us per pass.", "",
+             "| launch | kernel | per pass | workgroups | dispatches | avg (us) | median (us) | min (us) | "
+             "algorithmic MB | GB/s at avg | % of 8 TB/s |",
+             "|---|---|---|---|---|---|---|---|---|---|---|"]
+    report = {"workload": manifest["workload"], "fetch_scale": fs, "write_scale": ws, "labels": {}, "kernels": {}}
+    pass_us = pass_bytes = 0.0
+    for label, rows in timed.items():
+        durs = sorted(v / 1e3 for _, v, _, _ in rows)
+        avg = sum(durs) / len(durs)
+        mb = sum(b for *_, b in rows) / len(rows)
+        kernels = sorted({k for k, *_ in rows})
+        wgs = sorted({w for _, _, w, _ in rows})
+        gbs = mb / (avg * 1e-6) / 1e9
+        pass_us += avg * per_pass[label]
+        pass_bytes += mb * per_pass[label]
+        lines.append(f"| {label} | {', '.join(kernels)} | {per_pass[label]} | {', '.join(map(str, wgs))} | {len(rows)} "
+                     f"| {avg:.2f} | {durs[len(durs) // 2]:.2f} | {durs[0]:.2f} | {mb / 1e6:.2f} | {gbs:.0f} "
+                     f"| {100 * gbs / HBM_PEAK_GBS:.1f} |")
+        report["labels"][label] = {"kernels": kernels, "per_pass": per_pass[label], "avg_us": avg,
+                                   "algorithmic_bytes_per_launch": mb}
+    lines += ["", f"One pass: {pass_us:.1f} us summed over its launches' average durations, "
+              f"{pass_bytes / 1e6:.1f} MB algorithmic, {pass_bytes / (pass_us * 1e-6) / 1e9:.0f} GB/s "
+              f"({100 * pass_bytes / (pass_us * 1e-6) / 1e9 / HBM_PEAK_GBS:.1f}% of 8 TB/s)."]
+    report["pass_us"], report["pass_bytes"] = pass_us, pass_bytes
+    plans = [v / 1e3 for _, k, v, _ in trace if k == PLAN_KERNEL]
+    if plans:
+        lines += ["", f"{PLAN_KERNEL}: {len(plans)} dispatches, avg {sum(plans) / len(plans):.2f} us, "
+                  f"min {min(plans):.2f} us."]
+        report["plan_avg_us"] = sum(plans) / len(plans)
+    if fetch and write:
+        lines += ["", f"HBM bytes per launch: FETCH_SIZE x {fs:.4f}, WRITE_SIZE x {ws:.4f} (KiB; the scales make a "
+                  f"plain {args.copy_bytes}-byte copy read and write exactly its size).", "",
+                  "| launch | FETCH_SIZE (KiB, raw) | WRITE_SIZE (KiB, raw) | measured MB | algorithmic MB | ratio |",
+                  "|---|---|---|---|---|---|"]
+        t_pass = 0.0
+        for label in timed:
+            f = sum(v for _, v, _, _ in fetch[label]) / len(fetch[label])
+            w = sum(v for _, v, _, _ in write[label]) / len(write[label])
+            meas = 1024.0 * (f * fs + w * ws)
+            alg = report["labels"][label]["algorithmic_bytes_per_launch"]
+            t_pass += meas * per_pass[label]
+            lines.append(f"| {label} | {f:.1f} | {w:.1f} | {meas / 1e6:.2f} | {alg / 1e6:.2f} | {meas / alg:.3f} |")
+            report["labels"][label].update(fetch_kib=f, write_kib=w, traffic_bytes_per_launch=meas)
+            for k in report["labels"][label]["kernels"]:
+                report["kernels"].setdefault(k, {"traffic_bytes_per_launch": meas, "algorithmic_bytes_per_launch": alg})
+        report["pass_traffic_bytes"] = t_pass
+        lines += ["", f"One pass moves {t_pass / 1e6:.1f} MB measured against {pass_bytes / 1e6:.1f} MB algorithmic "
+                  f"({t_pass / pass_bytes:.3f})."]
+    print("\n".join(lines))
+    if args.reduce_json:
+        with open(args.reduce_json, "w", encoding="utf-8") as fh:
+            json.dump(report, fh, indent=1)
+    return 0
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
@@ -1207,7 +1600,24 @@ def main(argv=None) -> int:
                    help="most distinct adapters per churn sub-batch (the cache has 32 slots)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                    help="only copy a BYTES-sized device buffer 5 times (calibrates HBM byte counters) and exit")
+    p.add_argument("--launch-profile", choices=["isolated", "decode", "prefill"],
+                   help="only issue this workload's LoRA launches in fixed passes (for rocprofv3) and write --manifest")
+    p.add_argument("--manifest", default="gpurun_out/launch_manifest.json")
+    p.add_argument("--profile-passes", type=int, default=20)
+    p.add_argument("--profile-warmup", type=int, default=3)
+    p.add_argument("--profile-plans", type=int, default=20, help="device plan builds before the passes")
+    p.add_argument("--reduce-profile", action="store_true",
+                   help="no GPU: reduce rocprofv3 CSVs of a --launch-profile run into markdown tables")
+    p.add_argument("--trace", help="kernel_trace.csv of the profiled run")
+    p.add_argument("--fetch", help="counter_collection.csv of a --pmc FETCH_SIZE run")
+    p.add_argument("--write", help="counter_collection.csv of a --pmc WRITE_SIZE run")
+    p.add_argument("--copy-fetch", help="counter_collection.csv of --pmc FETCH_SIZE over --copy-probe")
+    p.add_argument("--copy-write", help="counter_collection.csv of --pmc WRITE_SIZE over --copy-probe")
+    p.add_argument("--copy-bytes", type=int, default=268435456)
+    p.add_argument("--reduce-json", help="write the reduced figures here as JSON")
     args = p.parse_args(argv)
+    if args.reduce_profile:
+        return reduce_profile(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path; run with --gpus 1", file=sys.stderr)
         return 2
@@ -1222,6 +1632,8 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": args.copy_probe, "copies": 5}), flush=True)
         return 0
+    if args.launch_profile:
+        return launch_profile(args)
     iso = run_isolated(args)
     _log(f"isolated: {iso['value']} GB/s")
     result = {
@@ -1255,7 +1667,8 @@ def main(argv=None) -> int:
         if not args.no_churn:
             workloads["churn"] = run_churn(args)
         if not args.no_deberta:
-            workloads["deberta"] = run_deberta(torch.device("cuda", 0))
+            workloads["deberta"] = run_deberta(torch.device("cuda", 0),
+                                                cpu_budget_s=None if args.no_cpu_baseline else args.cpu_seconds)
         result["workloads"] = workloads
     print(json.dumps(result), flush=True)
     return 0
