@@ -637,6 +637,56 @@ def sequence_roofline(what: str, nbytes: int, ms: float, launches: int, workload
             "traffic_note": f"HBM bytes of one sequence from profiles/sgmv_{workload}_traffic.json"}
 
 
+def time_operator_api(sets: list, reps: int) -> dict:
+    """sgmv_lora_a_fwd then sgmv_lora_b_fwd (the reference's operator API) on the isolated op's shapes.
+
+    The adapters of the workload in the reference's slot layout (A
+    [17, 4096, 16], B [17, 16, 4096], zero past each rank; index = the
+    cache slot, 0 = rank 0), each token a row of one position; x and the base
+    output rotate over the same input sets as the other timings.
+    """
+    from polylora_amd import sgmv
+
+    wl = sets[0]
+    cache = wl.cache
+    S, K, N, R = cache.num_slots, wl.x.shape[1], wl.y.shape[1], 16
+    wa = torch.zeros(S, K, R, dtype=wl.x.dtype)
+    wb = torch.zeros(S, R, N, dtype=wl.x.dtype)
+    ranks = torch.zeros(S, dtype=torch.int32)
+    scal = torch.zeros(S, dtype=torch.float32)
+    for slot in range(1, S):
+        aid = cache.slot_to_adapter[slot]
+        got = None if aid is None else wl.adapters[aid].get("op")
+        if got is None:
+            continue
+        a, b, alpha = got
+        r = a.shape[0]
+        wa[slot, :, :r] = a.t()
+        wb[slot, :r, :] = b.t()
+        ranks[slot], scal[slot] = r, alpha / r
+    dev = wl.x.device
+    wa, wb, ranks, scal = wa.to(dev), wb.to(dev), ranks.to(dev), scal.to(dev)
+    widx = wl.row_slot
+    seq = wl.seq_lens
+    xs = [w.x.view(-1, 1, K) for w in sets]
+    ys = [w.y.view(-1, 1, N) for w in sets]
+
+    def pair(i):
+        tmp = sgmv.sgmv_lora_a_fwd(xs[i], wa, seq, widx, ranks)
+        sgmv.sgmv_lora_b_fwd(tmp, wb, seq, widx, ranks, scal, ys[i])
+
+    for i in range(2 * len(sets)):
+        pair(i % len(sets))
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(reps):
+        pair(i % len(sets))
+    t1.record()
+    torch.cuda.synchronize()
+    return {"pair_ms": t0.elapsed_time(t1) / reps}
+
+
 def run_isolated(args) -> dict:
     from polylora_amd import sgmv
 
@@ -666,6 +716,8 @@ def run_isolated(args) -> dict:
     fused = sgmv.fused_ok(base_set.plan, base_set.cache, K)
     if fused:
         f_ms = time_launches([FusedLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets], reps) / n_sets
+
+    op_ms = time_operator_api(sets, max(20, args.steps // 2))["pair_ms"]
 
     # a step is one lora_apply call through the Python host API (plan already
     # built, inputs resident); the calls queue back to back, so the device,
@@ -703,6 +755,11 @@ def run_isolated(args) -> dict:
             "split_shrink_ms": round(sh_ms, 5),
             "split_expand_ms": round(ex_ms, 5),
             "split_pair_gbs": round(nb["total"] / ((sh_ms + ex_ms) * 1e-3) / 1e9, 1),
+            "operator_api_pair_ms": round(op_ms, 5),
+            "operator_api_pair_gbs": round(nb["total"] / (op_ms * 1e-3) / 1e9, 1),
+            "operator_api_note": "sgmv_lora_a_fwd + sgmv_lora_b_fwd with the reference's slot layout and a "
+                                 "model-dtype intermediate, host calls back to back (8 launches: repack, plan, "
+                                 "shrink, finish; repack, plan, gather, expand); GB/s counts the op's bytes",
         },
         "roofline": {
             "kernel": kernel,

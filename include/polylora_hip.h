@@ -11,6 +11,9 @@
  * repository root):
  *   pl_sgmv_lora_a_ref  <- src/polylora/sgmv.py:141-175  sgmv_lora_a_fwd
  *   pl_sgmv_lora_b_ref  <- src/polylora/sgmv.py:278-328  sgmv_lora_b_fwd
+ *   pl_sgmv_ref_workspace_bytes
+ *                          (size of their MFMA path's workspace; the Triton
+ *                          kernels of the reference allocate nothing)
  *   pl_plan_build       <- src/polylora/sgmv.py:29-61    _build_flat_schedule
  *                          (one device-side plan per forward instead of a
  *                          host-synchronising schedule per layer)
@@ -255,28 +258,50 @@ int pl_lora_apply_rows(int32_t dtype, const void* x, int64_t ldx, int32_t K, voi
                        const int32_t* seq_lens, int32_t rows, int32_t row_len, float* tmp,
                        int32_t ldt, int32_t epilogue, void* stream);
 
+/* Workspace bytes of the MFMA path of pl_sgmv_lora_a_ref (which = 0: K =
+ * in_features, n = n_max) or pl_sgmv_lora_b_ref (which = 1: K = k_max, n =
+ * N) for these sizes, or 0 when that path does not take the shape (K of the
+ * shrink or N of the expand not a whole number of 16-byte chunks, n_max or
+ * k_max above 64, more than PL_MAX_SLOTS - 1 adapters, or an empty call):
+ * then the row kernels run and no workspace is needed. */
+int64_t pl_sgmv_ref_workspace_bytes(int32_t dtype, int32_t which, int32_t B, int32_t M, int32_t K,
+                                    int32_t n, int32_t num_adapters);
+
 /* Reference-layout shrink (sgmv.py:141-175): out[b][m][n] = T(sum_k x[b][m][k] *
- * w[widx[b]][k][n]) for m < seq_lens[b], n < ranks[widx[b]] * stack_num.
- * x [B][M][K] contiguous; w [num_adapters][K][n_max] with element strides;
- * out [B][M][n_max] contiguous.  Rows with widx outside [0, num_adapters)
- * are skipped. */
+ * w[widx[b]][k][n]) for m < min(seq_lens[b], M), n < min(ranks[widx[b]] *
+ * stack_num, n_max); every other element of out is left as it was (the
+ * reference allocates it with torch.empty).  x [B][M][K] contiguous; w
+ * [num_adapters][K][n_max] with element strides; out [B][M][n_max]
+ * contiguous.  Rows with widx outside [0, num_adapters) are skipped.
+ * With a 256-byte aligned workspace of at least
+ * pl_sgmv_ref_workspace_bytes(dtype, 0, ...) bytes (when that is nonzero)
+ * and a 16-byte aligned x, the call runs on the MFMA path: the weights of
+ * every adapter are repacked into the slot arena's block layout inside the
+ * workspace, a device plan groups the rows by adapter, and the tiled shrink
+ * runs (4 launches, no host synchronisation).  Otherwise, or with a null
+ * workspace, one wave per token row computes it.  A workspace that is too
+ * small or misaligned is an error (PL_ERR_ARG). */
 int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K,
                        const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
                        int32_t num_adapters, int32_t n_max,
                        const int32_t* seq_lens, const int32_t* weight_indices,
-                       const int32_t* lora_ranks, int32_t stack_num, void* out, void* stream);
+                       const int32_t* lora_ranks, int32_t stack_num, void* out,
+                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Reference-layout expand (sgmv.py:278-328): out[b][m][n] = T(T(scale * sum_{k<rank}
- * x[b][m][k] * w[widx[b]][k][n]) + out[b][m][n]) for m < seq_lens[b], rank > 0.
- * x [B][M][k_max] contiguous; w [num_adapters][k_max][N] with element strides;
- * out [B][M][N] contiguous (updated in place).  Rows with widx outside
- * [0, num_adapters) are skipped. */
+ * x[b][m][k] * w[widx[b]][k][n]) + out[b][m][n]) for m < min(seq_lens[b], M),
+ * rank = min(ranks[widx[b]], k_max) > 0.  x [B][M][k_max] contiguous; w
+ * [num_adapters][k_max][N] with element strides; out [B][M][N] contiguous
+ * (updated in place).  Rows with widx outside [0, num_adapters) are
+ * skipped.  Workspace and paths as for pl_sgmv_lora_a_ref (which = 1; the
+ * MFMA path needs a 16-byte aligned out): the intermediate x is gathered
+ * into one fp32 plane and the tiled expand adds the scaled delta. */
 int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max,
                        const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
                        int32_t num_adapters, int32_t N,
                        const int32_t* seq_lens, const int32_t* weight_indices,
                        const int32_t* lora_ranks, const float* scalings, void* out,
-                       void* stream);
+                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Bytes of the static device scratch behind pl_lora_apply_noalloc. */
 #define PL_NOALLOC_SCRATCH_BYTES (32 << 20)

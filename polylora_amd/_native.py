@@ -16,6 +16,7 @@ import torch  # noqa: F401  (loads the HIP runtime the library must share)
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libpolylora_hip.so"
 
 PL_F32, PL_BF16, PL_F16 = 0, 1, 2
+PL_OK, PL_ERR_ARG, PL_ERR_ALIGN, PL_ERR_LAUNCH, PL_ERR_LIMIT = 0, 1, 2, 3, 4
 PL_EPI_FALLBACK, PL_EPI_TRITON = 0, 1
 PL_MAX_SLOTS = 4096
 PL_GROUP_TOKENS_SHORT, PL_GROUP_TOKENS_LONG = 16, 64
@@ -77,13 +78,14 @@ _SIGNATURES: dict[str, tuple] = {
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
         c_int32, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_int32, c_void_p,
     ),
+    "pl_sgmv_ref_workspace_bytes": (c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32),
     "pl_sgmv_lora_a_ref": (
         c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
-        c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
+        c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_void_p,
     ),
     "pl_sgmv_lora_b_ref": (
         c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
-        c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+        c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
     ),
     "pl_lora_apply_noalloc": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
@@ -95,7 +97,7 @@ _SIGNATURES: dict[str, tuple] = {
     "pl_check_right_padded": (c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p),
 }
 _RESTYPES = {"pl_last_error": ctypes.c_char_p, "pl_plan_group_capacity": c_int64, "pl_shrink_workspace_bytes": c_int64,
-             "pl_host_alloc": c_void_p}
+             "pl_host_alloc": c_void_p, "pl_sgmv_ref_workspace_bytes": c_int64}
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

@@ -24,7 +24,7 @@ LIB_PATH = LIB_DIR / "libpolylora_hip.so"
 INCLUDE_DIR = PACKAGE_DIR.parent / "include"
 
 ARCH = "gfx950"
-SOURCES = ("capi.hip", "plan.hip", "sgmv_tiled.hip", "sgmv_fused.hip", "sgmv_rows.hip")
+SOURCES = ("capi.hip", "plan.hip", "sgmv_tiled.hip", "sgmv_fused.hip", "sgmv_rows.hip", "sgmv_refop.hip")
 HIPCC_FLAGS = (
     f"--offload-arch={ARCH}",
     "-O3",

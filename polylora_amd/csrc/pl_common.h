@@ -166,3 +166,20 @@ int pl_launch_status(const char* what);
 
 static inline int pl_elem_size(int dtype) { return dtype == PL_F32 ? 4 : 2; }
 static inline int pl_chunk_elems(int dtype) { return dtype == PL_F32 ? 4 : 8; }
+
+// MFMA path of the reference-layout operator API (sgmv_refop.hip).  Both
+// return PL_REFOP_DECLINED, having launched nothing, when there is no
+// workspace or the shape is not one the tiled kernels take; the caller then
+// runs the row kernels.
+constexpr int PL_REFOP_DECLINED = -100;
+int pl_refop_shrink(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K, const void* w,
+                    int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t num_adapters,
+                    int32_t n_max, const int32_t* seq_lens, const int32_t* weight_indices,
+                    const int32_t* lora_ranks, int32_t stack_num, void* out, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+int pl_refop_expand(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max,
+                    const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
+                    int32_t num_adapters, int32_t N, const int32_t* seq_lens,
+                    const int32_t* weight_indices, const int32_t* lora_ranks,
+                    const float* scalings, void* out, void* workspace, int64_t workspace_bytes,
+                    void* stream);

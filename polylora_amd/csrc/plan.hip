@@ -26,6 +26,20 @@
 namespace {
 
 constexpr int kPlanThreads = 1024;
+// Rows a plan thread keeps in registers: the first kPlanThreads * kPlanCached
+// rows are read once, with all of a thread's loads in flight together, and
+// serve both passes over the rows.  Rows beyond them are read per pass.
+constexpr int kPlanCached = 8;
+
+// Slot and clamped length of row b, or slot 0 for a row that gets no tokens.
+__device__ __forceinline__ void pl_plan_row(const int32_t* __restrict__ row_slot,
+                                            const int32_t* __restrict__ seq_lens, int b,
+                                            int row_len, int S, int& s, int& L) {
+  s = row_slot[b];
+  L = seq_lens[b];
+  L = L < 0 ? 0 : (L > row_len ? row_len : L);
+  if (s <= 0 || s >= S || L <= 0) s = 0;
+}
 
 // First slot-major group index of XCD chunk x (x = 0..8) of n groups.
 __device__ __forceinline__ int pl_chunk_lo(int x, int n) { return (int)(((int64_t)x * n) / 8); }
@@ -61,13 +75,34 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   const int S = num_slots;
 
   for (int s = tid; s < S; s += kPlanThreads) cnt[s] = 0;
+  // this thread's cached rows tid + q * kPlanThreads: all loads first
+  int rs[kPlanCached], rl[kPlanCached];
+#pragma unroll
+  for (int q = 0; q < kPlanCached; ++q) {
+    const int b = tid + q * kPlanThreads;
+    rs[q] = 0;
+    rl[q] = 0;
+    if (b < rows) {
+      rs[q] = row_slot[b];
+      rl[q] = seq_lens[b];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kPlanCached; ++q) {
+    int L = rl[q];
+    L = L < 0 ? 0 : (L > row_len ? row_len : L);
+    if (rs[q] <= 0 || rs[q] >= S || L <= 0) rs[q] = 0;
+    rl[q] = L;
+  }
   __syncthreads();
 
-  for (int b = tid; b < rows; b += kPlanThreads) {
-    const int s = row_slot[b];
-    int L = seq_lens[b];
-    L = L < 0 ? 0 : (L > row_len ? row_len : L);
-    if (s > 0 && s < S && L > 0) atomicAdd(&cnt[s], L);
+#pragma unroll
+  for (int q = 0; q < kPlanCached; ++q)
+    if (rs[q] > 0) atomicAdd(&cnt[rs[q]], rl[q]);
+  for (int b = tid + kPlanCached * kPlanThreads; b < rows; b += kPlanThreads) {
+    int s, L;
+    pl_plan_row(row_slot, seq_lens, b, row_len, S, s, L);
+    if (s > 0) atomicAdd(&cnt[s], L);
   }
   __syncthreads();
 
@@ -158,11 +193,18 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
 
   if (row_len <= 16) {
     // short rows (decode, flattened tokens): one thread per row
-    for (int b = tid; b < rows; b += kPlanThreads) {
-      const int s = row_slot[b];
-      int L = seq_lens[b];
-      L = L < 0 ? 0 : (L > row_len ? row_len : L);
-      if (s > 0 && s < S && L > 0) {
+#pragma unroll
+    for (int q = 0; q < kPlanCached; ++q) {
+      if (rs[q] > 0) {
+        const int p = off[rs[q]] + atomicAdd(&cnt[rs[q]], rl[q]);
+        const int base = (tid + q * kPlanThreads) * row_len;
+        for (int m = 0; m < rl[q]; ++m) tok[p + m] = base + m;
+      }
+    }
+    for (int b = tid + kPlanCached * kPlanThreads; b < rows; b += kPlanThreads) {
+      int s, L;
+      pl_plan_row(row_slot, seq_lens, b, row_len, S, s, L);
+      if (s > 0) {
         const int p = off[s] + atomicAdd(&cnt[s], L);
         const int base = b * row_len;
         for (int m = 0; m < L; ++m) tok[p + m] = base + m;
@@ -171,10 +213,9 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   } else {
     // long rows (prefill): one wave per row
     for (int b = wave; b < rows; b += kPlanThreads / 64) {
-      const int s = row_slot[b];
-      int L = seq_lens[b];
-      L = L < 0 ? 0 : (L > row_len ? row_len : L);
-      if (s > 0 && s < S && L > 0) {
+      int s, L;
+      pl_plan_row(row_slot, seq_lens, b, row_len, S, s, L);
+      if (s > 0) {
         int p = 0;
         if (lane == 0) p = off[s] + atomicAdd(&cnt[s], L);
         p = __shfl(p, 0);

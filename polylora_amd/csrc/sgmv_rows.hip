@@ -2,9 +2,11 @@
 //
 // They serve two callers: the reference-layout operator API
 // (sgmv_lora_a_fwd / sgmv_lora_b_fwd, sgmv.py:141-175 and :278-328, weights
-// [slots][k][n] with arbitrary strides) and MultiLoraLinear shapes the tiled
-// kernels reject (K or N not a multiple of the 16-byte chunk, unaligned rows).
-// Throughput is not their goal; the tiled kernels carry the hot path.
+// [slots][k][n] with arbitrary strides) where its MFMA path (sgmv_refop.hip)
+// declines the shape or gets no workspace, and MultiLoraLinear shapes the
+// tiled kernels reject (K or N not a multiple of the 16-byte chunk,
+// unaligned rows).  Throughput is not their goal; the tiled kernels carry
+// the hot path.
 //
 // Shrink: one wave per token row; lanes stride K, each rank column is a
 // wave-wide dot product finished with a butterfly reduction.
@@ -183,7 +185,8 @@ extern "C" int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32
                                   const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
                                   int32_t num_adapters, int32_t n_max, const int32_t* seq_lens,
                                   const int32_t* weight_indices, const int32_t* lora_ranks,
-                                  int32_t stack_num, void* out, void* stream) {
+                                  int32_t stack_num, void* out, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
   if (!valid_dtype(dtype)) {
     pl_set_error("unsupported dtype code %d", dtype);
     return PL_ERR_ARG;
@@ -198,6 +201,10 @@ extern "C" int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32
     pl_set_error("pl_sgmv_lora_a_ref: null pointer");
     return PL_ERR_ARG;
   }
+  const int fast = pl_refop_shrink(dtype, x, B, M, K, w, w_s0, w_s1, w_s2, num_adapters, n_max,
+                                   seq_lens, weight_indices, lora_ranks, stack_num, out, workspace,
+                                   workspace_bytes, stream);
+  if (fast != PL_REFOP_DECLINED) return fast;
   const int64_t grid = (rows + 3) / 4;
   if (grid > 0x7fffffffLL) {
     pl_set_error("pl_sgmv_lora_a_ref: too many rows");
@@ -217,7 +224,7 @@ extern "C" int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32
                                   int64_t w_s2, int32_t num_adapters, int32_t N,
                                   const int32_t* seq_lens, const int32_t* weight_indices,
                                   const int32_t* lora_ranks, const float* scalings, void* out,
-                                  void* stream) {
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
   if (!valid_dtype(dtype)) {
     pl_set_error("unsupported dtype code %d", dtype);
     return PL_ERR_ARG;
@@ -232,6 +239,10 @@ extern "C" int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32
     pl_set_error("pl_sgmv_lora_b_ref: null pointer");
     return PL_ERR_ARG;
   }
+  const int fast = pl_refop_expand(dtype, x, B, M, k_max, w, w_s0, w_s1, w_s2, num_adapters, N,
+                                   seq_lens, weight_indices, lora_ranks, scalings, out, workspace,
+                                   workspace_bytes, stream);
+  if (fast != PL_REFOP_DECLINED) return fast;
   const int32_t nblk = (N + 255) / 256;
   if (rows * nblk > 0x7fffffffLL) {
     pl_set_error("pl_sgmv_lora_b_ref: grid too large");

@@ -730,6 +730,21 @@ def _check_row_meta(B: int, num_adapters: int, seq_lens, weight_indices, lora_ra
         raise ValueError(f"lora_ranks / scalings must have an entry for each of the {num_adapters} adapters")
 
 
+def _ref_workspace(lib, x: torch.Tensor, which: int, B: int, M: int, K: int, n: int, num_adapters: int):
+    """Workspace of the operator API's MFMA path: (256-byte aligned uint8 view, bytes), or (None, 0).
+
+    Taken from torch's caching allocator for this call only; the allocator
+    hands the block to later work on the same stream only after this call's
+    kernels, which run in stream order.
+    """
+    nbytes = int(lib.pl_sgmv_ref_workspace_bytes(_native.dtype_code(x.dtype), which, B, M, K, n, num_adapters))
+    if nbytes <= 0:
+        return None, 0
+    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=x.device)
+    pad = (-buf.data_ptr()) % 256
+    return buf[pad : pad + nbytes], nbytes
+
+
 def sgmv_lora_a_fwd(
     x: torch.Tensor,  # (B, M, K)
     weights: torch.Tensor,  # (num_adapters, K, N_max)
@@ -757,6 +772,7 @@ def sgmv_lora_a_fwd(
     seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
     _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks)
     lib = _native.load()
+    ws, ws_bytes = _ref_workspace(lib, x, 0, B, M, K, N_max, int(weights.shape[0]))
     _native.check(
         lib.pl_sgmv_lora_a_ref(
             _native.dtype_code(x.dtype),
@@ -775,6 +791,8 @@ def sgmv_lora_a_fwd(
             lora_ranks.data_ptr(),
             int(stack_num),
             output.data_ptr(),
+            0 if ws is None else ws.data_ptr(),
+            ws_bytes,
             _stream(x.device),
         ),
         "pl_sgmv_lora_a_ref",
@@ -812,6 +830,7 @@ def sgmv_lora_b_fwd(
     scalings = scalings.to(torch.float32).contiguous()
     _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, scalings)
     lib = _native.load()
+    ws, ws_bytes = _ref_workspace(lib, x, 1, B, M, K_max, N, int(weights.shape[0]))
     _native.check(
         lib.pl_sgmv_lora_b_ref(
             _native.dtype_code(x.dtype),
@@ -830,6 +849,8 @@ def sgmv_lora_b_fwd(
             lora_ranks.data_ptr(),
             scalings.data_ptr(),
             work.data_ptr(),
+            0 if ws is None else ws.data_ptr(),
+            ws_bytes,
             _stream(x.device),
         ),
         "pl_sgmv_lora_b_ref",

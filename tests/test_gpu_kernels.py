@@ -34,7 +34,8 @@ def _adapters(gen, ranks, fin, fout, module="m", extra_module=None):
 @pytest.mark.parametrize("group_tokens", [16, 64])
 @pytest.mark.parametrize(
     "rows,row_len,num_slots,seed",
-    [(1, 1, 2, 0), (7, 3, 5, 1), (256, 1, 65, 2), (32, 1024, 9, 3), (4096, 1, 17, 4), (3, 200, 4096, 5), (0, 5, 3, 6)],
+    [(1, 1, 2, 0), (7, 3, 5, 1), (256, 1, 65, 2), (32, 1024, 9, 3), (4096, 1, 17, 4), (3, 200, 4096, 5), (0, 5, 3, 6),
+     (10000, 1, 33, 7), (9000, 2, 5, 8)],
 )
 def test_plan_matches_oracle(gpu, rows, row_len, num_slots, seed, group_tokens):
     _announce(test="plan", rows=rows, row_len=row_len, num_slots=num_slots, group_tokens=group_tokens)

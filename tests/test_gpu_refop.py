@@ -1,0 +1,204 @@
+"""The reference-layout operator API (sgmv_lora_a_fwd / sgmv_lora_b_fwd, sgmv.py:141-175, :278-328).
+
+Both entry points have an MFMA path (weights repacked into the slot arena's
+block layout in a workspace, a device plan, the tiled shrink or expand) and
+the row kernels for shapes that path does not take.  Each is checked against
+the oracle's restatement of the operators (oracle.lora.sgmv_shrink_reference
+/ sgmv_expand_reference), and the two paths against each other.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.lora import sgmv_expand_reference, sgmv_shrink_reference
+from polylora_amd import _native, sgmv
+from tests._util import tol_for
+
+pytestmark = pytest.mark.gpu
+
+
+def _announce(**kw):
+    print("case:", ", ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _call_a(x, w, seq, widx, ranks, stack_num, *, mfma: bool):
+    """pl_sgmv_lora_a_ref through the C-ABI, with (MFMA path) or without (row kernels) a workspace."""
+    lib = _native.load()
+    B, M, K = x.shape
+    n_max = w.shape[2]
+    out = torch.full((B, M, n_max), 7.0, device=x.device, dtype=x.dtype)  # untouched entries stay 7
+    ws, nbytes = sgmv._ref_workspace(lib, x, 0, B, M, K, n_max, w.shape[0]) if mfma else (None, 0)
+    if mfma:
+        assert ws is not None, "the MFMA path declined this shape"
+    _native.check(lib.pl_sgmv_lora_a_ref(_native.dtype_code(x.dtype), x.data_ptr(), B, M, K, w.data_ptr(), *w.stride(),
+                                         w.shape[0], n_max, seq.data_ptr(), widx.data_ptr(), ranks.data_ptr(),
+                                         stack_num, out.data_ptr(), 0 if ws is None else ws.data_ptr(), nbytes,
+                                         torch.cuda.current_stream().cuda_stream), "pl_sgmv_lora_a_ref")
+    return out
+
+
+def _call_b(x, w, seq, widx, ranks, scal, base, *, mfma: bool):
+    lib = _native.load()
+    B, M, k_max = x.shape
+    N = w.shape[2]
+    out = base.clone()
+    ws, nbytes = sgmv._ref_workspace(lib, x, 1, B, M, k_max, N, w.shape[0]) if mfma else (None, 0)
+    if mfma:
+        assert ws is not None, "the MFMA path declined this shape"
+    _native.check(lib.pl_sgmv_lora_b_ref(_native.dtype_code(x.dtype), x.data_ptr(), B, M, k_max, w.data_ptr(),
+                                         *w.stride(), w.shape[0], N, seq.data_ptr(), widx.data_ptr(),
+                                         ranks.data_ptr(), scal.data_ptr(), out.data_ptr(),
+                                         0 if ws is None else ws.data_ptr(), nbytes,
+                                         torch.cuda.current_stream().cuda_stream), "pl_sgmv_lora_b_ref")
+    return out
+
+
+def _case(g, Bt, M, K, N, S, R, stack_num, dtype, gpu):
+    x = torch.randn(Bt, M, K, generator=g).to(dtype)
+    wa = (torch.randn(S, K, R * stack_num, generator=g) * 0.05).to(dtype)
+    wb = (torch.randn(S, R, N, generator=g) * 0.05).to(dtype)
+    ranks = torch.randint(0, R + 1, (S,), generator=g, dtype=torch.int32)
+    ranks[0] = 0
+    ranks[-1] = R
+    scal = torch.rand(S, generator=g) * 4
+    seq = torch.randint(0, M + 3, (Bt,), generator=g, dtype=torch.int32)  # some beyond M
+    widx = torch.randint(0, S, (Bt,), generator=g, dtype=torch.int32)
+    dev = [t.to(gpu) for t in (x, wa, wb, ranks, scal, seq, widx)]
+    return (x, wa, wb, ranks, scal, seq, widx), dev
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("stack_num", [1, 2])
+@pytest.mark.parametrize("Bt,M,K,N,S,R", [(6, 10, 96, 80, 4, 8), (9, 70, 256, 136, 5, 32), (40, 1, 512, 64, 7, 16)])
+def test_mfma_and_row_paths_match_the_oracle(gpu, dtype, stack_num, Bt, M, K, N, S, R):
+    _announce(test="refop_paths", dtype=dtype, stack_num=stack_num, shape=(Bt, M, K, N, S, R))
+    g = torch.Generator().manual_seed(Bt * 7 + stack_num)
+    (x, wa, wb, ranks, scal, seq, widx), (dx, dwa, dwb, dranks, dscal, dseq, dwidx) = _case(
+        g, Bt, M, K, N, S, R, stack_num, dtype, gpu)
+    exp_tmp, valid = sgmv_shrink_reference(x, wa, seq, widx, ranks, stack_num)
+    outs = {}
+    for mfma in (True, False):
+        tmp = _call_a(dx, dwa, dseq, dwidx, dranks, stack_num, mfma=mfma).cpu()
+        torch.testing.assert_close(tmp[valid], exp_tmp[valid], **tol_for(dtype))
+        assert bool((tmp[~valid] == 7).all()), "entries outside the defined region were written"
+        outs[mfma] = tmp
+    torch.testing.assert_close(outs[True][valid], outs[False][valid], **tol_for(dtype))
+    # expand over the oracle's intermediate
+    base = torch.randn(Bt, M, N, generator=g).to(dtype)
+    xb = exp_tmp[:, :, :R].contiguous()
+    expect = sgmv_expand_reference(xb, wb, seq, widx, ranks, scal, base)
+    for mfma in (True, False):
+        out = _call_b(xb.to(gpu), dwb, dseq, dwidx, dranks, dscal, base.to(gpu), mfma=mfma).cpu()
+        torch.testing.assert_close(out, expect, **tol_for(dtype))
+        untouched = (ranks[widx.long()] == 0) | (seq <= 0)
+        assert torch.equal(out[untouched], base[untouched])
+
+
+def test_unaligned_shapes_take_the_row_kernels(gpu):
+    """K = 97, N = 75: no 16-byte chunks, so the MFMA path declines and the row kernels answer."""
+    _announce(test="refop_unaligned")
+    lib = _native.load()
+    assert int(lib.pl_sgmv_ref_workspace_bytes(_native.PL_BF16, 0, 4, 3, 97, 8, 3)) == 0
+    assert int(lib.pl_sgmv_ref_workspace_bytes(_native.PL_BF16, 1, 4, 3, 8, 75, 3)) == 0
+    assert int(lib.pl_sgmv_ref_workspace_bytes(_native.PL_BF16, 0, 4, 3, 96, 72, 3)) == 0  # rank above 64
+    g = torch.Generator().manual_seed(5)
+    (x, wa, wb, ranks, scal, seq, widx), (dx, dwa, dwb, dranks, dscal, dseq, dwidx) = _case(
+        g, 4, 3, 97, 75, 3, 8, 1, torch.bfloat16, gpu)
+    tmp = sgmv.sgmv_lora_a_fwd(dx, dwa, dseq, dwidx, dranks).cpu()
+    exp_tmp, valid = sgmv_shrink_reference(x, wa, seq, widx, ranks)
+    torch.testing.assert_close(tmp[valid], exp_tmp[valid], **tol_for(torch.bfloat16))
+    base = torch.randn(4, 3, 75, generator=g).bfloat16()
+    out = sgmv.sgmv_lora_b_fwd(exp_tmp.to(gpu), dwb, dseq, dwidx, dranks, dscal, base.to(gpu)).cpu()
+    torch.testing.assert_close(out, sgmv_expand_reference(exp_tmp, wb, seq, widx, ranks, scal, base),
+                               **tol_for(torch.bfloat16))
+
+
+def test_decode_rows_and_out_of_range_indices(gpu):
+    """M = 1 rows with seq_len 513 (a KV mask's length) act as min(seq_len, M) = 1; indices -1 and S are skipped."""
+    _announce(test="refop_decode_rows")
+    g = torch.Generator().manual_seed(9)
+    Bt, K, N, S, R = 64, 1024, 512, 6, 16
+    x = torch.randn(Bt, 1, K, generator=g).bfloat16()
+    wa = (torch.randn(S, K, R, generator=g) * 0.05).bfloat16()
+    wb = (torch.randn(S, R, N, generator=g) * 0.05).bfloat16()
+    ranks = torch.tensor([0, 4, 8, 16, 12, 16], dtype=torch.int32)
+    scal = torch.tensor([0.0, 8.0, 4.0, 2.0, 2.5, 2.0])
+    seq = torch.full((Bt,), 513, dtype=torch.int32)
+    widx = torch.randint(0, S, (Bt,), generator=g, dtype=torch.int32)
+    widx[3], widx[10] = -1, S
+    ok = (widx >= 0) & (widx < S)
+    tmp = _call_a(x.to(gpu), wa.to(gpu), seq.to(gpu), widx.to(gpu), ranks.to(gpu), 1, mfma=True).cpu()
+    exp_tmp, valid = sgmv_shrink_reference(x[ok], wa, seq[ok], widx[ok], ranks)
+    torch.testing.assert_close(tmp[ok][valid], exp_tmp[valid], **tol_for(torch.bfloat16))
+    assert bool((tmp[~ok] == 7).all())
+    base = torch.randn(Bt, 1, N, generator=g).bfloat16()
+    xb = torch.zeros(Bt, 1, R, dtype=torch.bfloat16)
+    xb[ok] = exp_tmp
+    out = _call_b(xb.to(gpu), wb.to(gpu), seq.to(gpu), widx.to(gpu), ranks.to(gpu), scal.to(gpu), base.to(gpu),
+                  mfma=True).cpu()
+    expect = base.clone()
+    expect[ok] = sgmv_expand_reference(exp_tmp, wb, seq[ok], widx[ok], ranks, scal, base[ok])
+    torch.testing.assert_close(out, expect, **tol_for(torch.bfloat16))
+    assert torch.equal(out[~ok], base[~ok])
+
+
+def test_isolated_op_shapes_through_the_operator_api(gpu):
+    """4096 rows of one token, K = N = 4096, 17 adapters of ranks {0,4,8,16}, Dirichlet segments: the
+    isolated op's shapes in the reference's own layout, shrink then expand, against the oracle."""
+    _announce(test="refop_isolated_4096")
+    from bench import _dirichlet_segments
+
+    rng = np.random.default_rng(1002)
+    g = torch.Generator().manual_seed(1002)
+    T, K, N, S, R = 4096, 4096, 4096, 17, 16
+    ranks = torch.tensor([[0, 4, 8, 16][s % 4] for s in range(S)], dtype=torch.int32)
+    scal = torch.tensor([32.0 / r if r else 0.0 for r in ranks.tolist()])
+    wa = (torch.randn(S, K, R, generator=g) * 0.02).bfloat16()
+    wb = (torch.randn(S, R, N, generator=g) * 0.02).bfloat16()
+    seg = _dirichlet_segments(rng, T, S)
+    widx = torch.tensor(np.repeat(np.arange(S), seg), dtype=torch.int32)
+    seq = torch.ones(T, dtype=torch.int32)
+    x = torch.randn(T, 1, K, generator=g).bfloat16()
+    base = torch.randn(T, 1, N, generator=g).bfloat16()
+    dev = {k: v.to(gpu) for k, v in dict(x=x, wa=wa, wb=wb, ranks=ranks, scal=scal, seq=seq, widx=widx).items()}
+    tmp = sgmv.sgmv_lora_a_fwd(dev["x"], dev["wa"], dev["seq"], dev["widx"], dev["ranks"])
+    out = sgmv.sgmv_lora_b_fwd(tmp[:, :, :R].contiguous(), dev["wb"], dev["seq"], dev["widx"], dev["ranks"],
+                               dev["scal"], base.to(gpu))
+    exp_tmp, valid = sgmv_shrink_reference(x, wa, seq, widx, ranks)
+    got_tmp = tmp.cpu()
+    torch.testing.assert_close(got_tmp[valid], exp_tmp[valid], **tol_for(torch.bfloat16))
+    # the expand checked on the intermediate it was given (invalid entries zeroed for the oracle)
+    xb = torch.where(valid, got_tmp, torch.zeros((), dtype=torch.bfloat16))[:, :, :R].contiguous()
+    expect = sgmv_expand_reference(xb, wb, seq, widx, ranks, scal, base)
+    torch.testing.assert_close(out.cpu(), expect, rtol=2e-2, atol=1e-2)
+    zero = ranks[widx.long()] == 0
+    assert torch.equal(out.cpu()[zero], base[zero])
+
+
+def test_workspace_errors_are_reported(gpu):
+    """A workspace below the size the call needs, or misaligned, is an error, not a silent fallback."""
+    _announce(test="refop_ws_errors")
+    lib = _native.load()
+    x = torch.randn(4, 2, 64, device=gpu).bfloat16()
+    w = torch.randn(3, 64, 8, device=gpu).bfloat16()
+    seq = torch.full((4,), 2, dtype=torch.int32, device=gpu)
+    widx = torch.tensor([0, 1, 2, 1], dtype=torch.int32, device=gpu)
+    ranks = torch.tensor([2, 4, 8], dtype=torch.int32, device=gpu)
+    out = torch.empty(4, 2, 8, device=gpu).bfloat16()
+    need = int(lib.pl_sgmv_ref_workspace_bytes(_native.PL_BF16, 0, 4, 2, 64, 8, 3))
+    assert need > 0
+    ws = torch.empty(need + 512, dtype=torch.uint8, device=gpu)
+    base = ws.data_ptr() + (-ws.data_ptr()) % 256
+    s = torch.cuda.current_stream().cuda_stream
+    args = (_native.PL_BF16, x.data_ptr(), 4, 2, 64, w.data_ptr(), *w.stride(), 3, 8, seq.data_ptr(),
+            widx.data_ptr(), ranks.data_ptr(), 1, out.data_ptr())
+    assert lib.pl_sgmv_lora_a_ref(*args, ctypes.c_void_p(base), need - 256, s) == _native.PL_ERR_ARG
+    assert b"workspace" in lib.pl_last_error()
+    assert lib.pl_sgmv_lora_a_ref(*args, ctypes.c_void_p(base + 16), need, s) == _native.PL_ERR_ARG
+    assert lib.pl_sgmv_lora_a_ref(*args, ctypes.c_void_p(base), need, s) == 0
+    torch.cuda.synchronize()
