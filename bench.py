@@ -637,7 +637,7 @@ def sequence_roofline(what: str, nbytes: int, ms: float, launches: int, workload
             "traffic_note": f"HBM bytes of one sequence from profiles/sgmv_{workload}_traffic.json"}
 
 
-def time_operator_api(sets: list, reps: int) -> dict:
+def time_operator_api(sets: list, reps: int, keep: bool = False) -> dict:
     """sgmv_lora_a_fwd then sgmv_lora_b_fwd (the reference's operator API) on the isolated op's shapes.
 
     The adapters of the workload in the reference's slot layout (A
@@ -675,6 +675,8 @@ def time_operator_api(sets: list, reps: int) -> dict:
         tmp = sgmv.sgmv_lora_a_fwd(xs[i], wa, seq, widx, ranks)
         sgmv.sgmv_lora_b_fwd(tmp, wb, seq, widx, ranks, scal, ys[i])
 
+    if keep:
+        return {"pair": pair}
     for i in range(2 * len(sets)):
         pair(i % len(sets))
     torch.cuda.synchronize()
@@ -1394,7 +1396,7 @@ def run_churn(args) -> dict:
 
 # ----------------------------------------------------------------------------- main
 # ----------------------------------------------------------------------------- launch profiles
-SEQUENCE_KERNELS = ("pl_shrink", "pl_expand", "pl_lora_fused")
+SEQUENCE_KERNELS = ("pl_shrink", "pl_expand", "pl_lora_fused", "pl_refop", "pl_plan")
 PLAN_KERNEL = "pl_plan_kernel"
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
@@ -1416,7 +1418,7 @@ def launch_profile(args) -> int:
     kind = args.launch_profile
     gen = torch.Generator(device=device).manual_seed(7)
     t_build = time.perf_counter()
-    if kind == "isolated":
+    if kind in ("isolated", "operator"):
         base_set = isolated_sgmv_workload(device)
         nb = isolated_sgmv_bytes(base_set, 4096, 4096)
         sets = [base_set] + [IsolatedSgmv(base_set.cache, base_set.adapters, base_set.ranks,
@@ -1424,14 +1426,28 @@ def launch_profile(args) -> int:
                                           base_set.row_slot, base_set.seq_lens, base_set.plan, base_set.seg_lens)
                              for _ in range(8)]
         seq = []
-        for wl in sets:
-            seq.append(("fused op", "fused", FusedLaunch(wl.x, wl.y, wl.cache, "op", wl.plan), nb["total"]))
-        for wl in sets:
-            sp = SgmvLaunch(wl.x, wl.y, wl.cache, "op", wl.plan)
-            seq += [("split shrink", "shrink", sp.shrink, nb["shrink"]), ("split expand", "expand", sp.expand, nb["expand"])]
+        if kind == "isolated":
+            for wl in sets:
+                seq.append(("fused op", "fused", FusedLaunch(wl.x, wl.y, wl.cache, "op", wl.plan), nb["total"]))
+            for wl in sets:
+                sp = SgmvLaunch(wl.x, wl.y, wl.cache, "op", wl.plan)
+                seq += [("split shrink", "shrink", sp.shrink, nb["shrink"]),
+                        ("split expand", "expand", sp.expand, nb["expand"])]
+            desc = ("isolated SGMV bf16, T=4096 tokens, K=N=4096, 16 slots + base, ranks {0,4,8,16}, 9 rotated input "
+                    "sets: the fused launch on each set, then the split shrink + expand on each")
+        else:
+            pair = time_operator_api(sets, 1, keep=True)["pair"]
+            for i in range(len(sets)):
+                # one host call pair issues 8 dispatches; the first entry issues them all
+                steps = ["shrink: repack A", "shrink: plan", "shrink: MFMA", "shrink: finish", "expand: repack B",
+                         "expand: plan", "expand: gather", "expand: MFMA"]
+                part_bytes = {"shrink: MFMA": nb["shrink"], "expand: MFMA": nb["expand"]}
+                for j, label in enumerate(steps):
+                    fn = (lambda i=i: pair(i)) if j == 0 else (lambda: None)
+                    seq.append((label, "operator", fn, part_bytes.get(label, 0)))
+            desc = ("reference operator API (sgmv_lora_a_fwd + sgmv_lora_b_fwd) on the isolated op's shapes, "
+                    "reference slot layout, 9 rotated input sets")
         cache, row_slot, seq_lens, tpr, distinct = base_set.cache, base_set.row_slot, base_set.seq_lens, 1, 16
-        desc = ("isolated SGMV bf16, T=4096 tokens, K=N=4096, 16 slots + base, ranks {0,4,8,16}, 9 rotated input "
-                "sets: the fused launch on each set, then the split shrink + expand on each")
     else:
         if kind == "decode":
             wl = decode_workload(device, layers=args.decode_layers, kv_cache=False)
@@ -1595,9 +1611,9 @@ def reduce_profile(args) -> int:
         gbs = mb / (avg * 1e-6) / 1e9
         pass_us += avg * per_pass[label]
         pass_bytes += mb * per_pass[label]
+        rate = f"{gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f}" if mb else "- | -"
         lines.append(f"| {label} | {', '.join(kernels)} | {per_pass[label]} | {', '.join(map(str, wgs))} | {len(rows)} "
-                     f"| {avg:.2f} | {durs[len(durs) // 2]:.2f} | {durs[0]:.2f} | {mb / 1e6:.2f} | {gbs:.0f} "
-                     f"| {100 * gbs / HBM_PEAK_GBS:.1f} |")
+                     f"| {avg:.2f} | {durs[len(durs) // 2]:.2f} | {durs[0]:.2f} | {mb / 1e6:.2f} | {rate} |")
         report["labels"][label] = {"kernels": kernels, "per_pass": per_pass[label], "avg_us": avg,
                                    "algorithmic_bytes_per_launch": mb}
     lines += ["", f"One pass: {pass_us:.1f} us summed over its launches' average durations, "
@@ -1621,13 +1637,14 @@ def reduce_profile(args) -> int:
             meas = 1024.0 * (f * fs + w * ws)
             alg = report["labels"][label]["algorithmic_bytes_per_launch"]
             t_pass += meas * per_pass[label]
-            lines.append(f"| {label} | {f:.1f} | {w:.1f} | {meas / 1e6:.2f} | {alg / 1e6:.2f} | {meas / alg:.3f} |")
+            ratio = f"{meas / alg:.3f}" if alg else "-"
+            lines.append(f"| {label} | {f:.1f} | {w:.1f} | {meas / 1e6:.2f} | {alg / 1e6:.2f} | {ratio} |")
             report["labels"][label].update(fetch_kib=f, write_kib=w, traffic_bytes_per_launch=meas)
             for k in report["labels"][label]["kernels"]:
                 report["kernels"].setdefault(k, {"traffic_bytes_per_launch": meas, "algorithmic_bytes_per_launch": alg})
         report["pass_traffic_bytes"] = t_pass
         lines += ["", f"One pass moves {t_pass / 1e6:.1f} MB measured against {pass_bytes / 1e6:.1f} MB algorithmic "
-                  f"({t_pass / pass_bytes:.3f})."]
+                  f"({t_pass / max(1.0, pass_bytes):.3f})."]
     print("\n".join(lines))
     if args.reduce_json:
         with open(args.reduce_json, "w", encoding="utf-8") as fh:
@@ -1657,7 +1674,7 @@ def main(argv=None) -> int:
                    help="most distinct adapters per churn sub-batch (the cache has 32 slots)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                    help="only copy a BYTES-sized device buffer 5 times (calibrates HBM byte counters) and exit")
-    p.add_argument("--launch-profile", choices=["isolated", "decode", "prefill"],
+    p.add_argument("--launch-profile", choices=["isolated", "decode", "prefill", "operator"],
                    help="only issue this workload's LoRA launches in fixed passes (for rocprofv3) and write --manifest")
     p.add_argument("--manifest", default="gpurun_out/launch_manifest.json")
     p.add_argument("--profile-passes", type=int, default=20)

@@ -7,9 +7,9 @@
 // b*row_len + m, m < L (the slicing x[b, :seq_len] of layers.py:127).
 //
 // Steps: per-slot token counts (LDS atomics), one block-wide exclusive scan
-// of counts and of group counts, group emission, then the token indices of
-// each row are copied to the slot's segment (one thread per row for rows of
-// up to 16 tokens, one wave per row for longer ones).  Row order inside a
+// of counts and of group counts, group emission (one thread per group), then
+// the token indices of each row are copied to the slot's segment (one thread
+// per row for rows of up to 16 tokens, one wave per row for longer ones).  Row order inside a
 // segment follows LDS atomic order and is not fixed; no consumer depends on
 // it.
 //
@@ -30,6 +30,23 @@ constexpr int kPlanThreads = 1024;
 // rows are read once, with all of a thread's loads in flight together, and
 // serve both passes over the rows.  Rows beyond them are read per pass.
 constexpr int kPlanCached = 8;
+
+// Sum over the wave of v (0 <= v < 2^bits) and over the lanes below this
+// one, from one ballot per bit: independent instructions, where a shuffle
+// scan is a chain of LDS permutes.
+__device__ __forceinline__ void pl_wave_sum(int v, int bits, int& excl, int& total) {
+  const uint64_t below = __lanemask_lt();
+  excl = 0;
+  total = 0;
+  for (int b = 0; b < bits; ++b) {
+    const uint64_t m = __ballot((v >> b) & 1);
+    total += __popcll(m) << b;
+    excl += __popcll(m & below) << b;
+  }
+}
+
+// Bits that hold any row length up to row_len.
+__device__ __forceinline__ int pl_len_bits(int row_len) { return 32 - __clz(row_len | 1); }
 
 // Slot and clamped length of row b, or slot 0 for a row that gets no tokens.
 __device__ __forceinline__ void pl_plan_row(const int32_t* __restrict__ row_slot,
@@ -96,9 +113,22 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   }
   __syncthreads();
 
+  // A wave whose rows all use one slot (a batch sorted by adapter) adds
+  // them with one atomic: 64 lanes adding to one LDS counter serialize
+  // (4096 rows sorted by slot: 3.3 us, shuffled: 1.0 us).
+  const int len_bits = pl_len_bits(row_len);
 #pragma unroll
-  for (int q = 0; q < kPlanCached; ++q)
-    if (rs[q] > 0) atomicAdd(&cnt[rs[q]], rl[q]);
+  for (int q = 0; q < kPlanCached; ++q) {
+    if (__ballot(rs[q] > 0) == 0) continue;  // wave-uniform
+    const int k0 = __builtin_amdgcn_readfirstlane(rs[q]);
+    if (__all(rs[q] == k0)) {
+      int excl, total;
+      pl_wave_sum(rl[q], len_bits, excl, total);
+      if (lane == 0) atomicAdd(&cnt[k0], total);
+    } else if (rs[q] > 0) {
+      atomicAdd(&cnt[rs[q]], rl[q]);
+    }
+  }
   for (int b = tid + kPlanCached * kPlanThreads; b < rows; b += kPlanThreads) {
     int s, L;
     pl_plan_row(row_slot, seq_lens, b, row_len, S, s, L);
@@ -159,19 +189,27 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   }
   __syncthreads();
 
-  for (int s = tid; s < S; s += kPlanThreads) {
-    const int c = cnt[s];
-    const int ng = (c + group_tokens - 1) / group_tokens;
-    for (int q = 0; q < ng; ++q) {
-      const int64_t p = pl_plan_position(goff[s] + q, tg);
-      if (p < group_cap) {
-        pl_group gr;
-        gr.slot = s;
-        gr.start = off[s] + q * group_tokens;
-        gr.len = min(group_tokens, c - q * group_tokens);
-        gr.reserved = 0;
-        groups[p] = gr;
-      }
+  // One thread per group (a slot can have hundreds): the group's slot is
+  // the last s with goff[s] <= gi (a slot with no groups shares its goff
+  // with the next slot, so the last such s is the one that has groups).
+  for (int gi = tid; gi < tg; gi += kPlanThreads) {
+    int lo = 0, hi = S - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (goff[mid] <= gi)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int q = gi - goff[lo];
+    const int64_t p = pl_plan_position(gi, tg);
+    if (p < group_cap) {
+      pl_group gr;
+      gr.slot = lo;
+      gr.start = off[lo] + q * group_tokens;
+      gr.len = min(group_tokens, cnt[lo] - q * group_tokens);
+      gr.reserved = 0;
+      groups[p] = gr;
     }
   }
   // Every other position up to the capacity holds an empty group (slot 0,
@@ -195,8 +233,19 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     // short rows (decode, flattened tokens): one thread per row
 #pragma unroll
     for (int q = 0; q < kPlanCached; ++q) {
+      if (__ballot(rs[q] > 0) == 0) continue;  // wave-uniform
+      const int k0 = __builtin_amdgcn_readfirstlane(rs[q]);
+      int p = 0;
+      if (__all(rs[q] == k0)) {
+        int excl, total;
+        pl_wave_sum(rl[q], len_bits, excl, total);
+        int p0 = 0;
+        if (lane == 0) p0 = off[k0] + atomicAdd(&cnt[k0], total);
+        p = __builtin_amdgcn_readfirstlane(p0) + excl;
+      } else if (rs[q] > 0) {
+        p = off[rs[q]] + atomicAdd(&cnt[rs[q]], rl[q]);
+      }
       if (rs[q] > 0) {
-        const int p = off[rs[q]] + atomicAdd(&cnt[rs[q]], rl[q]);
         const int base = (tid + q * kPlanThreads) * row_len;
         for (int m = 0; m < rl[q]; ++m) tok[p + m] = base + m;
       }
