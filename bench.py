@@ -1652,6 +1652,25 @@ def reduce_profile(args) -> int:
     return 0
 
 
+def _release_between_workloads() -> None:
+    """Free what the previous workload left: its model and adapters, and their page-locked memory.
+
+    Page-locked host memory is limited per process; the decode workload's
+    adapter images (~10 GB) would otherwise stay locked in the recycle pool
+    next to the churn catalog's 56 GiB.
+    """
+    import gc
+
+    from polylora_amd.slot_image import release_locked_free
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    freed = release_locked_free()
+    if freed:
+        _log(f"released {freed / 2**30:.1f} GiB of page-locked memory")
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
@@ -1739,8 +1758,10 @@ def main(argv=None) -> int:
                 del pm
                 torch.cuda.empty_cache()
         if not args.no_churn:
+            _release_between_workloads()
             workloads["churn"] = run_churn(args)
         if not args.no_deberta:
+            _release_between_workloads()
             workloads["deberta"] = run_deberta(torch.device("cuda", 0),
                                                 cpu_budget_s=None if args.no_cpu_baseline else args.cpu_seconds)
         result["workloads"] = workloads

@@ -32,6 +32,8 @@
  *                          (sgmv.py:141-175 stack_num reads x once)
  *   pl_slot_upload      <- src/polylora/cache.py:119-150 _load_adapter_into_slot
  *                          (host->device copy of one adapter into a slot)
+ *   pl_host_copy_async  <- the same for an image in pageable memory: its
+ *                          copy into page-locked staging, in stream order
  *   pl_check_right_padded <- src/polylora/context.py:37-45 assert_right_padded
  */
 #ifndef POLYLORA_HIP_H
@@ -342,6 +344,14 @@ int pl_host_free(void* ptr);
  * row into the slot table, both asynchronously on `stream`. */
 int pl_slot_upload(void* arena_dst, const void* host_src, int64_t nbytes, void* table_dst,
                    const void* table_src, int64_t table_bytes, void* stream);
+
+/* Host -> host copy of nbytes run in `stream`'s order as a host function
+ * (split over up to 8 threads), for an adapter image held in pageable memory:
+ * its copy into a page-locked staging buffer that a pl_slot_upload queued
+ * behind it (on this stream, or on another after an event) reads.  The
+ * caller never waits; dst and src stay valid until the stream has passed
+ * the copy. */
+int pl_host_copy_async(void* dst, const void* src, int64_t nbytes, void* stream);
 
 /* flag[0] |= 1 if (mask[b][s] != 0) != (s < seq_lens[b]) for any element.
  * mask_dtype: 0 int64, 1 int32, 2 uint8/bool, 3 f32, 4 bf16, 5 f16. */

@@ -91,6 +91,7 @@ _SIGNATURES: dict[str, tuple] = {
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
         c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p,
     ),
+    "pl_host_copy_async": (c_void_p, c_void_p, c_int64, c_void_p),
     "pl_host_alloc": (c_int64,),
     "pl_host_free": (c_void_p,),
     "pl_slot_upload": (c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p),

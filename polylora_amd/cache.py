@@ -122,8 +122,14 @@ class GpuAdapterCache:
         self._slot_last_use: dict[int, torch.cuda.Event | None] = {}
         self._slot_ready: dict[int, torch.cuda.Event] = {}
         self._pending: list[tuple] = []
+        self._deferred_writes: dict | None = None  # slot -> image, while ensure_resident runs
+        self._use_seq = 0  # mark_used calls so far
+        self._slot_use_seq: dict[int, int] = {}  # slot -> _use_seq of its last recorded use
         # device pointers kept by the launch helpers belong to this arena and table
         self.__dict__.pop("_launch_args", None)
+        # the staging stream and its events belong to the device (the pinned buffers do not)
+        self.__dict__.pop("_staging_stream", None)
+        self.__dict__.pop("_staging_read", None)
 
     @property
     def A(self) -> Mapping:
@@ -171,11 +177,16 @@ class GpuAdapterCache:
             raise RuntimeError("Batch needs more adapters than GPU cache capacity")
         self._reap_pending()
         loaded: list[int] = []
-        for adapter_id in sorted(needed):
-            if adapter_id not in self.adapter_to_slot:
-                slot = self._allocate_or_evict(needed)
-                self._load_adapter_into_slot(adapter_id, slot)
-                loaded.append(slot)
+        self._deferred_writes = {}
+        try:
+            for adapter_id in sorted(needed):
+                if adapter_id not in self.adapter_to_slot:
+                    slot = self._allocate_or_evict(needed)
+                    self._load_adapter_into_slot(adapter_id, slot)
+                    loaded.append(slot)
+        finally:
+            writes, self._deferred_writes = self._deferred_writes, None
+            self._issue_writes(writes)
         for adapter_id in needed:  # set order, as cache.py:73-74
             self._touch(adapter_id)
         self._sync_cpu_eviction_exclusions()
@@ -204,9 +215,33 @@ class GpuAdapterCache:
             return
         event = torch.cuda.Event()
         event.record(torch.cuda.current_stream(self.device))
+        self._use_seq += 1
         for slot in slots:
             if slot > 0:
                 self._slot_last_use[slot] = event
+                self._slot_use_seq[slot] = self._use_seq
+
+    def _issue_writes(self, writes: dict) -> None:
+        """Enqueue one residency call's slot writes, slots whose readers finished longest ago first.
+
+        The slot numbers are settled (the reference's policy, cache.py:97-117);
+        only the order of the uploads on the side stream is chosen here.  An
+        upload waits for the last reader of its slot, and the side stream runs
+        its uploads in order, so one upload into a slot the running forward
+        still reads would hold back every upload queued after it, also those
+        into slots nothing reads any more.  Free slots go first, then slots by
+        the age of their last recorded use, then slots handed out and not yet
+        marked (their readers are the latest work on the compute stream).
+        """
+        def age(slot: int) -> float:
+            if slot not in self._slot_last_use:
+                return -1.0
+            if self._slot_last_use[slot] is None:
+                return float("inf")
+            return float(self._slot_use_seq.get(slot, 0))
+
+        for slot in sorted(writes, key=age):
+            self._write_slot_now(slot, writes[slot])
 
     def to(self, device: torch.device, dtype: torch.dtype) -> None:
         device = torch.device(device)
@@ -267,7 +302,18 @@ class GpuAdapterCache:
         return self.store.image(adapter, self.layout)
 
     def _write_slot(self, slot: int, packed: AdapterImage | None) -> None:
-        """Copy an adapter image (or nothing, for a cleared slot) and its table row into `slot`."""
+        """Copy an adapter image (or nothing, for a cleared slot) and its table row into `slot`.
+
+        Inside ``ensure_resident`` the write is only recorded (the last write
+        to a slot wins: an eviction's clear is followed by the new occupant's
+        load) and issued at the end of the call by ``_issue_writes``.
+        """
+        if self._deferred_writes is not None:
+            self._deferred_writes[slot] = packed
+            return
+        self._write_slot_now(slot, packed)
+
+    def _write_slot_now(self, slot: int, packed: AdapterImage | None) -> None:
         base = (slot - 1) * self.layout.slot_bytes
         if packed is None:
             row = np.zeros_like(self.table_host[slot])
@@ -297,56 +343,63 @@ class GpuAdapterCache:
         previous = self._slot_ready.get(slot)
         if previous is not None:
             side.wait_event(previous)
-        ring_slot = None
-        if nbytes and not packed.pinned:
-            image, ring_slot = self._stage(image, nbytes)
+        staging, ring_index = self._stage(image, nbytes) if nbytes and not packed.pinned else (None, None)
         row_pinned = torch.from_numpy(row).pin_memory()
         with torch.cuda.device(self.device):
             _native.check(
-                lib.pl_slot_upload(
-                    self.arena.data_ptr() + base,
-                    image.data_ptr() if nbytes else None,
-                    nbytes,
-                    self.table.data_ptr() + slot * self._row_bytes,
-                    row_pinned.data_ptr(),
-                    self._row_bytes,
-                    side.cuda_stream,
-                ),
+                lib.pl_slot_upload(self.arena.data_ptr() + base,
+                                   (staging if staging is not None else image).data_ptr() if nbytes else None, nbytes,
+                                   self.table.data_ptr() + slot * self._row_bytes, row_pinned.data_ptr(),
+                                   self._row_bytes, side.cuda_stream),
                 "pl_slot_upload",
             )
         ready = torch.cuda.Event()
         ready.record(side)
         self._slot_ready[slot] = ready
-        self._pending.append((ready, image, row_pinned))
-        if ring_slot is not None:
-            self._staging_busy[ring_slot] = ready  # the buffer is reused once this upload is done
+        if ring_index is not None:
+            self._staging_read[ring_index] = ready  # the buffer's next fill waits for this DMA
+        # the source image, the staging buffer and the row stay alive until the upload has run
+        self._pending.append((ready, image, row_pinned, staging))
 
     # Page-locked staging buffers for images held in pageable memory.  The
     # runtime's own copy from pageable memory blocks the calling thread until
     # the side stream reaches it, i.e. until the forward that last read the
     # slot has finished, so the host could no longer queue work ahead of the
-    # GPU.  Instead the host copies the image into the next staging buffer of
-    # a small ring (waiting only if that buffer's previous upload is still in
-    # flight) and the DMA engine copies from there asynchronously.
-    STAGING_BUFFERS = 4
+    # GPU.  Instead the copy of such an image into the next buffer of a ring
+    # runs as a host function on a staging stream (pl_host_copy_async, 8
+    # threads), and the upload stream's DMA from that buffer waits for it with
+    # an event.  The host copy waits only for the DMA that last read its
+    # buffer, not for the slot's readers, so it runs while the upload stream
+    # is busy with other DMAs or waiting for a forward; the calling thread
+    # never waits.
+    STAGING_BUFFERS = 8
 
-    def _stage(self, image: torch.Tensor, nbytes: int) -> tuple[torch.Tensor, int | None]:
-        """(page-locked copy of the image, its ring index), or (the image, None) without locked memory."""
+    def _stage(self, image: torch.Tensor, nbytes: int) -> tuple[torch.Tensor | None, int | None]:
+        """Queue the image's copy into the next staging buffer; (buffer, ring index), or (None, None)."""
         from .slot_image import host_bytes
 
-        ring = self.__dict__.setdefault("_staging", [None] * self.STAGING_BUFFERS)
-        busy = self.__dict__.setdefault("_staging_busy", [None] * self.STAGING_BUFFERS)
-        i = self.__dict__.get("_staging_next", 0) % self.STAGING_BUFFERS
-        if busy[i] is not None:
-            busy[i].synchronize()  # the upload that last used this buffer has read it
-            busy[i] = None
+        n = self.STAGING_BUFFERS
+        ring = self.__dict__.setdefault("_staging", [None] * n)
+        read = self.__dict__.setdefault("_staging_read", [None] * n)
+        i = self.__dict__.get("_staging_next", 0) % n
         buf = ring[i]
         if buf is None or buf.numel() < nbytes:
+            # a replaced buffer stays referenced by the pending uploads that use it
             buf, pinned = host_bytes(nbytes, pin=True)
             if not pinned:
-                return image, None  # no page-locked memory left: the runtime stages the copy itself
+                return None, None  # no page-locked memory left: the runtime stages the copy itself
             ring[i] = buf
-        buf[:nbytes].copy_(image[:nbytes])
+            read[i] = None
+        stage = self.__dict__.get("_staging_stream")
+        if stage is None:
+            stage = self._staging_stream = torch.cuda.Stream(self.device)
+        if read[i] is not None:
+            stage.wait_event(read[i])  # the DMA that last read this buffer is done
+        _native.check(_native.load().pl_host_copy_async(buf.data_ptr(), image.data_ptr(), nbytes, stage.cuda_stream),
+                      "pl_host_copy_async")
+        filled = torch.cuda.Event()
+        filled.record(stage)
+        self._side_stream.wait_event(filled)
         self._staging_next = i + 1
         return buf, i
 

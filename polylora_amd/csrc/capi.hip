@@ -1,6 +1,9 @@
 // C-ABI utilities: error reporting, version, pointer probe, slot upload.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
+
+#include <thread>
 
 #include "pl_common.h"
 
@@ -100,6 +103,66 @@ extern "C" int pl_slot_upload(void* arena_dst, const void* host_src, int64_t nby
       pl_set_error("pl_slot_upload: table copy failed: %s", hipGetErrorString(err));
       return PL_ERR_LAUNCH;
     }
+  }
+  return PL_OK;
+}
+
+namespace {
+
+// A host -> host copy run in a stream's order (hipLaunchHostFunc).  Large
+// copies are split over a few threads (one thread moves ~10 GB/s).
+struct pl_staged_copy {
+  void* dst;
+  const void* src;
+  int64_t n;
+};
+
+constexpr int kStageThreads = 8;
+constexpr int64_t kStageSplitMin = 8 << 20;
+
+void pl_staged_copy_run(void* arg) {
+  pl_staged_copy* c = static_cast<pl_staged_copy*>(arg);
+  char* dst = static_cast<char*>(c->dst);
+  const char* src = static_cast<const char*>(c->src);
+  const int64_t n = c->n;
+  if (n < kStageSplitMin) {
+    memcpy(dst, src, (size_t)n);
+  } else {
+    const int64_t part = ((n + kStageThreads - 1) / kStageThreads + 4095) & ~(int64_t)4095;
+    std::thread workers[kStageThreads - 1];
+    for (int i = 1; i < kStageThreads; ++i) {
+      const int64_t lo = i * part;
+      const int64_t len = lo >= n ? 0 : (n - lo < part ? n - lo : part);
+      workers[i - 1] = std::thread([=] {
+        if (len > 0) memcpy(dst + lo, src + lo, (size_t)len);
+      });
+    }
+    memcpy(dst, src, (size_t)(part < n ? part : n));
+    for (auto& w : workers) w.join();
+  }
+  delete c;
+}
+
+}  // namespace
+
+// Host -> host copy of nbytes from `src` to `dst` run in `stream`'s order as
+// a host function (hipLaunchHostFunc), split over a few threads: the copy of
+// a pageable adapter image into a page-locked staging buffer, which a DMA
+// queued behind it (on this stream, or on another after an event) then
+// reads.  The calling thread never waits; both buffers must stay valid until
+// the stream has passed the copy.
+extern "C" int pl_host_copy_async(void* dst, const void* src, int64_t nbytes, void* stream) {
+  if (nbytes <= 0 || !dst || !src) {
+    pl_set_error("pl_host_copy_async: bad arguments");
+    return PL_ERR_ARG;
+  }
+  pl_staged_copy* c = new pl_staged_copy{dst, src, nbytes};
+  const hipError_t err =
+      hipLaunchHostFunc(reinterpret_cast<hipStream_t>(stream), pl_staged_copy_run, c);
+  if (err != hipSuccess) {
+    delete c;
+    pl_set_error("pl_host_copy_async: %s", hipGetErrorString(err));
+    return PL_ERR_LAUNCH;
   }
   return PL_OK;
 }

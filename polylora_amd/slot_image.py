@@ -178,6 +178,26 @@ def host_bytes(nbytes: int, pin: bool | None = None) -> tuple[torch.Tensor, bool
 _locked_free: dict[int, list[int]] = {}
 
 
+def release_locked_free() -> int:
+    """Return the page-locked buffers no image uses to the system; the bytes released.
+
+    For a caller that is done with a set of adapters (e.g. between workloads)
+    and wants their page-locked memory back before pinning others: the
+    system limits page-locked memory per process.  ``hipHostFree`` may wait
+    for the device, so this is not for the middle of serving.
+    """
+    from . import _native
+
+    freed = 0
+    lib = _native.load()
+    for n, ptrs in list(_locked_free.items()):
+        while ptrs:
+            _native.check(lib.pl_host_free(ptrs.pop()), "pl_host_free")
+            freed += n
+    _locked_free.clear()
+    return freed
+
+
 class AdapterImage:
     """One adapter packed for a ``SlotLayout``.
 
