@@ -1262,13 +1262,13 @@ def run_prefill(args, pm) -> dict:
 def run_churn(args) -> dict:
     """Adapter churn: 1024 rank-16 adapters on all 7 targets, 32 GPU slots, batch 128, Zipf(0.9) ids.
 
-    Each step's rows are split, in row order, into sub-batches of at most
-    `--churn-sub-distinct` distinct adapters (at most 32, the slot count: the
-    reference raises beyond it, cache.py:65-66).  The default, 24, leaves a
-    running forward's slots alone for at least 8 of the next sub-batch's
-    loads, which then copy while it computes (measured on MI355X, 10 steps:
-    748 tok/s at 32, 788 at 28, 810-846 at 24, 752 at 20, 700 at 16, where
-    the doubled forward count outweighs the better overlap).  Every sub-batch is one
+    Each step's rows are split, when the step starts, into sub-batches of at
+    most `--churn-sub-distinct` distinct adapters (at most 32, the slot count:
+    the reference raises beyond it, cache.py:65-66): the adapters resident
+    then first, each sub-batch taking every row of its adapters (see
+    sub_batches).  The default, 24, leaves a running forward's slots alone
+    for at least 8 of the next sub-batch's loads, which then copy while it
+    computes.  Every sub-batch is one
     forward of one new token per row (empty KV cache), preceded by the loads
     its adapters need.  Loads go to the side stream and a slot is rewritten
     only after the forwards that read it; the host never waits for the GPU,
@@ -1304,14 +1304,22 @@ def run_churn(args) -> dict:
     limit = args.churn_sub_distinct
 
     def sub_batches(ids):
-        out, cur, seen = [], [], set()
-        for a in ids:
-            if a not in seen and len(seen) == limit:
-                out.append(cur)
-                cur, seen = [], set()
-            cur.append(a)
-            seen.add(a)
-        out.append(cur)
+        """A step's rows cut into sub-batches of at most `limit` distinct adapters.
+
+        The adapters already resident when the step starts come first, then
+        the step's others in order of first appearance; a sub-batch takes
+        every row of its adapters (rows keep their order).  Against cutting
+        the rows in order, this loads fewer adapters (an adapter is never met
+        again in a later sub-batch of the step) and runs fewer forwards
+        (ceil(distinct / limit) per step).
+        """
+        resident_now = pm.adapter_cache.adapter_to_slot
+        distinct = list(dict.fromkeys(ids))
+        order = [a for a in distinct if a in resident_now] + [a for a in distinct if a not in resident_now]
+        out = []
+        for i in range(0, len(order), limit):
+            chunk = set(order[i : i + limit])
+            out.append([a for a in ids if a in chunk])
         return out
 
     hot = catalog[:32]
@@ -1327,35 +1335,38 @@ def run_churn(args) -> dict:
     vocab = pm.base_model.config.vocab_size
     gen = torch.Generator(device=device).manual_seed(1005)
 
-    def run(batches):
+    def run(batches, split=False):
+        """Forward every sub-batch (or, with split, every step cut at its start); (s, tokens, loads, sub-batches)."""
         n_tok = 0
         loads0 = pm.adapter_cache.loads
+        done = []
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         progress = _Progress("churn")
         with torch.inference_mode():
-            for i, sub in enumerate(batches):
-                progress.tick(f"sub-batch {i + 1}/{len(batches)}")
-                x = torch.randint(0, vocab, (len(sub), 1), generator=gen, device=device)
-                # a (fresh) KV cache, as in decoding; without one, transformers
-                # checks position_ids for packed sequences, which waits for the
-                # GPU every forward
-                pm(input_ids=x, adapter_ids=sub, past_key_values=DynamicCache(config=pm.base_model.config),
-                   use_cache=True)
-                n_tok += len(sub)
+            for i, item in enumerate(batches):
+                progress.tick(f"{'step' if split else 'sub-batch'} {i + 1}/{len(batches)}")
+                for sub in sub_batches(item) if split else [item]:
+                    x = torch.randint(0, vocab, (len(sub), 1), generator=gen, device=device)
+                    # a (fresh) KV cache, as in decoding; without one, transformers
+                    # checks position_ids for packed sequences, which waits for the
+                    # GPU every forward
+                    pm(input_ids=x, adapter_ids=sub, past_key_values=DynamicCache(config=pm.base_model.config),
+                       use_cache=True)
+                    n_tok += len(sub)
+                    done.append(sub)
         torch.cuda.synchronize()
-        return time.perf_counter() - t0, n_tok, pm.adapter_cache.loads - loads0
+        return time.perf_counter() - t0, n_tok, pm.adapter_cache.loads - loads0, done
 
-    churn_batches = [sub for ids in steps[2:] for sub in sub_batches(ids)]
-    run([sub for ids in steps[:2] for sub in sub_batches(ids)])
-    churn_s, n_tok, loads = run(churn_batches)
+    _, _, _, warm_batches = run(steps[:2], split=True)
+    churn_s, n_tok, loads, churn_batches = run(steps[2:], split=True)
     # compute alone: the same sub-batches, every adapter resident
-    run([resident(sub) for ids in steps[:2] for sub in sub_batches(ids)])
-    comp_s, _, comp_loads = run([resident(sub) for sub in churn_batches])
+    run([resident(sub) for sub in warm_batches])
+    comp_s, _, comp_loads, _ = run([resident(sub) for sub in churn_batches])
     # the all-resident hot set: the same rows with ids folded onto 32 adapters, whole 128-row steps
     hot_steps = [[hot[int(i) % 32] for i in d] for d in draws]
     run(hot_steps[:2])
-    hot_s, hot_tok, hot_loads = run(hot_steps[2:])
+    hot_s, hot_tok, hot_loads, _ = run(hot_steps[2:])
     img = store.adapters[catalog[0]].image.data
     image_bytes = int(img.numel())
     pinned_images = sum(1 for a in catalog if store.adapters[a].image.pinned)
@@ -1377,7 +1388,8 @@ def run_churn(args) -> dict:
            "pinned_note": "page-locked memory is limited to about 65 GiB per process on this host; the "
                           "first (Zipf-hottest) images are pinned, the rest pageable and staged",
            "catalog_build_s": round(t_cat, 1),
-           "sub_batch_max_distinct": limit, "sub_batches": len(churn_batches), "slot_loads": loads, "loads_per_step": round(loads / args.churn_steps, 1),
+           "sub_batch_max_distinct": limit, "sub_batches": len(churn_batches),
+           "split": "per step: resident adapters first, all rows of an adapter in one sub-batch", "slot_loads": loads, "loads_per_step": round(loads / args.churn_steps, 1),
            "adapter_image_bytes": image_bytes, "h2d_bytes_per_step": round(loads * image_bytes / args.churn_steps),
            "pinned_h2d_gbs": round(h2d_gbs, 1),
            "tokens_per_s_churn": round(n_tok / churn_s, 1), "tokens_per_s_hot_set": round(hot_tok / hot_s, 1),
