@@ -412,7 +412,8 @@ def isolated_sgmv_workload(device, seed: int = 1002, T: int = 4096, K: int = 409
     seq_lens = torch.ones(T, dtype=torch.int32, device=device)
     x = torch.randn(T, K, generator=gen).to(dtype).to(device)
     base = torch.randn(T, N, generator=gen).to(dtype).to(device)
-    plan = sgmv.SgmvPlan(row_slot, seq_lens, 1, cache.num_slots, distinct_slots=slots)
+    # the op's plan: tokens of rank-0 slots need no work and take no group positions
+    plan = sgmv.SgmvPlan(row_slot, seq_lens, 1, cache.num_slots, distinct_slots=slots, active=cache.ranks["op"])
     return IsolatedSgmv(cache, adapters, ranks, x, base, base.clone(), row_slot, seq_lens, plan, seg)
 
 

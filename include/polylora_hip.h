@@ -146,6 +146,17 @@ int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows
                   int32_t row_len, int32_t num_slots, int32_t group_tokens, int32_t* tok,
                   pl_group* groups, int32_t* meta, int64_t group_cap, void* stream);
 
+/* pl_plan_build for one module's launches: rows whose slot s has
+ * slot_active[s * active_stride] <= 0 (e.g. the module's rank column of the
+ * slot table, which is 0 for slots whose adapter lacks the module) are left
+ * out like base rows, so they take no group positions and the groups of the
+ * slots with work are spread evenly over the XCDs.  Such a plan serves only
+ * launches for which those rows need no work. */
+int pl_plan_build_active(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,
+                         int32_t row_len, int32_t num_slots, const int32_t* slot_active,
+                         int64_t active_stride, int32_t group_tokens, int32_t* tok,
+                         pl_group* groups, int32_t* meta, int64_t group_cap, void* stream);
+
 /* Number of K splits pl_sgmv_shrink uses for a requested count: the K range
  * is cut into at most k_splits pieces of whole MFMA steps. */
 int32_t pl_shrink_planes(int32_t dtype, int32_t K, int32_t k_splits, int32_t group_tokens);

@@ -42,6 +42,8 @@ _SIGNATURES: dict[str, tuple] = {
     "pl_is_device_pointer": (c_void_p,),
     "pl_plan_group_capacity": (c_int32, c_int32, c_int32, c_int32),
     "pl_plan_build": (c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p),
+    "pl_plan_build_active": (c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int32, c_void_p,
+                             c_void_p, c_void_p, c_int64, c_void_p),
     "pl_shrink_planes": (c_int32, c_int32, c_int32, c_int32),
     "pl_shrink_workspace_bytes": (c_int32, c_int32, c_int32, c_int32, c_int64, c_int32),
     "pl_sgmv_shrink": (

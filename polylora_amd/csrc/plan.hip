@@ -48,14 +48,16 @@ __device__ __forceinline__ void pl_wave_sum(int v, int bits, int& excl, int& tot
 // Bits that hold any row length up to row_len.
 __device__ __forceinline__ int pl_len_bits(int row_len) { return 32 - __clz(row_len | 1); }
 
-// Slot and clamped length of row b, or slot 0 for a row that gets no tokens.
+// Slot and clamped length of row b, or slot 0 for a row that gets no tokens
+// (its slot is 0, out of range or inactive, or its length is 0).
 __device__ __forceinline__ void pl_plan_row(const int32_t* __restrict__ row_slot,
                                             const int32_t* __restrict__ seq_lens, int b,
-                                            int row_len, int S, int& s, int& L) {
+                                            int row_len, int S, const uint8_t* act, int& s,
+                                            int& L) {
   s = row_slot[b];
   L = seq_lens[b];
   L = L < 0 ? 0 : (L > row_len ? row_len : L);
-  if (s <= 0 || s >= S || L <= 0) s = 0;
+  if (s <= 0 || s >= S || L <= 0 || !act[s]) s = 0;
 }
 
 // First slot-major group index of XCD chunk x (x = 0..8) of n groups.
@@ -79,9 +81,11 @@ __device__ __forceinline__ int pl_plan_positions(int n) { return (n + 7) / 8 * 8
 
 __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     const int32_t* __restrict__ row_slot, const int32_t* __restrict__ seq_lens, int32_t rows,
-    int32_t row_len, int32_t num_slots, int32_t group_tokens, int32_t* __restrict__ tok,
-    pl_group* __restrict__ groups, int32_t* __restrict__ meta, int64_t group_cap) {
+    int32_t row_len, int32_t num_slots, const int32_t* __restrict__ active, int64_t active_stride,
+    int32_t group_tokens, int32_t* __restrict__ tok, pl_group* __restrict__ groups,
+    int32_t* __restrict__ meta, int64_t group_cap) {
   __shared__ int32_t cnt[PL_MAX_SLOTS];
+  __shared__ uint8_t act[PL_MAX_SLOTS];  // slot s has work (active[s * stride] > 0, or no vector)
   __shared__ int32_t off[PL_MAX_SLOTS];
   __shared__ int32_t goff[PL_MAX_SLOTS];
   __shared__ int32_t wsum[2][kPlanThreads / 64];
@@ -91,7 +95,10 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   const int wave = tid >> 6;
   const int S = num_slots;
 
-  for (int s = tid; s < S; s += kPlanThreads) cnt[s] = 0;
+  for (int s = tid; s < S; s += kPlanThreads) {
+    cnt[s] = 0;
+    act[s] = active == nullptr || active[(int64_t)s * active_stride] > 0;
+  }
   // this thread's cached rows tid + q * kPlanThreads: all loads first
   int rs[kPlanCached], rl[kPlanCached];
 #pragma unroll
@@ -104,14 +111,14 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
       rl[q] = seq_lens[b];
     }
   }
+  __syncthreads();  // act[] is complete
 #pragma unroll
   for (int q = 0; q < kPlanCached; ++q) {
     int L = rl[q];
     L = L < 0 ? 0 : (L > row_len ? row_len : L);
-    if (rs[q] <= 0 || rs[q] >= S || L <= 0) rs[q] = 0;
+    if (rs[q] <= 0 || rs[q] >= S || L <= 0 || !act[rs[q]]) rs[q] = 0;
     rl[q] = L;
   }
-  __syncthreads();
 
   // A wave whose rows all use one slot (a batch sorted by adapter) adds
   // them with one atomic: 64 lanes adding to one LDS counter serialize
@@ -131,7 +138,7 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   }
   for (int b = tid + kPlanCached * kPlanThreads; b < rows; b += kPlanThreads) {
     int s, L;
-    pl_plan_row(row_slot, seq_lens, b, row_len, S, s, L);
+    pl_plan_row(row_slot, seq_lens, b, row_len, S, act, s, L);
     if (s > 0) atomicAdd(&cnt[s], L);
   }
   __syncthreads();
@@ -252,7 +259,7 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     }
     for (int b = tid + kPlanCached * kPlanThreads; b < rows; b += kPlanThreads) {
       int s, L;
-      pl_plan_row(row_slot, seq_lens, b, row_len, S, s, L);
+      pl_plan_row(row_slot, seq_lens, b, row_len, S, act, s, L);
       if (s > 0) {
         const int p = off[s] + atomicAdd(&cnt[s], L);
         const int base = b * row_len;
@@ -263,7 +270,7 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     // long rows (prefill): one wave per row
     for (int b = wave; b < rows; b += kPlanThreads / 64) {
       int s, L;
-      pl_plan_row(row_slot, seq_lens, b, row_len, S, s, L);
+      pl_plan_row(row_slot, seq_lens, b, row_len, S, act, s, L);
       if (s > 0) {
         int p = 0;
         if (lane == 0) p = off[s] + atomicAdd(&cnt[s], L);
@@ -313,10 +320,12 @@ extern "C" int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t
   return (n + 7) / 8 * 8;
 }
 
-extern "C" int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,
-                             int32_t row_len, int32_t num_slots, int32_t group_tokens,
-                             int32_t* tok, pl_group* groups, int32_t* meta, int64_t group_cap,
-                             void* stream) {
+namespace {
+
+int plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows, int32_t row_len,
+               int32_t num_slots, const int32_t* active, int64_t active_stride,
+               int32_t group_tokens, int32_t* tok, pl_group* groups, int32_t* meta,
+               int64_t group_cap, void* stream) {
   if (!meta || (rows > 0 && (!row_slot || !seq_lens || !tok || !groups))) {
     pl_set_error("pl_plan_build: null pointer");
     return PL_ERR_ARG;
@@ -324,6 +333,10 @@ extern "C" int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, i
   if (rows < 0 || row_len < 0 || num_slots < 1) {
     pl_set_error("pl_plan_build: bad sizes rows=%d row_len=%d num_slots=%d", rows, row_len,
                  num_slots);
+    return PL_ERR_ARG;
+  }
+  if (active != nullptr && active_stride < 0) {
+    pl_set_error("pl_plan_build: negative stride of the active-slot vector");
     return PL_ERR_ARG;
   }
   if (group_tokens != 16 && group_tokens != 64) {
@@ -345,8 +358,31 @@ extern "C" int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, i
   }
   hipLaunchKernelGGL(pl_plan_kernel, dim3(1), dim3(kPlanThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), row_slot, seq_lens, rows, row_len,
-                     num_slots, group_tokens, tok, groups, meta, group_cap);
+                     num_slots, active, active_stride, group_tokens, tok, groups, meta, group_cap);
   return pl_launch_status("pl_plan_build");
+}
+
+}  // namespace
+
+extern "C" int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,
+                             int32_t row_len, int32_t num_slots, int32_t group_tokens,
+                             int32_t* tok, pl_group* groups, int32_t* meta, int64_t group_cap,
+                             void* stream) {
+  return plan_build(row_slot, seq_lens, rows, row_len, num_slots, nullptr, 0, group_tokens, tok,
+                    groups, meta, group_cap, stream);
+}
+
+extern "C" int pl_plan_build_active(const int32_t* row_slot, const int32_t* seq_lens,
+                                    int32_t rows, int32_t row_len, int32_t num_slots,
+                                    const int32_t* slot_active, int64_t active_stride,
+                                    int32_t group_tokens, int32_t* tok, pl_group* groups,
+                                    int32_t* meta, int64_t group_cap, void* stream) {
+  if (!slot_active) {
+    pl_set_error("pl_plan_build_active: null active-slot vector");
+    return PL_ERR_ARG;
+  }
+  return plan_build(row_slot, seq_lens, rows, row_len, num_slots, slot_active, active_stride,
+                    group_tokens, tok, groups, meta, group_cap, stream);
 }
 
 extern "C" int pl_check_right_padded(const void* mask, int32_t mask_dtype, int32_t B, int32_t S,

@@ -5,7 +5,10 @@ Two levels:
 * ``sgmv_lora_a_fwd`` / ``sgmv_lora_b_fwd`` keep the reference operator
   signatures and tensor layouts (sgmv.py:141-175, :278-328): weights
   ``[adapters, K, N]``, per-row ``seq_lens`` / ``weight_indices`` /
-  ``lora_ranks`` (/ ``scalings``).  They run the row-based HIP kernels.
+  ``lora_ranks`` (/ ``scalings``).  With a workspace from torch's caching
+  allocator they run the MFMA path (weights repacked on the device, device
+  plan, tiled shrink or expand); shapes that path does not take run the
+  row-based HIP kernels.
 * ``SgmvPlan`` + ``lora_apply`` are what ``MultiLoraLinear`` uses: one device
   plan per forward (no host sync) and the MFMA-tiled shrink/expand over the
   packed slot arena of ``GpuAdapterCache``.
@@ -70,17 +73,24 @@ class SgmvPlan:
     per-row lengths; every wrapped Linear of the forward with this shape reuses
     it.  Buffers: ``tok`` [rows*row_len] sorted token indices, ``groups``
     [group_cap, 4] (slot, start, len, 0), ``meta`` [4] (num_groups,
-    num_tokens, group_tokens, 0).  ``distinct_slots`` (the number of different
+    num_tokens, group_tokens, positions in use).  ``distinct_slots`` (the number of different
     adapters in the batch, known on the host) picks the group size; without
     it the plan uses 64-token groups.
     """
 
     __slots__ = ("rows", "row_len", "num_slots", "group_tokens", "tokens_cap", "group_cap", "tok", "groups", "meta",
-                 "row_slot", "seq_lens", "distinct_slots", "launch_args")
+                 "row_slot", "seq_lens", "distinct_slots", "launch_args", "active")
 
     def __init__(self, row_slot: torch.Tensor, seq_lens: torch.Tensor, row_len: int, num_slots: int,
-                 distinct_slots: int | None = None, group_tokens: int | None = None) -> None:
+                 distinct_slots: int | None = None, group_tokens: int | None = None,
+                 active: torch.Tensor | None = None) -> None:
+        """``active`` (optional, int32 [num_slots], any stride, e.g. ``cache.ranks[module]``): rows whose
+        slot reads <= 0 there are left out, so a plan that serves one module spends no group
+        positions (and no XCD share) on slots without weights for it."""
         _require_gpu(row_slot, "SgmvPlan")
+        if active is not None and (active.dtype != torch.int32 or active.dim() != 1 or active.numel() < num_slots
+                                   or active.device != row_slot.device):
+            raise ValueError("active must be an int32 vector of num_slots entries on the row map's device")
         lib = _native.load()
         row_slot = _i32(row_slot)
         seq_lens = _i32(seq_lens)
@@ -103,23 +113,15 @@ class SgmvPlan:
         # the plan's arguments of the fused entry points, in their order
         self.launch_args = (self.tok.data_ptr(), self.groups.data_ptr(), self.meta.data_ptr(), max(1, self.group_cap),
                             self.group_tokens)
-        self.row_slot, self.seq_lens = row_slot, seq_lens
-        _native.check(
-            lib.pl_plan_build(
-                row_slot.data_ptr(),
-                seq_lens.data_ptr(),
-                rows,
-                self.row_len,
-                self.num_slots,
-                self.group_tokens,
-                self.tok.data_ptr(),
-                self.groups.data_ptr(),
-                self.meta.data_ptr(),
-                max(1, self.group_cap),
-                _stream(dev),
-            ),
-            "pl_plan_build",
-        )
+        self.row_slot, self.seq_lens, self.active = row_slot, seq_lens, active
+        out = (self.tok.data_ptr(), self.groups.data_ptr(), self.meta.data_ptr(), max(1, self.group_cap), _stream(dev))
+        if active is None:
+            _native.check(lib.pl_plan_build(row_slot.data_ptr(), seq_lens.data_ptr(), rows, self.row_len,
+                                            self.num_slots, self.group_tokens, *out), "pl_plan_build")
+        else:
+            _native.check(lib.pl_plan_build_active(row_slot.data_ptr(), seq_lens.data_ptr(), rows, self.row_len,
+                                                   self.num_slots, active.data_ptr(), active.stride(0),
+                                                   self.group_tokens, *out), "pl_plan_build_active")
 
 
 class _Workspace:

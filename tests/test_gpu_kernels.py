@@ -56,6 +56,24 @@ def test_plan_matches_oracle(gpu, rows, row_len, num_slots, seed, group_tokens):
     )
 
 
+@pytest.mark.parametrize("rows,row_len,num_slots,group_tokens,seed",
+                         [(4096, 1, 17, 16, 20), (300, 3, 40, 16, 21), (32, 1024, 9, 64, 22), (9000, 1, 70, 16, 23)])
+def test_plan_active_mask_matches_oracle(gpu, rows, row_len, num_slots, group_tokens, seed):
+    """Rows of inactive slots are left out exactly as rows of slot 0; the mask is read through its stride."""
+    _announce(test="plan_active", rows=rows, row_len=row_len, num_slots=num_slots)
+    g = torch.Generator().manual_seed(seed)
+    row_slot = torch.randint(-1, num_slots + 1, (rows,), generator=g, dtype=torch.int32)
+    seq_lens = torch.randint(-1, row_len + 2, (rows,), generator=g, dtype=torch.int32)
+    table = torch.randint(-2, 3, (num_slots, 8), generator=g, dtype=torch.int32)  # column 3: the mask
+    active = table[:, 3]
+    plan = sgmv.SgmvPlan(row_slot.to(gpu), seq_lens.to(gpu), row_len, num_slots, group_tokens=group_tokens,
+                         active=table.to(gpu)[:, 3])
+    torch.cuda.synchronize()
+    masked = [s if 0 < s < num_slots and int(active[s]) > 0 else 0 for s in row_slot.tolist()]
+    check_plan(plan.tok.cpu().numpy(), plan.groups.cpu().numpy(), plan.meta.cpu().numpy(), masked, seq_lens.tolist(),
+               row_len, num_slots, group_tokens=group_tokens)
+
+
 CASES = [
     # dtype, rows, M, K, N, ranks, max_rank, k_splits, seed
     (torch.bfloat16, 8, 5, 64, 32, [2, 3, 4], 4, None, 10),
