@@ -81,8 +81,11 @@ struct pl_fused_lds {
   enum { kXRow = 256 / (int)sizeof(T) + kPad };  // per-wave x tile [token][one step's K]
 };
 
+constexpr int kFXLoads = 4;  // x loads per lane per shrink step (4 rows of 256 bytes each)
+
 template <int DT, int JT, bool XNT>
 __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_group& grp, int len,
+                                              const int (&xtok)[kFXLoads],
                                               const pl_slot_entry& e, int rank, int job, int slice,
                                               pl_f32x4 (*red)[4][64],
                                               typename pl_traits<DT>::T* tt,
@@ -95,7 +98,7 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   constexpr int E = pl_traits<DT>::E;
   constexpr int kInstr = 4 * E;              // K covered by one wave load
   constexpr int kStep = kFCC * kInstr;       // K covered by one shrink step
-  constexpr int kXLoads = 4;                 // x loads per lane per step (4 rows of 256 bytes each)
+  constexpr int kXLoads = kFXLoads;
   static_assert(kStep * (int)sizeof(T) == 256, "one shrink step spans 256 bytes of each x row");
   constexpr int kRStep = 4 * E;              // ranks per expand MFMA step
   constexpr int kRSteps = (16 * JT + kRStep - 1) / kRStep;
@@ -117,18 +120,17 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
   const T* __restrict__ A = reinterpret_cast<const T*>(a.arena + e.a_off);
   // x is loaded in whole 128-byte lines: load i of a step brings rows
-  // 4i .. 4i+3, lane l taking row 4i + l/16 and 16-byte piece l%16 of the
-  // step's 256 bytes; the wave's LDS tile then hands each lane its MFMA
-  // operand chunks (row li, pieces cc*4 + lg)
+  // 4i .. 4i+3, lane l taking row 4i + l/16 (token xtok[i]) and 16-byte
+  // piece l%16 of the step's 256 bytes; the wave's LDS tile then hands each
+  // lane its MFMA operand chunks (row li, pieces cc*4 + lg)
   const int xr = lane >> 4;
   const int xp = lane & 15;
   const T* xrow[kXLoads];
   bool xok[kXLoads];
 #pragma unroll
   for (int i = 0; i < kXLoads; ++i) {
-    const int r = xr + 4 * i;
-    xok[i] = r < len;
-    xrow[i] = x + (int64_t)a.tok[grp.start + min(r, len - 1)] * a.ldx + xp * E;
+    xok[i] = xr + 4 * i < len;
+    xrow[i] = x + (int64_t)xtok[i] * a.ldx + xp * E;
   }
   T* __restrict__ xw = xtile + wave * 16 * L::kXRow;
   // y rows of the expand, addressed now so that their token indices are not
@@ -143,7 +145,13 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   for (int i = 0; i < kYLoads; ++i) {
     const int r = yr0 + kYRows * i;
     yok[i] = r < len;
-    yrow[i] = y + (int64_t)a.tok[grp.start + min(r, len - 1)] * ldy + yq * E;
+    // the y rows are the x rows when a step's y row spans 16 lanes
+    int t;
+    if constexpr (kYRows == 4 && kYLoads == kFXLoads)
+      t = xtok[i];
+    else
+      t = a.tok[grp.start + min(r, len - 1)];
+    yrow[i] = y + (int64_t)t * ldy + yq * E;
   }
   const int k0 = wave * a.kw;
   const int k1 = min(K, k0 + a.kw);
@@ -196,6 +204,9 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
     // second step may lie past k1 and then loads only zeros)
     pl_u32x4 xa[kXLoads], aa[JT][kFCC], xb[kXLoads], ab[JT][kFCC];
     load_k(xa, aa, k0);
+    // the staged intermediate's ranks past the reduced tiles must read as
+    // zeros (the reduction below writes ranks 0 .. 16*JT-1)
+    for (int i = tid; i < 16 * L::kTRow; i += kFThreads) tt[i] = (T)0.f;
     int kb = k0;
     for (; kb + 2 * kStep < k1; kb += 2 * kStep) {
       load_k(xb, ab, kb + kStep);
@@ -348,21 +359,26 @@ __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args
   grp.start += rt * 16;
   const int len = min(grp.len - rt * 16, 16);
   if (g >= n_groups || len <= 0) return;
+  // token indices of this lane's x rows (rows lane/16 + 4i), fetched in the
+  // same round trip as the slot entry: the asm statement takes them before
+  // the rank test, so the compiler cannot sink their loads behind it
+  int xtok[kFXLoads];
+#pragma unroll
+  for (int i = 0; i < kFXLoads; ++i)
+    xtok[i] = a.tok[grp.start + min((int)(threadIdx.x & 63) / 16 + 4 * i, len - 1)];
   const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module[job]];
+  asm volatile("" ::"v"(xtok[0]), "v"(xtok[1]), "v"(xtok[2]), "v"(xtok[3]));
   const int rank = min(e.rank, kFRankMax);  // the host guarantees rank <= kFRankMax
   if (rank <= 0) return;
 
-  // the staged intermediate's unused ranks must read as zeros
-  for (int i = threadIdx.x; i < 16 * L::kTRow; i += kFThreads) tt[i] = (T)0.f;
-
   const int jt = (rank + 15) >> 4;
   if (JTMAX == 1 || jt == 1)
-    pl_fused_body<DT, 1, XNT>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, 1, XNT>(a, grp, len, xtok, e, rank, job, slice, red, tt, dbuf, xtile);
   else if (JTMAX == 2 || jt == 2)
-    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX, XNT>(a, grp, len, e, rank, job, slice, red, tt, dbuf,
-                                                  xtile);
+    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX, XNT>(a, grp, len, xtok, e, rank, job, slice, red, tt,
+                                                  dbuf, xtile);
   else
-    pl_fused_body<DT, JTMAX, XNT>(a, grp, len, e, rank, job, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, JTMAX, XNT>(a, grp, len, xtok, e, rank, job, slice, red, tt, dbuf, xtile);
 }
 
 template <int DT, bool XNT>
