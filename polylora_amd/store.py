@@ -23,6 +23,7 @@ Reference: store.py:14-26 (types), :36-148 (disk tier), :160-436 (store).
 from __future__ import annotations
 
 import json
+import os
 import shutil
 import warnings
 from collections import OrderedDict
@@ -379,10 +380,14 @@ class DiskAdapterCache:
                 yield aid, DiskAdapterEntry(aid, home, str(record.get("peft_adapter_name", "default")))
 
     def _write_manifest(self) -> None:
+        # written beside the manifest and renamed over it: a process that dies
+        # mid-write leaves the previous manifest, never a truncated one
         listing = [{"adapter_id": e.adapter_id, "path": e.path.name, "peft_adapter_name": e.peft_adapter_name}
                    for e in self.entries.values()]
-        (self.cache_dir / self._MANIFEST_NAME).write_text(
-            json.dumps({"adapters": listing}, indent=2, sort_keys=True), encoding="utf-8")
+        target = self.cache_dir / self._MANIFEST_NAME
+        staging = target.with_name(f".{target.name}.{os.getpid()}.tmp")
+        staging.write_text(json.dumps({"adapters": listing}, indent=2, sort_keys=True), encoding="utf-8")
+        os.replace(staging, target)
 
     def _evict_if_needed(self, exclude: set[str] | None = None) -> None:
         if self.max_adapters is None or len(self.entries) <= self.max_adapters:

@@ -162,6 +162,26 @@ def test_disk_cache_evicts_oldest_directory(tmp_path):
     # the manifest survives a restart
     again = DiskAdapterCache(tmp_path / "disk", 2)
     assert list(again.entries) == ["b", "c"]
+    assert not [p for p in (tmp_path / "disk").iterdir() if p.name.endswith(".tmp")]
+
+
+def test_disk_cache_manifest_write_is_all_or_nothing(tmp_path, monkeypatch):
+    """A write that dies before the rename leaves the previous manifest whole."""
+    g = torch.Generator().manual_seed(7)
+    disk = DiskAdapterCache(tmp_path / "disk", 3)
+    src = _peft.write_adapter_dir(tmp_path / "src_a", _peft.make_lora_weights(g, _shapes(), 2), 2, 4)
+    disk.add_adapter("a", src)
+    before = (tmp_path / "disk" / "manifest.json").read_text()
+
+    def die(*_a, **_k):
+        raise OSError("killed mid-write")
+
+    monkeypatch.setattr("polylora_amd.store.os.replace", die)
+    with pytest.raises(OSError, match="killed mid-write"):
+        disk.add_adapter("b", src)
+    monkeypatch.undo()
+    assert (tmp_path / "disk" / "manifest.json").read_text() == before
+    assert list(DiskAdapterCache(tmp_path / "disk", 3).entries) == ["a"]
 
 
 def test_cpu_store_never_evicts_gpu_resident():
