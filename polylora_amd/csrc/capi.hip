@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <new>
 #include <thread>
 
 #include "pl_common.h"
@@ -133,12 +134,18 @@ void pl_staged_copy_run(void* arg) {
     for (int i = 1; i < kStageThreads; ++i) {
       const int64_t lo = i * part;
       const int64_t len = lo >= n ? 0 : (n - lo < part ? n - lo : part);
-      workers[i - 1] = std::thread([=] {
-        if (len > 0) memcpy(dst + lo, src + lo, (size_t)len);
-      });
+      if (len <= 0) continue;
+      try {
+        workers[i - 1] = std::thread([=] { memcpy(dst + lo, src + lo, (size_t)len); });
+      } catch (...) {
+        // no thread to be had (this runs as the runtime's callback, where an
+        // exception must not escape): this piece is copied here instead
+        memcpy(dst + lo, src + lo, (size_t)len);
+      }
     }
     memcpy(dst, src, (size_t)(part < n ? part : n));
-    for (auto& w : workers) w.join();
+    for (auto& w : workers)
+      if (w.joinable()) w.join();
   }
   delete c;
 }
@@ -156,7 +163,11 @@ extern "C" int pl_host_copy_async(void* dst, const void* src, int64_t nbytes, vo
     pl_set_error("pl_host_copy_async: bad arguments");
     return PL_ERR_ARG;
   }
-  pl_staged_copy* c = new pl_staged_copy{dst, src, nbytes};
+  pl_staged_copy* c = new (std::nothrow) pl_staged_copy{dst, src, nbytes};
+  if (!c) {
+    pl_set_error("pl_host_copy_async: out of host memory");
+    return PL_ERR_LIMIT;
+  }
   const hipError_t err =
       hipLaunchHostFunc(reinterpret_cast<hipStream_t>(stream), pl_staged_copy_run, c);
   if (err != hipSuccess) {
