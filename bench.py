@@ -761,8 +761,9 @@ def run_isolated(args) -> dict:
             "operator_api_pair_ms": round(op_ms, 5),
             "operator_api_pair_gbs": round(nb["total"] / (op_ms * 1e-3) / 1e9, 1),
             "operator_api_note": "sgmv_lora_a_fwd + sgmv_lora_b_fwd with the reference's slot layout and a "
-                                 "model-dtype intermediate, host calls back to back (8 launches: repack, plan, "
-                                 "shrink, finish; repack, plan, gather, expand); GB/s counts the op's bytes",
+                                 "model-dtype intermediate, host calls back to back (6 launches: repack, plan, "
+                                 "fused shrink phase; repack, plan, fused expand phase); GB/s counts the op's "
+                                 "bytes",
         },
         "roofline": {
             "kernel": kernel,
@@ -1451,10 +1452,11 @@ def launch_profile(args) -> int:
         else:
             pair = time_operator_api(sets, 1, keep=True)["pair"]
             for i in range(len(sets)):
-                # one host call pair issues 8 dispatches; the first entry issues them all
-                steps = ["shrink: repack A", "shrink: plan", "shrink: MFMA", "shrink: finish", "expand: repack B",
-                         "expand: plan", "expand: gather", "expand: MFMA"]
-                part_bytes = {"shrink: MFMA": nb["shrink"], "expand: MFMA": nb["expand"]}
+                # one host call pair issues 6 dispatches (these shapes have long adapter segments, so
+                # each call runs a phase of the fused kernel); the first entry issues them all
+                steps = ["shrink: repack A", "shrink: plan", "shrink: fused phase", "expand: repack B",
+                         "expand: plan", "expand: fused phase"]
+                part_bytes = {"shrink: fused phase": nb["shrink"], "expand: fused phase": nb["expand"]}
                 for j, label in enumerate(steps):
                     fn = (lambda i=i: pair(i)) if j == 0 else (lambda: None)
                     seq.append((label, "operator", fn, part_bytes.get(label, 0)))
@@ -1510,6 +1512,7 @@ def launch_profile(args) -> int:
     manifest = {"workload": desc, "kind": kind, "warmup": args.profile_warmup, "passes": args.profile_passes,
                 "plan_builds": args.profile_plans, "event_ms_per_pass": t0.elapsed_time(t1) / args.profile_passes,
                 "sequence": [{"label": l, "part": part, "bytes": int(b)} for l, part, _, b in seq]}
+    os.makedirs(os.path.dirname(os.path.abspath(args.manifest)), exist_ok=True)
     with open(args.manifest, "w", encoding="utf-8") as fh:
         json.dump(manifest, fh, indent=1)
     _log(f"profile {kind}: {manifest['event_ms_per_pass']:.4f} ms per pass; manifest {args.manifest}")

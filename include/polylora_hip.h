@@ -291,7 +291,10 @@ int64_t pl_sgmv_ref_workspace_bytes(int32_t dtype, int32_t which, int32_t B, int
  * and a 16-byte aligned x, the call runs on the MFMA path: the weights of
  * every adapter are repacked into the slot arena's block layout inside the
  * workspace, a device plan groups the rows by adapter, and the tiled shrink
- * runs (4 launches, no host synchronisation).  Otherwise, or with a null
+ * and a finish kernel write out (4 launches, no host synchronisation); with
+ * long adapter segments (B*M >= 1024 and >= 64 rows per adapter, K <= 16384)
+ * one launch of the fused kernel's shrink phase writes out instead (3
+ * launches).  Otherwise, or with a null
  * workspace, one wave per token row computes it.  A workspace that is too
  * small or misaligned is an error (PL_ERR_ARG). */
 int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K,
@@ -308,7 +311,9 @@ int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32
  * (updated in place).  Rows with widx outside [0, num_adapters) are
  * skipped.  Workspace and paths as for pl_sgmv_lora_a_ref (which = 1; the
  * MFMA path needs a 16-byte aligned out): the intermediate x is gathered
- * into one fp32 plane and the tiled expand adds the scaled delta. */
+ * into one fp32 plane and the tiled expand adds the scaled delta, or, with
+ * long adapter segments as above, the fused kernel's expand phase reads x
+ * directly. */
 int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max,
                        const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
                        int32_t num_adapters, int32_t N,

@@ -167,6 +167,19 @@ int pl_launch_status(const char* what);
 static inline int pl_elem_size(int dtype) { return dtype == PL_F32 ? 4 : 2; }
 static inline int pl_chunk_elems(int dtype) { return dtype == PL_F32 ? 4 : 8; }
 
+// One phase of the fused kernel (sgmv_fused.hip) over a one-module slot
+// table (module 0), one column slice, for the reference-layout operator API:
+//   PL_FUSED_SHRINK: y[tok][c] = T(sum_k x[tok][k] * A[c][k]) for c below the
+//     slot's rank (the rest of the row is not written); N and ldy describe y.
+//   PL_FUSED_EXPAND: y[tok] += the expand of the intermediate x[tok][0..rank)
+//     (model dtype, row stride ldx; K is unused).
+// Operands are checked by the caller.
+enum { PL_FUSED_FULL = 0, PL_FUSED_SHRINK = 1, PL_FUSED_EXPAND = 2 };
+int pl_fused_phase(int mode, int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
+                   int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
+                   int32_t ldt, const int32_t* tok, const pl_group* groups, const int32_t* meta,
+                   int64_t group_cap, int32_t group_tokens, int32_t epilogue, void* stream);
+
 // MFMA path of the reference-layout operator API (sgmv_refop.hip).  Both
 // return PL_REFOP_DECLINED, having launched nothing, when there is no
 // workspace or the shape is not one the tiled kernels take; the caller then

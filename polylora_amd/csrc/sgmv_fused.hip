@@ -28,6 +28,8 @@
 // Ranks up to 64 (4 tiles of 16) are held in registers; the kernel is
 // instantiated for at most 1, 2 or 4 rank tiles and each group runs the
 // narrowest body that covers its slot's rank.
+#include <type_traits>
+
 #include "pl_common.h"
 
 namespace {
@@ -83,7 +85,7 @@ struct pl_fused_lds {
 
 constexpr int kFXLoads = 4;  // x loads per lane per shrink step (4 rows of 256 bytes each)
 
-template <int DT, int JT, bool XNT>
+template <int DT, int JT, bool XNT, int MODE = PL_FUSED_FULL>
 __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_group& grp, int len,
                                               const int (&xtok)[kFXLoads],
                                               const pl_slot_entry& e, int rank, int job, int slice,
@@ -198,7 +200,17 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
 #pragma unroll
       for (int cc = 0; cc < kFCC; ++cc) acc[jt] = pl_mfma_chunk<DT>(xm[cc], af[jt][cc], acc[jt]);
   };
-  {
+  if constexpr (MODE == PL_FUSED_EXPAND) {
+    // the intermediate comes from the caller: x[token][0 .. rank), model
+    // dtype, row stride ldx; zeros past the rank and past the tile's tokens
+    for (int i = tid; i < 16 * L::kTRow; i += kFThreads) {
+      const int r = i / L::kTRow;
+      const int j = i - r * L::kTRow;
+      T v = (T)0.f;
+      if (r < len && j < rank) v = x[(int64_t)a.tok[grp.start + r] * a.ldx + j];
+      tt[i] = v;
+    }
+  } else {
     // double-buffered K loop over pairs of steps; the last pair is peeled
     // so that no loads past k1 are left in flight when the shrink ends (its
     // second step may lie past k1 and then loads only zeros)
@@ -254,25 +266,40 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   // a ring of kFStages steps: the loads of the next kFStages-1 steps are in
   // flight while one is applied; steps past c1 load only zeros
   pl_u32x4 bring[kFStages][kRSteps][kCT], yring[kFStages][kYLoads];
+  if constexpr (MODE != PL_FUSED_SHRINK) {
 #pragma unroll
-  for (int st = 0; st < kFStages - 1; ++st) load_n(bring[st], yring[st], c0 + st * kCols);
-
-  // the four wave partials summed in a fixed order, rounded once to T;
-  // acc[jt][v] holds (token 4*lg+v, rank jt*16+li)
-#pragma unroll
-  for (int jt = 0; jt < JT; ++jt) red[wave][jt][lane] = acc[jt];
-  __syncthreads();
-  if (tid < JT * 64) {
-    const int jt = tid >> 6;
-    const int l = tid & 63;
-    pl_f32x4 s = red[0][jt][l];
-#pragma unroll
-    for (int w = 1; w < kFWaves; ++w) s += red[w][jt][l];
-    const int j = jt * 16 + (l & 15);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) tt[((l >> 4) * 4 + v) * L::kTRow + j] = (T)(j < rank ? s[v] : 0.f);
+    for (int st = 0; st < kFStages - 1; ++st) load_n(bring[st], yring[st], c0 + st * kCols);
   }
-  __syncthreads();
+
+  if constexpr (MODE == PL_FUSED_EXPAND) {
+    __syncthreads();  // the staged intermediate is complete
+  } else {
+    // the four wave partials summed in a fixed order, rounded once to T;
+    // acc[jt][v] holds (token 4*lg+v, rank jt*16+li)
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) red[wave][jt][lane] = acc[jt];
+    __syncthreads();
+    if (tid < JT * 64) {
+      const int jt = tid >> 6;
+      const int l = tid & 63;
+      pl_f32x4 s = red[0][jt][l];
+#pragma unroll
+      for (int w = 1; w < kFWaves; ++w) s += red[w][jt][l];
+      const int j = jt * 16 + (l & 15);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) tt[((l >> 4) * 4 + v) * L::kTRow + j] = (T)(j < rank ? s[v] : 0.f);
+    }
+    __syncthreads();
+  }
+  if constexpr (MODE == PL_FUSED_SHRINK) {
+    // the rounded intermediate to y[token][0 .. rank); nothing else is written
+    for (int i = tid; i < len * rank; i += kFThreads) {
+      const int r = i / rank;
+      const int j = i - r * rank;
+      y[(int64_t)a.tok[grp.start + r] * ldy + j] = tt[r * L::kTRow + j];
+    }
+    return;
+  }
 
   // ---- expand over this wave's columns
   const float scale = e.scale;
@@ -334,7 +361,7 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   }
 }
 
-template <int DT, int JTMAX, bool XNT>
+template <int DT, int JTMAX, bool XNT, int MODE = PL_FUSED_FULL>
 __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args a) {
   typedef typename pl_traits<DT>::T T;
   typedef pl_fused_lds<DT> L;
@@ -373,12 +400,13 @@ __global__ __launch_bounds__(kFThreads, 2) void pl_lora_fused_tile(pl_fused_args
 
   const int jt = (rank + 15) >> 4;
   if (JTMAX == 1 || jt == 1)
-    pl_fused_body<DT, 1, XNT>(a, grp, len, xtok, e, rank, job, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, 1, XNT, MODE>(a, grp, len, xtok, e, rank, job, slice, red, tt, dbuf, xtile);
   else if (JTMAX == 2 || jt == 2)
-    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX, XNT>(a, grp, len, xtok, e, rank, job, slice, red, tt,
-                                                  dbuf, xtile);
+    pl_fused_body<DT, 2 < JTMAX ? 2 : JTMAX, XNT, MODE>(a, grp, len, xtok, e, rank, job, slice, red,
+                                                        tt, dbuf, xtile);
   else
-    pl_fused_body<DT, JTMAX, XNT>(a, grp, len, xtok, e, rank, job, slice, red, tt, dbuf, xtile);
+    pl_fused_body<DT, JTMAX, XNT, MODE>(a, grp, len, xtok, e, rank, job, slice, red, tt, dbuf,
+                                        xtile);
 }
 
 template <int DT, bool XNT>
@@ -506,6 +534,73 @@ extern "C" int pl_lora_fused_stacked(int32_t dtype, const void* x, int64_t ldx, 
     case PL_F16: return launch_fused<PL_F16>(a, jtmax, s);
     default: return launch_fused<PL_F32>(a, jtmax, s);
   }
+}
+
+namespace {
+
+template <int DT, int MODE>
+void launch_phase(const pl_fused_args& a, int jtmax, hipStream_t stream) {
+  const dim3 grid((unsigned)pl_xcd_grid(a.group_cap, a.sub));
+  if (jtmax <= 1)
+    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 1, false, MODE>), grid, dim3(kFThreads), 0, stream, a);
+  else if (jtmax == 2)
+    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 2, false, MODE>), grid, dim3(kFThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((pl_lora_fused_tile<DT, 4, false, MODE>), grid, dim3(kFThreads), 0, stream, a);
+}
+
+}  // namespace
+
+int pl_fused_phase(int mode, int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
+                   int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
+                   int32_t ldt, const int32_t* tok, const pl_group* groups, const int32_t* meta,
+                   int64_t group_cap, int32_t group_tokens, int32_t epilogue, void* stream) {
+  if ((mode != PL_FUSED_SHRINK && mode != PL_FUSED_EXPAND) || ldt <= 0 || ldt > kFRankMax ||
+      group_cap < 1 || group_cap > ((int64_t)1 << 24) || K <= 0 || N <= 0 ||
+      (group_tokens != PL_GROUP_TOKENS_SHORT && group_tokens != PL_GROUP_TOKENS_LONG)) {
+    pl_set_error("pl_fused_phase: bad arguments");
+    return PL_ERR_ARG;
+  }
+  const int E = dtype == PL_F32 ? 4 : 8;
+  pl_fused_args a;
+  a.x = x;
+  a.ldx = ldx;
+  a.K = K;
+  const int64_t step = (int64_t)kFCC * 4 * E;
+  const int64_t kq = (K + kFWaves - 1) / kFWaves;
+  a.kw = (int32_t)((kq + step - 1) / step * step);
+  a.arena = reinterpret_cast<const char*>(arena);
+  a.table = table;
+  a.num_modules = 1;
+  a.tok = tok;
+  a.groups = groups;
+  a.meta = meta;
+  a.group_cap = (int32_t)group_cap;
+  a.sub = group_tokens / 16;
+  a.slices = 1;
+  a.epilogue = epilogue;
+  a.n_jobs = 1;
+  a.module[0] = 0;
+  a.y[0] = y;
+  a.ldy[0] = ldy;
+  a.N[0] = N;
+  const int64_t per_wave = ((int64_t)N + kFWaves - 1) / kFWaves;
+  a.nw[0] = (int32_t)((per_wave + kFColsMax - 1) / kFColsMax * kFColsMax);
+  const int jtmax = (ldt + 15) / 16;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  auto go = [&](auto dt) {
+    constexpr int D = decltype(dt)::value;
+    if (mode == PL_FUSED_SHRINK)
+      launch_phase<D, PL_FUSED_SHRINK>(a, jtmax, s);
+    else
+      launch_phase<D, PL_FUSED_EXPAND>(a, jtmax, s);
+  };
+  switch (dtype) {
+    case PL_BF16: go(std::integral_constant<int, PL_BF16>()); break;
+    case PL_F16: go(std::integral_constant<int, PL_F16>()); break;
+    default: go(std::integral_constant<int, PL_F32>()); break;
+  }
+  return pl_launch_status(mode == PL_FUSED_SHRINK ? "pl_fused_phase(shrink)" : "pl_fused_phase(expand)");
 }
 
 extern "C" int pl_lora_fused(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,

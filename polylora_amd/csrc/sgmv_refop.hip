@@ -19,6 +19,11 @@
 //      expand: pl_refop_gather loads the model-dtype intermediate into one
 //      fp32 plane (zero past each row's rank), then pl_sgmv_expand adds
 //      T(scale * sum) into the output in the reference's rounding order.
+//      With long adapter segments (at least 1024 rows and 64 per adapter)
+//      step 3 is one launch of a phase of the fused kernel instead
+//      (pl_fused_phase): the shrink reduces each 16-token tile in LDS and
+//      writes T(sum) straight into out, the expand stages the caller's
+//      intermediate in LDS and adds the deltas into out.
 //
 // The repack reads every adapter's weights once per call (the reference's
 // weight tensor is the caller's, and may change between calls); for the
@@ -238,6 +243,16 @@ void refop_dispatch(int32_t dtype, F&& launch) {
 
 bool aligned256(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 255) == 0; }
 
+// Long adapter segments (the fused kernel's regime, as sgmv.fused_ok picks it
+// on the forward path): one workgroup per 16-token tile does the whole
+// reduction of a call and hands the result straight to the caller's tensor,
+// with no split planes and no finish or gather launch.  Few tokens per
+// adapter keep the split kernels, which spread each adapter's weights over
+// many more workgroups.
+bool refop_fused(const refop_layout& L, int32_t num_adapters, int32_t K) {
+  return L.tokens >= 1024 && L.tokens >= (int64_t)64 * num_adapters && K <= 16384;
+}
+
 int refop_prep(int32_t dtype, const refop_layout& L, char* ws, const void* w, int64_t s0,
                int64_t s1, int64_t s2, int32_t num_adapters, int which, int32_t width,
                int32_t rank_cap, int32_t stack_num, const int32_t* ranks, const float* scalings,
@@ -311,6 +326,10 @@ int pl_refop_shrink(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t 
   st = pl_plan_build(row_slot, seq_lens, B, M, num_adapters + 1, L.group_tokens, tok, groups, meta,
                      L.group_cap, stream);
   if (st) return st;
+  if (refop_fused(L, num_adapters, K))
+    return pl_fused_phase(PL_FUSED_SHRINK, dtype, x, K, K, out, n_max, n_max, ws + L.arena, table,
+                          L.ldt, tok, groups, meta, L.group_cap, L.group_tokens, PL_EPI_FALLBACK,
+                          stream);
   st = pl_sgmv_shrink(dtype, x, K, K, ws + L.arena, table, 1, 0, tok, groups, meta, L.group_cap,
                       L.group_tokens, planes, L.total - L.plane, L.ldt, L.tokens, L.k_splits,
                       stream);
@@ -352,6 +371,10 @@ int pl_refop_expand(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t 
   st = pl_plan_build(row_slot, seq_lens, B, M, num_adapters + 1, L.group_tokens, tok, groups, meta,
                      L.group_cap, stream);
   if (st) return st;
+  if (refop_fused(L, num_adapters, k_max))
+    return pl_fused_phase(PL_FUSED_EXPAND, dtype, x, k_max, k_max, out, N, N, ws + L.arena, table,
+                          L.ldt, tok, groups, meta, L.group_cap, L.group_tokens, PL_EPI_TRITON,
+                          stream);
   refop_dispatch(dtype, [&](auto dt) {
     hipLaunchKernelGGL(pl_refop_gather<decltype(dt)::value>, dim3((unsigned)L.group_cap),
                        dim3(kThreads), 0, s, x, k_max, L.ldt, groups, tok, table, plane);

@@ -1,8 +1,9 @@
 """The reference-layout operator API (sgmv_lora_a_fwd / sgmv_lora_b_fwd, sgmv.py:141-175, :278-328).
 
 Both entry points have an MFMA path (weights repacked into the slot arena's
-block layout in a workspace, a device plan, the tiled shrink or expand) and
-the row kernels for shapes that path does not take.  Each is checked against
+block layout in a workspace, a device plan, then the tiled shrink or expand,
+or for long adapter segments a phase of the fused kernel) and the row
+kernels for shapes that path does not take.  Each is checked against
 the oracle's restatement of the operators (oracle.lora.sgmv_shrink_reference
 / sgmv_expand_reference), and the two paths against each other.
 """
@@ -74,7 +75,10 @@ def _case(g, Bt, M, K, N, S, R, stack_num, dtype, gpu):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("stack_num", [1, 2])
-@pytest.mark.parametrize("Bt,M,K,N,S,R", [(6, 10, 96, 80, 4, 8), (9, 70, 256, 136, 5, 32), (40, 1, 512, 64, 7, 16)])
+# the first three take the split kernels (few tokens per adapter); the last two have long adapter
+# segments and take the fused kernel's shrink and expand phases (16- and 64-token groups)
+@pytest.mark.parametrize("Bt,M,K,N,S,R", [(6, 10, 96, 80, 4, 8), (9, 70, 256, 136, 5, 32), (40, 1, 512, 64, 7, 16),
+                                          (24, 96, 256, 136, 5, 32), (40, 256, 128, 64, 4, 16)])
 def test_mfma_and_row_paths_match_the_oracle(gpu, dtype, stack_num, Bt, M, K, N, S, R):
     _announce(test="refop_paths", dtype=dtype, stack_num=stack_num, shape=(Bt, M, K, N, S, R))
     g = torch.Generator().manual_seed(Bt * 7 + stack_num)
