@@ -48,6 +48,21 @@ __device__ __forceinline__ void pl_wave_sum(int v, int bits, int& excl, int& tot
 // Bits that hold any row length up to row_len.
 __device__ __forceinline__ int pl_len_bits(int row_len) { return 32 - __clz(row_len | 1); }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves (register
+// to register, no LDS): a Hillis-Steele scan inside each row of 16 lanes
+// (row_shr 1, 2, 4, 8; lanes whose source lies before the row add 0), then
+// lane 15 of rows 0 and 2 into rows 1 and 3 (row_bcast:15) and lane 31
+// into rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ int pl_wave_scan_incl(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2 and 3
+  return v;
+}
+
 // Slot and clamped length of row b, or slot 0 for a row that gets no tokens
 // (its slot is 0, out of range or inactive, or its length is 0).
 __device__ __forceinline__ void pl_plan_row(const int32_t* __restrict__ row_slot,
@@ -84,10 +99,12 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     int32_t row_len, int32_t num_slots, const int32_t* __restrict__ active, int64_t active_stride,
     int32_t group_tokens, int32_t* __restrict__ tok, pl_group* __restrict__ groups,
     int32_t* __restrict__ meta, int64_t group_cap) {
-  __shared__ int32_t cnt[PL_MAX_SLOTS];
+  // 16-byte aligned: each thread reads its 4 counters and writes its 4
+  // offsets with one LDS access (a stride-4 word access conflicts 8 ways)
+  __shared__ __attribute__((aligned(16))) int32_t cnt[PL_MAX_SLOTS];
   __shared__ uint8_t act[PL_MAX_SLOTS];  // slot s has work (active[s * stride] > 0, or no vector)
-  __shared__ int32_t off[PL_MAX_SLOTS];
-  __shared__ int32_t goff[PL_MAX_SLOTS];
+  __shared__ __attribute__((aligned(16))) int32_t off[PL_MAX_SLOTS];
+  __shared__ __attribute__((aligned(16))) int32_t goff[PL_MAX_SLOTS];
   __shared__ int32_t wsum[2][kPlanThreads / 64];
 
   const int tid = threadIdx.x;
@@ -143,27 +160,23 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   }
   __syncthreads();
 
-  // Each thread owns 4 consecutive slots (PL_MAX_SLOTS == 4 * kPlanThreads).
+  // Each thread owns 4 consecutive slots (PL_MAX_SLOTS == 4 * kPlanThreads);
+  // counters past the slot count were never cleared and are not used.
+  static_assert(PL_MAX_SLOTS == 4 * kPlanThreads, "four slots per plan thread");
+  const int4 c4 = reinterpret_cast<const int4*>(cnt)[tid];
+  const int cq[4] = {c4.x, c4.y, c4.z, c4.w};
   int loc_t[4], loc_g[4];
   int st = 0, sg = 0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const int s = tid * 4 + q;
-    const int c = s < S ? cnt[s] : 0;
+    const int c = tid * 4 + q < S ? cq[q] : 0;
     loc_t[q] = st;
     loc_g[q] = sg;
     st += c;
     sg += (c + group_tokens - 1) / group_tokens;
   }
-  int it = st, ig = sg;
-  for (int d = 1; d < 64; d <<= 1) {
-    const int t1 = __shfl_up(it, d);
-    const int g1 = __shfl_up(ig, d);
-    if (lane >= d) {
-      it += t1;
-      ig += g1;
-    }
-  }
+  const int it = pl_wave_scan_incl(st);
+  const int ig = pl_wave_scan_incl(sg);
   if (lane == 63) {
     wsum[0][wave] = it;
     wsum[1][wave] = ig;
@@ -180,14 +193,11 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   }
   const int ex_t = wt + it - st;
   const int ex_g = wg + ig - sg;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int s = tid * 4 + q;
-    if (s < S) {
-      off[s] = ex_t + loc_t[q];
-      goff[s] = ex_g + loc_g[q];
-    }
-  }
+  // entries past the slot count are written too (never read)
+  reinterpret_cast<int4*>(off)[tid] =
+      make_int4(ex_t + loc_t[0], ex_t + loc_t[1], ex_t + loc_t[2], ex_t + loc_t[3]);
+  reinterpret_cast<int4*>(goff)[tid] =
+      make_int4(ex_g + loc_g[0], ex_g + loc_g[1], ex_g + loc_g[2], ex_g + loc_g[3]);
   if (tid == 0) {
     meta[0] = tg;
     meta[1] = tt;
@@ -235,6 +245,9 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
   __syncthreads();
   for (int s = tid; s < S; s += kPlanThreads) cnt[s] = 0;  // reused as fill counters
   __syncthreads();
+  // the token list holds rows * row_len entries; a position outside it is
+  // never written (the offsets above keep every token inside it)
+  const int64_t cap = (int64_t)rows * row_len;
 
   if (row_len <= 16) {
     // short rows (decode, flattened tokens): one thread per row
@@ -254,7 +267,8 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
       }
       if (rs[q] > 0) {
         const int base = (tid + q * kPlanThreads) * row_len;
-        for (int m = 0; m < rl[q]; ++m) tok[p + m] = base + m;
+        for (int m = 0; m < rl[q]; ++m)
+          if (p + m < cap) tok[p + m] = base + m;
       }
     }
     for (int b = tid + kPlanCached * kPlanThreads; b < rows; b += kPlanThreads) {
@@ -263,7 +277,8 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
       if (s > 0) {
         const int p = off[s] + atomicAdd(&cnt[s], L);
         const int base = b * row_len;
-        for (int m = 0; m < L; ++m) tok[p + m] = base + m;
+        for (int m = 0; m < L; ++m)
+          if (p + m < cap) tok[p + m] = base + m;
       }
     }
   } else {
@@ -276,7 +291,8 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
         if (lane == 0) p = off[s] + atomicAdd(&cnt[s], L);
         p = __shfl(p, 0);
         const int base = b * row_len;
-        for (int m = lane; m < L; m += 64) tok[p + m] = base + m;
+        for (int m = lane; m < L; m += 64)
+          if (p + m < cap) tok[p + m] = base + m;
       }
     }
   }
