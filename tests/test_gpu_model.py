@@ -444,6 +444,60 @@ def test_llama_prefill_right_padded_bf16(gpu):
     assert torch.equal(again, got)
 
 
+def test_llama_fp16_prefill_then_decode(gpu):
+    """An fp16 model: right-padded prefill (fused kernel, stacked siblings on the second forward), then a
+    decode step on a KV cache (split kernels); every wrapped Linear against the oracle."""
+    _announce(test="llama_fp16")
+    from transformers import DynamicCache
+
+    dt = torch.float16
+    base, cfg = _tiny_llama(15, dt, gpu)
+    pm = PolyLoraModel(copy.deepcopy(base), PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=4, max_rank=32)).eval()
+    g = torch.Generator().manual_seed(15)
+    ads = {f"h{i}": (_peft.make_lora_weights(g, _shapes(pm), r, std=0.05), 2.0 * r) for i, r in enumerate([8, 16, 32, 24])}
+    for aid, (w, alpha) in ads.items():
+        pm.adapter_store.add_adapter_from_peft_state_dict(aid, _peft.state_dict(w), pm.target_module_names, alpha)
+    B, S = 8, 160
+    lens = torch.randint(80, S + 1, (B,), generator=g)
+    mask = (torch.arange(S)[None, :] < lens[:, None]).long().to(gpu)
+    ids = torch.randint(0, 211, (B, S), generator=g).to(gpu)
+    adapter_ids = [f"h{i // 2}" for i in range(B)]
+    om, bank = _oracle(base, LLAMA_TARGETS, ads, 32, dt, gpu)
+    for _ in range(2):  # the second forward takes the stacked sibling launches
+        with torch.inference_mode(), _per_layer_check(pm, ads, dt) as checked:
+            got = pm(input_ids=ids, attention_mask=mask, adapter_ids=adapter_ids).last_hidden_state
+        assert checked.count == len(pm.target_module_names)
+    with torch.inference_mode():
+        want = oracle_model.run(om, bank, adapter_ids, input_ids=ids, attention_mask=mask).last_hidden_state
+    valid = mask.bool()
+    diff = (got[valid].float() - want[valid].float()).norm() / want[valid].float().norm()
+    assert float(diff) < 5e-3, float(diff)
+    # decode: one token per row on a 64-position cache, a base row among them
+    past = 64
+    kv = [(torch.randn(B, 2, past, 32, generator=g).to(gpu, dt), torch.randn(B, 2, past, 32, generator=g).to(gpu, dt))
+          for _ in range(2)]
+
+    def cache():
+        c = DynamicCache(config=cfg)
+        for layer, (k, v) in enumerate(kv):
+            c.update(k.clone(), v.clone(), layer)
+        return c
+
+    step_ids = ["__base__"] + adapter_ids[1:]
+    tok = torch.randint(0, 211, (B, 1), generator=g).to(gpu)
+    dmask = torch.ones(B, past + 1, dtype=torch.long, device=gpu)
+    with torch.inference_mode(), _per_layer_check(pm, ads, dt) as checked:
+        got = pm(input_ids=tok, attention_mask=dmask, past_key_values=cache(), use_cache=True,
+                 adapter_ids=step_ids).last_hidden_state
+    assert checked.count == len(pm.target_module_names)
+    with torch.inference_mode():
+        want = oracle_model.run(om, bank, step_ids, input_ids=tok, attention_mask=dmask, past_key_values=cache(),
+                                use_cache=True).last_hidden_state
+        plain = base(input_ids=tok, attention_mask=dmask, past_key_values=cache(), use_cache=True).last_hidden_state
+    torch.testing.assert_close(got.float(), want.float(), **BF16)
+    assert torch.equal(got[0], plain[0])
+
+
 def test_adapter_churn_matches_fallback(gpu):
     """Many adapters through few slots: uploads on the side stream, every step against the fallback."""
     _announce(test="churn")
