@@ -25,7 +25,7 @@ Also reported in the same JSON line (``workloads``):
   tokens/s against an all-resident hot set, H2D bytes, copy/compute overlap.
 * ``deberta`` DeBERTa-v3-base shape, fp32, 5 adapters, B=8, S=128 (tokens/s).
 
-``--gpus`` above 1 exits: this build measures one GPU.
+``--gpus`` above 1 exits: the library runs and measures on one GPU.
 """
 
 from __future__ import annotations
@@ -1720,7 +1720,7 @@ def main(argv=None) -> int:
                    help="only copy a BYTES-sized device buffer 5 times (calibrates HBM byte counters) and exit")
     p.add_argument("--launch-profile", choices=["isolated", "decode", "prefill", "operator"],
                    help="only issue this workload's LoRA launches in fixed passes (for rocprofv3) and write --manifest")
-    p.add_argument("--manifest", default="gpurun_out/launch_manifest.json")
+    p.add_argument("--manifest", default="launch_profile/manifest.json")
     p.add_argument("--profile-passes", type=int, default=20)
     p.add_argument("--profile-warmup", type=int, default=3)
     p.add_argument("--profile-plans", type=int, default=20, help="device plan builds before the passes")
@@ -1737,7 +1737,7 @@ def main(argv=None) -> int:
     if args.reduce_profile:
         return reduce_profile(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path; run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: the library has no multi-GPU path; run with --gpus 1", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)

@@ -1,8 +1,8 @@
 """Oracle: CPU restatement of Knowledgator/PolyLoRA's LoRA path.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
-the ``cpu_baseline`` leg of ``bench.py`` import this package, and only as the
-checker (or, in ``bench.py``, as the timed CPU baseline).  The product package
+the ``cpu_baseline`` leg of ``bench.py`` import this package, and only for
+expected values (or, in ``bench.py``, as the timed CPU baseline).  The product package
 ``polylora_amd`` never imports, links or runs anything from here.
 
 Modules (each function cites the reference file:line it restates):
@@ -21,5 +21,6 @@ inputs, the textbook LoRA closed form y = W x + b + (alpha / r) B A x,
 invariants (rank-0 and padding rows bitwise base, weights beyond the rank
 never read, linearity in B), planted mistakes that the checks must catch,
 and the assertions of the reference's own tests.  The reference ships no
-golden vectors; ``tests/golden/`` holds vectors this build wrote.
+golden vectors, and every function is pinned by the checks above, so no
+vectors are recorded from the reference.
 """

@@ -1,7 +1,7 @@
 """CPU restatement of the reference LoRA math and operator semantics (test infrastructure).
 
 All functions are device-agnostic torch; tests run them on CPU tensors (or,
-for same-process comparisons, on the GPU tensors of the run) as the checker.
+for same-process comparisons, on the GPU tensors of the run) as the expected values.
 """
 
 from __future__ import annotations

@@ -4,7 +4,7 @@ Token semantics follow the fallback's slicing x[b, :seq_len] (layers.py:127)
 and the clamps of layers.py:91-108: row b contributes tokens b*M + m for
 m < min(max(seq_len_b, 0), M), unless its slot is the base slot 0 (rank 0 in
 every module, cache.py:32-34).  Grouping into runs of at most 64 tokens per
-slot is this build's own schedule (the reference tiles per row,
+slot is this library's own schedule (the reference tiles per row,
 sgmv.py:29-61), so only its invariants are checked, not an order, except
 the placement of the group records: the slot-major group list is cut into 8
 contiguous chunks, one per XCD, and the i-th group of chunk x is stored at

@@ -1,4 +1,4 @@
-"""Pins the oracle (CPU restatement of the reference) before it is trusted as the checker.
+"""Pins the oracle (CPU restatement of the reference) before the GPU tests compare against it.
 
 Each oracle function is checked against something that does not share its
 code: fp64 brute-force loops on tiny inputs, the textbook LoRA closed form
