@@ -1461,10 +1461,11 @@ def launch_profile(args) -> int:
         else:
             pair = time_operator_api(sets, 1, keep=True)["pair"]
             for i in range(len(sets)):
-                # one host call pair issues 6 dispatches (these shapes have long adapter segments, so
-                # each call runs a phase of the fused kernel); the first entry issues them all
-                steps = ["shrink: repack A", "shrink: plan", "shrink: fused phase", "expand: repack B",
-                         "expand: plan", "expand: fused phase"]
+                # one host call pair issues 4 dispatches (the repack and the plan share a launch;
+                # these shapes have long adapter segments, so each call runs a phase of the fused
+                # kernel); the first entry issues them all
+                steps = ["shrink: repack A + plan", "shrink: fused phase", "expand: repack B + plan",
+                         "expand: fused phase"]
                 part_bytes = {"shrink: fused phase": nb["shrink"], "expand: fused phase": nb["expand"]}
                 for j, label in enumerate(steps):
                     fn = (lambda i=i: pair(i)) if j == 0 else (lambda: None)

@@ -288,13 +288,13 @@ int64_t pl_sgmv_ref_workspace_bytes(int32_t dtype, int32_t which, int32_t B, int
  * contiguous.  Rows with widx outside [0, num_adapters) are skipped.
  * With a 256-byte aligned workspace of at least
  * pl_sgmv_ref_workspace_bytes(dtype, 0, ...) bytes (when that is nonzero)
- * and a 16-byte aligned x, the call runs on the MFMA path: the weights of
- * every adapter are repacked into the slot arena's block layout inside the
- * workspace, a device plan groups the rows by adapter, and the tiled shrink
- * and a finish kernel write out (4 launches, no host synchronisation); with
- * long adapter segments (B*M >= 1024 and >= 64 rows per adapter, K <= 16384)
- * one launch of the fused kernel's shrink phase writes out instead (3
- * launches).  Otherwise, or with a null
+ * and a 16-byte aligned x, the call runs on the MFMA path: one launch
+ * repacks the weights of every adapter into the slot arena's block layout
+ * inside the workspace and builds the device plan that groups the rows by
+ * adapter, then the tiled shrink and a finish kernel write out (3 launches,
+ * no host synchronisation); with long adapter segments (B*M >= 1024 and >=
+ * 64 rows per adapter, K <= 16384) one launch of the fused kernel's shrink
+ * phase writes out instead (2 launches).  Otherwise, or with a null
  * workspace, one wave per token row computes it.  A workspace that is too
  * small or misaligned is an error (PL_ERR_ARG). */
 int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K,

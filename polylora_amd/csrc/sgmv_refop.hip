@@ -4,23 +4,24 @@
 // Those calls take adapter weights in the reference's own slot layout
 // (w [num_adapters][k][n] with any element strides) and a per-row adapter
 // index, and pass the LoRA intermediate between them as a model-dtype tensor
-// [B][M][n].  Each call here runs four launches on the caller's stream, all
-// inside a caller-provided workspace:
+// [B][M][n].  Each call here runs two or three launches on the caller's
+// stream, all inside a caller-provided workspace:
 //
-//   1. pl_refop_prep: the row -> slot map of the plan (adapter i -> slot
-//      i+1; rows whose adapter index is out of range or whose rank is 0 get
-//      slot 0 and are left alone, as the reference's kernels skip them), the
-//      slot table, and the adapters' weights repacked into the MFMA block
-//      layout of the slot arena (A as [rank][K], B as [N][rank8]).  Ranks,
-//      scales and indices stay on the device: no host synchronisation.
-//   2. pl_plan_build over (B rows of M tokens).
-//   3. shrink: pl_sgmv_shrink into fp32 split planes, then pl_refop_finish
+//   1. pl_refop_prep_plan: workgroup (0, 0) writes the slot table and builds
+//      the plan over (B rows of M tokens) straight from the adapter index
+//      (adapter i -> slot i+1; rows whose adapter index is out of range or
+//      whose rank is 0 get slot 0 and are left alone, as the reference's
+//      kernels skip them); the other workgroups repack the adapters'
+//      weights into the MFMA block layout of the slot arena (A as [rank][K],
+//      B as [N][rank8]).  Ranks, scales and indices stay on the device: no
+//      host synchronisation.
+//   2. shrink: pl_sgmv_shrink into fp32 split planes, then pl_refop_finish
 //      writes out[b][m][n] = T(sum of the planes) for n < rank * stack_num;
 //      expand: pl_refop_gather loads the model-dtype intermediate into one
 //      fp32 plane (zero past each row's rank), then pl_sgmv_expand adds
 //      T(scale * sum) into the output in the reference's rounding order.
 //      With long adapter segments (at least 1024 rows and 64 per adapter)
-//      step 3 is one launch of a phase of the fused kernel instead
+//      step 2 is one launch of a phase of the fused kernel instead
 //      (pl_fused_phase): the shrink reduces each 16-token tile in LDS and
 //      writes T(sum) straight into out, the expand stages the caller's
 //      intermediate in LDS and adds the deltas into out.
@@ -35,6 +36,7 @@
 #include <type_traits>
 
 #include "pl_common.h"
+#include "pl_plan_body.h"
 
 namespace {
 
@@ -53,7 +55,7 @@ struct refop_layout {
   int64_t tokens;     // B * M
   int64_t slot_bytes;
   // byte offsets inside the workspace
-  int64_t meta, groups, tok, row_slot, table, arena, plane, total;
+  int64_t meta, groups, tok, table, arena, plane, total;
 };
 
 // which: 0 = shrink (K = in_features, n = n_max), 1 = expand (K = k_max, n = N).
@@ -94,8 +96,6 @@ bool refop_plan_layout(int32_t dtype, int which, int32_t B, int32_t M, int32_t K
   o += align256(16 * L.group_cap);
   L.tok = o;
   o += align256(4 * T);
-  L.row_slot = o;
-  o += align256(4 * (int64_t)B);
   L.table = o;
   o += align256((int64_t)sizeof(pl_slot_entry) * (num_adapters + 1));
   L.arena = o;
@@ -117,11 +117,17 @@ struct refop_prep_args {
   const int32_t* ranks;
   const float* scalings;  // expand only
   const int32_t* widx;
-  int32_t B;
   char* arena;
   int64_t slot_bytes;
   pl_slot_entry* table;
-  int32_t* row_slot;
+  // the plan
+  const int32_t* seq_lens;
+  int32_t B, M;
+  int32_t group_tokens;
+  int64_t group_cap;
+  int32_t* tok;
+  pl_group* groups;
+  int32_t* meta;
 };
 
 // Rank a slot holds for adapter s: rank * stack_num columns of the shrink,
@@ -131,21 +137,17 @@ __device__ __forceinline__ int pl_refop_rank(const refop_prep_args& a, int s) {
   return (int)(r < 0 ? 0 : (r > a.rank_cap ? a.rank_cap : r));
 }
 
-// Grid: x covers the largest repacked matrix (and the rows, and the table),
-// y = adapter s for s < num_adapters, y = num_adapters for the row map and
-// the table.
+// Grid: y = 0, x = 0 writes the slot table and builds the plan (the other
+// workgroups of row y = 0 have nothing to do); y = s + 1 repacks adapter s,
+// x covering its matrix.  The plan's slot for row b is adapter widx[b] + 1
+// when widx[b] is in range and ranks[widx[b]] > 0 (the same test as
+// pl_refop_rank(a, widx[b]) > 0, since stack_num >= 1 and rank_cap >= 1).
 template <int DT>
-__global__ __launch_bounds__(kThreads) void pl_refop_prep(refop_prep_args a) {
+__global__ __launch_bounds__(kPlanThreads) void pl_refop_prep_plan(refop_prep_args a) {
   typedef typename pl_traits<DT>::T T;
-  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  const int s = blockIdx.y;
-  if (s == a.num_adapters) {
-    if (e < a.B) {
-      const int w = a.widx[e];
-      const bool ok = w >= 0 && w < a.num_adapters && pl_refop_rank(a, w) > 0;
-      a.row_slot[e] = ok ? w + 1 : 0;
-    }
-    if (e <= a.num_adapters) {
+  if (blockIdx.y == 0) {
+    if (blockIdx.x != 0) return;
+    for (int e = threadIdx.x; e <= a.num_adapters; e += kPlanThreads) {
       pl_slot_entry en;
       en.rank = 0;
       en.scale = 0.f;
@@ -154,17 +156,21 @@ __global__ __launch_bounds__(kThreads) void pl_refop_prep(refop_prep_args a) {
       en.a_off = 0;
       en.b_off = 0;
       if (e > 0) {
-        const int r = pl_refop_rank(a, (int)e - 1);
+        const int r = pl_refop_rank(a, e - 1);
         en.rank = r;
         en.scale = a.which == 1 ? a.scalings[e - 1] : 1.f;
         en.rank8 = (r + 7) & ~7;
-        en.a_off = (e - 1) * a.slot_bytes;
+        en.a_off = (int64_t)(e - 1) * a.slot_bytes;
         en.b_off = en.a_off;
       }
       a.table[e] = en;
     }
+    pl_plan_body<true>(a.widx, a.ranks, a.num_adapters, a.seq_lens, a.B, a.M, a.num_adapters + 1,
+                       nullptr, 0, a.group_tokens, a.tok, a.groups, a.meta, a.group_cap);
     return;
   }
+  const int s = blockIdx.y - 1;
+  const int64_t e = (int64_t)blockIdx.x * kPlanThreads + threadIdx.x;
   const int r = pl_refop_rank(a, s);
   if (r == 0) return;
   // the slot's matrix [R][C] in logical order, columns fastest: A [r][K], B [N][rank8]
@@ -253,10 +259,14 @@ bool refop_fused(const refop_layout& L, int32_t num_adapters, int32_t K) {
   return L.tokens >= 1024 && L.tokens >= (int64_t)64 * num_adapters && K <= 16384;
 }
 
+// The slot table, the plan and the repacked weights (pl_refop_prep_plan).
+// The layout fixes the plan's sizes: group_tokens 16 or 64, num_adapters + 1
+// <= PL_MAX_SLOTS slots, B * M < 2^31 tokens and group_cap at the bound of
+// pl_plan_group_capacity, the checks pl_plan_build makes.
 int refop_prep(int32_t dtype, const refop_layout& L, char* ws, const void* w, int64_t s0,
                int64_t s1, int64_t s2, int32_t num_adapters, int which, int32_t width,
                int32_t rank_cap, int32_t stack_num, const int32_t* ranks, const float* scalings,
-               const int32_t* widx, int32_t B, hipStream_t s) {
+               const int32_t* widx, int32_t B, int32_t M, const int32_t* seq_lens, hipStream_t s) {
   refop_prep_args a;
   a.w = w;
   a.s0 = s0;
@@ -270,23 +280,28 @@ int refop_prep(int32_t dtype, const refop_layout& L, char* ws, const void* w, in
   a.ranks = ranks;
   a.scalings = scalings;
   a.widx = widx;
-  a.B = B;
   a.arena = ws + L.arena;
   a.slot_bytes = L.slot_bytes;
   a.table = reinterpret_cast<pl_slot_entry*>(ws + L.table);
-  a.row_slot = reinterpret_cast<int32_t*>(ws + L.row_slot);
+  a.seq_lens = seq_lens;
+  a.B = B;
+  a.M = M;
+  a.group_tokens = L.group_tokens;
+  a.group_cap = L.group_cap;
+  a.tok = reinterpret_cast<int32_t*>(ws + L.tok);
+  a.groups = reinterpret_cast<pl_group*>(ws + L.groups);
+  a.meta = reinterpret_cast<int32_t*>(ws + L.meta);
   const int64_t mat = which == 0 ? (int64_t)rank_cap * width : (int64_t)width * round8(rank_cap);
-  const int64_t items = std::max<int64_t>(std::max<int64_t>(mat, B), num_adapters + 1);
-  const int64_t gx = (items + kThreads - 1) / kThreads;
+  const int64_t gx = (mat + kPlanThreads - 1) / kPlanThreads;
   if (gx > 0x7fffffffLL) {
     pl_set_error("reference-layout repack grid too large");
     return PL_ERR_LIMIT;
   }
   refop_dispatch(dtype, [&](auto dt) {
-    hipLaunchKernelGGL(pl_refop_prep<decltype(dt)::value>, dim3((unsigned)gx, num_adapters + 1),
-                       dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(pl_refop_prep_plan<decltype(dt)::value>,
+                       dim3((unsigned)gx, num_adapters + 1), dim3(kPlanThreads), 0, s, a);
   });
-  return pl_launch_status("pl_refop_prep");
+  return pl_launch_status("pl_refop_prep_plan");
 }
 
 }  // namespace
@@ -315,17 +330,13 @@ int pl_refop_shrink(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t 
   char* ws = reinterpret_cast<char*>(workspace);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int st = refop_prep(dtype, L, ws, w, w_s0, w_s1, w_s2, num_adapters, 0, K, n_max, stack_num,
-                      lora_ranks, nullptr, weight_indices, B, s);
+                      lora_ranks, nullptr, weight_indices, B, M, seq_lens, s);
   if (st) return st;
   int32_t* meta = reinterpret_cast<int32_t*>(ws + L.meta);
   pl_group* groups = reinterpret_cast<pl_group*>(ws + L.groups);
   int32_t* tok = reinterpret_cast<int32_t*>(ws + L.tok);
-  const int32_t* row_slot = reinterpret_cast<const int32_t*>(ws + L.row_slot);
   const pl_slot_entry* table = reinterpret_cast<const pl_slot_entry*>(ws + L.table);
   float* planes = reinterpret_cast<float*>(ws + L.plane);
-  st = pl_plan_build(row_slot, seq_lens, B, M, num_adapters + 1, L.group_tokens, tok, groups, meta,
-                     L.group_cap, stream);
-  if (st) return st;
   if (refop_fused(L, num_adapters, K))
     return pl_fused_phase(PL_FUSED_SHRINK, dtype, x, K, K, out, n_max, n_max, ws + L.arena, table,
                           L.ldt, tok, groups, meta, L.group_cap, L.group_tokens, PL_EPI_FALLBACK,
@@ -360,17 +371,13 @@ int pl_refop_expand(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t 
   char* ws = reinterpret_cast<char*>(workspace);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int st = refop_prep(dtype, L, ws, w, w_s0, w_s1, w_s2, num_adapters, 1, N, k_max, 1, lora_ranks,
-                      scalings, weight_indices, B, s);
+                      scalings, weight_indices, B, M, seq_lens, s);
   if (st) return st;
   int32_t* meta = reinterpret_cast<int32_t*>(ws + L.meta);
   pl_group* groups = reinterpret_cast<pl_group*>(ws + L.groups);
   int32_t* tok = reinterpret_cast<int32_t*>(ws + L.tok);
-  const int32_t* row_slot = reinterpret_cast<const int32_t*>(ws + L.row_slot);
   const pl_slot_entry* table = reinterpret_cast<const pl_slot_entry*>(ws + L.table);
   float* plane = reinterpret_cast<float*>(ws + L.plane);
-  st = pl_plan_build(row_slot, seq_lens, B, M, num_adapters + 1, L.group_tokens, tok, groups, meta,
-                     L.group_cap, stream);
-  if (st) return st;
   if (refop_fused(L, num_adapters, k_max))
     return pl_fused_phase(PL_FUSED_EXPAND, dtype, x, k_max, k_max, out, N, N, ws + L.arena, table,
                           L.ldt, tok, groups, meta, L.group_cap, L.group_tokens, PL_EPI_TRITON,
