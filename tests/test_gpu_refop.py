@@ -184,6 +184,40 @@ def test_isolated_op_shapes_through_the_operator_api(gpu):
     assert torch.equal(out.cpu()[zero], base[zero])
 
 
+@pytest.mark.parametrize("Bt,M", [(3000, 1), (1600, 64)])
+def test_more_adapters_than_plan_threads(gpu, Bt, M):
+    """1500 adapters: the slot table and the plan's slot counts span more entries than the plan
+    workgroup has threads.  3000 one-token rows take the split kernels; 1600 rows of 64 tokens (at
+    least 64 per adapter) take the fused kernel's phases.  Rank-0 adapters and indices -1 and S are
+    skipped."""
+    _announce(test="refop_many_adapters", Bt=Bt, M=M)
+    g = torch.Generator().manual_seed(Bt + M)
+    K, N, S, R = 128, 64, 1500, 8
+    x = torch.randn(Bt, M, K, generator=g).bfloat16()
+    wa = (torch.randn(S, K, R, generator=g) * 0.05).bfloat16()
+    wb = (torch.randn(S, R, N, generator=g) * 0.05).bfloat16()
+    ranks = torch.randint(1, R + 1, (S,), generator=g, dtype=torch.int32)
+    ranks[::7] = 0
+    scal = torch.rand(S, generator=g) * 4
+    seq = torch.randint(0, M + 2, (Bt,), generator=g, dtype=torch.int32)
+    widx = torch.randint(0, S, (Bt,), generator=g, dtype=torch.int32)
+    widx[5], widx[17] = -1, S
+    ok = (widx >= 0) & (widx < S)
+    d = {k: v.to(gpu) for k, v in dict(x=x, wa=wa, wb=wb, ranks=ranks, scal=scal, seq=seq, widx=widx).items()}
+    tmp = _call_a(d["x"], d["wa"], d["seq"], d["widx"], d["ranks"], 1, mfma=True).cpu()
+    exp_tmp, valid = sgmv_shrink_reference(x[ok], wa, seq[ok], widx[ok], ranks)
+    torch.testing.assert_close(tmp[ok][valid], exp_tmp[valid], **tol_for(torch.bfloat16))
+    assert bool((tmp[ok][~valid] == 7).all()) and bool((tmp[~ok] == 7).all())
+    base = torch.randn(Bt, M, N, generator=g).bfloat16()
+    xb = torch.zeros(Bt, M, R, dtype=torch.bfloat16)
+    xb[ok] = exp_tmp
+    out = _call_b(xb.to(gpu), d["wb"], d["seq"], d["widx"], d["ranks"], d["scal"], base.to(gpu), mfma=True).cpu()
+    expect = base.clone()
+    expect[ok] = sgmv_expand_reference(exp_tmp, wb, seq[ok], widx[ok], ranks, scal, base[ok])
+    torch.testing.assert_close(out, expect, **tol_for(torch.bfloat16))
+    assert torch.equal(out[~ok], base[~ok])
+
+
 def test_workspace_errors_are_reported(gpu):
     """A workspace below the size the call needs, or misaligned, is an error, not a silent fallback."""
     _announce(test="refop_ws_errors")
