@@ -762,8 +762,8 @@ def run_isolated(args) -> dict:
             "operator_api_pair_ms": round(op_ms, 5),
             "operator_api_pair_gbs": round(nb["total"] / (op_ms * 1e-3) / 1e9, 1),
             "operator_api_note": "sgmv_lora_a_fwd + sgmv_lora_b_fwd with the reference's slot layout and a "
-                                 "model-dtype intermediate, host calls back to back (6 launches: repack, plan, "
-                                 "fused shrink phase; repack, plan, fused expand phase); GB/s counts the op's "
+                                 "model-dtype intermediate, host calls back to back (4 launches: repack + plan, "
+                                 "fused shrink phase; repack + plan, fused expand phase); GB/s counts the op's "
                                  "bytes",
         },
         "roofline": {
