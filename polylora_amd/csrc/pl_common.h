@@ -81,6 +81,11 @@ __device__ __forceinline__ pl_xcd_slot pl_xcd_map(int per_group) {
   const int gq = s / per_group;
   return {gq * kXcds + x, s - gq * per_group};
 }
+// A launch of `blocks` workgroups of `threads` threads fits a grid
+// dimension: the dispatch packet counts work-items in 32 bits.
+static inline bool pl_grid_fits(int64_t blocks, int threads) {
+  return blocks >= 0 && blocks <= (int64_t)0xffffffffLL / threads;
+}
 static inline int64_t pl_xcd_grid(int64_t group_cap, int64_t per_group) {
   return (group_cap + kXcds - 1) / kXcds * kXcds * per_group;
 }

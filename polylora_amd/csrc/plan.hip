@@ -130,7 +130,7 @@ extern "C" int pl_check_right_padded(const void* mask, int32_t mask_dtype, int32
   const int64_t n = (int64_t)B * S;
   if (n == 0) return PL_OK;
   const int64_t grid = (n + 255) / 256;
-  if (grid > 0x7fffffffLL) {
+  if (!pl_grid_fits(grid, 256)) {
     pl_set_error("pl_check_right_padded: mask too large");
     return PL_ERR_LIMIT;
   }

@@ -505,7 +505,8 @@ extern "C" int pl_lora_fused_stacked(int32_t dtype, const void* x, int64_t ldx, 
         ((int64_t)N[j] + (int64_t)slices * kFWaves - 1) / ((int64_t)slices * kFWaves);
     a.nw[j] = (int32_t)((per_wave + kFColsMax - 1) / kFColsMax * kFColsMax);
   }
-  if (pl_xcd_grid(group_cap, (int64_t)n_modules * (group_tokens / 16) * slices) > 0x7fffffffLL) {
+  if (!pl_grid_fits(pl_xcd_grid(group_cap, (int64_t)n_modules * (group_tokens / 16) * slices),
+                    kFThreads)) {
     pl_set_error("pl_lora_fused: grid of %lld groups too large", (long long)group_cap);
     return PL_ERR_LIMIT;
   }
@@ -560,6 +561,10 @@ int pl_fused_phase(int mode, int32_t dtype, const void* x, int64_t ldx, int32_t 
       (group_tokens != PL_GROUP_TOKENS_SHORT && group_tokens != PL_GROUP_TOKENS_LONG)) {
     pl_set_error("pl_fused_phase: bad arguments");
     return PL_ERR_ARG;
+  }
+  if (!pl_grid_fits(pl_xcd_grid(group_cap, group_tokens / 16), kFThreads)) {
+    pl_set_error("pl_fused_phase: grid of %lld groups too large", (long long)group_cap);
+    return PL_ERR_LIMIT;
   }
   const int E = dtype == PL_F32 ? 4 : 8;
   pl_fused_args a;

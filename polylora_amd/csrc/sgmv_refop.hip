@@ -293,7 +293,7 @@ int refop_prep(int32_t dtype, const refop_layout& L, char* ws, const void* w, in
   a.meta = reinterpret_cast<int32_t*>(ws + L.meta);
   const int64_t mat = which == 0 ? (int64_t)rank_cap * width : (int64_t)width * round8(rank_cap);
   const int64_t gx = (mat + kPlanThreads - 1) / kPlanThreads;
-  if (gx > 0x7fffffffLL) {
+  if (!pl_grid_fits(gx, kPlanThreads)) {
     pl_set_error("reference-layout repack grid too large");
     return PL_ERR_LIMIT;
   }

@@ -206,7 +206,7 @@ extern "C" int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32
                                    workspace_bytes, stream);
   if (fast != PL_REFOP_DECLINED) return fast;
   const int64_t grid = (rows + 3) / 4;
-  if (grid > 0x7fffffffLL) {
+  if (!pl_grid_fits(grid, 256)) {
     pl_set_error("pl_sgmv_lora_a_ref: too many rows");
     return PL_ERR_LIMIT;
   }
@@ -244,7 +244,7 @@ extern "C" int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32
                                    workspace_bytes, stream);
   if (fast != PL_REFOP_DECLINED) return fast;
   const int32_t nblk = (N + 255) / 256;
-  if (rows * nblk > 0x7fffffffLL) {
+  if (!pl_grid_fits(rows * nblk, 256)) {
     pl_set_error("pl_sgmv_lora_b_ref: grid too large");
     return PL_ERR_LIMIT;
   }
@@ -285,7 +285,7 @@ extern "C" int pl_lora_apply_rows(int32_t dtype, const void* x, int64_t ldx, int
     return PL_ERR_ARG;
   }
   const int32_t nblk = (N + 255) / 256;
-  if (T * nblk > 0x7fffffffLL) {
+  if (!pl_grid_fits(T * nblk, 256)) {
     pl_set_error("pl_lora_apply_rows: grid too large");
     return PL_ERR_LIMIT;
   }

@@ -731,7 +731,7 @@ int prepare_shrink(pl_shrink_args& a, int32_t dtype, const void* x, int64_t ldx,
   const int32_t rank_tiles = group_cap * planes * n_jobs >= kShortWideMinBlocks ? 4 : 2;
   const int32_t rank_passes = (ldt + 16 * rank_tiles - 1) / (16 * rank_tiles);
   const int32_t sub = group_tokens / 16;
-  if (group_cap * planes * rank_passes * sub * n_jobs > 0x7fffffffLL) {
+  if (!pl_grid_fits(group_cap * planes * rank_passes * sub * n_jobs, 256)) {
     pl_set_error("shrink grid too large");
     return PL_ERR_LIMIT;
   }
@@ -808,7 +808,7 @@ int prepare_expand(pl_expand_args& a, int32_t dtype, void* const* ws, int32_t ld
     pl_set_error("bad epilogue mode %d", epilogue);
     return PL_ERR_ARG;
   }
-  if (group_cap * n_chunks * (group_tokens / 16) > 0x7fffffffLL) {
+  if (!pl_grid_fits(group_cap * n_chunks * (group_tokens / 16), 256)) {
     pl_set_error("expand grid too large");
     return PL_ERR_LIMIT;
   }

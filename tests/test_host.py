@@ -471,6 +471,9 @@ def test_library_host_side_errors_without_gpu():
     st = lib.pl_lora_apply_noalloc(_native.PL_BF16, fake, 4096, 4096, fake, 4096, 4096, fake, fake, 1, 0, fake,
                                    fake, 4, 1, 17, 32, 64, 8, 0, None)
     assert st == 1 and b"bad sizes" in lib.pl_last_error()
+    # a grid counts its work-items in 32 bits: 2^32 mask elements at 256 per workgroup do not fit
+    st = lib.pl_check_right_padded(fake, 0, 65536, 65536, fake, fake, None)
+    assert st == 4 and b"too large" in lib.pl_last_error()
 
 
 def test_no_cpu_fallback_in_product_ops():
