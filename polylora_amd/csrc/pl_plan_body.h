@@ -72,16 +72,16 @@ __device__ __forceinline__ int pl_wave_scan_incl(int v) {
 // Where a row's slot comes from: a row -> slot map (pl_plan_build,
 // ADAPTER_ROWS false: rows[b]), or a per-row adapter index as the
 // reference's operator API passes it (ADAPTER_ROWS true: adapter i = rows[b]
-// -> slot i + 1; an index outside [0, num_adapters) or an adapter whose
-// ranks[i] is 0 -> slot 0).  The pointers stay plain restrict parameters so
-// that the token stores are known not to alias them.
+// -> slot i + 1; an index outside [0, num_adapters) -> slot 0, and slot
+// i + 1 is active only when ranks[i] > 0, so an adapter of rank 0 gets no
+// tokens either).  The pointer stays a plain restrict parameter so that the
+// token stores are known not to alias it.
 template <bool ADAPTER_ROWS>
-__device__ __forceinline__ int pl_row_slot(const int32_t* __restrict__ rows,
-                                           const int32_t* __restrict__ ranks, int num_adapters,
+__device__ __forceinline__ int pl_row_slot(const int32_t* __restrict__ rows, int num_adapters,
                                            int b) {
   if constexpr (ADAPTER_ROWS) {
     const int w = rows[b];
-    return w >= 0 && w < num_adapters && ranks[w] > 0 ? w + 1 : 0;
+    return w >= 0 && w < num_adapters ? w + 1 : 0;
   } else {
     return rows[b];
   }
@@ -90,12 +90,11 @@ __device__ __forceinline__ int pl_row_slot(const int32_t* __restrict__ rows,
 // Slot and clamped length of row b, or slot 0 for a row that gets no tokens
 // (its slot is 0, out of range or inactive, or its length is 0).
 template <bool ADAPTER_ROWS>
-__device__ __forceinline__ void pl_plan_row(const int32_t* __restrict__ row_src,
-                                            const int32_t* __restrict__ ranks, int num_adapters,
+__device__ __forceinline__ void pl_plan_row(const int32_t* __restrict__ row_src, int num_adapters,
                                             const int32_t* __restrict__ seq_lens, int b,
                                             int row_len, int S, const uint8_t* act, int& s,
                                             int& L) {
-  s = pl_row_slot<ADAPTER_ROWS>(row_src, ranks, num_adapters, b);
+  s = pl_row_slot<ADAPTER_ROWS>(row_src, num_adapters, b);
   L = seq_lens[b];
   L = L < 0 ? 0 : (L > row_len ? row_len : L);
   if (s <= 0 || s >= S || L <= 0 || !act[s]) s = 0;
@@ -120,8 +119,10 @@ __device__ __forceinline__ bool pl_plan_position_used(int64_t p, int n) {
 // Positions a plan of n groups spans: 8 * ceil(n / 8).
 __device__ __forceinline__ int pl_plan_positions(int n) { return (n + 7) / 8 * 8; }
 
-// The plan, built by one workgroup of kPlanThreads threads; row_src, ranks
-// and num_adapters as for pl_row_slot.
+// The plan, built by one workgroup of kPlanThreads threads.  row_src and
+// num_adapters as for pl_row_slot; with ADAPTER_ROWS, slot s > 0 is active
+// when ranks[s - 1] > 0 (active is then unused), otherwise when there is no
+// active vector or active[s * active_stride] > 0.
 template <bool ADAPTER_ROWS>
 __device__ __forceinline__ void pl_plan_body(
     const int32_t* __restrict__ row_src, const int32_t* __restrict__ ranks, int32_t num_adapters,
@@ -135,6 +136,7 @@ __device__ __forceinline__ void pl_plan_body(
   __shared__ uint8_t act[PL_MAX_SLOTS];  // slot s has work (active[s * stride] > 0, or no vector)
   __shared__ __attribute__((aligned(16))) int32_t off[PL_MAX_SLOTS];
   __shared__ __attribute__((aligned(16))) int32_t goff[PL_MAX_SLOTS];
+  __shared__ int32_t fill[PL_MAX_SLOTS];  // tokens placed per slot by the scatter
   __shared__ int32_t wsum[2][kPlanThreads / 64];
 
   const int tid = threadIdx.x;
@@ -144,7 +146,11 @@ __device__ __forceinline__ void pl_plan_body(
 
   for (int s = tid; s < S; s += kPlanThreads) {
     cnt[s] = 0;
-    act[s] = active == nullptr || active[(int64_t)s * active_stride] > 0;
+    fill[s] = 0;
+    if constexpr (ADAPTER_ROWS)
+      act[s] = s > 0 && ranks[s - 1] > 0;
+    else
+      act[s] = active == nullptr || active[(int64_t)s * active_stride] > 0;
   }
   // this thread's cached rows tid + q * kPlanThreads: all loads first
   int rs[kPlanCached], rl[kPlanCached];
@@ -154,7 +160,7 @@ __device__ __forceinline__ void pl_plan_body(
     rs[q] = 0;
     rl[q] = 0;
     if (b < rows) {
-      rs[q] = pl_row_slot<ADAPTER_ROWS>(row_src, ranks, num_adapters, b);
+      rs[q] = pl_row_slot<ADAPTER_ROWS>(row_src, num_adapters, b);
       rl[q] = seq_lens[b];
     }
   }
@@ -185,7 +191,7 @@ __device__ __forceinline__ void pl_plan_body(
   }
   for (int b = tid + kPlanCached * kPlanThreads; b < rows; b += kPlanThreads) {
     int s, L;
-    pl_plan_row<ADAPTER_ROWS>(row_src, ranks, num_adapters, seq_lens, b, row_len, S, act, s, L);
+    pl_plan_row<ADAPTER_ROWS>(row_src, num_adapters, seq_lens, b, row_len, S, act, s, L);
     if (s > 0) atomicAdd(&cnt[s], L);
   }
   __syncthreads();
@@ -272,11 +278,10 @@ __device__ __forceinline__ void pl_plan_body(
       groups[p] = gr;
     }
   }
-  __syncthreads();
-  for (int s = tid; s < S; s += kPlanThreads) cnt[s] = 0;  // reused as fill counters
-  __syncthreads();
-  // the token list holds rows * row_len entries; a position outside it is
-  // never written (the offsets above keep every token inside it)
+  // the scatter reads off[] (complete since the last barrier) and fill[]
+  // (cleared before the first one), so it needs no barrier after the groups
+  // are written.  The token list holds rows * row_len entries; a position
+  // outside it is never written (the offsets above keep every token inside)
   const int64_t cap = (int64_t)rows * row_len;
 
   if (row_len <= 16) {
@@ -290,10 +295,10 @@ __device__ __forceinline__ void pl_plan_body(
         int excl, total;
         pl_wave_sum(rl[q], len_bits, excl, total);
         int p0 = 0;
-        if (lane == 0) p0 = off[k0] + atomicAdd(&cnt[k0], total);
+        if (lane == 0) p0 = off[k0] + atomicAdd(&fill[k0], total);
         p = __builtin_amdgcn_readfirstlane(p0) + excl;
       } else if (rs[q] > 0) {
-        p = off[rs[q]] + atomicAdd(&cnt[rs[q]], rl[q]);
+        p = off[rs[q]] + atomicAdd(&fill[rs[q]], rl[q]);
       }
       if (rs[q] > 0) {
         const int base = (tid + q * kPlanThreads) * row_len;
@@ -303,9 +308,9 @@ __device__ __forceinline__ void pl_plan_body(
     }
     for (int b = tid + kPlanCached * kPlanThreads; b < rows; b += kPlanThreads) {
       int s, L;
-      pl_plan_row<ADAPTER_ROWS>(row_src, ranks, num_adapters, seq_lens, b, row_len, S, act, s, L);
+      pl_plan_row<ADAPTER_ROWS>(row_src, num_adapters, seq_lens, b, row_len, S, act, s, L);
       if (s > 0) {
-        const int p = off[s] + atomicAdd(&cnt[s], L);
+        const int p = off[s] + atomicAdd(&fill[s], L);
         const int base = b * row_len;
         for (int m = 0; m < L; ++m)
           if (p + m < cap) tok[p + m] = base + m;
@@ -315,10 +320,10 @@ __device__ __forceinline__ void pl_plan_body(
     // long rows (prefill): one wave per row
     for (int b = wave; b < rows; b += kPlanThreads / 64) {
       int s, L;
-      pl_plan_row<ADAPTER_ROWS>(row_src, ranks, num_adapters, seq_lens, b, row_len, S, act, s, L);
+      pl_plan_row<ADAPTER_ROWS>(row_src, num_adapters, seq_lens, b, row_len, S, act, s, L);
       if (s > 0) {
         int p = 0;
-        if (lane == 0) p = off[s] + atomicAdd(&cnt[s], L);
+        if (lane == 0) p = off[s] + atomicAdd(&fill[s], L);
         p = __shfl(p, 0);
         const int base = b * row_len;
         for (int m = lane; m < L; m += 64)
