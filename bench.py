@@ -1269,16 +1269,17 @@ def run_churn(args) -> dict:
     most `--churn-sub-distinct` distinct adapters (at most 32, the slot count:
     the reference raises beyond it, cache.py:65-66): the adapters resident
     then first, each sub-batch taking every row of its adapters (see
-    sub_batches).  The default, 24, leaves a running forward's slots alone
-    for at least 8 of the next sub-batch's loads, which then copy while it
-    computes.  Every sub-batch is one
+    sub_batches).  Every sub-batch is one
     forward of one new token per row (empty KV cache), preceded by the loads
-    its adapters need.  Loads go to the side stream and a slot is rewritten
-    only after the forwards that read it; the host never waits for the GPU,
+    its adapters need.  Loads go to the side stream, into the arena's spare
+    regions, so they copy while the forward that reads the slots' current
+    regions computes; a slot's table row switches to its new region after
+    that forward.  The host never waits for the GPU,
     so it queues the next sub-batch's loads and forward while the device is
     still copying and computing.  Every adapter of the catalog is its own
-    84 MB pinned slot image (the store's one host copy of it; 86 GB for 1024
-    adapters).  Compared with the same rows restricted to 32 resident adapters
+    84 MB slot image (the store's one host copy of it; 86 GB for 1024
+    adapters), page-locked up to `--churn-pinned-gib` and pageable beyond
+    (loaded through the staging ring).  Compared with the same rows restricted to 32 resident adapters
     (no loads).
     """
     from transformers import DynamicCache
@@ -1715,7 +1716,7 @@ def main(argv=None) -> int:
     p.add_argument("--churn-catalog", type=int, default=1024, help="adapters in the churn catalog, each its own image")
     p.add_argument("--churn-pinned-gib", type=float, default=56.0,
                    help="page-locked bytes for churn catalog images; the rest are pageable")
-    p.add_argument("--churn-sub-distinct", type=int, default=24, choices=range(1, 33), metavar="1..32",
+    p.add_argument("--churn-sub-distinct", type=int, default=32, choices=range(1, 33), metavar="1..32",
                    help="most distinct adapters per churn sub-batch (the cache has 32 slots)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                    help="only copy a BYTES-sized device buffer 5 times (calibrates HBM byte counters) and exit")

@@ -5,8 +5,11 @@ Reference layout: per wrapped module, dense ``A[slots, in, max_rank]``,
 adapter load is ~10 small default-stream ops per module and zero-fills the
 whole slot.
 
-Here every slot s >= 1 owns one contiguous region of ``slot_bytes`` in a
-single device arena.  The store holds each adapter as its slot image
+Here the weights of slot s >= 1 fill one region of ``slot_bytes`` in a
+single device arena, found through the slot's table row (the kernels read
+every A and B offset from it).  The arena has more regions than slots (up to
+one spare per slot, within ``SPARE_REGION_BYTES``).  The store holds each
+adapter as its slot image
 (``slot_image.AdapterImage``, pinned, model dtype): for each module it has
 weights for, A as ``[rank][in]`` (= PEFT lora_A) then B as ``[out][rank8]``
 (= PEFT lora_B, rank padded to a multiple of 8 with zeros), each part
@@ -15,11 +18,16 @@ dimension cut into tiles of 16 rows, each tile stored as consecutive 64-byte
 column blocks, so that a kernel's 16-row x 64-byte operand load reads
 contiguous memory.  The cache binds its layout to the store, which packs
 every adapter added afterwards straight into that image.
-Loading is one host->device copy of that image plus one copy of the slot's
-table row (32 bytes per module: rank, scale, rank8, A and B offsets), both
-on a side stream that first waits for the last forward that read the slot;
-the compute stream waits on the copy's event before the next forward's
-kernels.  Slot 0 is the base adapter: its table row stays all zero.
+Loading is one host->device copy of that image, on a side stream, into a
+free region: one that no slot points at and whose last readers have finished
+(the copy waits for them), so the copy runs while the forward that reads the
+slot's current region is still computing.  The slot's table row (32 bytes
+per module: rank, scale, rank8, A and B offsets) is then written on the
+compute stream, after the copy's event and after every kernel queued before
+it, and the region the slot held before becomes free once that write has run
+(and the slot's last recorded reader, when mark_used recorded one).  With no
+free region the image is rewritten in place, after the slot's readers.  Slot
+0 is the base adapter: its table row stays all zero.
 
 ``ranks[module]`` and ``scales[module]`` remain int32 / fp32 device tensors
 indexed by slot (views into the table), as in the reference.  ``A`` and
@@ -31,7 +39,7 @@ the set-iteration order of ``ensure_resident``'s touch loop.
 
 from __future__ import annotations
 
-from collections import OrderedDict
+from collections import OrderedDict, deque
 from collections.abc import Mapping
 
 import numpy as np
@@ -97,12 +105,21 @@ class GpuAdapterCache:
         self._allocate()
 
     # ------------------------------------------------------------------ storage
+    # Device memory for spare arena regions (at most one per slot): a load
+    # copies into a spare region while a running forward still reads the
+    # slot's current one.  0 turns them off (loads then rewrite a slot in
+    # place, after its readers).  Read when the arena is allocated.
+    SPARE_REGION_BYTES = 4 << 30
+
     def _allocate(self) -> None:
         self.layout = SlotLayout(list(self.module_specs.values()), self.dtype, self.config.max_rank)
         # adapters added from now on are packed straight into this layout's slot images
         self.store.bind_layout(self.layout)
         n_mod = len(self.module_specs)
-        arena_bytes = max(1, (self.num_slots - 1) * self.layout.slot_bytes)
+        slots = self.num_slots - 1
+        self.spare_regions = int(min(slots, self.SPARE_REGION_BYTES // max(1, self.layout.slot_bytes)))
+        self.num_regions = slots + self.spare_regions
+        arena_bytes = max(1, self.num_regions * self.layout.slot_bytes)
         self.arena = torch.empty(arena_bytes, dtype=torch.uint8, device=self.device)
         self.table = torch.zeros((self.num_slots, n_mod, _ENTRY_INTS), dtype=torch.int32, device=self.device)
         self.table_host = np.zeros((self.num_slots, n_mod, _ENTRY_INTS), dtype=np.int32)
@@ -120,7 +137,17 @@ class GpuAdapterCache:
         # covered that hand-out yet (its readers are then somewhere on the
         # compute stream, and a rewrite waits for everything queued there)
         self._slot_last_use: dict[int, torch.cuda.Event | None] = {}
-        self._slot_ready: dict[int, torch.cuda.Event] = {}
+        # slot -> the arena region holding its adapter (None: no adapter)
+        self._slot_region: list[int | None] = [None] * self.num_slots
+        # regions no slot points at, the longest free first, each with the
+        # events a copy into it must wait for (its last readers)
+        self._free_regions: deque = deque((region, ()) for region in range(self.num_regions))
+        # one residency call's table rows, written together by _flush_rows:
+        # the slots to write, the copies they wait for, and the regions they
+        # release (with the slots' last recorded readers)
+        self._rows_dirty: set[int] = set()
+        self._rows_ready: list = []
+        self._rows_release: list[tuple[int, tuple]] = []
         self._pending: list[tuple] = []
         self._deferred_writes: dict | None = None  # slot -> image, while ensure_resident runs
         self._use_seq = 0  # mark_used calls so far
@@ -187,13 +214,10 @@ class GpuAdapterCache:
         finally:
             writes, self._deferred_writes = self._deferred_writes, None
             self._issue_writes(writes)
+            self._flush_rows()
         for adapter_id in needed:  # set order, as cache.py:73-74
             self._touch(adapter_id)
         self._sync_cpu_eviction_exclusions()
-        if self.device.type == "cuda" and loaded:
-            compute = torch.cuda.current_stream(self.device)
-            for slot in loaded:
-                compute.wait_event(self._slot_ready[slot])
         slots = [0 if aid == base_id else self.adapter_to_slot[aid] for aid in adapter_ids]
         for slot in set(slots):
             if slot > 0:
@@ -256,10 +280,7 @@ class GpuAdapterCache:
         for slot, aid in resident:
             adapter = self.store.adapters.get(aid) or self.store.get(aid)
             self._write_slot(slot, self._packed(adapter))
-        if self.device.type == "cuda" and resident:
-            compute = torch.cuda.current_stream(self.device)
-            for slot, _ in resident:
-                compute.wait_event(self._slot_ready[slot])
+        self._flush_rows()
 
     def _allocate_or_evict(self, needed: set[str]) -> int:
         for slot in range(1, self.num_slots):
@@ -313,12 +334,41 @@ class GpuAdapterCache:
             return
         self._write_slot_now(slot, packed)
 
+    def slot_offset(self, slot: int) -> int | None:
+        """Byte offset in the arena of the region holding slot `slot`'s adapter, or None."""
+        region = self._slot_region[slot]
+        return None if region is None else region * self.layout.slot_bytes
+
+    def _take_region(self, slot: int) -> tuple[int, tuple, bool]:
+        """A region for slot `slot`'s new image: (region, events to wait for, wait for the compute stream).
+
+        The region free longest, else one this residency call released
+        (its readers are queued on the compute stream), else the slot's own
+        region (its readers: the slot's last recorded use, or, when none was
+        recorded, the compute stream).
+        """
+        if self._free_regions:
+            region, waits = self._free_regions.popleft()
+            return region, waits, False
+        if self._rows_release:
+            region, waits = self._rows_release.pop(0)
+            return region, waits, True
+        region = self._slot_region[slot]
+        if region is None:
+            raise RuntimeError("no arena region is free")  # more slots than regions: cannot happen
+        last = self._slot_last_use.get(slot)
+        return region, (() if last is None else (last,)), slot in self._slot_last_use and last is None
+
     def _write_slot_now(self, slot: int, packed: AdapterImage | None) -> None:
-        base = (slot - 1) * self.layout.slot_bytes
+        """Copy an image into a region for `slot` and record the slot's new table row."""
+        old = self._slot_region[slot]
         if packed is None:
+            region, waits, wait_compute = None, (), False
             row = np.zeros_like(self.table_host[slot])
-            image, nbytes = None, 0
+            image, nbytes, base = None, 0, 0
         else:
+            region, waits, wait_compute = self._take_region(slot)
+            base = region * self.layout.slot_bytes
             row = packed.rows.copy()
             has = row[:, 0] > 0
             row64 = row.view(np.int64)
@@ -326,40 +376,73 @@ class GpuAdapterCache:
             row64[has, 3] += base
             image, nbytes = packed.data, packed.nbytes
         self.table_host[slot] = row
+        self._slot_region[slot] = region
+        if old is not None and old != region:
+            last = self._slot_last_use.get(slot)
+            self._rows_release.append((old, () if last is None else (last,)))
+        self._slot_last_use.pop(slot, None)  # the old occupant's readers now guard its old region
+        self._rows_dirty.add(slot)
         if self.device.type != "cuda":
             if nbytes:
                 self.arena[base : base + nbytes].copy_(image[:nbytes])
-            self.table[slot].copy_(torch.from_numpy(row))
+            return
+        if not nbytes:
             return
         lib = _native.load()
         side = self._side_stream
-        if slot in self._slot_last_use:
-            last = self._slot_last_use.pop(slot)
-            if last is None:
-                # readers not marked: they are among the work queued on the compute stream
-                side.wait_stream(torch.cuda.current_stream(self.device))
-            else:
-                side.wait_event(last)  # the previous occupant may still be read
-        previous = self._slot_ready.get(slot)
-        if previous is not None:
-            side.wait_event(previous)
-        staging, ring_index = self._stage(image, nbytes) if nbytes and not packed.pinned else (None, None)
-        row_pinned = torch.from_numpy(row).pin_memory()
+        if wait_compute:
+            side.wait_stream(torch.cuda.current_stream(self.device))
+        for event in waits:
+            side.wait_event(event)
+        staging, ring_index = self._stage(image, nbytes) if not packed.pinned else (None, None)
         with torch.cuda.device(self.device):
             _native.check(
-                lib.pl_slot_upload(self.arena.data_ptr() + base,
-                                   (staging if staging is not None else image).data_ptr() if nbytes else None, nbytes,
-                                   self.table.data_ptr() + slot * self._row_bytes, row_pinned.data_ptr(),
-                                   self._row_bytes, side.cuda_stream),
+                lib.pl_slot_upload(self.arena.data_ptr() + base, (staging if staging is not None else image).data_ptr(),
+                                   nbytes, None, None, 0, side.cuda_stream),
                 "pl_slot_upload",
             )
         ready = torch.cuda.Event()
         ready.record(side)
-        self._slot_ready[slot] = ready
+        self._rows_ready.append(ready)
         if ring_index is not None:
             self._staging_read[ring_index] = ready  # the buffer's next fill waits for this DMA
-        # the source image, the staging buffer and the row stay alive until the upload has run
-        self._pending.append((ready, image, row_pinned, staging))
+        # the source image and the staging buffer stay alive until the upload has run
+        self._pending.append((ready, image, staging))
+
+    def _flush_rows(self) -> None:
+        """Write the recorded table rows and free the regions they no longer point at.
+
+        On a GPU the rows go in one copy on the compute stream, after the
+        uploads they describe and after every kernel queued so far (the
+        readers of the rows being replaced); the released regions wait for
+        that point, and for the slots' last recorded readers, before a copy
+        reuses them.
+        """
+        dirty, self._rows_dirty = self._rows_dirty, set()
+        ready, self._rows_ready = self._rows_ready, []
+        release, self._rows_release = self._rows_release, []
+        if not dirty:
+            self._free_regions.extend(release)
+            return
+        lo, hi = min(dirty), max(dirty) + 1
+        if self.device.type != "cuda":
+            self.table[lo:hi].copy_(torch.from_numpy(self.table_host[lo:hi]))
+            self._free_regions.extend(release)
+            return
+        compute = torch.cuda.current_stream(self.device)
+        for event in ready:
+            compute.wait_event(event)
+        rows = torch.from_numpy(self.table_host[lo:hi].copy()).pin_memory()
+        with torch.cuda.device(self.device):
+            _native.check(
+                _native.load().pl_slot_upload(None, None, 0, self.table.data_ptr() + lo * self._row_bytes,
+                                              rows.data_ptr(), (hi - lo) * self._row_bytes, compute.cuda_stream),
+                "pl_slot_upload",
+            )
+        written = torch.cuda.Event()
+        written.record(compute)
+        self._free_regions.extend((region, waits + (written,)) for region, waits in release)
+        self._pending.append((written, rows))
 
     # Page-locked staging buffers for images held in pageable memory.  The
     # runtime's own copy from pageable memory blocks the calling thread until

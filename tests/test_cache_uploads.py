@@ -5,13 +5,17 @@ checked against oracle/slots.py in test_host.py; here only the uploads are
 observed: one per slot per ensure_resident call (an eviction's clear is
 replaced by the new occupant's load), issued free slots first, then by the
 age of each slot's last recorded reader, then slots handed out and not yet
-marked.
+marked.  Each load goes to an arena region no slot points at when one is
+free (the arena's spare regions), else to the slot's own region; the
+regions held by slots and the free ones always partition the arena.
 """
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
+from polylora_amd.cache import GpuAdapterCache
 from tests._util import make_cache, peft_layer
 
 SHAPES = {"m": (32, 24)}
@@ -76,5 +80,60 @@ def test_slot_numbers_do_not_depend_on_upload_order():
         for slot in range(1, a.num_slots):  # the bytes each resident image occupies (the rest is never read)
             aid = a.slot_to_adapter[slot]
             if aid is not None:
-                base, n = (slot - 1) * a.layout.slot_bytes, a.store.adapters[aid].image.nbytes
-                assert torch.equal(a.arena[base : base + n], b.arena[base : base + n])
+                n = a.store.adapters[aid].image.nbytes
+                oa, ob = a.slot_offset(slot), b.slot_offset(slot)  # the regions may differ
+                assert torch.equal(a.arena[oa : oa + n], b.arena[ob : ob + n])
+
+
+def _regions_consistent(cache):
+    held = [r for r in cache._slot_region[1:] if r is not None]
+    free = [r for r, _ in cache._free_regions]
+    assert len(held) == len(set(held)), "two slots share a region"
+    assert sorted(held + free) == list(range(cache.num_regions)), "a region is lost or listed twice"
+    for slot in range(1, cache.num_slots):
+        aid = cache.slot_to_adapter[slot]
+        assert (aid is None) == (cache.slot_offset(slot) is None)
+        if aid is not None:
+            image = cache.store.adapters[aid].image
+            off = cache.slot_offset(slot)
+            assert torch.equal(cache.arena[off : off + image.nbytes], image.data[: image.nbytes])
+            rows = cache.table[slot].numpy().view(np.int64)  # A and B offsets point into the region
+            has = cache.table[slot, :, 0].numpy() > 0
+            assert ((rows[has, 2] >= off) & (rows[has, 3] < off + cache.layout.slot_bytes)).all()
+
+
+def test_loads_go_to_spare_regions_and_free_the_old_ones():
+    """A reload copies into a region no slot points at; the evicted adapter's region is freed."""
+    cache = _cache(6, 3)
+    assert cache.spare_regions == 3 and cache.num_regions == 6
+    cache.ensure_resident(["a0", "a1", "a2"])
+    before = {cache.adapter_to_slot[a]: cache._slot_region[cache.adapter_to_slot[a]] for a in ("a0", "a1", "a2")}
+    cache.ensure_resident(["a3"])  # evicts the least recently used adapter
+    slot = cache.adapter_to_slot["a3"]
+    assert cache._slot_region[slot] != before[slot]
+    assert before[slot] in [r for r, _ in cache._free_regions]
+    _regions_consistent(cache)
+
+
+def test_without_spare_regions_loads_rewrite_in_place(monkeypatch):
+    monkeypatch.setattr(GpuAdapterCache, "SPARE_REGION_BYTES", 0)
+    cache = _cache(6, 3)
+    assert cache.spare_regions == 0 and cache.num_regions == 3
+    cache.ensure_resident(["a0", "a1", "a2"])
+    offsets = [cache.slot_offset(s) for s in range(1, 4)]
+    for batch in (["a3"], ["a4", "a0"], ["a5", "a1", "a2"]):
+        cache.ensure_resident(batch)
+        assert [cache.slot_offset(s) for s in range(1, 4)] == offsets
+        _regions_consistent(cache)
+
+
+def test_region_bookkeeping_over_random_batches():
+    g = np.random.default_rng(11)
+    cache = _cache(10, 4)
+    for _ in range(40):
+        batch = [f"a{i}" for i in g.choice(10, size=int(g.integers(1, 5)), replace=False)]
+        cache.ensure_resident(batch)
+        _regions_consistent(cache)
+        for aid in batch:
+            slot = cache.adapter_to_slot[aid]
+            assert int(cache.ranks["m"][slot]) == int(cache.store.adapters[aid].layers["m"].rank)

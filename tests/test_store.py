@@ -56,7 +56,7 @@ def test_bound_store_holds_only_the_packed_image(dtype):
     # and the slot holds exactly that image
     cache.ensure_resident(["a"])
     slot = cache.adapter_to_slot["a"]
-    base = (slot - 1) * cache.layout.slot_bytes
+    base = cache.slot_offset(slot)
     assert torch.equal(cache.arena[base : base + ad.image.nbytes], ad.image.data[: ad.image.nbytes])
 
 
