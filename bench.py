@@ -319,7 +319,7 @@ def cpu_baseline_deberta(wl: DebertaWorkload, budget_s: float) -> dict:
             oracle_model.run(m, bank, wl.adapter_ids, **inputs)
             reps += 1
             el = time.perf_counter() - t0
-            if el >= budget_s or reps >= 50:
+            if el >= budget_s:
                 break
     per = el / reps
     return _cpu_record(round(valid / per, 1), "tokens/s", threads,
@@ -461,7 +461,7 @@ def cpu_baseline_isolated(wl: IsolatedSgmv, nbytes: int, budget_s: float) -> dic
         reference_forward(xs, bs, seq, widx, A, B, ranks, scales)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 50:
+        if el >= budget_s:
             break
     per = el / reps
     return _cpu_record(round(nbytes / per / 1e9, 4), "GB/s", threads,
@@ -1044,7 +1044,7 @@ def cpu_baseline_layer(pm, adapter_ids: list, budget_s: float, lens: list | None
             reference_forward(x, base, seq_lens, widx, A, B, ranks, scales)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 20:
+        if el >= budget_s:
             break
     per_layer = el / reps
     layers = pm.base_model.config.num_hidden_layers
