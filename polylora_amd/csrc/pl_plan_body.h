@@ -12,9 +12,10 @@
 // Steps: per-slot token counts (LDS atomics), one block-wide exclusive scan
 // of counts and of group counts, group emission (one thread per group), then
 // the token indices of each row are copied to the slot's segment (one thread
-// per row for rows of up to 16 tokens, one wave per row for longer ones).  Row order inside a
-// segment follows LDS atomic order and is not fixed; no consumer depends on
-// it.
+// per row for rows of up to 16 tokens, one wave per row for longer ones; a
+// second set of LDS counters places them, so this step needs no barrier
+// after the emission).  Row order inside a segment follows LDS atomic order
+// and is not fixed; no consumer depends on it.
 //
 // Group placement.  Kernels give the work items of the group at position p
 // to XCD p % 8 (workgroups are dealt to the 8 XCDs round-robin).  The plan
@@ -29,7 +30,6 @@
 #include "pl_common.h"
 
 namespace {
-
 
 constexpr int kPlanThreads = 1024;
 // Rows a plan thread keeps in registers: the first kPlanThreads * kPlanCached
@@ -332,6 +332,5 @@ __device__ __forceinline__ void pl_plan_body(
     }
   }
 }
-
 
 }  // namespace
