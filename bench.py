@@ -1095,6 +1095,110 @@ def _eager_ms(fn, reps: int) -> float:
     return (time.perf_counter() - t0) / reps * 1e3
 
 
+def decode_graph_trace(args) -> int:
+    """Replay the decode step's HIP graph without adapters, then with them, for a kernel trace.
+
+    Each graph is warmed up and captured as in _graph_ms and replayed twice
+    (one burst of kernels), then, after a pause, `--profile-passes` times (the
+    timed burst); pauses of 0.3 s separate the bursts, so that
+    reduce_graph_trace can tell them apart in the trace.
+    """
+    from polylora_amd.context import use_lora_context
+
+    device = torch.device("cuda", 0)
+    wl = decode_workload(device, layers=args.decode_layers)
+    pm = wl.model
+    B = len(wl.adapter_ids)
+    ctx = pm.prepare_lora_context(wl.adapter_ids, None, B, 1, device)
+
+    def lora_step():
+        with use_lora_context(ctx):
+            return _decode_step(wl, True)
+
+    reps = args.profile_passes
+    with torch.inference_mode():
+        for name, fn in (("base", lambda: _decode_step(wl, False)), ("lora", lora_step)):
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for _ in range(2):
+                    fn()
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn()
+            for _ in range(2):
+                g.replay()
+            torch.cuda.synchronize()
+            time.sleep(0.3)
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(reps):
+                g.replay()
+            t1.record()
+            torch.cuda.synchronize()
+            _log(f"graph trace: {name} step {t0.elapsed_time(t1) / reps:.3f} ms per replay")
+            time.sleep(0.3)
+    print(json.dumps({"graph_trace": "decode", "replays": reps}), flush=True)
+    return 0
+
+
+def reduce_graph_trace(args) -> int:
+    """Per-kernel time of one decode step replay, without and with adapters, from a kernel trace.
+
+    The trace's kernels are cut into bursts at idle stretches of over 100 ms:
+    per graph, base first, a warm-up burst and then the burst of its
+    `--profile-passes` timed replays, so the timed bursts are the third and
+    the first from the end.
+    """
+    import csv
+    from collections import defaultdict
+
+    with open(args.trace, newline="") as f:
+        rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]) for r in csv.DictReader(f))
+    bursts, cur = [], rows[:1]
+    for r in rows[1:]:
+        if r[0] - cur[-1][1] > 100_000_000:
+            bursts.append(cur)
+            cur = [r]
+        else:
+            cur.append(r)
+    bursts.append(cur)
+    n = args.profile_passes
+    if len(bursts) < 3 or len(bursts[-3]) % n or len(bursts[-1]) % n:
+        print("the trace does not end with a --graph-trace run's bursts", file=sys.stderr)
+        return 1
+    steps = {"base": bursts[-3], "lora": bursts[-1]}
+    per = {}
+    for name, b in steps.items():
+        us, cnt = defaultdict(float), defaultdict(int)
+        for s, e, k in b:
+            key = k.split("(")[0].split("<")[0].strip().removeprefix("void ")[:60]
+            us[key] += (e - s) / 1e3 / n
+            cnt[key] += 1
+        idle = sum(max(0, s1 - e0) for (_, e0, _), (s1, _, _) in zip(b, b[1:])) / 1e3 / n
+        per[name] = {"wall_ms": (b[-1][1] - b[0][0]) / 1e6 / n, "busy_ms": sum(us.values()) / 1e3,
+                     "idle_ms": idle / 1e3, "kernels": len(b) / n, "us": us, "count": cnt}
+    lines = ["| kernel | base (us per step) | with adapters (us per step) | difference | launches per step (base / with) |",
+             "|---|---|---|---|---|"]
+    keys = sorted(set(per["base"]["us"]) | set(per["lora"]["us"]),
+                  key=lambda k: -(per["base"]["us"].get(k, 0.0) + per["lora"]["us"].get(k, 0.0)))
+    for k in keys:
+        b, l = per["base"]["us"].get(k, 0.0), per["lora"]["us"].get(k, 0.0)
+        lines.append(f"| {k} | {b:.1f} | {l:.1f} | {l - b:+.1f} | {per['base']['count'].get(k, 0) // n} / "
+                     f"{per['lora']['count'].get(k, 0) // n} |")
+    lines.append("")
+    for name in ("base", "lora"):
+        p = per[name]
+        lines.append(f"{name}: {p['wall_ms']:.3f} ms per replay from first kernel start to last kernel end, "
+                     f"{p['busy_ms']:.3f} ms of kernel time, {p['idle_ms']:.3f} ms between kernels, "
+                     f"{p['kernels']:.0f} kernels.")
+    print("\n".join(lines))
+    return 0
+
+
 def run_decode(args) -> dict:
     from polylora_amd.context import use_lora_context
 
@@ -1735,9 +1839,15 @@ def main(argv=None) -> int:
     p.add_argument("--copy-write", help="counter_collection.csv of --pmc WRITE_SIZE over --copy-probe")
     p.add_argument("--copy-bytes", type=int, default=268435456)
     p.add_argument("--reduce-json", help="write the reduced figures here as JSON")
+    p.add_argument("--graph-trace", action="store_true",
+                   help="replay the decode step's graph without and with adapters, for a kernel trace")
+    p.add_argument("--reduce-graph-trace", action="store_true",
+                   help="print per-kernel time per step from the --trace of a --graph-trace run")
     args = p.parse_args(argv)
     if args.reduce_profile:
         return reduce_profile(args)
+    if args.reduce_graph_trace:
+        return reduce_graph_trace(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the library has no multi-GPU path; run with --gpus 1", file=sys.stderr)
         return 2
@@ -1754,6 +1864,8 @@ def main(argv=None) -> int:
         return 0
     if args.launch_profile:
         return launch_profile(args)
+    if args.graph_trace:
+        return decode_graph_trace(args)
     iso = run_isolated(args)
     _log(f"isolated: {iso['value']} GB/s")
     result = {

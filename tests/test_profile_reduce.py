@@ -117,3 +117,36 @@ def test_reduce_rejects_too_few_dispatches(tmp_path):
     _write(tmp_path / "t.csv", TRACE_COLS, _trace_rows(3))
     with pytest.raises(ValueError, match="the manifest needs 18"):
         bench.reduce_profile(_args(tmp_path))
+
+
+def test_reduce_graph_trace_splits_bursts_and_compares_steps(tmp_path, capsys):
+    """bench.py --reduce-graph-trace: base and LoRA timed bursts, per-kernel time per step."""
+    rows, t, did = [], 0, 1
+
+    def burst(kernels, reps):
+        nonlocal t, did
+        for _ in range(reps):
+            for name, dur in kernels:
+                rows.append(dict(Kind="KERNEL_DISPATCH", Agent_Id=1, Queue_Id=1, Dispatch_Id=did, Kernel_Name=name,
+                                 Start_Timestamp=t, End_Timestamp=t + dur, Workgroup_Size_X=256, Workgroup_Size_Y=1,
+                                 Workgroup_Size_Z=1, Grid_Size_X=256, Grid_Size_Y=1, Grid_Size_Z=1))
+                did, t = did + 1, t + dur + 1000
+        t += 300_000_000  # the pause between bursts
+
+    base = [("Cijk_gemm(args)", 50_000), ("attn_fwd(args)", 100_000)]
+    lora = [("Cijk_gemm(args)", 50_000), ("void pl_shrink_short<__hip_bfloat16, 4>(pl_shrink_args)", 10_000),
+            ("void pl_expand_short<__hip_bfloat16, 4, 32>(pl_expand_args)", 12_000), ("attn_fwd(args)", 100_000)]
+    burst(base, 2)
+    burst(base, 5)
+    burst(lora, 2)
+    burst(lora, 5)
+    _write(tmp_path / "t.csv", TRACE_COLS, rows)
+    assert bench.main(["--reduce-graph-trace", "--trace", str(tmp_path / "t.csv"), "--profile-passes", "5"]) == 0
+    out = capsys.readouterr().out
+    assert "| pl_shrink_short | 0.0 | 10.0 | +10.0 | 0 / 1 |" in out
+    assert "| pl_expand_short | 0.0 | 12.0 | +12.0 | 0 / 1 |" in out
+    assert "| attn_fwd | 100.0 | 100.0 | +0.0 | 1 / 1 |" in out
+    assert "base: " in out and "2 kernels." in out and "4 kernels." in out
+    # a trace without the four bursts is refused
+    _write(tmp_path / "short.csv", TRACE_COLS, rows[:4])
+    assert bench.main(["--reduce-graph-trace", "--trace", str(tmp_path / "short.csv"), "--profile-passes", "5"]) == 1
