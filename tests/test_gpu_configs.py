@@ -72,9 +72,12 @@ def _sub_batches(ids, limit):
     return out
 
 
-def test_churn_config_every_layer_against_the_oracle(gpu):
-    """Config 5 shapes on 2 layers: 96 distinct rank-16 adapters (40 pinned, 56 pageable) through 32 slots."""
-    _announce(test="churn_config")
+@pytest.mark.parametrize("limit", [24, 32])
+def test_churn_config_every_layer_against_the_oracle(gpu, limit):
+    """Config 5 shapes on 2 layers: 96 distinct rank-16 adapters (40 pinned, 56 pageable) through 32 slots,
+    in sub-batches of at most `limit` distinct adapters (at 32 every slot is in use, and each load copies
+    into a spare arena region while the previous sub-batch's forward reads the slot's old one)."""
+    _announce(test="churn_config", limit=limit)
     from transformers import DynamicCache
 
     from bench import build_llama
@@ -103,7 +106,7 @@ def test_churn_config_every_layer_against_the_oracle(gpu):
     with torch.inference_mode(), _per_layer_check(pm, ads, torch.bfloat16) as checked:
         for step in range(3):
             ids = [names[int(i)] for i in rng.choice(96, size=128, p=w)]
-            for sub in _sub_batches(ids, 24):
+            for sub in _sub_batches(ids, limit):
                 x = torch.randint(0, vocab, (len(sub), 1), generator=gen, device=gpu)
                 pm(input_ids=x, adapter_ids=sub, past_key_values=DynamicCache(config=model.config), use_cache=True)
                 forwards += 1
