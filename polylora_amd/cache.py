@@ -135,7 +135,8 @@ class GpuAdapterCache:
         # slot -> the event after the last work known to read it, or None when
         # the slot was handed out by ensure_resident and no mark_used has
         # covered that hand-out yet (its readers are then somewhere on the
-        # compute stream, and a rewrite waits for everything queued there)
+        # compute stream, and an in-place rewrite waits for everything queued
+        # there)
         self._slot_last_use: dict[int, torch.cuda.Event | None] = {}
         # slot -> the arena region holding its adapter (None: no adapter)
         self._slot_region: list[int | None] = [None] * self.num_slots
@@ -203,14 +204,12 @@ class GpuAdapterCache:
         if len(needed) > self.config.max_gpu_adapters:
             raise RuntimeError("Batch needs more adapters than GPU cache capacity")
         self._reap_pending()
-        loaded: list[int] = []
         self._deferred_writes = {}
         try:
             for adapter_id in sorted(needed):
                 if adapter_id not in self.adapter_to_slot:
                     slot = self._allocate_or_evict(needed)
                     self._load_adapter_into_slot(adapter_id, slot)
-                    loaded.append(slot)
         finally:
             writes, self._deferred_writes = self._deferred_writes, None
             self._issue_writes(writes)
@@ -230,10 +229,12 @@ class GpuAdapterCache:
     def mark_used(self, slots: set[int]) -> None:
         """Record that every reader of these slots is enqueued on the current stream, up to now.
 
-        A later rewrite of such a slot then waits for this point of the stream
-        only.  A slot handed out by ``ensure_resident`` and not marked since
-        (the ``prepare_lora_context`` + ``use_lora_context`` path) is rewritten
-        only after everything queued on the compute stream at the rewrite.
+        When such a slot gets a new adapter, its old region is reused only
+        after this point of the stream (and after the table row's switch), and
+        an in-place rewrite waits for this point only.  A slot handed out by
+        ``ensure_resident`` and not marked since (the ``prepare_lora_context``
+        + ``use_lora_context`` path) is taken to be read by everything queued
+        on the compute stream.
         """
         if self.device.type != "cuda" or not slots:
             return
