@@ -213,27 +213,46 @@ __device__ __forceinline__ void pl_plan_body(
   }
   const int it = pl_wave_scan_incl(st);
   const int ig = pl_wave_scan_incl(sg);
-  if (lane == 63) {
-    wsum[0][wave] = it;
-    wsum[1][wave] = ig;
-  }
-  __syncthreads();
-  int wt = 0, wg = 0, tt = 0, tg = 0;
-  for (int w = 0; w < kPlanThreads / 64; ++w) {
-    if (w < wave) {
-      wt += wsum[0][w];
-      wg += wsum[1][w];
+  int ex_t, ex_g, tt, tg;
+  if (S <= 4 * 64) {
+    // every count is in wave 0's slots: its scan is the whole prefix, and
+    // the totals reach the other waves through LDS at the barrier below
+    ex_t = it - st;
+    ex_g = ig - sg;
+    tt = __shfl(it, 63);
+    tg = __shfl(ig, 63);
+    if (tid == 63) {
+      wsum[0][0] = it;
+      wsum[1][0] = ig;
     }
-    tt += wsum[0][w];
-    tg += wsum[1][w];
+  } else {
+    if (lane == 63) {
+      wsum[0][wave] = it;
+      wsum[1][wave] = ig;
+    }
+    __syncthreads();
+    int wt = 0, wg = 0;
+    tt = 0;
+    tg = 0;
+    for (int w = 0; w < kPlanThreads / 64; ++w) {
+      if (w < wave) {
+        wt += wsum[0][w];
+        wg += wsum[1][w];
+      }
+      tt += wsum[0][w];
+      tg += wsum[1][w];
+    }
+    ex_t = wt + it - st;
+    ex_g = wg + ig - sg;
   }
-  const int ex_t = wt + it - st;
-  const int ex_g = wg + ig - sg;
-  // entries past the slot count are written too (never read)
-  reinterpret_cast<int4*>(off)[tid] =
-      make_int4(ex_t + loc_t[0], ex_t + loc_t[1], ex_t + loc_t[2], ex_t + loc_t[3]);
-  reinterpret_cast<int4*>(goff)[tid] =
-      make_int4(ex_g + loc_g[0], ex_g + loc_g[1], ex_g + loc_g[2], ex_g + loc_g[3]);
+  // entries past the slot count are written too (never read); with at most
+  // 256 slots the other waves' entries are past it
+  if (S > 4 * 64 || wave == 0) {
+    reinterpret_cast<int4*>(off)[tid] =
+        make_int4(ex_t + loc_t[0], ex_t + loc_t[1], ex_t + loc_t[2], ex_t + loc_t[3]);
+    reinterpret_cast<int4*>(goff)[tid] =
+        make_int4(ex_g + loc_g[0], ex_g + loc_g[1], ex_g + loc_g[2], ex_g + loc_g[3]);
+  }
   if (tid == 0) {
     meta[0] = tg;
     meta[1] = tt;
@@ -241,6 +260,10 @@ __device__ __forceinline__ void pl_plan_body(
     meta[3] = pl_plan_positions(tg);
   }
   __syncthreads();
+  if (S <= 4 * 64) {
+    tt = wsum[0][0];
+    tg = wsum[1][0];
+  }
 
   // One thread per group (a slot can have hundreds): the group's slot is
   // the last s with goff[s] <= gi (a slot with no groups shares its goff
