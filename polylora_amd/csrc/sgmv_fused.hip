@@ -202,14 +202,22 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
   };
   if constexpr (MODE == PL_FUSED_EXPAND) {
     // the intermediate comes from the caller: x[token][0 .. rank), model
-    // dtype, row stride ldx; zeros past the rank and past the tile's tokens
-    for (int i = tid; i < 16 * L::kTRow; i += kFThreads) {
-      const int r = i / L::kTRow;
-      const int j = i - r * L::kTRow;
-      T v = (T)0.f;
-      if (r < len && j < rank) v = x[(int64_t)a.tok[grp.start + r] * a.ldx + j];
-      tt[i] = v;
-    }
+    // dtype, row stride ldx; zeros past the rank and past the tile's tokens.
+    // Thread (row 4*wave + lg, ranks 4*li .. +3): the row's token index is
+    // xtok[wave] (row lg + 4*wave), already loaded, so the four element
+    // loads go out together
+    static_assert(kFThreads == 16 * 16 && kFRankMax == 4 * 16, "one thread per row and 4 ranks");
+    const int r = 4 * wave + lg;
+    const int j0 = 4 * li;
+    int t = xtok[0];
+#pragma unroll
+    for (int i = 1; i < kFXLoads; ++i)
+      if (wave == i) t = xtok[i];
+    const T* xr = x + (int64_t)t * a.ldx;
+    T4 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = (r < len && j0 + q < rank) ? xr[j0 + q] : (T)0.f;
+    *reinterpret_cast<T4*>(tt + r * L::kTRow + j0) = v;
   } else {
     // double-buffered K loop over pairs of steps; the last pair is peeled
     // so that no loads past k1 are left in flight when the shrink ends (its
