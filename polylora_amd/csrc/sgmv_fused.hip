@@ -300,11 +300,21 @@ __device__ __forceinline__ void pl_fused_body(const pl_fused_args& a, const pl_g
     __syncthreads();
   }
   if constexpr (MODE == PL_FUSED_SHRINK) {
-    // the rounded intermediate to y[token][0 .. rank); nothing else is written
-    for (int i = tid; i < len * rank; i += kFThreads) {
-      const int r = i / rank;
-      const int j = i - r * rank;
-      y[(int64_t)a.tok[grp.start + r] * ldy + j] = tt[r * L::kTRow + j];
+    // the rounded intermediate to y[token][0 .. rank); nothing else is
+    // written.  Thread (row 4*wave + lg, ranks 4*li .. +3), the row's token
+    // index from the prologue's registers (xtok[wave] holds row lg + 4*wave)
+    const int r = 4 * wave + lg;
+    const int j0 = 4 * li;
+    if (r < len) {
+      int t = xtok[0];
+#pragma unroll
+      for (int i = 1; i < kFXLoads; ++i)
+        if (wave == i) t = xtok[i];
+      const T4 v = *reinterpret_cast<const T4*>(tt + r * L::kTRow + j0);
+      T* yr = y + (int64_t)t * ldy;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (j0 + q < rank) yr[j0 + q] = v[q];
     }
     return;
   }
