@@ -35,7 +35,9 @@ def _adapters(gen, ranks, fin, fout, module="m", extra_module=None):
 @pytest.mark.parametrize(
     "rows,row_len,num_slots,seed",
     [(1, 1, 2, 0), (7, 3, 5, 1), (256, 1, 65, 2), (32, 1024, 9, 3), (4096, 1, 17, 4), (3, 200, 4096, 5), (0, 5, 3, 6),
-     (10000, 1, 33, 7), (9000, 2, 5, 8)],
+     (10000, 1, 33, 7), (9000, 2, 5, 8),
+     # at most 256 slots one wave scans the slot counts; from 257 on every wave takes part
+     (5000, 1, 256, 9), (5000, 1, 257, 10), (3000, 2, 1025, 11)],
 )
 def test_plan_matches_oracle(gpu, rows, row_len, num_slots, seed, group_tokens):
     _announce(test="plan", rows=rows, row_len=row_len, num_slots=num_slots, group_tokens=group_tokens)
