@@ -72,18 +72,23 @@ def _sub_batches(ids, limit):
     return out
 
 
-@pytest.mark.parametrize("limit", [24, 32])
-def test_churn_config_every_layer_against_the_oracle(gpu, limit):
+@pytest.mark.parametrize("limit,spare", [(24, True), (32, True), (32, False)])
+def test_churn_config_every_layer_against_the_oracle(gpu, limit, spare, monkeypatch):
     """Config 5 shapes on 2 layers: 96 distinct rank-16 adapters (40 pinned, 56 pageable) through 32 slots,
     in sub-batches of at most `limit` distinct adapters (at 32 every slot is in use, and each load copies
-    into a spare arena region while the previous sub-batch's forward reads the slot's old one)."""
-    _announce(test="churn_config", limit=limit)
+    into a spare arena region while the previous sub-batch's forward reads the slot's old one; without
+    spare regions each load rewrites its slot in place after that forward)."""
+    _announce(test="churn_config", limit=limit, spare=spare)
     from transformers import DynamicCache
 
     from bench import build_llama
+    from polylora_amd.cache import GpuAdapterCache
 
+    if not spare:
+        monkeypatch.setattr(GpuAdapterCache, "SPARE_REGION_BYTES", 0)
     model = build_llama(gpu, layers=2, seed=1005)
     pm = PolyLoraModel(model, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=32, max_rank=16)).eval()
+    assert pm.adapter_cache.spare_regions == (32 if spare else 0)
     shapes = {s.name: (s.in_features, s.out_features) for s in pm.module_specs}
     image_bytes = sum(16 * (fi + fo) * 2 for fi, fo in shapes.values())
     pm.adapter_store.pinned_bytes_limit = 40 * image_bytes  # the rest stay pageable: loads go through staging
