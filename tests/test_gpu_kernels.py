@@ -97,6 +97,9 @@ CASES = [
     (torch.bfloat16, 2048, 1, 1024, 512, [80, 128, 8, 64, 33], 128, 4, 23),
     # 16 K splits: the expand sums 16 planes
     (torch.bfloat16, 24, 2, 4096, 768, [8, 64, 32], 64, 16, 24),
+    # fp16 at the decode shapes, and on the wide short shrink with 32-rank expand blocks
+    (torch.float16, 256, 1, 4096, 4096, [8, 16, 32, 64], 64, None, 25),
+    (torch.float16, 2048, 1, 1024, 3072, [8, 16, 32, 64, 8, 16, 32, 64], 64, 4, 26),
 ]
 
 
