@@ -31,7 +31,9 @@ free region the image is rewritten in place, after the slot's readers.  Slot
 
 ``ranks[module]`` and ``scales[module]`` remain int32 / fp32 device tensors
 indexed by slot (views into the table), as in the reference.  ``A`` and
-``B`` return reference-layout tensors materialised from the arena on request.
+``B`` return reference-layout tensors materialised from the arena on request;
+writes into them raise (``SlotWeightsSnapshot``), since they would not reach
+the arena the kernels read.
 
 Slot choice, LRU order and error behaviour follow cache.py:60-162, including
 the set-iteration order of ``ensure_resident``'s touch loop.
@@ -55,15 +57,65 @@ __all__ = ["GpuAdapterCache", "ModuleSpec", "SlotLayout", "tile_rows", "untile_r
 _ENTRY_INTS = _native.SLOT_ENTRY_INT32S  # int32 words per (slot, module) entry
 
 
+_NOT_WRITES = {"requires_grad_", "share_memory_", "retain_grad", "__set_state__"}
+_AUGMENTED = {"__setitem__", "__iadd__", "__isub__", "__imul__", "__itruediv__", "__ifloordiv__", "__imod__",
+              "__ipow__", "__iand__", "__ior__", "__ixor__", "__ilshift__", "__irshift__", "__imatmul__"}
+
+
+class SlotWeightsSnapshot(torch.Tensor):
+    """A reference-layout copy of slot weights (``cache.A[m]`` / ``cache.B[m]``) that refuses writes.
+
+    In the reference these are the live slot tensors the kernels read
+    (cache.py:43-56).  Here the kernels read the packed arena, and this
+    tensor is built from it on access, so a write into it would be lost
+    without a trace: every in-place op, item assignment or ``out=`` into it
+    or into a view of it raises RuntimeError instead.  Results that do not
+    share its memory (``clone()``, arithmetic) are plain tensors.
+    """
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        name = getattr(func, "__name__", "")
+        target = args[0] if args else None
+        write = name in _AUGMENTED or (name.endswith("_") and not name.endswith("__") and name not in _NOT_WRITES)
+        outs = kwargs.get("out")
+        outs = outs if isinstance(outs, (tuple, list)) else (outs,)
+        if (write and isinstance(target, cls)) or any(isinstance(o, cls) for o in outs):
+            raise RuntimeError(
+                f"GpuAdapterCache.A/.B are reference-layout copies of the packed slot arena; {name} into one "
+                "would not reach the kernels.  Load changed weights as an adapter instead "
+                "(add_adapter_from_peft_state_dict / load_adapter_from_disk).")
+        with torch._C.DisableTorchFunctionSubclass():
+            ret = func(*args, **kwargs)
+        return _keep_views(ret, target, cls)
+
+
+def _keep_views(ret, source, cls):
+    """Outputs that share ``source``'s memory stay snapshots (so writes through them raise); others are plain."""
+    if isinstance(ret, (tuple, list)):
+        return type(ret)(_keep_views(r, source, cls) for r in ret)
+    if isinstance(ret, torch.Tensor) and isinstance(source, torch.Tensor):
+        try:
+            shared = ret.untyped_storage().data_ptr() == source.untyped_storage().data_ptr()
+        except RuntimeError:
+            shared = False
+        if shared and ret.untyped_storage().nbytes() > 0:
+            return ret.as_subclass(cls)
+        if type(ret) is not torch.Tensor:
+            return ret.as_subclass(torch.Tensor)
+    return ret
+
+
 class _ReferenceLayoutWeights(Mapping):
-    """``cache.A`` / ``cache.B`` in the reference layout, built from the arena on access."""
+    """``cache.A`` / ``cache.B`` in the reference layout, built from the arena on access (write-protected)."""
 
     def __init__(self, cache: "GpuAdapterCache", side: str) -> None:
         self._cache = cache
         self._side = side
 
     def __getitem__(self, name: str) -> torch.Tensor:
-        return self._cache._materialize(name, self._side)
+        return self._cache._materialize(name, self._side).as_subclass(SlotWeightsSnapshot)
 
     def __iter__(self):
         return iter(self._cache.module_specs)

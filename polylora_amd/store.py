@@ -145,7 +145,8 @@ class CpuAdapter:
 
         Raises the reference's slot-load errors (cache.py:129-136) for a rank
         above the layout's cap or a module of the wrong shape.  With
-        ``keep_source=False`` the PEFT tensors are dropped once packed.
+        ``keep_source=False`` the PEFT tensors are dropped once packed, unless
+        packing rounded them (a source dtype wider than the layout's).
         """
         if self._image is not None and self._image.layout.key == layout.key:
             return self._image
@@ -167,12 +168,22 @@ class CpuAdapter:
         for name, (lora_a, lora_b, _, _) in present.items():
             builder.put(name, lora_a, lora_b)
         image = builder.finish()
+        # the source tensors stay whenever packing rounded them: a later layout of
+        # another dtype packs from them, as the reference converts its source-dtype
+        # copy at every slot load (store.py:240-241, cache.py:139)
+        keep_source = keep_source or (self._modules is not None and any(
+            rounds(a.dtype, layout.dtype) or rounds(b.dtype, layout.dtype) for a, b, _, _ in present.values()))
         # modules outside the layout are not part of any slot and are not kept
         self._ranks = {n: self._ranks[n] for n in self._ranks if n in specs} if not keep_source else self._ranks
         self._image = image
         if not keep_source:
             self._modules = None
         return image
+
+
+def rounds(src: torch.dtype, dst: torch.dtype) -> bool:
+    """Whether converting values of dtype ``src`` to ``dst`` can change them."""
+    return src != dst and not (dst == torch.float32 and src in (torch.bfloat16, torch.float16))
 
 
 # --------------------------------------------------------------------------- PEFT files
@@ -425,7 +436,9 @@ class CpuAdapterStore:
     Adapters that are resident on the GPU (``set_eviction_exclusions``) are
     never evicted.  With a slot layout bound (``bind_layout``, done by the GPU
     cache) every adapter added is packed into its pinned slot image at once
-    and its PEFT tensors are not kept.
+    and its PEFT tensors are not kept, unless packing rounded them (source
+    dtype wider than the layout's): those stay, in their own dtype, so that a
+    later layout of another dtype packs from them.
     """
 
     def __init__(
@@ -483,7 +496,8 @@ class CpuAdapterStore:
         self.layout = layout
 
     def image(self, adapter: CpuAdapter, layout: SlotLayout) -> AdapterImage:
-        """``adapter`` packed for ``layout``; its PEFT tensors are dropped when that is the bound layout."""
+        """``adapter`` packed for ``layout``; its PEFT tensors are dropped when that is the bound layout
+        and packing did not round them."""
         bound = self.layout is not None and self.layout.key == layout.key
         return adapter.image_for(layout, keep_source=not bound, pin=self.pin_image)
 
@@ -573,8 +587,9 @@ class CpuAdapterStore:
                 raise ValueError(f"Adapter {adapter_id!r} has non-positive rank for {name!r}")
             if int(lora_b.shape[1]) != rank:
                 raise ValueError(f"LoRA A/B rank mismatch for adapter {adapter_id!r}, module {name!r}")
-            if self.layout is None:
-                # held until a layout is bound: an owned CPU copy, independent of the caller's tensors
+            if self.layout is None or rounds(lora_a.dtype, self.layout.dtype) or rounds(lora_b.dtype, self.layout.dtype):
+                # held beside or instead of the image (no layout bound yet, or packing rounds
+                # them): an owned CPU copy in the source dtype, independent of the caller's tensors
                 lora_a, lora_b = lora_a.to("cpu", copy=True), lora_b.to("cpu", copy=True)
             modules[name] = _Module(lora_a, lora_b, rank, float(lora_alpha) / rank)
         self._insert(adapter_id, modules, config)

@@ -12,6 +12,10 @@
 * Decode (32 Llama-3-8B layers, 64 slots, ranks {8,16,32,64}, 256 rows over
   a 512-token KV cache, Zipf(1.1) with 10% base rows): one decode step with
   all 224 wrapped layers checked.
+* Prefill through the model (2 Llama-3-8B layers, 32 rows x 1024, U[512,1024]
+  right-padded lengths, 8 adapters of ranks 16 and 32, 4 rows each): two
+  forwards of PolyLoraModel, one fused launch per Linear and then the stacked
+  fused launches, all 14 wrapped layers checked each time.
 """
 
 from __future__ import annotations
@@ -148,3 +152,57 @@ def test_decode_config_step_every_layer_against_the_oracle(gpu):
                  adapter_ids=wl.adapter_ids).last_hidden_state
     assert checked.count == len(pm.target_module_names) == 224
     assert torch.isfinite(out.float()).all()
+
+
+def test_prefill_config_through_the_model_every_layer_against_the_oracle(gpu, monkeypatch):
+    """PolyLoraModel.forward (model.py:75-85) -> MultiLoraLinear (layers.py:33-62) at the prefill batch on two
+    Llama-3-8B-shaped layers: the plan takes 64-token groups; the first forward runs one fused launch per
+    Linear, the second the stacked fused launches for q/k/v and gate/up; every wrapped layer against the
+    oracle on the inputs it saw, both times."""
+    _announce(test="prefill_config_model")
+    from bench import add_random_adapters, build_llama
+
+    model = build_llama(gpu, layers=2, seed=1004, attn="pl_safe_fp32")
+    pm = PolyLoraModel(model, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=64, max_rank=64)).eval()
+    names = [f"pf{i}" for i in range(8)]
+    ranks = {n: (16 if i < 4 else 32) for i, n in enumerate(names)}
+    add_random_adapters(pm, ranks, seed=1004, device=gpu)
+    ads = {aid: (_StoreWeights(pm.adapter_store.adapters[aid]), 2.0 * r) for aid, r in ranks.items()}
+    rng = np.random.default_rng(1004)
+    B, S = 32, 1024
+    lens = rng.integers(512, S + 1, size=B)
+    adapter_ids = [names[i // 4] for i in range(B)]
+    mask = (torch.arange(S)[None, :] < torch.as_tensor(lens)[:, None]).long().to(gpu)
+    gen = torch.Generator(device=gpu).manual_seed(1004)
+    ids = torch.randint(0, model.config.vocab_size, (B, S), generator=gen, device=gpu)
+    launches = []
+    single, stacked = sgmv._fused_launch, sgmv.lora_fused_stacked
+
+    def record_single(x, y, cache, module_name, plan, *a, **k):
+        launches.append(("single", module_name.rsplit(".", 1)[-1], plan.group_tokens))
+        return single(x, y, cache, module_name, plan, *a, **k)
+
+    def record_stacked(x, ys, cache, module_names, plan, *a, **k):
+        launches.append(("stacked", tuple(n.rsplit(".", 1)[-1] for n in module_names), plan.group_tokens))
+        return stacked(x, ys, cache, module_names, plan, *a, **k)
+
+    monkeypatch.setattr(sgmv, "_fused_launch", record_single)
+    monkeypatch.setattr(sgmv, "lora_fused_stacked", record_stacked)
+    outs = []
+    for forward in range(2):
+        launches.clear()
+        with torch.inference_mode(), _per_layer_check(pm, ads, torch.bfloat16, label=f"prefill forward {forward}") as chk:
+            outs.append(pm(input_ids=ids, attention_mask=mask, adapter_ids=adapter_ids).last_hidden_state.clone())
+        assert chk.count == len(pm.target_module_names) == 14 and chk.calls == 14
+        assert {gt for _, _, gt in launches} == {64}, launches  # 64-token groups: the prefill plan
+        kinds = sorted(launches)
+        if forward == 0:
+            assert kinds == sorted(("single", m, 64) for m in LLAMA_TARGETS * 2), kinds
+        else:
+            want = [("single", "o_proj", 64), ("single", "down_proj", 64), ("stacked", ("q_proj", "k_proj", "v_proj"), 64),
+                    ("stacked", ("gate_proj", "up_proj"), 64)] * 2
+            assert kinds == sorted(want), kinds
+    valid = mask.bool()
+    assert torch.isfinite(outs[1][valid].float()).all()
+    assert torch.equal(outs[0], outs[1])  # stacked launches give the single launches' results bit for bit
+

@@ -327,14 +327,16 @@ def test_prefill_config_stacked_fused_bf16(gpu):
 
 def test_decode_config_stacked_split_bf16(gpu):
     """Decode size: 256 rows of one token, 64 adapters of ranks {8,16,32,64}, Zipf(1.1) choice with 10%
-    base rows; q/k/v of a 4096-wide model through one stacked shrink and one stacked expand, and
-    down_proj (K=14336, 8 K splits) alone, every row against the oracle."""
+    base rows; every module of a Llama-3-8B layer as the decode step launches it: q/k/v through one
+    stacked shrink and one stacked expand, o (4096 -> 4096) alone, gate/up (4096 -> 14336 each) stacked,
+    and down (K=14336, more K splits) alone, every row against the oracle at the plain tolerance."""
     _announce(test="decode_config_stacked_split")
     from bench import zipf_ids
 
     g = torch.Generator().manual_seed(1003)
     rng = np.random.default_rng(1003)
-    shapes = {"q": (4096, 4096), "k": (4096, 1024), "v": (4096, 1024), "down": (14336, 4096)}
+    shapes = {"q": (4096, 4096), "k": (4096, 1024), "v": (4096, 1024), "o": (4096, 4096), "gate": (4096, 14336),
+              "up": (4096, 14336), "down": (14336, 4096)}
     names = [f"d{i:02d}" for i in range(64)]
     ranks = {n: int(rng.choice([8, 16, 32, 64])) for n in names}
     adapters = {n: {m: peft_layer(g, fi, fo, ranks[n], 2.0 * ranks[n]) for m, (fi, fo) in shapes.items()} for n in names}
@@ -346,19 +348,23 @@ def test_decode_config_stacked_split_bf16(gpu):
     plan = sgmv.SgmvPlan(row_slot, seq, 1, cache.num_slots, distinct_slots=distinct)
     assert plan.group_tokens == 16 and not sgmv.fused_ok(plan, cache, 4096)
     gg = torch.Generator(device=gpu).manual_seed(1003)
-    xs = {K: torch.randn(256, K, generator=gg, device=gpu).to(torch.bfloat16) for K in (4096, 14336)}
+    xs = {m: torch.randn(256, fi, generator=gg, device=gpu).to(torch.bfloat16) for m, (fi, fo) in shapes.items()}
+    for m in ("k", "v"):
+        xs[m] = xs["q"]
+    xs["up"] = xs["gate"]
     base = {m: torch.randn(256, fo, generator=gg, device=gpu).to(torch.bfloat16) for m, (fi, fo) in shapes.items()}
-    qkv = ["q", "k", "v"]
     ys = {m: base[m].clone() for m in shapes}
-    results = sgmv.lora_shrink_stacked(xs[4096], cache, qkv, plan)
-    sgmv.lora_expand_stacked(results, [ys[m] for m in qkv], cache, qkv)
-    res = sgmv.lora_shrink(xs[14336], cache, "down", plan)
-    sgmv.lora_expand(res, ys["down"], cache, "down")
+    for run in (["q", "k", "v"], ["gate", "up"]):
+        results = sgmv.lora_shrink_stacked(xs[run[0]], cache, run, plan)
+        sgmv.lora_expand_stacked(results, [ys[m] for m in run], cache, run)
+    for m in ("o", "down"):
+        res = sgmv.lora_shrink(xs[m], cache, m, plan)
+        sgmv.lora_expand(res, ys[m], cache, m)
     torch.cuda.synchronize()
     for m, (fi, fo) in shapes.items():
         A, Bm, rk, sc = (t.to(gpu) for t in oracle_slot_tensors(cache, adapters, m, torch.bfloat16))
-        expect = reference_forward(xs[fi].view(256, 1, fi), base[m].view(256, 1, fo), seq, row_slot, A, Bm, rk, sc)
-        torch.testing.assert_close(ys[m].view(256, 1, fo), expect, rtol=2e-2, atol=1e-2)
+        expect = reference_forward(xs[m].view(256, 1, fi), base[m].view(256, 1, fo), seq, row_slot, A, Bm, rk, sc)
+        torch.testing.assert_close(ys[m].view(256, 1, fo), expect, rtol=2e-2, atol=1e-2, msg=lambda s, m=m: f"{m}: {s}")
         untouched = (row_slot == 0)
         assert torch.equal(ys[m][untouched], base[m][untouched])
 

@@ -100,6 +100,27 @@ def test_dtype_change_after_fused_forward(gpu):
     assert float(diff) < 1e-2, float(diff)
 
 
+def test_dtype_widening_repacks_from_source_weights(gpu):
+    """fp32 PEFT adapters added to a bf16 model, a bf16 forward, then .to(float32): the fp32 forward (a resident
+    adapter rewritten into the new arena, and one loaded for the first time) matches the fp32 oracle at rtol
+    1e-5, which the bf16-rounded weights would miss (store.py:240-241, cache.py:139 convert at every load)."""
+    _announce(test="dtype_widening")
+    base, cfg = _tiny_llama(43, torch.bfloat16, gpu)
+    pm = PolyLoraModel(copy.deepcopy(base), PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=2,
+                                                           max_rank=16)).eval()
+    g = torch.Generator().manual_seed(43)
+    ads = _add_adapters(pm, g, [8, 16, 4], "w")
+    ids = torch.randint(0, 211, (4, 5), generator=g).to(gpu)
+    with torch.inference_mode(), _per_layer_check(pm, ads, torch.bfloat16, label="bf16") as checked:
+        pm(input_ids=ids, adapter_ids=["w0", "w1", "__base__", "w0"])
+    assert checked.count == len(pm.target_module_names)
+    pm.to(torch.float32)  # the adapter cache follows at the next forward (model.py:75-85 infers the dtype)
+    with torch.inference_mode(), _per_layer_check(pm, ads, torch.float32, label="fp32") as checked:
+        pm(input_ids=ids, adapter_ids=["w0", "w2", "w2", "__base__"])  # w0 resident since bf16, w2 loaded now
+    assert pm.adapter_cache.dtype == torch.float32
+    assert checked.count == len(pm.target_module_names)
+
+
 def test_prepare_context_eviction_waits_for_queued_readers(gpu):
     """max_gpu_adapters=1: a forward for "a" under prepare_lora_context/use_lora_context sits behind a long
     queue of GPU work when prepare_lora_context(["b"]) evicts "a"; its output is still "a"'s."""

@@ -262,19 +262,35 @@ def test_closed_form_catches_planted_oracle_mistakes(monkeypatch, mutant, name):
     assert not torch.allclose(got, want, **FP32), (mutant.__name__, name)
 
 
-def test_sum_bound_accepts_an_operand_ulp_and_rejects_wrong_deltas():
-    """The per-layer GPU check's bound: an ulp of the operands at a cancellation passes, mistakes fail."""
-    from tests.test_gpu_model import BF16, assert_close_sum
+def test_counted_parity_exempts_one_operand_ulp_at_a_cancellation_and_nothing_else():
+    """The per-layer GPU check: plain rtol/atol everywhere; a cancellation one ulp of the operands off is exempt
+    but counted and capped; wrong deltas, two-ulp misses and too many exemptions fail."""
+    from tests._util import CountedParity, ulp_of
 
+    assert float(ulp_of(torch.tensor(2.5), torch.bfloat16)) == 2.0 ** -6
+    assert float(ulp_of(torch.tensor(1.0), torch.bfloat16)) == 2.0 ** -7
+    assert float(ulp_of(torch.tensor(3.0), torch.float32)) == 2.0 ** -22
+    assert float(ulp_of(torch.tensor(0.0), torch.bfloat16)) == 0.0
     g = torch.Generator().manual_seed(7)
-    base = (torch.randn(64, 256, generator=g) * 2).bfloat16()
-    delta = (torch.randn(64, 256, generator=g) * 2).bfloat16()
+    base = (torch.randn(512, 256, generator=g) * 2).bfloat16()
+    delta = (torch.randn(512, 256, generator=g) * 2).bfloat16()
     want = (base.float() + delta.float()).bfloat16()
-    delta[0, 0] = -base[0, 0]  # exact cancellation: want 0, got one ulp of |base|
-    want[0, 0] = 0
+    base[0, 0], delta[0, 0] = 2.25, -2.125  # want 0.125, one ulp of the operands is 2**-6
+    want[0, 0] = 0.125
     got = want.clone()
-    got[0, 0] = torch.finfo(torch.bfloat16).eps * base[0, 0].abs().float()
-    assert_close_sum(got, want, base, BF16)
+    got[0, 0] = 0.125 + 2.0 ** -6  # beyond atol + rtol * |want| = 0.0125
+    p = CountedParity(torch.bfloat16, "t")
+    p.check(got, want, base)
+    assert p.exempt == 1 and p.checked == got.numel()
+    p.finish()  # 1 <= 1e-5 * 131072
+    two = got.clone()
+    two[0, 0] = 0.125 + 2.0 ** -5  # two ulps: not exempt
+    with pytest.raises(AssertionError):
+        CountedParity(torch.bfloat16).check(two, want, base)
+    p = CountedParity(torch.bfloat16)
+    p.check(got[:64], want[:64], base[:64])  # one exemption in 16384 elements: over the cap
+    with pytest.raises(AssertionError):
+        p.finish()
     for wrong in (base.float() + 2 * delta.float(), base.float(), base.float() - delta.float()):
         with pytest.raises(AssertionError):
-            assert_close_sum(wrong.bfloat16(), want, base, BF16)
+            CountedParity(torch.bfloat16).check(wrong.bfloat16(), want, base)

@@ -37,13 +37,14 @@ def _weights(seed, rank, modules=None):
     return _peft.make_lora_weights(torch.Generator().manual_seed(seed), SHAPES, rank, modules=modules)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_bound_store_holds_only_the_packed_image(dtype):
+@pytest.mark.parametrize("dtype,src", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
+                                       (torch.float32, torch.bfloat16)])
+def test_bound_store_holds_only_the_packed_image(dtype, src):
     store, cache = _bound(dtype)
-    w = _weights(0, 5)
+    w = {m: (a.to(src), b.to(src)) for m, (a, b) in _weights(0, 5).items()}
     store.add_adapter_from_peft_state_dict("a", _peft.state_dict(w), list(SHAPES), lora_alpha=10)
     ad = store.adapters["a"]
-    assert ad.image is not None and ad._modules is None  # no PEFT tensors kept beside the image
+    assert ad.image is not None and ad._modules is None  # packing is exact: no PEFT tensors kept beside the image
     for mod, (a, b) in w.items():
         lw = ad.layers[mod]
         assert lw.rank == 5 and lw.scale == 2.0
@@ -95,13 +96,17 @@ def test_read_safetensors_matches_the_library(tmp_path):
 
 
 @pytest.mark.parametrize("fmt", ["safetensors", "bin"])
-def test_disk_load_packs_straight_into_the_image(tmp_path, fmt):
-    w = _weights(3, 4)
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float32])
+def test_disk_load_packs_straight_into_the_image(tmp_path, fmt, src):
+    w = {m: (a.to(src), b.to(src)) for m, (a, b) in _weights(3, 4).items()}
     path = _peft.write_adapter_dir(tmp_path / "ad", w, 4, 8, fmt=fmt)
     store, cache = _bound()
     store.load_adapter_from_disk("d", path, list(SHAPES))
     ad = store.adapters["d"]
-    assert ad._modules is None
+    # bf16 files into a bf16 layout: only the image; fp32 files: their fp32 copy stays too
+    assert (ad._modules is None) == (src == torch.bfloat16)
+    for mod, (a, b) in w.items():
+        assert torch.equal(ad.layers[mod].A, a.t()) and torch.equal(ad.layers[mod].B, b.t())
     free = CpuAdapterStore()
     free.add_adapter_from_peft_state_dict("d", _peft.state_dict(w), list(SHAPES), lora_alpha=8)
     assert torch.equal(free.adapters["d"].image_for(cache.layout).data, ad.image.data)
@@ -156,3 +161,57 @@ def test_dtype_change_repacks_resident_adapters():
     for mod, (a, b) in w.items():
         assert torch.equal(store.adapters["r"].layers[mod].A, a.t().bfloat16())
     assert torch.equal(cache.A["enc.q_proj"][cache.adapter_to_slot["r"], :, :3], w["enc.q_proj"][0].t().bfloat16())
+
+
+def test_source_dtype_kept_when_packing_rounds_and_a_later_dtype_packs_from_it():
+    """fp32 PEFT tensors into a bf16-bound store keep their fp32 copy (the reference holds the source dtype and
+    converts at every slot load, store.py:240-241, cache.py:139): after the cache moves to fp32, the adapter's
+    slot image and its CpuLayerWeights are the fp32 values exactly, for adapters added before and after."""
+    store, cache = _bound(torch.bfloat16)
+    w = _weights(3, 4)
+    store.add_adapter_from_peft_state_dict("early", _peft.state_dict(w), list(SHAPES), lora_alpha=8)
+    ad = store.adapters["early"]
+    assert ad.image.layout.dtype == torch.bfloat16 and ad._modules is not None
+    for mod, (a, b) in w.items():
+        assert ad.layers[mod].A.dtype == torch.float32 and torch.equal(ad.layers[mod].A, a.t())
+    cache.ensure_resident(["early"])
+    cache.to(torch.device("cpu"), torch.float32)
+    w2 = _weights(4, 3)
+    store.add_adapter_from_peft_state_dict("late", _peft.state_dict(w2), list(SHAPES), lora_alpha=6)
+    assert store.adapters["late"]._modules is None  # fp32 into fp32: exact, nothing kept beside the image
+    for aid, ws in (("early", w), ("late", w2)):
+        img = store.image(store.adapters[aid], cache.layout)
+        assert img.layout.dtype == torch.float32
+        for mod, (a, b) in ws.items():
+            got_a, got_b, _ = img.lora_tensors(mod)
+            assert torch.equal(got_a, a) and torch.equal(got_b, b), (aid, mod)
+    # the resident adapter was rewritten into the fp32 arena from its fp32 source
+    slot = cache.adapter_to_slot["early"]
+    img = store.adapters["early"].image
+    off = cache.slot_offset(slot)
+    assert torch.equal(cache.arena[off : off + img.nbytes], img.data[: img.nbytes])
+
+
+def test_reference_layout_slot_tensors_refuse_writes():
+    """cache.A[m] / cache.B[m] hold the reference layout (cache.py:43-56) as copies of the arena: reads work, and
+    every write into them or a view of them raises instead of being lost."""
+    store, cache = _bound(torch.float32)
+    w = _weights(0, 4)
+    store.add_adapter_from_peft_state_dict("a", _peft.state_dict(w), list(SHAPES), lora_alpha=8)
+    cache.ensure_resident(["a"])
+    slot = cache.adapter_to_slot["a"]
+    for mod, (a, b) in w.items():
+        A, B = cache.A[mod], cache.B[mod]
+        assert torch.equal(A[slot, :, :4], a.t()) and torch.equal(B[slot, :4, :], b.t())
+        assert not A[slot, :, 4:].any() and not A[0].any()
+    A = cache.A["enc.q_proj"]
+    writes = [lambda: A[slot, :, :2].zero_(), lambda: A.copy_(torch.zeros_like(A)), lambda: A.__setitem__(slot, 0.0),
+              lambda: torch.add(A, 1, out=A), lambda: A[slot].add_(1), lambda: A.view(-1).fill_(0),
+              lambda: A.__iadd__(1)]
+    for write in writes:
+        with pytest.raises(RuntimeError, match="would not reach the kernels"):
+            write()
+    c = A.clone()
+    c.add_(1)  # a copy is an ordinary tensor
+    assert type(c) is torch.Tensor and type(A * 2) is torch.Tensor
+    assert torch.equal(cache.A["enc.q_proj"], A)  # nothing was written
