@@ -544,6 +544,44 @@ class StackedLaunch:
         self.n.check(self.lib.pl_sgmv_expand_stacked(*self.expand_args), "pl_sgmv_expand_stacked")
 
 
+class DecodeLaunch:
+    """Sibling Linears fed the same x: shrink and expand in one launch with the hand-off inside it
+    (pl_lora_decode_stacked), arguments bound once; its own planes and zeroed hand-off counters."""
+
+    def __init__(self, x, ys, cache, modules, plan, k_splits=None):
+        import ctypes
+
+        from polylora_amd import _native, sgmv
+
+        self.lib, self.n = _native.load(), _native
+        s = torch.cuda.current_stream().cuda_stream
+        dt = _native.dtype_code(x.dtype)
+        K = int(x.shape[1])
+        n = len(modules)
+        splits = k_splits if k_splits is not None else sgmv.choose_k_splits(plan.group_cap, K, x.dtype)
+        rows = max(1, plan.tokens_cap)
+        ldt = -(-cache.rank8_cap // 32) * 32
+        gt = plan.group_tokens
+        cap = max(1, plan.group_cap)
+        nbytes = int(self.lib.pl_shrink_workspace_bytes(dt, K, splits, gt, rows, ldt))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=x.device) for _ in modules]
+        ints = int(self.lib.pl_decode_counter_ints(cap, n))
+        self.counters = torch.zeros(ints, dtype=torch.int32, device=x.device)
+        self.mods = (ctypes.c_int32 * n)(*(cache.module_index[m] for m in modules))
+        self.ptrs = (ctypes.c_void_p * n)(*(b.data_ptr() for b in bufs))
+        self.yptrs = (ctypes.c_void_p * n)(*(y.data_ptr() for y in ys))
+        self.ldys = (ctypes.c_int64 * n)(*(y.stride(0) for y in ys))
+        self.Ns = (ctypes.c_int32 * n)(*(int(y.shape[1]) for y in ys))
+        self.args = (dt, x.data_ptr(), x.stride(0), K, cache.arena.data_ptr(), cache.table.data_ptr(),
+                     len(cache.module_index), n, self.mods, self.ptrs, plan.tok.data_ptr(), plan.groups.data_ptr(),
+                     plan.meta.data_ptr(), cap, gt, nbytes, ldt, rows, splits, self.yptrs, self.ldys, self.Ns,
+                     _native.PL_EPI_FALLBACK, self.counters.data_ptr(), ints, sgmv.DECODE_SPIN_LIMIT, s)
+        self.keep = (x, ys, bufs, plan)
+
+    def __call__(self):
+        self.n.check(self.lib.pl_lora_decode_stacked(*self.args), "pl_lora_decode_stacked")
+
+
 class FusedLaunch:
     """One wrapped Linear's fused shrink+expand (pl_lora_fused) with its arguments bound once."""
 
@@ -621,6 +659,16 @@ def _profiled(workload: str, *keys):
         for k in keys:
             data = data[k]
         return int(round(float(data)))
+    except (OSError, ValueError, KeyError, TypeError):
+        return None
+
+
+def _profiled_plan_us(workload: str):
+    """Average pl_plan_kernel duration (us) in the committed launch profile of `workload`, or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"sgmv_{workload}_traffic.json")
+    try:
+        with open(path, encoding="utf-8") as fh:
+            return round(float(json.load(fh)["plan_avg_us"]), 2)
     except (OSError, ValueError, KeyError, TypeError):
         return None
 
@@ -722,6 +770,14 @@ def run_isolated(args) -> dict:
         f_ms = time_launches([FusedLaunch(wl.x, wl.y, wl.cache, "op", wl.plan) for wl in sets], reps) / n_sets
 
     op_ms = time_operator_api(sets, max(20, args.steps // 2))["pair_ms"]
+    # the op with its plan: the device plan build and the op's launch(es), back to back
+    stream_h = torch.cuda.current_stream().cuda_stream
+    if fused:
+        with_plan = [f for wl in sets for f in (lambda: base_set.plan.rebuild(stream_h),
+                                                FusedLaunch(wl.x, wl.y, wl.cache, "op", wl.plan))]
+    else:
+        with_plan = [f for l in launches for f in (lambda: base_set.plan.rebuild(stream_h), l.shrink, l.expand)]
+    wp_ms = time_launches(with_plan, reps) / n_sets
 
     # a step is one lora_apply call through the Python host API (plan already
     # built, inputs resident); the calls queue back to back, so the device,
@@ -753,7 +809,14 @@ def run_isolated(args) -> dict:
             "algorithmic_bytes_per_step": nb["total"],
             "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
             "input_sets_rotated": n_sets,
-            "timing": "lora_apply calls back to back, device events around the timed steps",
+            "timing": "lora_apply calls back to back, device events around the timed steps; the device plan "
+                      "(pl_plan_build_active over the 4096 rows) is built once before the timed region, as a "
+                      "model forward builds it once for all of its wrapped Linears",
+            "plan_kernel_us_profiled": _profiled_plan_us("isolated"),
+            "op_with_plan_ms": round(wp_ms, 5),
+            "op_with_plan_gbs": round(nb["total"] / (wp_ms * 1e-3) / 1e9, 1),
+            "op_with_plan_note": "the plan build and the op's launch back to back per step, arguments bound once; "
+                                 "GB/s counts the op's bytes",
             "plan_group_tokens": base_set.plan.group_tokens,
             "lora_apply_kernels": "pl_lora_fused (one launch)" if fused else "pl_sgmv_shrink + pl_sgmv_expand",
             "split_shrink_ms": round(sh_ms, 5),
@@ -906,10 +969,12 @@ def forward_launch_sequence(pm, plan, xs: dict, T: int, gen) -> list:
     Sibling Linears that read the same input (q/k/v, gate/up) share one
     stacked launch, as MultiLoraLinear does once it has seen a forward.  Where
     the plan suits the fused kernel each set takes one pl_lora_fused(_stacked)
-    launch; otherwise one stacked shrink and one stacked expand.  Every module
-    type writes its own y, so siblings in one launch never share an output.
+    launch; decode-sized batches one pl_lora_decode_stacked launch (split
+    shrink and expand with the hand-off inside the launch); otherwise one
+    stacked shrink and one stacked expand.  Every module type writes its own
+    y, so siblings in one launch never share an output.
     """
-    from polylora_amd import sgmv
+    from polylora_amd import layers, sgmv
 
     cache = pm.adapter_cache
     device = cache.device
@@ -934,6 +999,10 @@ def forward_launch_sequence(pm, plan, xs: dict, T: int, gen) -> list:
             f = (FusedLaunch(xs[k], outs[0], cache, names[0], plan) if len(names) == 1
                  else StackedFusedLaunch(xs[k], outs, cache, names, plan))
             out.append(LaunchEntry(f"{tag} fused", "fused", names, f, f))
+            continue
+        if T < layers.OVERLAP_MIN_TOKENS and cache.decode_handoff and sgmv.decode_ok(plan):
+            d = DecodeLaunch(xs[k], outs, cache, names, plan)
+            out.append(LaunchEntry(f"{tag} decode", "fused", names, d, d))
             continue
         st = StackedLaunch(xs[k], outs, cache, names, plan)
         out.append(LaunchEntry(f"{tag} shrink", "shrink", names, st.shrink, st))
@@ -1230,15 +1299,24 @@ def run_decode(args) -> dict:
         out["lora_kernels_ms"] = round(kern_ms, 4)
         out["lora_kernels_gbs"] = round(kt["bytes"] / (kern_ms * 1e-3) / 1e9, 1)
         out["lora_kernels_pct_hbm"] = round(100 * kt["bytes"] / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
-        out["roofline"] = sequence_roofline("one decode step's LoRA launches (pl_shrink_short, pl_expand_short)",
+        out["roofline"] = sequence_roofline("one decode step's LoRA launches (pl_decode_fused: split-K shrink and "
+                                            "expand with the hand-off inside each launch)",
                                             kt["bytes"], kern_ms, kt["launches"], "decode")
-        out["lora_kernels_shrink_ms"] = round(kt["shrink_ms"], 4)
-        out["lora_kernels_expand_ms"] = round(kt["expand_ms"], 4)
         out["per_op_us_shrink_expand"] = kt["per_type_us"]
         out["lora_kernel_launches_per_step"] = kt["launches"]
-        out["lora_kernels_timing"] = ("the forward's launch sequence (one stacked shrink and one stacked expand for "
-                                      "q/k/v and for gate/up, a shrink and an expand for o and down) back to back "
-                                      "without the base model")
+        out["lora_kernels_timing"] = ("the forward's launch sequence (one launch each for q/k/v stacked, o, "
+                                      "gate/up stacked and down, shrink and expand inside it) back to back without "
+                                      "the base model")
+        # the same sequence as separate shrink and expand launches, for comparison
+        pm.adapter_cache.decode_handoff = False
+        try:
+            ks = time_lora_ops(pm, wl.adapter_ids, 1, torch.ones(B, dtype=torch.int32, device=device), reps=5)
+        finally:
+            pm.adapter_cache.decode_handoff = True
+        out["lora_kernels_ms_split_pairs"] = round(ks["pairs_ms"], 4)
+        out["lora_kernel_launches_split_pairs"] = ks["launches"]
+        out["lora_kernels_split_pairs_shrink_ms"] = round(ks["shrink_ms"], 4)
+        out["lora_kernels_split_pairs_expand_ms"] = round(ks["expand_ms"], 4)
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_layer(pm, wl.adapter_ids, args.cpu_seconds)
         _log(f"decode: kernels {out['lora_kernels_gbs']} GB/s")
@@ -1524,7 +1602,7 @@ def run_churn(args) -> dict:
 
 # ----------------------------------------------------------------------------- main
 # ----------------------------------------------------------------------------- launch profiles
-SEQUENCE_KERNELS = ("pl_shrink", "pl_expand", "pl_lora_fused", "pl_refop", "pl_plan")
+SEQUENCE_KERNELS = ("pl_shrink", "pl_expand", "pl_lora_fused", "pl_decode_fused", "pl_refop", "pl_plan")
 PLAN_KERNEL = "pl_plan_kernel"
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
@@ -1582,8 +1660,12 @@ def launch_profile(args) -> int:
         if kind == "decode":
             wl = decode_workload(device, layers=args.decode_layers, kv_cache=False)
             pm, ids, tpr, lens = wl.model, wl.adapter_ids, 1, [1] * len(wl.adapter_ids)
+            split = getattr(args, "profile_split_pairs", False)
+            pm.adapter_cache.decode_handoff = not split
             desc = (f"Llama-3-8B-shaped decode, {args.decode_layers} layers, 256 rows x 1 token, 64 slots, ranks "
-                    "{8,16,32,64}, Zipf(1.1) with 10% base rows: one forward's LoRA launches")
+                    "{8,16,32,64}, Zipf(1.1) with 10% base rows: one forward's LoRA launches"
+                    + (" as separate shrink and expand launches" if split else
+                       " (shrink and expand in one launch per module set)"))
         else:
             from polylora_amd import PolyLoraConfig, PolyLoraModel
 
@@ -1830,6 +1912,8 @@ def main(argv=None) -> int:
     p.add_argument("--profile-passes", type=int, default=20)
     p.add_argument("--profile-warmup", type=int, default=3)
     p.add_argument("--profile-plans", type=int, default=20, help="device plan builds before the passes")
+    p.add_argument("--profile-split-pairs", action="store_true",
+                   help="decode: separate shrink and expand launches instead of the one-launch hand-off")
     p.add_argument("--reduce-profile", action="store_true",
                    help="no GPU: reduce rocprofv3 CSVs of a --launch-profile run into markdown tables")
     p.add_argument("--trace", help="kernel_trace.csv of the profiled run")

@@ -26,6 +26,11 @@
  *                          (sgmv.py:141-175 stack_num reads x once)
  *   pl_lora_apply       <- src/polylora/layers.py:42-53  (shrink then expand,
  *                          the LoRA half of MultiLoraLinear.forward)
+ *   pl_lora_decode_stacked <- src/polylora/sgmv.py:63-138 and :178-275 in one
+ *                          launch for decode-sized batches (the pair of
+ *                          Triton kernels of layers.py:45-53, split-K with a
+ *                          hand-off inside the launch)
+ *   pl_decode_counter_ints (size of its hand-off counters)
  *   pl_lora_fused       <- src/polylora/sgmv.py:63-138 and :178-275 in one
  *                          launch (both Triton kernels of layers.py:45-53)
  *   pl_lora_fused_stacked <- the same for sibling Linears in one launch
@@ -221,6 +226,38 @@ int pl_sgmv_expand_stacked(int32_t dtype, void* const* ws, int32_t ldt, int64_t 
                            const int32_t* tok, const pl_group* groups, const int32_t* meta,
                            int64_t group_cap, int32_t group_tokens, void* const* y,
                            const int64_t* ldy, const int32_t* N, int32_t epilogue, void* stream);
+
+/* Shrink and expand of 1..PL_MAX_STACKED_MODULES sibling Linears in ONE
+ * launch, for plans of 16-token groups (decode): module modules[i] adds the
+ * LoRA delta of x [*, ldx] (K columns) into y[i] [*, ldy[i]] of N[i]
+ * columns, bitwise equal to pl_sgmv_shrink_stacked followed by
+ * pl_sgmv_expand_stacked with the same ws, k_splits and epilogue.  The
+ * shrink workgroups come first in the grid and write their fp32 partial
+ * planes to ws[i] with agent-scope stores; each expand workgroup waits until
+ * every shrink workgroup of its (group, module) has arrived on a counter in
+ * `counters`, then reads the planes.  ldt must be a multiple of 32 here (so
+ * that no 128-byte line of the planes holds rows of two groups).  `counters`
+ * holds counter_ints >= pl_decode_counter_ints(group_cap, n_modules) int32s,
+ * must be all zero before the first call and is all zero again after each
+ * call (the last reader of each counter resets it), so it is reused call
+ * after call without a clear; calls that share it must not overlap (one
+ * stream).  A wait gives up after spin_limit polls of its counter and then
+ * sets counters[0] (the status word) to 1 (the results of that call are
+ * undefined); otherwise it stays 0.  Every other argument is as for
+ * pl_sgmv_shrink_stacked and pl_sgmv_expand_stacked. */
+int pl_lora_decode_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K, const void* arena,
+                           const pl_slot_entry* table, int32_t num_modules, int32_t n_modules,
+                           const int32_t* modules, void* const* ws, const int32_t* tok,
+                           const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                           int32_t group_tokens, int64_t ws_bytes, int32_t ldt, int64_t tmp_rows,
+                           int32_t k_splits, void* const* y, const int64_t* ldy, const int32_t* N,
+                           int32_t epilogue, int32_t* counters, int64_t counter_ints,
+                           int32_t spin_limit, void* stream);
+
+/* int32 words of hand-off counters pl_lora_decode_stacked needs: 64 per
+ * counter (one 256-byte line each), for the status and group_cap * n_modules
+ * counters. */
+int64_t pl_decode_counter_ints(int64_t group_cap, int32_t n_modules);
 
 /* Shrink followed by expand on one stream (one call per wrapped Linear). */
 int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y, int64_t ldy,

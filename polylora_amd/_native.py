@@ -62,6 +62,12 @@ _SIGNATURES: dict[str, tuple] = {
         c_int32, c_void_p, c_int32, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
         c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
     ),
+    "pl_lora_decode_stacked": (
+        c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
+        c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int64, c_int32, c_int64, c_int32, c_void_p,
+        c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p,
+    ),
+    "pl_decode_counter_ints": (c_int64, c_int32),
     "pl_lora_apply": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
         c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_int64,
@@ -100,7 +106,7 @@ _SIGNATURES: dict[str, tuple] = {
     "pl_check_right_padded": (c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p),
 }
 _RESTYPES = {"pl_last_error": ctypes.c_char_p, "pl_plan_group_capacity": c_int64, "pl_shrink_workspace_bytes": c_int64,
-             "pl_host_alloc": c_void_p, "pl_sgmv_ref_workspace_bytes": c_int64}
+             "pl_host_alloc": c_void_p, "pl_sgmv_ref_workspace_bytes": c_int64, "pl_decode_counter_ints": c_int64}
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

@@ -37,6 +37,12 @@ HIPCC_FLAGS = (
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # The only global atomics are the decode hand-off's single-lane counter
+    # updates; left alone, the atomic optimizer rewrites each into a wave-wide
+    # form that waits for the atomic's result at once, where the kernel means
+    # to check it only at the end of the workgroup.
+    "-mllvm",
+    "-amdgpu-atomic-optimizer-strategy=None",
 )
 
 

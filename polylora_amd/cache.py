@@ -150,6 +150,10 @@ class GpuAdapterCache:
         self.stacked_runs: dict[tuple, tuple[str, ...]] = {}
         # False: every wrapped Linear computes its own LoRA delta (no sibling runs)
         self.stack_siblings = True
+        # decode-sized batches (16-token plan groups, fewer than 2048 tokens):
+        # shrink and expand in one launch (pl_lora_decode_stacked); False runs
+        # them as two launches
+        self.decode_handoff = True
         # module name -> its MultiLoraLinear, so the first Linear of a run can
         # compute its siblings' outputs
         self.wrapped: dict[str, object] = {}

@@ -152,14 +152,113 @@ constexpr int kShortMaxPlanes = 16;
 // (5.9 against 6.6 us).
 constexpr int kExpandNarrowMinBlocks = 1536;
 
-template <int DT, int JT>
-__global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
+// One-launch shrink -> expand hand-off of the decode path
+// (pl_lora_decode_stacked): the shrink workgroups come first in the grid, and
+// an expand workgroup of (group, module) starts on the group's planes once
+// every shrink workgroup of that (group, module) has arrived.
+//
+// Visibility across the XCDs' separate L2s without a device-wide fence (an
+// L2 write-back and invalidate): the planes are written with agent-scope
+// stores, which write through the writer's L2; each shrink workgroup arrives
+// with one agent-scope atomic add on its (group, module) counter, after all
+// of its stores are acknowledged; an expand wave reads the counter at agent
+// scope (its first load, then polls) and only then loads the planes, with
+// ordinary loads.  Those cannot hit a stale line: every plane row is whole
+// 128-byte lines (ldt a multiple of 32), so no line holds rows of two
+// groups; a group's lines are read only after all of its writers have
+// arrived; and each launch starts with the L2s invalidated, as every kernel
+// launch does.
+//
+// Progress: workgroups are dispatched in block order on each XCD, so every
+// shrink workgroup has started before any expand workgroup waits, and a
+// shrink workgroup waits on nothing: each wait ends.  The wait is also
+// bounded by spin_limit polls; a wait that runs out sets the status word
+// (counters[0]) to 1 and goes on with whatever planes it finds.  The last
+// expand workgroup of a (group, module) puts its counter back to 0, so the
+// counters start every launch at zero without a clear (and the launch can be
+// recorded in a HIP graph).
+//
+// Measured on MI355X (decode layer of a Llama-3-8B shape, 256 rows, 47
+// adapters): with every counter in one cache line, the polls and arrivals
+// queued on one memory channel and the launches took 4x the split pair; a
+// workgroup-wide wait (thread 0 polls, then a barrier) put one more round
+// trip on every expand workgroup's path; agent-scope plane loads another.
+// Each counter (and the status word) has a 256-byte line of its own: the
+// polls and arrivals of different (group, module)s then go to different
+// memory channels instead of queueing on one line.
+constexpr int kCounterStride = 64;  // int32s per counter
+struct pl_handoff {
+  int32_t* counters;   // status at [0], counter i at [(1 + i) * kCounterStride]
+  int32_t n_shrink;    // shrink workgroups at the start of the grid
+  int32_t arrivals;    // shrink workgroups per (group, module): planes x rank passes
+  int32_t spin_limit;  // polls before a wait gives up
+};
+
+__device__ __forceinline__ void pl_store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding:
+// expcnt 7, lgkmcnt 15): this thread's stores are acknowledged.
+__device__ __forceinline__ void pl_wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+__device__ __forceinline__ int32_t* pl_counter(const pl_handoff& h, int counter) {
+  return h.counters + (int64_t)(1 + counter) * kCounterStride;
+}
+
+__device__ __forceinline__ void pl_handoff_arrive(const pl_handoff& h, int counter) {
+  __hip_atomic_fetch_add(pl_counter(h, counter), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Each wave on its own: `seen` is the counter as first read; while fewer
+// than h.arrivals shrink workgroups have arrived, poll it again (the value is
+// the same in every lane, so the loop is uniform).  No barrier: a wave goes
+// on to its plane loads as soon as it has seen every arrival.
+__device__ __forceinline__ void pl_handoff_wait_wave(const pl_handoff& h, int counter, int seen) {
+  int polls = 0;
+  while (__builtin_amdgcn_readfirstlane(seen) < h.arrivals) {
+    if (++polls > h.spin_limit) {
+      if ((threadIdx.x & 63) == 0)
+        __hip_atomic_store(h.counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(8);
+    seen = __hip_atomic_load(pl_counter(h, counter), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Departure, once every thread of the workgroup has read its planes (after a
+// barrier that follows the last plane read): thread 0 counts it, and the
+// last of the (group, module)'s `consumers` resets the counter.  The add is
+// issued by pl_handoff_depart and its result checked by pl_handoff_reset at
+// the very end of the workgroup, so its round trip overlaps the epilogue.
+__device__ __forceinline__ int pl_handoff_depart(const pl_handoff& h, int counter) {
+  int old = -1;
+  if (threadIdx.x == 0)
+    old = __hip_atomic_fetch_add(pl_counter(h, counter), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return old;
+}
+
+__device__ __forceinline__ void pl_handoff_reset(const pl_handoff& h, int counter, int old,
+                                                 int consumers) {
+  if (threadIdx.x == 0 && old == h.arrivals + consumers - 1)
+    __hip_atomic_store(pl_counter(h, counter), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int JT>
+constexpr int pl_shrink_short_lds() {
+  return kWaves * JT * 64 * (int)sizeof(pl_f32x4);
+}
+
+template <int DT, int JT, bool HANDOFF>
+__device__ __forceinline__ void pl_shrink_short_body(const pl_shrink_args& a, int block,
+                                                     char* smem, const pl_handoff& h) {
   typedef typename pl_traits<DT>::T T;
   constexpr int E = pl_traits<DT>::E;
   constexpr int kInstr = 4 * E;
   constexpr int kStep = kShortCC * kInstr;
   constexpr int kShortRanks = 16 * JT;
-  __shared__ pl_f32x4 red[kWaves][JT][64];
+  pl_f32x4 (*red)[JT][64] = reinterpret_cast<pl_f32x4 (*)[JT][64]>(smem);
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -169,8 +268,8 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
 
   // block -> (group g, K split c, rank pass rp, served module job); blocks
   // that read the same x rows are adjacent
-  const int job = blockIdx.x % a.n_jobs;
-  int rest = blockIdx.x / a.n_jobs;
+  const int job = block % a.n_jobs;
+  int rest = block / a.n_jobs;
   const int rp = rest % a.rank_passes;
   rest /= a.rank_passes;
   const int c = rest % a.k_splits;
@@ -184,7 +283,13 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
   const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module[job]];
   const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
   const int rb = rp * kShortRanks;
-  if (rb >= rank) return;
+  if (rb >= rank) {
+    // a pass past the rank stores nothing; with a hand-off it still arrives
+    // (the expand waits for every pass of a slot that has this module)
+    if constexpr (HANDOFF)
+      if (tid == 0 && rank > 0) pl_handoff_arrive(h, g * a.n_jobs + job);
+    return;
+  }
   const int K = a.K;
   const T* __restrict__ x = reinterpret_cast<const T*>(a.x);
   const T* __restrict__ A = reinterpret_cast<const T*>(a.arena + e.a_off);
@@ -260,10 +365,26 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int prow = (l >> 4) * 4 + v;
-        if (prow < len) out[(int64_t)(grp.start + prow) * a.ldt + j] = s[v];
+        if (prow < len) {
+          if constexpr (HANDOFF)
+            pl_store_agent(out + (int64_t)(grp.start + prow) * a.ldt + j, s[v]);
+          else
+            out[(int64_t)(grp.start + prow) * a.ldt + j] = s[v];
+        }
       }
     }
   }
+  if constexpr (HANDOFF) {
+    pl_wait_stores();  // this thread's planes have reached the agent's coherence point
+    __syncthreads();   // ... and every other thread's
+    if (tid == 0) pl_handoff_arrive(h, g * a.n_jobs + job);
+  }
+}
+
+template <int DT, int JT>
+__global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
+  __shared__ __attribute__((aligned(16))) char smem[pl_shrink_short_lds<JT>()];
+  pl_shrink_short_body<DT, JT, false>(a, blockIdx.x, smem, pl_handoff{});
 }
 
 // Long-group shrink (64-token groups, e.g. prefill): one workgroup per
@@ -587,6 +708,250 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   }
 }
 
+template <int DT, int RB>
+constexpr int pl_expand_short_lds() {
+  typedef pl_expand_shape<DT> S;
+  return (16 * (RB + S::kPad) + 16 * S::kLdsRow) * (int)sizeof(typename pl_traits<DT>::T);
+}
+
+// pl_expand_short with the hand-off of pl_lora_decode_stacked: the same work
+// per workgroup, but the counter is read first, B and the y rows load before
+// the wait for it, the planes after it, and the workgroup departs once its
+// planes are staged.  (Kept apart from
+// pl_expand_short: compiled as a shared function body, the plain kernel took
+// 97 instead of 90 VGPRs, one wave per SIMD fewer.)
+template <int DT, int PMAX, int RB>
+__device__ __forceinline__ void pl_expand_handoff_body(const pl_expand_args& a, int block,
+                                                       char* smem, const pl_handoff& h) {
+  typedef typename pl_traits<DT>::T T;
+  typedef typename pl_traits<DT>::T4 T4;
+  typedef typename pl_traits<DT>::T8 T8;
+  typedef pl_expand_shape<DT> S;
+  constexpr int E = pl_traits<DT>::E;
+  constexpr int kStep = 4 * E;                        // rank slots per MFMA step
+  constexpr int kRB = RB;                             // ranks per staged block
+  constexpr int kSteps = kRB / kStep;                 // MFMA steps per staged rank block
+  constexpr int kTRow = kRB + S::kPad;                // LDS row of the staged intermediate
+  constexpr int kYPer = 16 / S::kYRowsPerPass;        // y rows per thread
+  T* tt = reinterpret_cast<T*>(smem);                 // [16][kTRow]
+  T* delta = tt + 16 * kTRow;                         // [16][S::kLdsRow]
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+
+  // block -> (group g, column chunk c of module job, 16-token sub-tile rt);
+  // the sub-tiles of one chunk, which read the same B rows, are adjacent
+  const int rt = block % a.sub;
+  const int gc = block / a.sub;
+  const int g = gc / a.n_chunks;
+  const int cg = gc - g * a.n_chunks;
+  int job = 0;
+#pragma unroll
+  for (int j = 1; j < kMaxJobs; ++j)
+    if (j < a.n_jobs && cg >= a.chunk0[j]) job = j;
+  const int c = cg - a.chunk0[job];
+  // the (group, module) counter's first read is this workgroup's first load:
+  // it is back by the time B and the y rows are in flight, so a workgroup
+  // that starts after the shrink has finished does not wait a round trip
+  const int counter = g * a.n_jobs + job;
+  const int seen = __hip_atomic_load(pl_counter(h, counter), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the group count and the group record load together (every record below
+  // the capacity is readable); the record is used only for g below the count
+  const int n_groups = a.meta[3];  // positions in use (the plan spreads groups over them)
+  pl_group grp = a.groups[g];
+  grp.start += rt * 16;
+  const int len = min(grp.len - rt * 16, 16);
+  if (g >= n_groups || len <= 0) return;
+  const pl_slot_entry e = a.table[(int64_t)grp.slot * a.num_modules + a.module[job]];
+  const int rank = min(e.rank, a.ldt);  // the host guarantees rank <= ldt
+  if (rank <= 0) return;
+  const int r8 = e.rank8;
+  const int N = a.N[job];
+  const int n_base = c * S::kChunk;
+  const float scale = e.scale;
+  const float scale_t = pl_round<DT>(scale);
+  const int n0 = n_base + wave * S::kColsWave;
+  const T* __restrict__ Bc = reinterpret_cast<const T*>(a.arena + e.b_off);
+
+  // Load order: the y rows' token indices, then B and the planes of the
+  // first rank block, then the y rows (their addresses need the indices).
+  // The load counter retires in order, so waiting for the indices does not
+  // wait for B or the planes.
+  const int yq = tid % S::kYLanes;
+  const int yr0 = tid / S::kYLanes;
+  const int ycol = n_base + yq * E;
+  T* __restrict__ y = reinterpret_cast<T*>(a.y[job]);
+  int yt[kYPer];
+#pragma unroll
+  for (int i = 0; i < kYPer; ++i) yt[i] = a.tok[grp.start + min(yr0 + S::kYRowsPerPass * i, len - 1)];
+
+  // planes -> staged intermediate: thread (token sp, ranks rb + sq .. +4);
+  // the waves past the 16 tokens' rows stage nothing and load no planes
+  constexpr int kStageLanes = kRB / 4;  // threads per token row
+  constexpr int kStageThreads = 16 * kStageLanes;
+  static_assert(kStageThreads <= 256 && kStageThreads % 64 == 0, "whole waves stage a rank block");
+  const bool stager = kStageThreads == 256 || wave * 64 < kStageThreads;  // wave-uniform
+  const int sp = tid / kStageLanes;
+  const int sq = (tid % kStageLanes) * 4;
+  const float* srow = a.planes[job] + (int64_t)(grp.start + (sp < len ? sp : 0)) * a.ldt;
+
+  pl_u32x4 bf[kSteps][S::kCT];
+  pl_u32x4 pv[PMAX];
+  // B rows n0 + ct*16 + li and the planes of ranks rb .. rb+RB-1
+  auto load_b = [&](int rb) {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      // B's MFMA blocks: the 16-column tile at nb (nt columns), rank block
+      // j0 (wb wide) starts at nb*r8 + j0*nt
+      const int j0 = rb + s * kStep;
+      const int wb = min(kStep, r8 - j0);
+#pragma unroll
+      for (int ct = 0; ct < S::kCT; ++ct) {
+        const int nb = n0 + ct * 16;
+        const int nt = min(16, N - nb);
+        bf[s][ct] = pl_ld16_nt_or0(Bc + (int64_t)nb * r8 + (int64_t)j0 * nt + li * wb + lg * E,
+                                li < nt && j0 + lg * E < r8);
+      }
+    }
+  };
+  // PMAX loads per thread, the plane index clamped to the last plane; only
+  // the first k_splits are summed
+  auto load_p = [&](int rb) {
+    if (stager) {
+      const int jr = rb + sq;
+      const bool sok = sp < len && jr < rank;
+      const float* sbase = srow + jr;
+#pragma unroll
+      for (int q = 0; q < PMAX; ++q)
+        pv[q] = pl_ld16_or0(sbase + (int64_t)min(q, a.k_splits - 1) * a.plane, sok);
+    }
+  };
+  auto load_block = [&](int rb) {
+    load_b(rb);
+    load_p(rb);
+  };
+
+  // delta^T tiles [columns x tokens]: acc[ct][v] = delta(column n0 + ct*16 + 4*lg + v, token li)
+  pl_f32x4 acc[S::kCT];
+#pragma unroll
+  for (int ct = 0; ct < S::kCT; ++ct) acc[ct] = pl_f32x4{0.f, 0.f, 0.f, 0.f};
+  // planes summed in split order, masked at the rank, rounded once to T,
+  // staged in LDS and multiplied with B
+  auto use_block = [&](int rb) {
+    if (rb > 0) __syncthreads();  // the previous rank block's MFMA reads are done
+    if (stager) {
+      const int jr = rb + sq;
+      const bool sok = sp < len && jr < rank;
+      pl_f32x4 sum = __builtin_bit_cast(pl_f32x4, pv[0]);
+#pragma unroll
+      for (int q = 1; q < PMAX; ++q)
+        if (q < a.k_splits) sum += __builtin_bit_cast(pl_f32x4, pv[q]);
+      T4 tv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tv[i] = (T)((sok && jr + i < rank) ? sum[i] : 0.f);
+      *reinterpret_cast<T4*>(tt + sp * kTRow + sq) = tv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      if (rb + s * kStep < r8) {
+        const pl_u32x4 tf = *reinterpret_cast<const pl_u32x4*>(tt + li * kTRow + s * kStep + lg * E);
+#pragma unroll
+        for (int ct = 0; ct < S::kCT; ++ct) acc[ct] = pl_mfma_chunk<DT>(bf[s][ct], tf, acc[ct]);
+      }
+    }
+  };
+
+  pl_u32x4 yv[kYPer];
+  T* yptr[kYPer];
+  auto load_y = [&]() {
+#pragma unroll
+    for (int i = 0; i < kYPer; ++i) {
+      const int r = yr0 + S::kYRowsPerPass * i;
+      yptr[i] = (r < len && ycol < N) ? y + (int64_t)yt[i] * a.ldy[job] + ycol : nullptr;
+      yv[i] = pl_ld16_or0(yptr[i], yptr[i] != nullptr);
+    }
+  };
+  // B and y do not depend on the shrink: they load while the planes are awaited
+  load_b(0);
+  load_y();
+  pl_handoff_wait_wave(h, counter, seen);
+  load_p(0);
+  __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first use
+  use_block(0);
+  for (int rb = kRB; rb < r8; rb += kRB) {
+    load_block(rb);
+    __builtin_amdgcn_sched_barrier(0);
+    use_block(rb);
+  }
+
+  // scale and round in the epilogue's order, stage in LDS as [token][column]
+  T* drow = delta + li * S::kLdsRow + wave * S::kColsWave;
+#pragma unroll
+  for (int ct = 0; ct < S::kCT; ++ct) {
+    T4 d;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) d[v] = (T)pl_delta<DT>(acc[ct][v], scale, scale_t, a.epilogue);
+    *reinterpret_cast<T4*>(drow + ct * 16 + lg * 4) = d;
+  }
+  __syncthreads();
+  // y = T(y + delta), all rows in registers first (every y load is then
+  // complete, so the departure below is the only access left in flight)
+  pl_u32x4 yo[kYPer];
+#pragma unroll
+  for (int i = 0; i < kYPer; ++i) {
+    const int r = yr0 + S::kYRowsPerPass * i;
+    const pl_u32x4 dv = *reinterpret_cast<const pl_u32x4*>(delta + min(r, 15) * S::kLdsRow + yq * E);
+    if constexpr (E == 8) {
+      T8 yy = __builtin_bit_cast(T8, yv[i]);
+      const T8 dd = __builtin_bit_cast(T8, dv);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) yy[q] = (T)((float)yy[q] + (float)dd[q]);
+      yo[i] = __builtin_bit_cast(pl_u32x4, yy);
+    } else {
+      pl_f32x4 yy = __builtin_bit_cast(pl_f32x4, yv[i]);
+      yy += __builtin_bit_cast(pl_f32x4, dv);
+      yo[i] = __builtin_bit_cast(pl_u32x4, yy);
+    }
+  }
+  // every wave is past its last plane read (the staging of the last rank block)
+  const int departed = pl_handoff_depart(h, counter);
+#pragma unroll
+  for (int i = 0; i < kYPer; ++i)
+    if (yptr[i] != nullptr) *reinterpret_cast<pl_u32x4*>(yptr[i]) = yo[i];
+  const int chunks = (job + 1 < a.n_jobs ? a.chunk0[job + 1] : a.n_chunks) - a.chunk0[job];
+  pl_handoff_reset(h, counter, departed, chunks * a.sub);
+}
+
+// Shrink and expand of the decode path in one launch (see pl_handoff): the
+// first h.n_shrink workgroups are pl_shrink_short's, the rest
+// pl_expand_short's, sharing one LDS buffer.
+// The 4-plane, 32-rank-block form (the big decode expands: q/k/v, gate/up)
+// is held to 96 VGPRs, five waves per SIMD like the plain expand it replaces
+// (90 VGPRs); the others would spill at that size.
+template <int PMAX, int RB>
+constexpr int pl_decode_min_blocks() {
+  return PMAX == 4 && RB == 32 ? 5 : 2;
+}
+
+template <int DT, int JT, int PMAX, int RB>
+__global__ __launch_bounds__(256, (pl_decode_min_blocks<PMAX, RB>())) void pl_decode_fused(
+    pl_shrink_args sa, pl_expand_args ea,
+                                                         pl_handoff h) {
+  constexpr int kLds = pl_shrink_short_lds<JT>() > pl_expand_short_lds<DT, RB>()
+                           ? pl_shrink_short_lds<JT>()
+                           : pl_expand_short_lds<DT, RB>();
+  __shared__ __attribute__((aligned(16))) char smem[kLds];
+  const int b = (int)blockIdx.x;
+  if (b < h.n_shrink)
+    pl_shrink_short_body<DT, JT, true>(sa, b, smem, h);
+  else
+    pl_expand_handoff_body<DT, PMAX, RB>(ea, b - h.n_shrink, smem, h);
+}
+
 template <int DT>
 int launch_shrink(const pl_shrink_args& a, int64_t group_cap, hipStream_t stream) {
   if (a.sub == 1) {
@@ -621,6 +986,32 @@ int launch_expand(const pl_expand_args& a, int64_t group_cap, hipStream_t stream
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int DT, int JT>
+int launch_decode_jt(const pl_shrink_args& sa, const pl_expand_args& ea, const pl_handoff& h,
+                     int64_t expand_grid, hipStream_t stream) {
+  const dim3 grid((unsigned)(h.n_shrink + expand_grid));
+  if (ea.k_splits <= 4 && expand_grid >= kExpandNarrowMinBlocks)
+    hipLaunchKernelGGL((pl_decode_fused<DT, JT, 4, 32>), grid, dim3(256), 0, stream, sa, ea, h);
+  else if (ea.k_splits <= 4)
+    hipLaunchKernelGGL((pl_decode_fused<DT, JT, 4, 64>), grid, dim3(256), 0, stream, sa, ea, h);
+  else if (ea.k_splits <= 8)
+    hipLaunchKernelGGL((pl_decode_fused<DT, JT, 8, 64>), grid, dim3(256), 0, stream, sa, ea, h);
+  else
+    hipLaunchKernelGGL((pl_decode_fused<DT, JT, kShortMaxPlanes, 64>), grid, dim3(256), 0, stream,
+                       sa, ea, h);
+  return pl_launch_status("pl_lora_decode_stacked");
+}
+
+template <int DT>
+int launch_decode(const pl_shrink_args& sa, const pl_expand_args& ea, pl_handoff h,
+                  int64_t group_cap, hipStream_t stream) {
+  const int64_t expand_grid = group_cap * ea.n_chunks * ea.sub;
+  if (h.n_shrink + expand_grid <= 0) return PL_OK;
+  if (sa.rank_tiles == 4) return launch_decode_jt<DT, 4>(sa, ea, h, expand_grid, stream);
+  return launch_decode_jt<DT, 2>(sa, ea, h, expand_grid, stream);
+}
+
 
 int check_common(int32_t dtype, const void* arena, const pl_slot_entry* table,
                  int32_t num_modules, int32_t module, const int32_t* tok,
@@ -944,6 +1335,74 @@ extern "C" int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t 
   st = dispatch_shrink(dtype, sa, group_cap, s);
   if (st) return st;
   return dispatch_expand(dtype, ea, group_cap, s);
+}
+
+extern "C" int64_t pl_decode_counter_ints(int64_t group_cap, int32_t n_modules) {
+  if (group_cap < 0 || n_modules < 1 || n_modules > kMaxJobs) return 0;
+  return (1 + group_cap * n_modules) * kCounterStride;
+}
+
+extern "C" int pl_lora_decode_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K,
+                                      const void* arena, const pl_slot_entry* table,
+                                      int32_t num_modules, int32_t n_modules,
+                                      const int32_t* modules, void* const* ws,
+                                      const int32_t* tok, const pl_group* groups,
+                                      const int32_t* meta, int64_t group_cap,
+                                      int32_t group_tokens, int64_t ws_bytes, int32_t ldt,
+                                      int64_t tmp_rows, int32_t k_splits, void* const* y,
+                                      const int64_t* ldy, const int32_t* N, int32_t epilogue,
+                                      int32_t* counters, int64_t counter_ints,
+                                      int32_t spin_limit, void* stream) {
+  if (group_tokens != 16) {
+    pl_set_error("pl_lora_decode_stacked: plans of 16-token groups only (got %d)", group_tokens);
+    return PL_ERR_ARG;
+  }
+  if (ldt % 32 != 0) {
+    // every plane row is then whole 128-byte lines, so no line holds rows of
+    // two groups and the planes can be read through the L2 (see pl_handoff)
+    pl_set_error("pl_lora_decode_stacked: ldt must be a multiple of 32 (got %d)", ldt);
+    return PL_ERR_ARG;
+  }
+  pl_shrink_args sa;
+  int st = prepare_shrink(sa, dtype, x, ldx, K, arena, table, num_modules, n_modules, modules, ws,
+                          tok, groups, meta, group_cap, group_tokens, ws_bytes, ldt, tmp_rows,
+                          k_splits);
+  if (st) return st;
+  pl_expand_args ea;
+  st = prepare_expand(ea, dtype, ws, ldt, tmp_rows, sa.k_splits, arena, table, num_modules,
+                      n_modules, modules, tok, groups, meta, group_cap, group_tokens, y, ldy, N,
+                      epilogue);
+  if (st) return st;
+  if (!counters || (reinterpret_cast<uintptr_t>(counters) & 3u) != 0) {
+    pl_set_error("pl_lora_decode_stacked: null or misaligned hand-off counters");
+    return PL_ERR_ARG;
+  }
+  if (counter_ints < pl_decode_counter_ints(group_cap, n_modules)) {
+    pl_set_error("pl_lora_decode_stacked: %lld hand-off counters, %lld needed", (long long)counter_ints,
+                 (long long)pl_decode_counter_ints(group_cap, n_modules));
+    return PL_ERR_ARG;
+  }
+  if (spin_limit < 1) {
+    pl_set_error("pl_lora_decode_stacked: spin_limit must be positive");
+    return PL_ERR_ARG;
+  }
+  const int64_t n_shrink = group_cap * sa.k_splits * sa.rank_passes * n_modules;
+  const int64_t n_expand = group_cap * ea.n_chunks * ea.sub;
+  if (!pl_grid_fits(n_shrink + n_expand, 256) || n_shrink > 0x7fffffff) {
+    pl_set_error("pl_lora_decode_stacked: grid too large");
+    return PL_ERR_LIMIT;
+  }
+  pl_handoff h;
+  h.counters = counters;
+  h.n_shrink = (int32_t)n_shrink;
+  h.arrivals = sa.k_splits * sa.rank_passes;
+  h.spin_limit = spin_limit;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case PL_BF16: return launch_decode<PL_BF16>(sa, ea, h, group_cap, s);
+    case PL_F16: return launch_decode<PL_F16>(sa, ea, h, group_cap, s);
+    default: return launch_decode<PL_F32>(sa, ea, h, group_cap, s);
+  }
 }
 
 // ---------------------------------------------------------------------------

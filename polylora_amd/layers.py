@@ -106,6 +106,14 @@ class MultiLoraLinear(nn.Module):
         run_out = self._run_forward(x, x2, plan, lora_ctx, reshape, main, fused)
         if run_out is not None:
             return run_out
+        if not fused and rows * row_len < OVERLAP_MIN_TOKENS and cache.decode_handoff and sgmv.decode_ok(plan):
+            # decode-sized batches: base GEMM, then shrink and expand in one launch
+            self._observe_call(x, _version_of(x), lora_ctx.stack)
+            base = self.base_layer(x)
+            base_3d = reshape(base)
+            y2 = base_3d.view(rows * row_len, base_3d.shape[-1])
+            sgmv.lora_decode_stacked(x2, [y2], cache, [self.module_name], plan, stream=main)
+            return base_3d.reshape(base.shape)
         if fused:
             # long adapter segments: base GEMM, then one fused shrink+expand launch
             self._observe_call(x, _version_of(x), lora_ctx.stack)
@@ -175,6 +183,7 @@ class MultiLoraLinear(nn.Module):
             return None
         self._observe_call(x, version, stack)
         tokens = x2.shape[0]
+        done = fused  # the outputs are complete after the launches below
         if fused:
             # long adapter segments: every sibling's base GEMM, then one fused
             # launch for all of them
@@ -190,10 +199,18 @@ class MultiLoraLinear(nn.Module):
                 results = sgmv.lora_shrink_stacked(x2, cache, list(run), plan, stream=side.cuda_stream)
             bases = [m.base_layer(x) for m in siblings]
             main_s.wait_stream(side)
+        elif cache.decode_handoff and sgmv.decode_ok(plan):
+            # decode-sized batches: every sibling's base GEMM, then one launch
+            # for all of their shrinks and expands
+            bases = [m.base_layer(x) for m in siblings]
+            outs = [reshape(b) for b in bases]
+            sgmv.lora_decode_stacked(x2, [o.view(tokens, o.shape[-1]) for o in outs], cache, list(run), plan,
+                                     stream=main)
+            done = True
         else:
             results = sgmv.lora_shrink_stacked(x2, cache, list(run), plan, stream=main)
             bases = [m.base_layer(x) for m in siblings]
-        if not fused:
+        if not done:
             outs = [reshape(b) for b in bases]
             sgmv.lora_expand_stacked(results, [o.view(tokens, o.shape[-1]) for o in outs], cache, list(run),
                                      stream=main)

@@ -79,7 +79,7 @@ class SgmvPlan:
     """
 
     __slots__ = ("rows", "row_len", "num_slots", "group_tokens", "tokens_cap", "group_cap", "tok", "groups", "meta",
-                 "row_slot", "seq_lens", "distinct_slots", "launch_args", "active")
+                 "row_slot", "seq_lens", "distinct_slots", "launch_args", "active", "_build")
 
     def __init__(self, row_slot: torch.Tensor, seq_lens: torch.Tensor, row_len: int, num_slots: int,
                  distinct_slots: int | None = None, group_tokens: int | None = None,
@@ -114,14 +114,22 @@ class SgmvPlan:
         self.launch_args = (self.tok.data_ptr(), self.groups.data_ptr(), self.meta.data_ptr(), max(1, self.group_cap),
                             self.group_tokens)
         self.row_slot, self.seq_lens, self.active = row_slot, seq_lens, active
-        out = (self.tok.data_ptr(), self.groups.data_ptr(), self.meta.data_ptr(), max(1, self.group_cap), _stream(dev))
+        out = (self.tok.data_ptr(), self.groups.data_ptr(), self.meta.data_ptr(), max(1, self.group_cap))
         if active is None:
-            _native.check(lib.pl_plan_build(row_slot.data_ptr(), seq_lens.data_ptr(), rows, self.row_len,
-                                            self.num_slots, self.group_tokens, *out), "pl_plan_build")
+            self._build = (lib.pl_plan_build, "pl_plan_build",
+                           (row_slot.data_ptr(), seq_lens.data_ptr(), rows, self.row_len, self.num_slots,
+                            self.group_tokens, *out))
         else:
-            _native.check(lib.pl_plan_build_active(row_slot.data_ptr(), seq_lens.data_ptr(), rows, self.row_len,
-                                                   self.num_slots, active.data_ptr(), active.stride(0),
-                                                   self.group_tokens, *out), "pl_plan_build_active")
+            self._build = (lib.pl_plan_build_active, "pl_plan_build_active",
+                           (row_slot.data_ptr(), seq_lens.data_ptr(), rows, self.row_len, self.num_slots,
+                            active.data_ptr(), active.stride(0), self.group_tokens, *out))
+        self.rebuild(_stream(dev))
+
+    def rebuild(self, stream: int | None = None) -> None:
+        """Build the plan again into the same buffers from the current contents of its row -> slot map,
+        lengths and active vector (on the current stream, or `stream`); nothing is allocated."""
+        fn, what, args = self._build
+        _native.check(fn(*args, _stream(self.tok.device) if stream is None else stream), what)
 
 
 class _Workspace:
@@ -664,6 +672,112 @@ def lora_expand_stacked(results: list, ys: list, cache, module_names: list, *,
             _stream(ys[0].device) if stream is None else stream,
         ),
         "pl_sgmv_expand_stacked",
+    )
+    return ys
+
+
+class _HandoffCounters:
+    """Zeroed int32 hand-off counters of pl_lora_decode_stacked for one (device, stream), grown on demand.
+
+    Every launch leaves them zero (each counter's last reader resets it), so
+    they are cleared only when allocated, on the current stream, which must be
+    the stream the launches run on; replaced buffers stay allocated for the
+    life of the process, so a HIP graph that recorded a launch keeps a valid
+    pointer.  Word 0 is the status a timed-out wait sets to 1.
+    """
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = device
+        self.buf: torch.Tensor | None = None
+        self.retired: list[torch.Tensor] = []
+
+    def get(self, ints: int) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < ints:
+            if self.buf is not None:
+                self.retired.append(self.buf)
+                ints = max(ints, 2 * self.buf.numel())
+            # cleared by a fill kernel on the current stream (the launch's stream),
+            # which a HIP graph being captured records like any other kernel
+            self.buf = torch.empty(max(64, ints), dtype=torch.int32, device=self.device).zero_()
+        return self.buf
+
+
+_COUNTERS: dict[tuple[int, int], _HandoffCounters] = {}
+
+# Polls of a hand-off counter before a waiting expand workgroup gives up (each
+# poll is one memory round trip plus a short sleep: well under a second in all,
+# against the tens of microseconds a launch's shrink takes).
+DECODE_SPIN_LIMIT = 1 << 16
+
+
+def handoff_counters(device: torch.device, stream: int) -> _HandoffCounters:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    hit = _COUNTERS.get(key)
+    if hit is None:
+        hit = _COUNTERS[key] = _HandoffCounters(device)
+    return hit
+
+
+def decode_ok(plan: SgmvPlan) -> bool:
+    """Whether a plan suits the one-launch decode path (pl_lora_decode_stacked): 16-token groups."""
+    return plan.group_tokens == 16
+
+
+def lora_decode_stacked(x: torch.Tensor, ys: list, cache, module_names: list, plan: SgmvPlan, *,
+                        k_splits: int | None = None, epilogue: int = _native.PL_EPI_FALLBACK,
+                        stream: int | None = None) -> list:
+    """Shrink and expand of 1..4 sibling Linears fed the same x in ONE launch (pl_lora_decode_stacked).
+
+    Adds each module's LoRA delta into ys[i] in place, bitwise equal to
+    lora_shrink_stacked followed by lora_expand_stacked on the same stream:
+    the expand workgroups of a group start on its partial sums as soon as
+    every shrink workgroup of that group has stored them, inside the launch.
+    For plans of 16-token groups (decode).  Uses the stream's shrink
+    workspaces (positions 0..n-1) and its hand-off counters.
+    """
+    _require_gpu(x, "lora_decode_stacked")
+    n = len(module_names)
+    if not 1 <= n <= _native.PL_MAX_STACKED_MODULES or len(ys) != n:
+        raise ValueError(f"a decode launch serves 1..{_native.PL_MAX_STACKED_MODULES} modules with one y each")
+    if not decode_ok(plan):
+        raise ValueError("lora_decode_stacked takes plans of 16-token groups")
+    specs, mods, arrays = _fused_set(cache, module_names)
+    K = int(x.shape[1]) if x.dim() == 2 else -1
+    if x.dim() != 2 or x.shape[0] != plan.tokens_cap or any(sp.in_features != K for sp in specs):
+        raise ValueError(f"x must be [{plan.tokens_cap}, in_features] for every module, got {list(x.shape)}")
+    if x.dtype != cache.dtype or x.device != cache.device:
+        raise TypeError(f"x {x.dtype} on {x.device} must match the adapter cache ({cache.dtype} on {cache.device})")
+    for y, spec in zip(ys, specs):
+        _require_gpu(y, "lora_decode_stacked")
+        if y.dim() != 2 or y.shape[0] != plan.tokens_cap or y.shape[1] != spec.out_features:
+            raise ValueError(f"y of {spec.name!r} must be [{plan.tokens_cap}, {spec.out_features}], got {list(y.shape)}")
+        if y.dtype != cache.dtype or y.device != cache.device:
+            raise TypeError(f"y {y.dtype} on {y.device} must match the adapter cache ({cache.dtype} on {cache.device})")
+    lib = _native.load()
+    dt = _native.dtype_code(x.dtype)
+    ldt = -(-cache.rank8_cap // 32) * 32  # plane rows of whole 128-byte lines
+    if stream is None:
+        stream = _stream(x.device)
+    rows = max(1, plan.tokens_cap)
+    splits, planes, nbytes = _shrink_geometry(lib, dt, K, x.dtype, plan, rows, ldt, k_splits)
+    wss, bufs, ptrs = _workspace_set(x.device, stream, n, nbytes)
+    for ws in wss:
+        ws.owner = None  # any earlier shrink's planes there are overwritten by this launch
+    cap = max(1, plan.group_cap)
+    need = int(lib.pl_decode_counter_ints(cap, n))
+    counters = handoff_counters(x.device, stream).get(need)
+    yp, ldy, nn_ = arrays
+    for i, y in enumerate(ys):
+        yp[i] = y.data_ptr()
+        ldy[i] = y.stride(0)
+    _native.check(
+        lib.pl_lora_decode_stacked(
+            dt, x.data_ptr(), x.stride(0), K, cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index),
+            n, mods, ptrs, plan.tok.data_ptr(), plan.groups.data_ptr(), plan.meta.data_ptr(), cap, plan.group_tokens,
+            min(b.numel() for b in bufs), ldt, rows, splits, yp, ldy, nn_, epilogue, counters.data_ptr(),
+            counters.numel(), DECODE_SPIN_LIMIT, stream,
+        ),
+        "pl_lora_decode_stacked",
     )
     return ys
 

@@ -564,10 +564,12 @@ def test_llama_decode_step_graph_replays(gpu):
     torch.testing.assert_close(want.float(), ref.float(), **BF16)
 
 
-def test_sibling_shrinks_are_stacked(gpu):
-    """q/k/v and gate/up are learned as siblings in the first forward; the second forward stacks their
-    shrinks and gives the same output bit for bit; both match the fallback."""
-    _announce(test="stacked_siblings")
+@pytest.mark.parametrize("handoff", [True, False])
+def test_sibling_shrinks_are_stacked(gpu, handoff):
+    """q/k/v and gate/up are learned as siblings in the first forward; the second forward serves each run in
+    one launch (shrink and expand with the hand-off inside it), or with `decode_handoff` off one stacked shrink
+    and one stacked expand, and gives the same output bit for bit; both match the fallback."""
+    _announce(test="stacked_siblings", handoff=handoff)
     base, cfg = _tiny_llama(15, torch.bfloat16, gpu)
     pm = PolyLoraModel(copy.deepcopy(base), PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=4, max_rank=32)).eval()
     g = torch.Generator().manual_seed(15)
@@ -583,19 +585,22 @@ def test_sibling_shrinks_are_stacked(gpu):
             p = f"layers.{layer}."
             assert (p + "self_attn.q_proj", p + "self_attn.k_proj", p + "self_attn.v_proj") in runs
             assert (p + "mlp.gate_proj", p + "mlp.up_proj") in runs
+        pm.adapter_cache.decode_handoff = handoff
         calls = []
-        stacked_expand = sgmv.lora_expand_stacked
+        name = "lora_decode_stacked" if handoff else "lora_expand_stacked"
+        launch = getattr(sgmv, name)
 
         def counting(*a, **k):
-            calls.append(tuple(a[3]))
-            return stacked_expand(*a, **k)
+            if len(a[3]) > 1:
+                calls.append(tuple(a[3]))
+            return launch(*a, **k)
 
-        sgmv.lora_expand_stacked = counting
+        setattr(sgmv, name, counting)
         try:
             second = pm(input_ids=ids, adapter_ids=adapter_ids).last_hidden_state
         finally:
-            sgmv.lora_expand_stacked = stacked_expand
-        # every run was computed whole by its first Linear: one stacked expand each
+            setattr(sgmv, name, launch)
+        # every run was computed whole by its first Linear: one stacked launch each
         assert sorted(calls) == sorted(runs), (calls, runs)
         om, bank = _oracle(base, LLAMA_TARGETS, ads, 32, torch.bfloat16, gpu)
         want = oracle_model.run(om, bank, adapter_ids, input_ids=ids).last_hidden_state
