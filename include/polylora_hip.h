@@ -14,6 +14,9 @@
  *   pl_sgmv_ref_workspace_bytes
  *                          (size of their MFMA path's workspace; the Triton
  *                          kernels of the reference allocate nothing)
+ *   pl_sgmv_lora_a_ref_parts, pl_sgmv_lora_b_ref_parts, pl_sgmv_ref_part_bytes
+ *                       <- the same two calls with the plan and the
+ *                          repacked weights kept by the caller across calls
  *   pl_plan_build       <- src/polylora/sgmv.py:29-61    _build_flat_schedule
  *                          (one device-side plan per forward instead of a
  *                          host-synchronising schedule per layer)
@@ -326,9 +329,11 @@ int64_t pl_sgmv_ref_workspace_bytes(int32_t dtype, int32_t which, int32_t B, int
  * With a 256-byte aligned workspace of at least
  * pl_sgmv_ref_workspace_bytes(dtype, 0, ...) bytes (when that is nonzero)
  * and a 16-byte aligned x, the call runs on the MFMA path: one launch
- * repacks the weights of every adapter into the slot arena's block layout
- * inside the workspace and builds the device plan that groups the rows by
- * adapter, then the tiled shrink and a finish kernel write out (3 launches,
+ * repacks the weights of every adapter some row uses into the slot arena's
+ * block layout inside the workspace (reading the reference layout with
+ * consecutive lanes on consecutive elements) and builds the device plan
+ * that groups the rows by adapter, then the tiled shrink and a finish
+ * kernel write out (3 launches,
  * no host synchronisation); with long adapter segments (B*M >= 1024 and >=
  * 64 rows per adapter, K <= 16384) one launch of the fused kernel's shrink
  * phase writes out instead (2 launches).  Otherwise, or with a null
@@ -357,6 +362,77 @@ int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32
                        const int32_t* seq_lens, const int32_t* weight_indices,
                        const int32_t* lora_ranks, const float* scalings, void* out,
                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The operator API's MFMA path in three caller-kept parts (codes for
+ * pl_sgmv_ref_part_bytes):
+ *   PL_REF_PART_PLAN     the plan (meta, group records, token list).  It
+ *                        depends on weight_indices, seq_lens, B, M and
+ *                        num_adapters only (not on ranks, weights or
+ *                        which), so one plan built by any call serves the
+ *                        shrink and the expand of every module that shares
+ *                        them.
+ *   PL_REF_PART_WEIGHTS  per-adapter pack marks, the slot table and the
+ *                        weights repacked into the MFMA block layout.  It
+ *                        depends on w, lora_ranks, stack_num (shrink) and
+ *                        scalings (expand).
+ *   PL_REF_PART_SCRATCH  the fp32 planes of one call (0 bytes when the
+ *                        fused kernel's phase serves the shape).
+ * Build flags of a call:
+ *   PL_REF_BUILD_PLAN    build the plan into the plan part.
+ *   PL_REF_PACK_USED     write the slot table and repack every adapter that
+ *                        some row's weight index names.
+ *   PL_REF_PACK_ALL      write the slot table and repack every adapter.
+ *   PL_REF_KEEP_PACKED   with a PACK flag: skip adapters the weights part
+ *                        marks as packed by an earlier call and mark the
+ *                        ones this call packs with `epoch`.  The marks, the
+ *                        first align256(4 * num_adapters) bytes of the
+ *                        weights part (align256 rounds up to a multiple of
+ *                        256), must be zero before its first such call, and
+ *                        `epoch` must be >= 1 and differ from every earlier
+ *                        call's on that part (a counter).
+ * A call without flags reads the plan and weights parts as earlier calls
+ * left them: the caller must rebuild them (with the flags, after zeroing
+ * the marks again) whenever what they depend on changes. */
+#define PL_REF_PART_PLAN 0
+#define PL_REF_PART_WEIGHTS 1
+#define PL_REF_PART_SCRATCH 2
+#define PL_REF_BUILD_PLAN 1
+#define PL_REF_PACK_USED 2
+#define PL_REF_PACK_ALL 4
+#define PL_REF_KEEP_PACKED 8
+
+/* Bytes of one part of the MFMA path of pl_sgmv_lora_a_ref_parts (which =
+ * 0, K = in_features, n = n_max) or pl_sgmv_lora_b_ref_parts (which = 1, K
+ * = k_max, n = N), or 0 for every part when that path does not take the
+ * shape (as pl_sgmv_ref_workspace_bytes). */
+int64_t pl_sgmv_ref_part_bytes(int32_t dtype, int32_t which, int32_t B, int32_t M, int32_t K,
+                               int32_t n, int32_t num_adapters, int32_t part);
+
+/* pl_sgmv_lora_a_ref with the plan, weights and scratch parts given
+ * separately (each 256-byte aligned and at least pl_sgmv_ref_part_bytes
+ * long; scratch may be NULL when its size is 0) and the build flags above:
+ * results are bit for bit those of pl_sgmv_lora_a_ref once the parts hold
+ * what the flags build.  Launches step 1 (table, plan, repack) only when a
+ * flag asks for it.  Shapes the MFMA path does not take run the row
+ * kernels and leave the parts alone.  Calls that share a part must be
+ * ordered (one stream). */
+int pl_sgmv_lora_a_ref_parts(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K,
+                             const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
+                             int32_t num_adapters, int32_t n_max, const int32_t* seq_lens,
+                             const int32_t* weight_indices, const int32_t* lora_ranks,
+                             int32_t stack_num, void* out, void* plan, int64_t plan_bytes,
+                             void* weights, int64_t weights_bytes, void* scratch,
+                             int64_t scratch_bytes, int32_t flags, int32_t epoch, void* stream);
+
+/* pl_sgmv_lora_b_ref with separate parts and build flags, as
+ * pl_sgmv_lora_a_ref_parts. */
+int pl_sgmv_lora_b_ref_parts(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max,
+                             const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
+                             int32_t num_adapters, int32_t N, const int32_t* seq_lens,
+                             const int32_t* weight_indices, const int32_t* lora_ranks,
+                             const float* scalings, void* out, void* plan, int64_t plan_bytes,
+                             void* weights, int64_t weights_bytes, void* scratch,
+                             int64_t scratch_bytes, int32_t flags, int32_t epoch, void* stream);
 
 /* Bytes of the static device scratch behind pl_lora_apply_noalloc. */
 #define PL_NOALLOC_SCRATCH_BYTES (32 << 20)

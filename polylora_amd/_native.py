@@ -22,6 +22,8 @@ PL_MAX_SLOTS = 4096
 PL_GROUP_TOKENS_SHORT, PL_GROUP_TOKENS_LONG = 16, 64
 PL_MAX_STACKED_MODULES = 4
 PL_NOALLOC_SCRATCH_BYTES = 32 << 20
+PL_REF_PART_PLAN, PL_REF_PART_WEIGHTS, PL_REF_PART_SCRATCH = 0, 1, 2
+PL_REF_BUILD_PLAN, PL_REF_PACK_USED, PL_REF_PACK_ALL, PL_REF_KEEP_PACKED = 1, 2, 4, 8
 SLOT_ENTRY_INT32S = 8  # sizeof(pl_slot_entry) / 4
 
 DTYPE_CODES = {torch.float32: PL_F32, torch.bfloat16: PL_BF16, torch.float16: PL_F16}
@@ -95,6 +97,17 @@ _SIGNATURES: dict[str, tuple] = {
         c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
         c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
     ),
+    "pl_sgmv_ref_part_bytes": (c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32),
+    "pl_sgmv_lora_a_ref_parts": (
+        c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
+        c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
+        c_void_p, c_int64, c_int32, c_int32, c_void_p,
+    ),
+    "pl_sgmv_lora_b_ref_parts": (
+        c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64, c_int32,
+        c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
+        c_void_p, c_int64, c_int32, c_int32, c_void_p,
+    ),
     "pl_lora_apply_noalloc": (
         c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
         c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p,
@@ -106,7 +119,8 @@ _SIGNATURES: dict[str, tuple] = {
     "pl_check_right_padded": (c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p),
 }
 _RESTYPES = {"pl_last_error": ctypes.c_char_p, "pl_plan_group_capacity": c_int64, "pl_shrink_workspace_bytes": c_int64,
-             "pl_host_alloc": c_void_p, "pl_sgmv_ref_workspace_bytes": c_int64, "pl_decode_counter_ints": c_int64}
+             "pl_host_alloc": c_void_p, "pl_sgmv_ref_workspace_bytes": c_int64, "pl_decode_counter_ints": c_int64,
+             "pl_sgmv_ref_part_bytes": c_int64}
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

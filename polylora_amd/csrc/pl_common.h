@@ -186,18 +186,30 @@ int pl_fused_phase(int mode, int32_t dtype, const void* x, int64_t ldx, int32_t 
                    int64_t group_cap, int32_t group_tokens, int32_t epilogue, void* stream);
 
 // MFMA path of the reference-layout operator API (sgmv_refop.hip).  Both
-// return PL_REFOP_DECLINED, having launched nothing, when there is no
-// workspace or the shape is not one the tiled kernels take; the caller then
-// runs the row kernels.
+// return PL_REFOP_DECLINED, having launched nothing, when there is neither a
+// workspace nor parts, or the shape is not one the tiled kernels take; the
+// caller then runs the row kernels.  With parts == nullptr the workspace of
+// pl_sgmv_ref_workspace_bytes bytes is split into the three parts and the
+// call builds the plan and packs the adapters its rows use.
 constexpr int PL_REFOP_DECLINED = -100;
+struct pl_refop_parts {
+  void* plan;
+  int64_t plan_bytes;
+  void* weights;
+  int64_t weights_bytes;
+  void* scratch;
+  int64_t scratch_bytes;
+  int32_t flags;  // PL_REF_* build flags
+  int32_t epoch;
+};
 int pl_refop_shrink(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K, const void* w,
                     int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t num_adapters,
                     int32_t n_max, const int32_t* seq_lens, const int32_t* weight_indices,
                     const int32_t* lora_ranks, int32_t stack_num, void* out, void* workspace,
-                    int64_t workspace_bytes, void* stream);
+                    int64_t workspace_bytes, const pl_refop_parts* parts, void* stream);
 int pl_refop_expand(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max,
                     const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
                     int32_t num_adapters, int32_t N, const int32_t* seq_lens,
                     const int32_t* weight_indices, const int32_t* lora_ranks,
                     const float* scalings, void* out, void* workspace, int64_t workspace_bytes,
-                    void* stream);
+                    const pl_refop_parts* parts, void* stream);

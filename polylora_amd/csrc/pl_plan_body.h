@@ -51,10 +51,12 @@ __device__ __forceinline__ int pl_wave_scan_incl(int v) {
 // Where a row's slot comes from: a row -> slot map (pl_plan_build,
 // ADAPTER_ROWS false: rows[b]), or a per-row adapter index as the
 // reference's operator API passes it (ADAPTER_ROWS true: adapter i = rows[b]
-// -> slot i + 1; an index outside [0, num_adapters) -> slot 0, and slot
-// i + 1 is active only when ranks[i] > 0, so an adapter of rank 0 gets no
-// tokens either).  The pointer stays a plain restrict parameter so that the
-// token stores are known not to alias it.
+// -> slot i + 1; an index outside [0, num_adapters) -> slot 0).  The plan
+// does not look at ranks: an adapter of rank 0 gets its groups like any
+// other, and every kernel that consumes the plan returns at once for a slot
+// whose table entry has rank 0, so one plan serves every module of a
+// forward, whatever each module's ranks.  The pointer stays a plain
+// restrict parameter so that the token stores are known not to alias it.
 template <bool ADAPTER_ROWS>
 __device__ __forceinline__ int pl_row_slot(const int32_t* __restrict__ rows, int num_adapters,
                                            int b) {
@@ -224,8 +226,7 @@ __device__ __forceinline__ void pl_plan_store4(const int (&s)[kPlanRun], const i
 }
 
 // The plan, built by one workgroup of kPlanThreads threads.  row_src and
-// num_adapters as for pl_row_slot; with ADAPTER_ROWS, slot s > 0 is active
-// when ranks[s - 1] > 0 (active is then unused), otherwise when there is no
+// num_adapters as for pl_row_slot; slot s > 0 is active when there is no
 // active vector or active[s * active_stride] > 0.
 //
 // All of it runs on one CU, whose four SIMDs issue one wave64 instruction
@@ -235,7 +236,7 @@ __device__ __forceinline__ void pl_plan_store4(const int (&s)[kPlanRun], const i
 // slots or groups run each step.
 template <bool ADAPTER_ROWS>
 __device__ __forceinline__ void pl_plan_body(
-    const int32_t* __restrict__ row_src, const int32_t* __restrict__ ranks, int32_t num_adapters,
+    const int32_t* __restrict__ row_src, int32_t num_adapters,
     const int32_t* __restrict__ seq_lens, int32_t rows,
     int32_t row_len, int32_t num_slots, const int32_t* __restrict__ active, int64_t active_stride,
     int32_t group_tokens, int32_t* __restrict__ tok, pl_group* __restrict__ groups,
@@ -272,12 +273,7 @@ __device__ __forceinline__ void pl_plan_body(
   }
   if (owns_slots) {
     int av[4] = {1, 1, 1, 1};
-    if constexpr (ADAPTER_ROWS) {
-      if (num_adapters > 0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) av[j] = ranks[min(max(4 * tid + j - 1, 0), num_adapters - 1)];
-      }
-    } else if (active != nullptr) {
+    if (active != nullptr) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) av[j] = active[(int64_t)min(4 * tid + j, S - 1) * active_stride];
     }

@@ -10,7 +10,7 @@ __global__ __launch_bounds__(kPlanThreads) void pl_plan_kernel(
     int32_t row_len, int32_t num_slots, const int32_t* __restrict__ active, int64_t active_stride,
     int32_t group_tokens, int32_t* __restrict__ tok, pl_group* __restrict__ groups,
     int32_t* __restrict__ meta, int64_t group_cap) {
-  pl_plan_body<false>(row_slot, nullptr, 0, seq_lens, rows, row_len, num_slots, active,
+  pl_plan_body<false>(row_slot, 0, seq_lens, rows, row_len, num_slots, active,
                       active_stride, group_tokens, tok, groups, meta, group_cap);
 }
 

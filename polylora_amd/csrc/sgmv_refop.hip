@@ -4,17 +4,33 @@
 // Those calls take adapter weights in the reference's own slot layout
 // (w [num_adapters][k][n] with any element strides) and a per-row adapter
 // index, and pass the LoRA intermediate between them as a model-dtype tensor
-// [B][M][n].  Each call here runs two or three launches on the caller's
-// stream, all inside a caller-provided workspace:
+// [B][M][n].  A call works in three caller-provided parts of device memory:
 //
-//   1. pl_refop_prep_plan: workgroup (0, 0) writes the slot table and builds
-//      the plan over (B rows of M tokens) straight from the adapter index
-//      (adapter i -> slot i+1; rows whose adapter index is out of range or
-//      whose rank is 0 get slot 0 and are left alone, as the reference's
-//      kernels skip them); the other workgroups repack the adapters'
-//      weights into the MFMA block layout of the slot arena (A as [rank][K],
-//      B as [N][rank8]).  Ranks, scales and indices stay on the device: no
-//      host synchronisation.
+//   plan     the plan over (B rows of M tokens): meta, group records, token
+//            list.  It depends only on the adapter index, the row lengths
+//            and B, M, num_adapters, so one plan serves the shrink and the
+//            expand of every module of a forward.
+//   weights  per-adapter pack marks, the slot table (rank, scale, offsets)
+//            and the adapters' weights repacked into the MFMA block layout
+//            of the slot arena (A as [rank][K], B as [N][rank8]).  It
+//            depends on w, the ranks, the scalings and stack_num.
+//   scratch  the fp32 split planes of this call.
+//
+// The build flags say what a call must (re)build; a caller that keeps the
+// plan and weights parts across calls (keyed on what they depend on)
+// passes none of them and skips step 1:
+//
+//   1. pl_refop_prep (only with PL_REF_BUILD_PLAN or a PL_REF_PACK_* flag):
+//      workgroup (0, 0) writes the slot table and builds the plan straight
+//      from the adapter index (adapter i -> slot i + 1, an index out of
+//      range -> slot 0); the workgroups of row y = s + 1 repack adapter s:
+//      with PL_REF_PACK_USED only when some row uses it, with
+//      PL_REF_PACK_ALL always, and with PL_REF_KEEP_PACKED not when the
+//      weights part marks it packed at an earlier call.  Each repack unit
+//      reads a 64-row x 4-block panel of the reference layout with
+//      consecutive lanes on consecutive elements of its fastest dimension,
+//      transposes it through LDS and writes 16 whole MFMA blocks.  Ranks,
+//      scales and indices stay on the device: no host synchronisation.
 //   2. shrink: pl_sgmv_shrink into fp32 split planes, then pl_refop_finish
 //      writes out[b][m][n] = T(sum of the planes) for n < rank * stack_num;
 //      expand: pl_refop_gather loads the model-dtype intermediate into one
@@ -26,12 +42,12 @@
 //      writes T(sum) straight into out, the expand stages the caller's
 //      intermediate in LDS and adds the deltas into out.
 //
-// The repack reads every adapter's weights once per call (the reference's
-// weight tensor is the caller's, and may change between calls); for the
-// 16-adapter, rank-16, K = N = 4096 case that is 2 MB per call against 26 to
-// 52 MB of activations.  Shapes the tiled kernels do not take (K or N not a
-// whole number of 16-byte chunks, ranks above 64, misaligned pointers) fall
-// back to the row kernels of sgmv_rows.hip.
+// The plan gives every row with an adapter index in range its slot, rank 0
+// or not: every kernel of step 2 returns at once for a slot whose table
+// rank is 0, so those rows are left alone as the reference's kernels leave
+// them.  Shapes the tiled kernels do not take (K or N not a whole number of
+// 16-byte chunks, ranks above 64, misaligned pointers) fall back to the row
+// kernels of sgmv_rows.hip.
 #include <algorithm>
 #include <type_traits>
 
@@ -42,6 +58,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxRefRank = 64;  // rank capacity of the repacked slots (the tiled kernels' tested range)
+constexpr int kPackRows = 64;    // destination rows of one repack unit (4 MFMA tiles)
+constexpr int kPackBlocks = 4;   // 64-byte column blocks of one repack unit
+constexpr int kPackGridCap = 16; // repack workgroups per adapter (each loops over its units)
 
 int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 int32_t round8(int32_t v) { return (v + 7) & ~7; }
@@ -54,8 +73,12 @@ struct refop_layout {
   int32_t planes;     // planes the shrink writes (1 for the expand)
   int64_t tokens;     // B * M
   int64_t slot_bytes;
-  // byte offsets inside the workspace
-  int64_t meta, groups, tok, table, arena, plane, total;
+  // byte offsets inside the plan part
+  int64_t meta, groups, tok, plan_bytes;
+  // byte offsets inside the weights part
+  int64_t marks, table, arena, weights_bytes;
+  int64_t scratch_bytes;  // the planes
+  int64_t total;          // one workspace holding the three parts in this order
 };
 
 // which: 0 = shrink (K = in_features, n = n_max), 1 = expand (K = k_max, n = N).
@@ -96,15 +119,21 @@ bool refop_plan_layout(int32_t dtype, int which, int32_t B, int32_t M, int32_t K
   o += align256(16 * L.group_cap);
   L.tok = o;
   o += align256(4 * T);
+  L.plan_bytes = o;
+  o = 0;
+  L.marks = o;
+  o += align256(4 * (int64_t)num_adapters);
   L.table = o;
   o += align256((int64_t)sizeof(pl_slot_entry) * (num_adapters + 1));
   L.arena = o;
   o += L.slot_bytes * num_adapters;
-  L.plane = o;
-  o += align256((int64_t)L.planes * T * L.ldt * 4);
-  L.total = o;
+  L.weights_bytes = o;
+  L.scratch_bytes = align256((int64_t)L.planes * T * L.ldt * 4);
+  L.total = L.plan_bytes + L.weights_bytes + L.scratch_bytes;
   return true;
 }
+
+enum { kPackNone = 0, kPackUsed = 1, kPackAll = 2 };
 
 struct refop_prep_args {
   const void* w;
@@ -120,6 +149,11 @@ struct refop_prep_args {
   char* arena;
   int64_t slot_bytes;
   pl_slot_entry* table;
+  int32_t* marks;      // marks[s]: call epoch at which adapter s was packed, 0 = never
+  int32_t build_plan;
+  int32_t pack;        // kPackNone, kPackUsed or kPackAll
+  int32_t keep;        // consult and update marks
+  int32_t epoch;
   // the plan
   const int32_t* seq_lens;
   int32_t B, M;
@@ -137,57 +171,121 @@ __device__ __forceinline__ int pl_refop_rank(const refop_prep_args& a, int s) {
   return (int)(r < 0 ? 0 : (r > a.rank_cap ? a.rank_cap : r));
 }
 
-// Grid: y = 0, x = 0 writes the slot table and builds the plan (the other
-// workgroups of row y = 0 have nothing to do); y = s + 1 repacks adapter s,
-// x covering its matrix.  The plan's slot for row b is adapter widx[b] + 1
-// when widx[b] is in range and ranks[widx[b]] > 0 (the same test as
-// pl_refop_rank(a, widx[b]) > 0, since stack_num >= 1 and rank_cap >= 1).
+// One repack unit of adapter s: destination rows [i0, i0 + 64) and columns
+// [c0, c0 + 4W) of its [R][C] matrix (A [r][K]: i = rank, c = k; B
+// [N][rank8]: i = n, c = rank), element (i, c) = w[s][c][i] in the
+// reference layout (zero for c >= r in B).  Reads: lane l of a wave takes
+// row i0 + l, so a wave reads 64 consecutive elements of the source's
+// i-dimension (its fastest for the reference's contiguous tensors) at one
+// c.  Writes: the unit's 16 destination blocks (4 row tiles x 4 column
+// blocks), each rt * wb contiguous elements, consecutive threads on
+// consecutive elements.
 template <int DT>
-__global__ __launch_bounds__(kPlanThreads) void pl_refop_prep_plan(refop_prep_args a) {
+__device__ __forceinline__ void pl_refop_pack_unit(const refop_prep_args& a, int s, int r, int R,
+                                                   int C, int i0, int c0,
+                                                   typename pl_traits<DT>::T* tile) {
   typedef typename pl_traits<DT>::T T;
+  constexpr int W = 4 * pl_traits<DT>::E;  // elements of a 64-byte column block
+  constexpr int UC = kPackBlocks * W;      // columns of a unit
+  constexpr int LD = UC + 4 / (int)sizeof(T);  // row stride: an odd number of words
+  constexpr int kColsPerPass = kPlanThreads / kPackRows;
+  const int tid = threadIdx.x;
+  const int i_off = tid & (kPackRows - 1);
+  const int cq = tid / kPackRows;
+  const int i = i0 + i_off;
+  const int c_lim = a.which == 0 ? C : min(C, r);  // B's columns r..rank8-1 are zero
+  const T* __restrict__ w = reinterpret_cast<const T*>(a.w) + (int64_t)s * a.s0;
+  T v[UC / kColsPerPass];
+#pragma unroll
+  for (int k = 0; k < UC / kColsPerPass; ++k) {
+    const int c = c0 + cq + k * kColsPerPass;
+    v[k] = (i < R && c < c_lim) ? w[(int64_t)c * a.s1 + (int64_t)i * a.s2] : (T)0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < UC / kColsPerPass; ++k) tile[i_off * LD + cq + k * kColsPerPass] = v[k];
+  __syncthreads();
+  T* __restrict__ dst = reinterpret_cast<T*>(a.arena + (int64_t)s * a.slot_bytes);
+  constexpr int kBlockElems = 16 * W;
+  for (int f = tid; f < 4 * kPackBlocks * kBlockElems; f += kPlanThreads) {
+    const int blk = f / kBlockElems;  // tile-major: a tile's column blocks are adjacent in memory
+    const int e = f - blk * kBlockElems;
+    const int tt = blk / kPackBlocks;
+    const int cb = blk - tt * kPackBlocks;
+    const int t16 = i0 + 16 * tt;
+    const int cs = c0 + cb * W;
+    if (t16 >= R || cs >= C) continue;
+    const int rt = min(16, R - t16);
+    const int wb = min(W, C - cs);
+    if (e >= rt * wb) continue;
+    const int row = e / wb;
+    const int col = e - row * wb;
+    dst[(int64_t)t16 * C + (int64_t)cs * rt + e] = tile[(16 * tt + row) * LD + cb * W + col];
+  }
+  __syncthreads();  // the tile is reused by the next unit
+}
+
+// Grid: y = 0, x = 0 writes the slot table (when packing) and builds the
+// plan (when asked); the other workgroups of row y = 0 have nothing to do.
+// y = s + 1 repacks adapter s, the x workgroups striding over its units.
+template <int DT>
+__global__ __launch_bounds__(kPlanThreads) void pl_refop_prep(refop_prep_args a) {
+  typedef typename pl_traits<DT>::T T;
+  constexpr int W = 4 * pl_traits<DT>::E;
+  __shared__ T tile[kPackRows * (kPackBlocks * W + 4 / (int)sizeof(T))];
   if (blockIdx.y == 0) {
     if (blockIdx.x != 0) return;
-    for (int e = threadIdx.x; e <= a.num_adapters; e += kPlanThreads) {
-      pl_slot_entry en;
-      en.rank = 0;
-      en.scale = 0.f;
-      en.rank8 = 0;
-      en.reserved = 0;
-      en.a_off = 0;
-      en.b_off = 0;
-      if (e > 0) {
-        const int r = pl_refop_rank(a, e - 1);
-        en.rank = r;
-        en.scale = a.which == 1 ? a.scalings[e - 1] : 1.f;
-        en.rank8 = (r + 7) & ~7;
-        en.a_off = (int64_t)(e - 1) * a.slot_bytes;
-        en.b_off = en.a_off;
+    if (a.pack != kPackNone) {
+      for (int e = threadIdx.x; e <= a.num_adapters; e += kPlanThreads) {
+        pl_slot_entry en;
+        en.rank = 0;
+        en.scale = 0.f;
+        en.rank8 = 0;
+        en.reserved = 0;
+        en.a_off = 0;
+        en.b_off = 0;
+        if (e > 0) {
+          const int r = pl_refop_rank(a, e - 1);
+          en.rank = r;
+          en.scale = a.which == 1 ? a.scalings[e - 1] : 1.f;
+          en.rank8 = (r + 7) & ~7;
+          en.a_off = (int64_t)(e - 1) * a.slot_bytes;
+          en.b_off = en.a_off;
+        }
+        a.table[e] = en;
       }
-      a.table[e] = en;
     }
-    pl_plan_body<true>(a.widx, a.ranks, a.num_adapters, a.seq_lens, a.B, a.M, a.num_adapters + 1,
-                       nullptr, 0, a.group_tokens, a.tok, a.groups, a.meta, a.group_cap);
+    if (a.build_plan)
+      pl_plan_body<true>(a.widx, a.num_adapters, a.seq_lens, a.B, a.M, a.num_adapters + 1,
+                         nullptr, 0, a.group_tokens, a.tok, a.groups, a.meta, a.group_cap);
     return;
   }
   const int s = blockIdx.y - 1;
-  const int64_t e = (int64_t)blockIdx.x * kPlanThreads + threadIdx.x;
+  if (a.keep) {
+    // packed at an earlier call: skip.  Within this call every workgroup of
+    // s reads 0 or this call's epoch and packs its units.
+    const int prev = a.marks[s];
+    if (prev != 0 && prev != a.epoch) return;
+  }
   const int r = pl_refop_rank(a, s);
-  if (r == 0) return;
-  // the slot's matrix [R][C] in logical order, columns fastest: A [r][K], B [N][rank8]
+  if (r == 0) {
+    if (a.keep && blockIdx.x == 0 && threadIdx.x == 0) a.marks[s] = a.epoch;  // nothing to pack
+    return;
+  }
+  if (a.pack == kPackUsed) {
+    int used = 0;
+    for (int b = threadIdx.x; b < a.B; b += kPlanThreads) used |= a.widx[b] == s;
+    if (!__syncthreads_or(used)) return;
+  }
+  // the slot's matrix [R][C]: A [r][K], B [N][rank8]
   const int R = a.which == 0 ? r : a.width;
   const int C = a.which == 0 ? a.width : ((r + 7) & ~7);
-  if (e >= (int64_t)R * C) return;
-  const int i = (int)(e / C);
-  const int c = (int)(e - (int64_t)i * C);
-  const T* w = reinterpret_cast<const T*>(a.w) + (int64_t)s * a.s0;
-  T v;
-  if (a.which == 0) {
-    v = w[(int64_t)c * a.s1 + (int64_t)i * a.s2];  // A[r=i][k=c] = w[s][k][r]
-  } else {
-    v = c < r ? w[(int64_t)c * a.s1 + (int64_t)i * a.s2] : (T)0.f;  // B[n=i][j=c] = w[s][j][n]
+  const int nc = (C + kPackBlocks * W - 1) / (kPackBlocks * W);
+  const int units = (R + kPackRows - 1) / kPackRows * nc;
+  for (int u = blockIdx.x; u < units; u += gridDim.x) {
+    const int q = u / nc;
+    pl_refop_pack_unit<DT>(a, s, r, R, C, q * kPackRows, (u - q * nc) * kPackBlocks * W, tile);
   }
-  T* dst = reinterpret_cast<T*>(a.arena + (int64_t)s * a.slot_bytes);
-  dst[pl_tile_off<DT>(i, c, R, C)] = v;
+  if (a.keep && threadIdx.x == 0) a.marks[s] = a.epoch;
 }
 
 // out[tok[p]][n] = T(sum of the planes at (p, n)) for n below the slot's rank:
@@ -216,7 +314,8 @@ __global__ __launch_bounds__(kThreads) void pl_refop_finish(const float* __restr
 }
 
 // plane[p][j] = x[tok[p]][j] for j below the slot's rank, 0 up to ldt: one
-// workgroup per plan group record.
+// workgroup per plan group record (groups of rank-0 slots are skipped: the
+// expand reads nothing of theirs).
 template <int DT>
 __global__ __launch_bounds__(kThreads) void pl_refop_gather(const void* __restrict__ x,
                                                             int32_t k_max, int32_t ldt,
@@ -228,6 +327,7 @@ __global__ __launch_bounds__(kThreads) void pl_refop_gather(const void* __restri
   const pl_group g = groups[blockIdx.x];
   if (g.len <= 0 || g.slot <= 0) return;
   const int r = table[g.slot].rank;
+  if (r <= 0) return;
   for (int idx = threadIdx.x; idx < g.len * ldt; idx += kThreads) {
     const int i = idx / ldt;
     const int j = idx - i * ldt;
@@ -259,15 +359,66 @@ bool refop_fused(const refop_layout& L, int32_t num_adapters, int32_t K) {
   return L.tokens >= 1024 && L.tokens >= (int64_t)64 * num_adapters && K <= 16384;
 }
 
-// The slot table, the plan and the repacked weights (pl_refop_prep_plan).
-// The layout fixes the plan's sizes: group_tokens 16 or 64, num_adapters + 1
-// <= PL_MAX_SLOTS slots, B * M < 2^31 tokens and group_cap at the bound of
+// The three parts of a call: the caller's, or one workspace split in order
+// plan | weights | scratch with the flags of a call that keeps nothing.
+// Returns PL_OK, PL_ERR_ARG for parts that are too small, misaligned or
+// missing, or PL_REFOP_DECLINED when there is nothing to work in.
+int refop_parts(const refop_layout& L, bool fused, void* workspace, int64_t workspace_bytes,
+                const pl_refop_parts* parts, const char* what, pl_refop_parts& P) {
+  if (parts == nullptr) {
+    if (!workspace) return PL_REFOP_DECLINED;
+    if (!aligned256(workspace) || workspace_bytes < L.total) {
+      pl_set_error("%s workspace: %lld bytes at %p, this call needs %lld 256-byte aligned", what,
+                   (long long)workspace_bytes, workspace, (long long)L.total);
+      return PL_ERR_ARG;
+    }
+    char* ws = reinterpret_cast<char*>(workspace);
+    P.plan = ws;
+    P.plan_bytes = L.plan_bytes;
+    P.weights = ws + L.plan_bytes;
+    P.weights_bytes = L.weights_bytes;
+    P.scratch = ws + L.plan_bytes + L.weights_bytes;
+    P.scratch_bytes = L.scratch_bytes;
+    P.flags = PL_REF_BUILD_PLAN | PL_REF_PACK_USED;
+    P.epoch = 0;
+    return PL_OK;
+  }
+  P = *parts;
+  const bool scratch_ok =
+      fused || (P.scratch && aligned256(P.scratch) && P.scratch_bytes >= L.scratch_bytes);
+  if (!P.plan || !aligned256(P.plan) || P.plan_bytes < L.plan_bytes || !P.weights ||
+      !aligned256(P.weights) || P.weights_bytes < L.weights_bytes || !scratch_ok) {
+    pl_set_error("%s parts: plan %lld bytes at %p, weights %lld at %p, scratch %lld at %p; this "
+                 "call needs %lld, %lld and %lld, each 256-byte aligned",
+                 what, (long long)P.plan_bytes, P.plan, (long long)P.weights_bytes, P.weights,
+                 (long long)P.scratch_bytes, P.scratch, (long long)L.plan_bytes,
+                 (long long)L.weights_bytes, fused ? 0LL : (long long)L.scratch_bytes);
+    return PL_ERR_ARG;
+  }
+  const int32_t known = PL_REF_BUILD_PLAN | PL_REF_PACK_USED | PL_REF_PACK_ALL | PL_REF_KEEP_PACKED;
+  if ((P.flags & ~known) != 0 || ((P.flags & PL_REF_KEEP_PACKED) && P.epoch < 1)) {
+    pl_set_error("%s: build flags 0x%x / epoch %d (PL_REF_KEEP_PACKED needs an epoch >= 1)", what,
+                 P.flags, P.epoch);
+    return PL_ERR_ARG;
+  }
+  return PL_OK;
+}
+
+// Step 1 (pl_refop_prep) when the flags ask for any of it.  The layout fixes
+// the plan's sizes: group_tokens 16 or 64, num_adapters + 1 <= PL_MAX_SLOTS
+// slots, B * M < 2^31 tokens and group_cap at the bound of
 // pl_plan_group_capacity, the checks pl_plan_build makes.
-int refop_prep(int32_t dtype, const refop_layout& L, char* ws, const void* w, int64_t s0,
-               int64_t s1, int64_t s2, int32_t num_adapters, int which, int32_t width,
+int refop_prep(int32_t dtype, const refop_layout& L, const pl_refop_parts& P, const void* w,
+               int64_t s0, int64_t s1, int64_t s2, int32_t num_adapters, int which, int32_t width,
                int32_t rank_cap, int32_t stack_num, const int32_t* ranks, const float* scalings,
                const int32_t* widx, int32_t B, int32_t M, const int32_t* seq_lens, hipStream_t s) {
   refop_prep_args a;
+  a.build_plan = (P.flags & PL_REF_BUILD_PLAN) ? 1 : 0;
+  a.pack = (P.flags & PL_REF_PACK_ALL) ? kPackAll : (P.flags & PL_REF_PACK_USED) ? kPackUsed
+                                                                                  : kPackNone;
+  if (!a.build_plan && a.pack == kPackNone) return PL_OK;
+  a.keep = (P.flags & PL_REF_KEEP_PACKED) ? 1 : 0;
+  a.epoch = P.epoch;
   a.w = w;
   a.s0 = s0;
   a.s1 = s1;
@@ -280,28 +431,33 @@ int refop_prep(int32_t dtype, const refop_layout& L, char* ws, const void* w, in
   a.ranks = ranks;
   a.scalings = scalings;
   a.widx = widx;
-  a.arena = ws + L.arena;
+  char* wp = reinterpret_cast<char*>(P.weights);
+  char* pp = reinterpret_cast<char*>(P.plan);
+  a.arena = wp + L.arena;
   a.slot_bytes = L.slot_bytes;
-  a.table = reinterpret_cast<pl_slot_entry*>(ws + L.table);
+  a.table = reinterpret_cast<pl_slot_entry*>(wp + L.table);
+  a.marks = reinterpret_cast<int32_t*>(wp + L.marks);
   a.seq_lens = seq_lens;
   a.B = B;
   a.M = M;
   a.group_tokens = L.group_tokens;
   a.group_cap = L.group_cap;
-  a.tok = reinterpret_cast<int32_t*>(ws + L.tok);
-  a.groups = reinterpret_cast<pl_group*>(ws + L.groups);
-  a.meta = reinterpret_cast<int32_t*>(ws + L.meta);
-  const int64_t mat = which == 0 ? (int64_t)rank_cap * width : (int64_t)width * round8(rank_cap);
-  const int64_t gx = (mat + kPlanThreads - 1) / kPlanThreads;
-  if (!pl_grid_fits(gx, kPlanThreads)) {
-    pl_set_error("reference-layout repack grid too large");
-    return PL_ERR_LIMIT;
-  }
+  a.tok = reinterpret_cast<int32_t*>(pp + L.tok);
+  a.groups = reinterpret_cast<pl_group*>(pp + L.groups);
+  a.meta = reinterpret_cast<int32_t*>(pp + L.meta);
+  // repack units of the largest matrix an adapter can have (rank = rank_cap)
+  const int W = 4 * pl_chunk_elems(dtype);
+  const int64_t Rmax = which == 0 ? rank_cap : width;
+  const int64_t Cmax = which == 0 ? width : round8(rank_cap);
+  const int64_t units = (Rmax + kPackRows - 1) / kPackRows *
+                        ((Cmax + kPackBlocks * W - 1) / (kPackBlocks * W));
+  const int64_t gx = a.pack == kPackNone ? 1 : std::min<int64_t>(units, kPackGridCap);
+  const int gy = a.pack == kPackNone ? 1 : num_adapters + 1;
   refop_dispatch(dtype, [&](auto dt) {
-    hipLaunchKernelGGL(pl_refop_prep_plan<decltype(dt)::value>,
-                       dim3((unsigned)gx, num_adapters + 1), dim3(kPlanThreads), 0, s, a);
+    hipLaunchKernelGGL(pl_refop_prep<decltype(dt)::value>, dim3((unsigned)gx, gy),
+                       dim3(kPlanThreads), 0, s, a);
   });
-  return pl_launch_status("pl_refop_prep_plan");
+  return pl_launch_status("pl_refop_prep");
 }
 
 }  // namespace
@@ -313,36 +469,50 @@ extern "C" int64_t pl_sgmv_ref_workspace_bytes(int32_t dtype, int32_t which, int
   return refop_plan_layout(dtype, which, B, M, K, n, num_adapters, L) ? L.total : 0;
 }
 
+extern "C" int64_t pl_sgmv_ref_part_bytes(int32_t dtype, int32_t which, int32_t B, int32_t M,
+                                          int32_t K, int32_t n, int32_t num_adapters,
+                                          int32_t part) {
+  refop_layout L;
+  if (which != 0 && which != 1) return 0;
+  if (!refop_plan_layout(dtype, which, B, M, K, n, num_adapters, L)) return 0;
+  switch (part) {
+    case PL_REF_PART_PLAN: return L.plan_bytes;
+    case PL_REF_PART_WEIGHTS: return L.weights_bytes;
+    case PL_REF_PART_SCRATCH: return refop_fused(L, num_adapters, K) ? 0 : L.scratch_bytes;
+    default: return 0;
+  }
+}
+
 int pl_refop_shrink(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K, const void* w,
                     int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t num_adapters,
                     int32_t n_max, const int32_t* seq_lens, const int32_t* weight_indices,
                     const int32_t* lora_ranks, int32_t stack_num, void* out, void* workspace,
-                    int64_t workspace_bytes, void* stream) {
+                    int64_t workspace_bytes, const pl_refop_parts* parts, void* stream) {
   refop_layout L;
-  if (!workspace || !refop_plan_layout(dtype, 0, B, M, K, n_max, num_adapters, L) ||
+  if (!refop_plan_layout(dtype, 0, B, M, K, n_max, num_adapters, L) ||
       (reinterpret_cast<uintptr_t>(x) & 15) != 0)
     return PL_REFOP_DECLINED;
-  if (!aligned256(workspace) || workspace_bytes < L.total) {
-    pl_set_error("sgmv_lora_a workspace: %lld bytes at %p, this call needs %lld 256-byte aligned",
-                 (long long)workspace_bytes, workspace, (long long)L.total);
-    return PL_ERR_ARG;
-  }
-  char* ws = reinterpret_cast<char*>(workspace);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  int st = refop_prep(dtype, L, ws, w, w_s0, w_s1, w_s2, num_adapters, 0, K, n_max, stack_num,
-                      lora_ranks, nullptr, weight_indices, B, M, seq_lens, s);
+  const bool fused = refop_fused(L, num_adapters, K);
+  pl_refop_parts P;
+  int st = refop_parts(L, fused, workspace, workspace_bytes, parts, "sgmv_lora_a", P);
   if (st) return st;
-  int32_t* meta = reinterpret_cast<int32_t*>(ws + L.meta);
-  pl_group* groups = reinterpret_cast<pl_group*>(ws + L.groups);
-  int32_t* tok = reinterpret_cast<int32_t*>(ws + L.tok);
-  const pl_slot_entry* table = reinterpret_cast<const pl_slot_entry*>(ws + L.table);
-  float* planes = reinterpret_cast<float*>(ws + L.plane);
-  if (refop_fused(L, num_adapters, K))
-    return pl_fused_phase(PL_FUSED_SHRINK, dtype, x, K, K, out, n_max, n_max, ws + L.arena, table,
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  st = refop_prep(dtype, L, P, w, w_s0, w_s1, w_s2, num_adapters, 0, K, n_max, stack_num,
+                  lora_ranks, nullptr, weight_indices, B, M, seq_lens, s);
+  if (st) return st;
+  char* pp = reinterpret_cast<char*>(P.plan);
+  char* wp = reinterpret_cast<char*>(P.weights);
+  int32_t* meta = reinterpret_cast<int32_t*>(pp + L.meta);
+  pl_group* groups = reinterpret_cast<pl_group*>(pp + L.groups);
+  int32_t* tok = reinterpret_cast<int32_t*>(pp + L.tok);
+  const pl_slot_entry* table = reinterpret_cast<const pl_slot_entry*>(wp + L.table);
+  if (fused)
+    return pl_fused_phase(PL_FUSED_SHRINK, dtype, x, K, K, out, n_max, n_max, wp + L.arena, table,
                           L.ldt, tok, groups, meta, L.group_cap, L.group_tokens, PL_EPI_FALLBACK,
                           stream);
-  st = pl_sgmv_shrink(dtype, x, K, K, ws + L.arena, table, 1, 0, tok, groups, meta, L.group_cap,
-                      L.group_tokens, planes, L.total - L.plane, L.ldt, L.tokens, L.k_splits,
+  float* planes = reinterpret_cast<float*>(P.scratch);
+  st = pl_sgmv_shrink(dtype, x, K, K, wp + L.arena, table, 1, 0, tok, groups, meta, L.group_cap,
+                      L.group_tokens, planes, L.scratch_bytes, L.ldt, L.tokens, L.k_splits,
                       stream);
   if (st) return st;
   refop_dispatch(dtype, [&](auto dt) {
@@ -358,36 +528,36 @@ int pl_refop_expand(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t 
                     int32_t num_adapters, int32_t N, const int32_t* seq_lens,
                     const int32_t* weight_indices, const int32_t* lora_ranks,
                     const float* scalings, void* out, void* workspace, int64_t workspace_bytes,
-                    void* stream) {
+                    const pl_refop_parts* parts, void* stream) {
   refop_layout L;
-  if (!workspace || !refop_plan_layout(dtype, 1, B, M, k_max, N, num_adapters, L) ||
+  if (!refop_plan_layout(dtype, 1, B, M, k_max, N, num_adapters, L) ||
       (reinterpret_cast<uintptr_t>(out) & 15) != 0)
     return PL_REFOP_DECLINED;
-  if (!aligned256(workspace) || workspace_bytes < L.total) {
-    pl_set_error("sgmv_lora_b workspace: %lld bytes at %p, this call needs %lld 256-byte aligned",
-                 (long long)workspace_bytes, workspace, (long long)L.total);
-    return PL_ERR_ARG;
-  }
-  char* ws = reinterpret_cast<char*>(workspace);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  int st = refop_prep(dtype, L, ws, w, w_s0, w_s1, w_s2, num_adapters, 1, N, k_max, 1, lora_ranks,
-                      scalings, weight_indices, B, M, seq_lens, s);
+  const bool fused = refop_fused(L, num_adapters, k_max);
+  pl_refop_parts P;
+  int st = refop_parts(L, fused, workspace, workspace_bytes, parts, "sgmv_lora_b", P);
   if (st) return st;
-  int32_t* meta = reinterpret_cast<int32_t*>(ws + L.meta);
-  pl_group* groups = reinterpret_cast<pl_group*>(ws + L.groups);
-  int32_t* tok = reinterpret_cast<int32_t*>(ws + L.tok);
-  const pl_slot_entry* table = reinterpret_cast<const pl_slot_entry*>(ws + L.table);
-  float* plane = reinterpret_cast<float*>(ws + L.plane);
-  if (refop_fused(L, num_adapters, k_max))
-    return pl_fused_phase(PL_FUSED_EXPAND, dtype, x, k_max, k_max, out, N, N, ws + L.arena, table,
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  st = refop_prep(dtype, L, P, w, w_s0, w_s1, w_s2, num_adapters, 1, N, k_max, 1, lora_ranks,
+                  scalings, weight_indices, B, M, seq_lens, s);
+  if (st) return st;
+  char* pp = reinterpret_cast<char*>(P.plan);
+  char* wp = reinterpret_cast<char*>(P.weights);
+  int32_t* meta = reinterpret_cast<int32_t*>(pp + L.meta);
+  pl_group* groups = reinterpret_cast<pl_group*>(pp + L.groups);
+  int32_t* tok = reinterpret_cast<int32_t*>(pp + L.tok);
+  const pl_slot_entry* table = reinterpret_cast<const pl_slot_entry*>(wp + L.table);
+  if (fused)
+    return pl_fused_phase(PL_FUSED_EXPAND, dtype, x, k_max, k_max, out, N, N, wp + L.arena, table,
                           L.ldt, tok, groups, meta, L.group_cap, L.group_tokens, PL_EPI_TRITON,
                           stream);
+  float* plane = reinterpret_cast<float*>(P.scratch);
   refop_dispatch(dtype, [&](auto dt) {
     hipLaunchKernelGGL(pl_refop_gather<decltype(dt)::value>, dim3((unsigned)L.group_cap),
                        dim3(kThreads), 0, s, x, k_max, L.ldt, groups, tok, table, plane);
   });
   st = pl_launch_status("pl_refop_gather");
   if (st) return st;
-  return pl_sgmv_expand(dtype, plane, L.ldt, L.tokens, 1, ws + L.arena, table, 1, 0, tok, groups,
+  return pl_sgmv_expand(dtype, plane, L.ldt, L.tokens, 1, wp + L.arena, table, 1, 0, tok, groups,
                         meta, L.group_cap, L.group_tokens, out, N, N, PL_EPI_TRITON, stream);
 }

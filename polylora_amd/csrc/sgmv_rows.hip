@@ -179,14 +179,13 @@ void pl_dispatch(int32_t dtype, F&& launch) {
   }
 }
 
-}  // namespace
-
-extern "C" int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K,
-                                  const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
-                                  int32_t num_adapters, int32_t n_max, const int32_t* seq_lens,
-                                  const int32_t* weight_indices, const int32_t* lora_ranks,
-                                  int32_t stack_num, void* out, void* workspace,
-                                  int64_t workspace_bytes, void* stream) {
+// The shrink of the operator API: the MFMA path in the parts given (or in
+// one workspace), else one wave per token row.
+int ref_a(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K, const void* w,
+          int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t num_adapters, int32_t n_max,
+          const int32_t* seq_lens, const int32_t* weight_indices, const int32_t* lora_ranks,
+          int32_t stack_num, void* out, void* workspace, int64_t workspace_bytes,
+          const pl_refop_parts* parts, void* stream) {
   if (!valid_dtype(dtype)) {
     pl_set_error("unsupported dtype code %d", dtype);
     return PL_ERR_ARG;
@@ -203,7 +202,7 @@ extern "C" int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32
   }
   const int fast = pl_refop_shrink(dtype, x, B, M, K, w, w_s0, w_s1, w_s2, num_adapters, n_max,
                                    seq_lens, weight_indices, lora_ranks, stack_num, out, workspace,
-                                   workspace_bytes, stream);
+                                   workspace_bytes, parts, stream);
   if (fast != PL_REFOP_DECLINED) return fast;
   const int64_t grid = (rows + 3) / 4;
   if (!pl_grid_fits(grid, 256)) {
@@ -219,12 +218,12 @@ extern "C" int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32
   return pl_launch_status("pl_sgmv_lora_a_ref");
 }
 
-extern "C" int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M,
-                                  int32_t k_max, const void* w, int64_t w_s0, int64_t w_s1,
-                                  int64_t w_s2, int32_t num_adapters, int32_t N,
-                                  const int32_t* seq_lens, const int32_t* weight_indices,
-                                  const int32_t* lora_ranks, const float* scalings, void* out,
-                                  void* workspace, int64_t workspace_bytes, void* stream) {
+// The expand of the operator API, as ref_a.
+int ref_b(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max, const void* w,
+          int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t num_adapters, int32_t N,
+          const int32_t* seq_lens, const int32_t* weight_indices, const int32_t* lora_ranks,
+          const float* scalings, void* out, void* workspace, int64_t workspace_bytes,
+          const pl_refop_parts* parts, void* stream) {
   if (!valid_dtype(dtype)) {
     pl_set_error("unsupported dtype code %d", dtype);
     return PL_ERR_ARG;
@@ -241,7 +240,7 @@ extern "C" int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32
   }
   const int fast = pl_refop_expand(dtype, x, B, M, k_max, w, w_s0, w_s1, w_s2, num_adapters, N,
                                    seq_lens, weight_indices, lora_ranks, scalings, out, workspace,
-                                   workspace_bytes, stream);
+                                   workspace_bytes, parts, stream);
   if (fast != PL_REFOP_DECLINED) return fast;
   const int32_t nblk = (N + 255) / 256;
   if (!pl_grid_fits(rows * nblk, 256)) {
@@ -256,6 +255,74 @@ extern "C" int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32
                        L, N, seq_lens, weight_indices, lora_ranks, scalings, out, nblk);
   });
   return pl_launch_status("pl_sgmv_lora_b_ref");
+}
+
+pl_refop_parts make_parts(void* plan, int64_t plan_bytes, void* weights, int64_t weights_bytes,
+                          void* scratch, int64_t scratch_bytes, int32_t flags, int32_t epoch) {
+  pl_refop_parts P;
+  P.plan = plan;
+  P.plan_bytes = plan_bytes;
+  P.weights = weights;
+  P.weights_bytes = weights_bytes;
+  P.scratch = scratch;
+  P.scratch_bytes = scratch_bytes;
+  P.flags = flags;
+  P.epoch = epoch;
+  return P;
+}
+
+}  // namespace
+
+extern "C" int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K,
+                                  const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
+                                  int32_t num_adapters, int32_t n_max, const int32_t* seq_lens,
+                                  const int32_t* weight_indices, const int32_t* lora_ranks,
+                                  int32_t stack_num, void* out, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  return ref_a(dtype, x, B, M, K, w, w_s0, w_s1, w_s2, num_adapters, n_max, seq_lens,
+               weight_indices, lora_ranks, stack_num, out, workspace, workspace_bytes, nullptr,
+               stream);
+}
+
+extern "C" int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M,
+                                  int32_t k_max, const void* w, int64_t w_s0, int64_t w_s1,
+                                  int64_t w_s2, int32_t num_adapters, int32_t N,
+                                  const int32_t* seq_lens, const int32_t* weight_indices,
+                                  const int32_t* lora_ranks, const float* scalings, void* out,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  return ref_b(dtype, x, B, M, k_max, w, w_s0, w_s1, w_s2, num_adapters, N, seq_lens,
+               weight_indices, lora_ranks, scalings, out, workspace, workspace_bytes, nullptr,
+               stream);
+}
+
+extern "C" int pl_sgmv_lora_a_ref_parts(int32_t dtype, const void* x, int32_t B, int32_t M,
+                                        int32_t K, const void* w, int64_t w_s0, int64_t w_s1,
+                                        int64_t w_s2, int32_t num_adapters, int32_t n_max,
+                                        const int32_t* seq_lens, const int32_t* weight_indices,
+                                        const int32_t* lora_ranks, int32_t stack_num, void* out,
+                                        void* plan, int64_t plan_bytes, void* weights,
+                                        int64_t weights_bytes, void* scratch,
+                                        int64_t scratch_bytes, int32_t flags, int32_t epoch,
+                                        void* stream) {
+  const pl_refop_parts P =
+      make_parts(plan, plan_bytes, weights, weights_bytes, scratch, scratch_bytes, flags, epoch);
+  return ref_a(dtype, x, B, M, K, w, w_s0, w_s1, w_s2, num_adapters, n_max, seq_lens,
+               weight_indices, lora_ranks, stack_num, out, nullptr, 0, &P, stream);
+}
+
+extern "C" int pl_sgmv_lora_b_ref_parts(int32_t dtype, const void* x, int32_t B, int32_t M,
+                                        int32_t k_max, const void* w, int64_t w_s0, int64_t w_s1,
+                                        int64_t w_s2, int32_t num_adapters, int32_t N,
+                                        const int32_t* seq_lens, const int32_t* weight_indices,
+                                        const int32_t* lora_ranks, const float* scalings,
+                                        void* out, void* plan, int64_t plan_bytes, void* weights,
+                                        int64_t weights_bytes, void* scratch,
+                                        int64_t scratch_bytes, int32_t flags, int32_t epoch,
+                                        void* stream) {
+  const pl_refop_parts P =
+      make_parts(plan, plan_bytes, weights, weights_bytes, scratch, scratch_bytes, flags, epoch);
+  return ref_b(dtype, x, B, M, k_max, w, w_s0, w_s1, w_s2, num_adapters, N, seq_lens,
+               weight_indices, lora_ranks, scalings, out, nullptr, 0, &P, stream);
 }
 
 extern "C" int pl_lora_apply_rows(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,

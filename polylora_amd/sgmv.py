@@ -23,7 +23,7 @@ import threading
 
 import torch
 
-from . import _native
+from . import _native, refop_cache
 
 __all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "lora_shrink", "lora_expand", "sgmv_lora_a_fwd",
            "sgmv_lora_b_fwd", "choose_k_splits", "choose_group_tokens", "side_stream", "lora_shrink_stacked",
@@ -838,27 +838,66 @@ def lora_apply_rows(
     return y
 
 
-def _check_row_meta(B: int, num_adapters: int, seq_lens, weight_indices, lora_ranks, scalings=None) -> None:
-    """Per-row and per-adapter vectors must cover every row and adapter the kernels index."""
+def _check_row_meta(B: int, num_adapters: int, seq_lens, weight_indices, lora_ranks, scalings=None,
+                    device=None) -> None:
+    """Per-row and per-adapter vectors must cover every row and adapter the kernels index, on `device`."""
+    if device is not None:
+        for name, t in (("seq_lens", seq_lens), ("weight_indices", weight_indices), ("lora_ranks", lora_ranks),
+                        ("scalings", scalings)):
+            if t is not None and t.device != device:
+                raise ValueError(f"{name} is on {t.device}; the kernels read it on {device}")
     if int(seq_lens.numel()) != B or int(weight_indices.numel()) != B:
         raise ValueError(f"seq_lens / weight_indices must have {B} entries")
     if int(lora_ranks.numel()) < num_adapters or (scalings is not None and int(scalings.numel()) < num_adapters):
         raise ValueError(f"lora_ranks / scalings must have an entry for each of the {num_adapters} adapters")
 
 
-def _ref_workspace(lib, x: torch.Tensor, which: int, B: int, M: int, K: int, n: int, num_adapters: int):
-    """Workspace of the operator API's MFMA path: (256-byte aligned uint8 view, bytes), or (None, 0).
+_REF_SIZES: dict = {}
 
-    Taken from torch's caching allocator for this call only; the allocator
-    hands the block to later work on the same stream only after this call's
-    kernels, which run in stream order.
+
+def _ref_parts(lib, x: torch.Tensor, which: int, B: int, M: int, K: int, n: int, weights: torch.Tensor,
+               seq_lens: torch.Tensor, weight_indices: torch.Tensor, lora_ranks: torch.Tensor,
+               scalings: torch.Tensor | None, stack_num: int):
+    """The parts of the operator API's MFMA path for this call, as the
+    pl_sgmv_lora_*_ref_parts arguments (plan, plan bytes, weights, weights
+    bytes, scratch, scratch bytes, flags, epoch) plus the tensors that must
+    stay alive until the launch is enqueued, or None when that path does not
+    take the shape (the row kernels then run).
+
+    The plan and weights parts come from refop_cache (kept across calls,
+    rebuilt when the tensors they depend on change) except while a HIP graph
+    is being captured, when every part is taken for this call only.  Parts
+    taken for one call come from torch's caching allocator, which hands a
+    block to later work on the same stream only after this call's kernels.
     """
-    nbytes = int(lib.pl_sgmv_ref_workspace_bytes(_native.dtype_code(x.dtype), which, B, M, K, n, num_adapters))
-    if nbytes <= 0:
-        return None, 0
-    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=x.device)
-    pad = (-buf.data_ptr()) % 256
-    return buf[pad : pad + nbytes], nbytes
+    dt = _native.dtype_code(x.dtype)
+    num_adapters = int(weights.shape[0])
+    skey = (dt, which, B, M, K, n, num_adapters)
+    sizes = _REF_SIZES.get(skey)
+    if sizes is None:
+        sizes = tuple(int(lib.pl_sgmv_ref_part_bytes(dt, which, B, M, K, n, num_adapters, p)) for p in range(3))
+        _REF_SIZES[skey] = sizes
+    plan_bytes, weights_bytes, scratch_bytes = sizes
+    if plan_bytes <= 0:
+        return None
+    device = x.device
+    scratch = refop_cache._aligned_buffer(scratch_bytes, device) if scratch_bytes else None
+    if torch.cuda.is_current_stream_capturing():
+        plan = refop_cache._aligned_buffer(plan_bytes, device)
+        wpart = refop_cache._aligned_buffer(weights_bytes, device)
+        flags, epoch = _native.PL_REF_BUILD_PLAN | _native.PL_REF_PACK_USED, 0
+    else:
+        stream = _stream(device)
+        plan, build = refop_cache.CACHE.plan(device, stream, B, M, num_adapters, seq_lens, weight_indices,
+                                             plan_bytes)
+        wpart, flags, epoch = refop_cache.CACHE.weights_part(
+            device, stream, which, weights, lora_ranks, scalings, int(stack_num), (K, n), weights_bytes,
+            refop_cache.marks_bytes(num_adapters))
+        if build:
+            flags |= _native.PL_REF_BUILD_PLAN
+    keep = (plan, wpart, scratch)
+    return (plan.data_ptr(), plan_bytes, wpart.data_ptr(), weights_bytes,
+            0 if scratch is None else scratch.data_ptr(), scratch_bytes, flags, epoch), keep
 
 
 def sgmv_lora_a_fwd(
@@ -885,34 +924,21 @@ def sgmv_lora_a_fwd(
     _require_gpu(x, "sgmv_lora_a_fwd")
     if weights.dtype != x.dtype:
         raise TypeError(f"weights dtype {weights.dtype} must match x dtype {x.dtype}")
+    seq_lens_in, weight_indices_in, lora_ranks_in = seq_lens, weight_indices, lora_ranks
     seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
-    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks)
+    if weights.device != x.device:
+        raise ValueError(f"weights are on {weights.device}, x on {x.device}")
+    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, device=x.device)
     lib = _native.load()
-    ws, ws_bytes = _ref_workspace(lib, x, 0, B, M, K, N_max, int(weights.shape[0]))
-    _native.check(
-        lib.pl_sgmv_lora_a_ref(
-            _native.dtype_code(x.dtype),
-            x.data_ptr(),
-            B,
-            M,
-            K,
-            weights.data_ptr(),
-            weights.stride(0),
-            weights.stride(1),
-            weights.stride(2),
-            int(weights.shape[0]),
-            N_max,
-            seq_lens.data_ptr(),
-            weight_indices.data_ptr(),
-            lora_ranks.data_ptr(),
-            int(stack_num),
-            output.data_ptr(),
-            0 if ws is None else ws.data_ptr(),
-            ws_bytes,
-            _stream(x.device),
-        ),
-        "pl_sgmv_lora_a_ref",
-    )
+    head = (_native.dtype_code(x.dtype), x.data_ptr(), B, M, K, weights.data_ptr(), weights.stride(0),
+            weights.stride(1), weights.stride(2), int(weights.shape[0]), N_max, seq_lens.data_ptr(),
+            weight_indices.data_ptr(), lora_ranks.data_ptr(), int(stack_num), output.data_ptr())
+    parts = _ref_parts(lib, x, 0, B, M, K, N_max, weights, seq_lens_in, weight_indices_in, lora_ranks_in, None,
+                       stack_num)
+    if parts is None:
+        _native.check(lib.pl_sgmv_lora_a_ref(*head, 0, 0, _stream(x.device)), "pl_sgmv_lora_a_ref")
+    else:
+        _native.check(lib.pl_sgmv_lora_a_ref_parts(*head, *parts[0], _stream(x.device)), "pl_sgmv_lora_a_ref_parts")
     return output
 
 
@@ -942,35 +968,22 @@ def sgmv_lora_b_fwd(
     if weights.dtype != x.dtype or output.dtype != x.dtype:
         raise TypeError("x, weights and base_output must share one dtype")
     work = output if output.is_contiguous() else output.contiguous()
+    seq_lens_in, weight_indices_in, lora_ranks_in, scalings_in = seq_lens, weight_indices, lora_ranks, scalings
     seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
     scalings = scalings.to(torch.float32).contiguous()
-    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, scalings)
+    if weights.device != x.device or output.device != x.device:
+        raise ValueError("x, weights and base_output must be on one device")
+    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, scalings, device=x.device)
     lib = _native.load()
-    ws, ws_bytes = _ref_workspace(lib, x, 1, B, M, K_max, N, int(weights.shape[0]))
-    _native.check(
-        lib.pl_sgmv_lora_b_ref(
-            _native.dtype_code(x.dtype),
-            x.data_ptr(),
-            B,
-            M,
-            K_max,
-            weights.data_ptr(),
-            weights.stride(0),
-            weights.stride(1),
-            weights.stride(2),
-            int(weights.shape[0]),
-            N,
-            seq_lens.data_ptr(),
-            weight_indices.data_ptr(),
-            lora_ranks.data_ptr(),
-            scalings.data_ptr(),
-            work.data_ptr(),
-            0 if ws is None else ws.data_ptr(),
-            ws_bytes,
-            _stream(x.device),
-        ),
-        "pl_sgmv_lora_b_ref",
-    )
+    head = (_native.dtype_code(x.dtype), x.data_ptr(), B, M, K_max, weights.data_ptr(), weights.stride(0),
+            weights.stride(1), weights.stride(2), int(weights.shape[0]), N, seq_lens.data_ptr(),
+            weight_indices.data_ptr(), lora_ranks.data_ptr(), scalings.data_ptr(), work.data_ptr())
+    parts = _ref_parts(lib, x, 1, B, M, K_max, N, weights, seq_lens_in, weight_indices_in, lora_ranks_in,
+                       scalings_in, 1)
+    if parts is None:
+        _native.check(lib.pl_sgmv_lora_b_ref(*head, 0, 0, _stream(x.device)), "pl_sgmv_lora_b_ref")
+    else:
+        _native.check(lib.pl_sgmv_lora_b_ref_parts(*head, *parts[0], _stream(x.device)), "pl_sgmv_lora_b_ref_parts")
     if work is not output:
         output.copy_(work)
     return output

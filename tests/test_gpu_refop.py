@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from oracle.lora import sgmv_expand_reference, sgmv_shrink_reference
-from polylora_amd import _native, sgmv
+from polylora_amd import _native, refop_cache, sgmv
 from tests._util import tol_for
 
 pytestmark = pytest.mark.gpu
@@ -27,13 +27,24 @@ def _announce(**kw):
     print("case:", ", ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
 
 
+def _workspace(lib, x, which, B, M, K, n, num_adapters):
+    """One 256-byte aligned workspace of pl_sgmv_ref_workspace_bytes bytes, or (None, 0) when the MFMA path
+    declines the shape."""
+    nbytes = int(lib.pl_sgmv_ref_workspace_bytes(_native.dtype_code(x.dtype), which, B, M, K, n, num_adapters))
+    if nbytes <= 0:
+        return None, 0
+    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=x.device)
+    pad = (-buf.data_ptr()) % 256
+    return buf[pad : pad + nbytes], nbytes
+
+
 def _call_a(x, w, seq, widx, ranks, stack_num, *, mfma: bool):
     """pl_sgmv_lora_a_ref through the C-ABI, with (MFMA path) or without (row kernels) a workspace."""
     lib = _native.load()
     B, M, K = x.shape
     n_max = w.shape[2]
     out = torch.full((B, M, n_max), 7.0, device=x.device, dtype=x.dtype)  # untouched entries stay 7
-    ws, nbytes = sgmv._ref_workspace(lib, x, 0, B, M, K, n_max, w.shape[0]) if mfma else (None, 0)
+    ws, nbytes = _workspace(lib, x, 0, B, M, K, n_max, w.shape[0]) if mfma else (None, 0)
     if mfma:
         assert ws is not None, "the MFMA path declined this shape"
     _native.check(lib.pl_sgmv_lora_a_ref(_native.dtype_code(x.dtype), x.data_ptr(), B, M, K, w.data_ptr(), *w.stride(),
@@ -48,7 +59,7 @@ def _call_b(x, w, seq, widx, ranks, scal, base, *, mfma: bool):
     B, M, k_max = x.shape
     N = w.shape[2]
     out = base.clone()
-    ws, nbytes = sgmv._ref_workspace(lib, x, 1, B, M, k_max, N, w.shape[0]) if mfma else (None, 0)
+    ws, nbytes = _workspace(lib, x, 1, B, M, k_max, N, w.shape[0]) if mfma else (None, 0)
     if mfma:
         assert ws is not None, "the MFMA path declined this shape"
     _native.check(lib.pl_sgmv_lora_b_ref(_native.dtype_code(x.dtype), x.data_ptr(), B, M, k_max, w.data_ptr(),
@@ -239,4 +250,166 @@ def test_workspace_errors_are_reported(gpu):
     assert b"workspace" in lib.pl_last_error()
     assert lib.pl_sgmv_lora_a_ref(*args, ctypes.c_void_p(base + 16), need, s) == _native.PL_ERR_ARG
     assert lib.pl_sgmv_lora_a_ref(*args, ctypes.c_void_p(base), need, s) == 0
+    torch.cuda.synchronize()
+
+
+def _fresh_cache():
+    refop_cache.configure()
+    for k in refop_cache.CACHE.stats:
+        refop_cache.CACHE.stats[k] = 0
+
+
+def _valid(seq, widx, ranks, M, n_max, stack_num=1):
+    """Mask of the shrink output the operator defines: m < min(seq_len, M), n < rank * stack_num."""
+    B = seq.shape[0]
+    ok = (widx >= 0) & (widx < ranks.shape[0])
+    r = torch.where(ok, ranks[widx.clamp(0, ranks.shape[0] - 1).long()], torch.zeros_like(widx)) * stack_num
+    m = torch.arange(M).view(1, M, 1)
+    n = torch.arange(n_max).view(1, 1, n_max)
+    return (m < seq.clamp(max=M).view(B, 1, 1)) & (n < r.view(B, 1, 1))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("Bt,M,K,N,S,R", [(40, 1, 512, 256, 9, 16), (24, 96, 256, 136, 5, 32)])
+def test_kept_parts_equal_a_fresh_workspace_call(gpu, dtype, Bt, M, K, N, S, R):
+    """sgmv_lora_a_fwd / sgmv_lora_b_fwd keep the plan and the repacked weights across calls.  The first
+    call packs only the adapters its rows use, the second the rest, later calls launch no repack, and
+    one plan serves the shrink and the expand.  Every call equals the C-ABI call with a fresh single
+    workspace bit for bit, also for a batch whose rows use only adapters the first batch did not; then
+    in-place writes to an adapter's weights, to a rank and to the adapter index are seen."""
+    _announce(test="refop_kept_parts", dtype=dtype, shape=(Bt, M, K, N, S, R))
+    _fresh_cache()
+    st = refop_cache.CACHE.stats
+    g = torch.Generator().manual_seed(Bt + K)
+    _, (dx, dwa, dwb, dranks, dscal, dseq, _) = _case(g, Bt, M, K, N, S, R, 1, dtype, gpu)
+    dranks[1:] = torch.randint(1, R + 1, (S - 1,), generator=g, dtype=torch.int32).to(gpu)
+    half = S // 2 + 1
+    idx = {1: (torch.arange(Bt) % half).to(torch.int32).to(gpu),
+           2: (half + torch.arange(Bt) % (S - half)).to(torch.int32).to(gpu)}
+    base = torch.randn(Bt, M, N, generator=g).to(dtype).to(gpu)
+
+    def check(w_idx, step):
+        want_a = _call_a(dx, dwa, dseq, w_idx, dranks, 1, mfma=True)
+        got_a = sgmv.sgmv_lora_a_fwd(dx, dwa, dseq, w_idx, dranks)
+        valid = _valid(dseq.cpu(), w_idx.cpu(), dranks.cpu(), M, R).to(gpu)
+        assert torch.equal(got_a[valid], want_a[valid]), step
+        want_b = _call_b(want_a, dwb, dseq, w_idx, dranks, dscal, base, mfma=True)
+        got_b = sgmv.sgmv_lora_b_fwd(want_a, dwb, dseq, w_idx, dranks, dscal, base.clone())
+        assert torch.equal(got_b, want_b), step
+
+    for step, which in enumerate([1, 1, 2, 2, 1]):
+        check(idx[which], step)
+    torch.cuda.synchronize()
+    assert (st["pack_used"], st["pack_all"], st["weights_hits"]) == (2, 2, 6), st
+    assert (st["plan_builds"], st["plan_hits"]) == (2, 8), st
+    dwa[1].mul_(2.0)  # adapter 1 (used by batch 1) changes in place
+    check(idx[1], "weights written")
+    assert st["pack_used"] == 3 and st["weights_hits"] == 7, st  # the shrink's part repacked, the expand's kept
+    dranks[2] = max(1, int(dranks[2]) // 2)
+    check(idx[1], "rank written")
+    assert st["pack_used"] == 5, st
+    idx[1][0] = S - 1
+    check(idx[1], "index written")
+    assert st["plan_builds"] == 3, st
+    torch.cuda.synchronize()
+
+
+def test_tensors_without_version_counter_are_not_kept(gpu):
+    _announce(test="refop_inference_tensors")
+    _fresh_cache()
+    g = torch.Generator().manual_seed(31)
+    _, (dx, dwa, dwb, dranks, dscal, dseq, dwidx) = _case(g, 16, 1, 256, 128, 5, 16, 1, torch.bfloat16, gpu)
+    with torch.inference_mode():
+        wi, idx_i = dwa.clone(), dwidx.clone()
+    for _ in range(2):
+        want = _call_a(dx, dwa, dseq, dwidx, dranks, 1, mfma=True)
+        got = sgmv.sgmv_lora_a_fwd(dx, wi, dseq, idx_i, dranks)
+        valid = _valid(dseq.cpu(), dwidx.cpu(), dranks.cpu(), 1, 16).to(gpu)
+        assert torch.equal(got[valid], want[valid])
+    st = refop_cache.CACHE.stats
+    assert st["uncached"] == 2 and st["plan_hits"] == 0 and st["plan_builds"] == 2, st
+    assert not refop_cache.CACHE.weights
+
+
+def test_kept_weights_die_with_their_tensor(gpu):
+    import gc
+
+    _announce(test="refop_dead_weights")
+    _fresh_cache()
+    g = torch.Generator().manual_seed(32)
+    _, (dx, dwa, dwb, dranks, dscal, dseq, dwidx) = _case(g, 16, 1, 256, 128, 5, 16, 1, torch.bfloat16, gpu)
+    w = dwa.clone()
+    sgmv.sgmv_lora_a_fwd(dx, w, dseq, dwidx, dranks)
+    assert len(refop_cache.CACHE.weights) == 1 and refop_cache.CACHE.bytes[dx.device] > 0
+    del w
+    gc.collect()
+    sgmv.sgmv_lora_a_fwd(dx, dwa, dseq, dwidx, dranks)  # the next call drops the dead entry
+    assert len(refop_cache.CACHE.weights) == 1
+    torch.cuda.synchronize()
+
+
+def test_operator_api_in_a_graph_replays(gpu):
+    """Shrink then expand captured in a HIP graph (every part taken for the captured call, nothing kept):
+    each replay, with eager work between replays, equals the eager result bit for bit."""
+    _announce(test="refop_graph")
+    _fresh_cache()
+    g = torch.Generator().manual_seed(33)
+    _, (dx, dwa, dwb, dranks, dscal, dseq, dwidx) = _case(g, 32, 1, 512, 256, 6, 16, 1, torch.bfloat16, gpu)
+    base = torch.randn(32, 1, 256, generator=g).bfloat16().to(gpu)
+    out = torch.empty_like(base)
+    tmp = torch.zeros(32, 1, 16, dtype=torch.bfloat16, device=gpu)
+
+    def step():
+        tmp.copy_(sgmv.sgmv_lora_a_fwd(dx, dwa, dseq, dwidx, dranks))
+        out.copy_(base)
+        sgmv.sgmv_lora_b_fwd(tmp, dwb, dseq, dwidx, dranks, dscal, out)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    valid = _valid(dseq.cpu(), dwidx.cpu(), dranks.cpu(), 1, 16).to(gpu)
+    want_tmp, want = tmp.clone(), out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for i in range(3):
+        out.fill_(float(i))
+        tmp.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(tmp[valid], want_tmp[valid]) and torch.equal(out, want), i
+
+
+def test_part_entry_points_reject_bad_flags(gpu):
+    """The part-based entry points refuse unknown flags, PL_REF_KEEP_PACKED without an epoch, and parts
+    below their sizes."""
+    _announce(test="refop_part_errors")
+    lib = _native.load()
+    x = torch.randn(4, 2, 64, device=gpu).bfloat16()
+    w = torch.randn(3, 64, 8, device=gpu).bfloat16()
+    seq = torch.full((4,), 2, dtype=torch.int32, device=gpu)
+    widx = torch.tensor([0, 1, 2, 1], dtype=torch.int32, device=gpu)
+    ranks = torch.tensor([2, 4, 8], dtype=torch.int32, device=gpu)
+    out = torch.empty(4, 2, 8, device=gpu).bfloat16()
+    sizes = [int(lib.pl_sgmv_ref_part_bytes(_native.PL_BF16, 0, 4, 2, 64, 8, 3, p)) for p in range(3)]
+    assert all(n > 0 for n in sizes)
+    bufs = [torch.zeros(n + 256, dtype=torch.uint8, device=gpu) for n in sizes]
+    ptrs = [b.data_ptr() + (-b.data_ptr()) % 256 for b in bufs]
+    s = torch.cuda.current_stream().cuda_stream
+    args = (_native.PL_BF16, x.data_ptr(), 4, 2, 64, w.data_ptr(), *w.stride(), 3, 8, seq.data_ptr(),
+            widx.data_ptr(), ranks.data_ptr(), 1, out.data_ptr())
+
+    def call(flags, epoch, shrink=0):
+        return lib.pl_sgmv_lora_a_ref_parts(*args, ptrs[0], sizes[0], ptrs[1], sizes[1] - shrink, ptrs[2], sizes[2],
+                                            flags, epoch, s)
+
+    assert call(16, 0) == _native.PL_ERR_ARG
+    assert call(_native.PL_REF_PACK_USED | _native.PL_REF_KEEP_PACKED, 0) == _native.PL_ERR_ARG
+    assert call(_native.PL_REF_BUILD_PLAN | _native.PL_REF_PACK_USED, 0, shrink=256) == _native.PL_ERR_ARG
+    assert b"parts" in lib.pl_last_error()
+    assert call(_native.PL_REF_BUILD_PLAN | _native.PL_REF_PACK_ALL | _native.PL_REF_KEEP_PACKED, 1) == 0
     torch.cuda.synchronize()
