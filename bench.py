@@ -34,6 +34,7 @@ import argparse
 from collections import Counter
 import json
 import os
+import re
 import platform
 import sys
 import time
@@ -1306,7 +1307,9 @@ def operator_api_decode_layer(pm, adapter_ids: list, reps: int = 30) -> dict:
     widx = cache.ensure_resident(adapter_ids)
     seq = torch.ones(B, dtype=torch.int32, device=device)
     mods = []
-    for spec in [s for s in pm.module_specs if ".layers.0." in s.name]:
+    layer0 = [s for s in pm.module_specs if re.search(r"(^|\.)layers\.0\.", s.name)]
+    assert len(layer0) == 7, [s.name for s in pm.module_specs[:8]]
+    for spec in layer0:
         K, N = spec.in_features, spec.out_features
         ranks = torch.zeros(S, dtype=torch.int32)
         for slot in range(1, S):

@@ -352,10 +352,10 @@ int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32
  * [num_adapters][k_max][N] with element strides; out [B][M][N] contiguous
  * (updated in place).  Rows with widx outside [0, num_adapters) are
  * skipped.  Workspace and paths as for pl_sgmv_lora_a_ref (which = 1; the
- * MFMA path needs a 16-byte aligned out): the intermediate x is gathered
- * into one fp32 plane and the tiled expand adds the scaled delta, or, with
- * long adapter segments as above, the fused kernel's expand phase reads x
- * directly. */
+ * MFMA path needs a 16-byte aligned out), except that after the repack +
+ * plan launch one launch of the fused kernel's expand phase reads x
+ * directly and adds the scaled delta into out, whatever the segment
+ * lengths. */
 int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max,
                        const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
                        int32_t num_adapters, int32_t N,

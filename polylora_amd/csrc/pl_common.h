@@ -177,13 +177,15 @@ static inline int pl_chunk_elems(int dtype) { return dtype == PL_F32 ? 4 : 8; }
 //   PL_FUSED_SHRINK: y[tok][c] = T(sum_k x[tok][k] * A[c][k]) for c below the
 //     slot's rank (the rest of the row is not written); N and ldy describe y.
 //   PL_FUSED_EXPAND: y[tok] += the expand of the intermediate x[tok][0..rank)
-//     (model dtype, row stride ldx; K is unused).
+//     (model dtype, row stride ldx; K is unused), the columns cut into
+//     `slices` ranges of their own workgroups (1 to 8; the shrink takes 1).
 // Operands are checked by the caller.
 enum { PL_FUSED_FULL = 0, PL_FUSED_SHRINK = 1, PL_FUSED_EXPAND = 2 };
 int pl_fused_phase(int mode, int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
                    int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
                    int32_t ldt, const int32_t* tok, const pl_group* groups, const int32_t* meta,
-                   int64_t group_cap, int32_t group_tokens, int32_t epilogue, void* stream);
+                   int64_t group_cap, int32_t group_tokens, int32_t slices, int32_t epilogue,
+                   void* stream);
 
 // MFMA path of the reference-layout operator API (sgmv_refop.hip).  Both
 // return PL_REFOP_DECLINED, having launched nothing, when there is neither a

@@ -559,7 +559,7 @@ namespace {
 
 template <int DT, int MODE>
 void launch_phase(const pl_fused_args& a, int jtmax, hipStream_t stream) {
-  const dim3 grid((unsigned)pl_xcd_grid(a.group_cap, a.sub));
+  const dim3 grid((unsigned)pl_xcd_grid(a.group_cap, (int64_t)a.sub * a.slices));
   if (jtmax <= 1)
     hipLaunchKernelGGL((pl_lora_fused_tile<DT, 1, false, MODE>), grid, dim3(kFThreads), 0, stream, a);
   else if (jtmax == 2)
@@ -573,14 +573,16 @@ void launch_phase(const pl_fused_args& a, int jtmax, hipStream_t stream) {
 int pl_fused_phase(int mode, int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
                    int64_t ldy, int32_t N, const void* arena, const pl_slot_entry* table,
                    int32_t ldt, const int32_t* tok, const pl_group* groups, const int32_t* meta,
-                   int64_t group_cap, int32_t group_tokens, int32_t epilogue, void* stream) {
+                   int64_t group_cap, int32_t group_tokens, int32_t slices, int32_t epilogue,
+                   void* stream) {
   if ((mode != PL_FUSED_SHRINK && mode != PL_FUSED_EXPAND) || ldt <= 0 || ldt > kFRankMax ||
       group_cap < 1 || group_cap > ((int64_t)1 << 24) || K <= 0 || N <= 0 ||
-      (group_tokens != PL_GROUP_TOKENS_SHORT && group_tokens != PL_GROUP_TOKENS_LONG)) {
+      (group_tokens != PL_GROUP_TOKENS_SHORT && group_tokens != PL_GROUP_TOKENS_LONG) ||
+      slices < 1 || slices > kFSliceMax || (mode == PL_FUSED_SHRINK && slices != 1)) {
     pl_set_error("pl_fused_phase: bad arguments");
     return PL_ERR_ARG;
   }
-  if (!pl_grid_fits(pl_xcd_grid(group_cap, group_tokens / 16), kFThreads)) {
+  if (!pl_grid_fits(pl_xcd_grid(group_cap, (int64_t)(group_tokens / 16) * slices), kFThreads)) {
     pl_set_error("pl_fused_phase: grid of %lld groups too large", (long long)group_cap);
     return PL_ERR_LIMIT;
   }
@@ -600,14 +602,14 @@ int pl_fused_phase(int mode, int32_t dtype, const void* x, int64_t ldx, int32_t 
   a.meta = meta;
   a.group_cap = (int32_t)group_cap;
   a.sub = group_tokens / 16;
-  a.slices = 1;
+  a.slices = slices;
   a.epilogue = epilogue;
   a.n_jobs = 1;
   a.module[0] = 0;
   a.y[0] = y;
   a.ldy[0] = ldy;
   a.N[0] = N;
-  const int64_t per_wave = ((int64_t)N + kFWaves - 1) / kFWaves;
+  const int64_t per_wave = ((int64_t)N + (int64_t)slices * kFWaves - 1) / ((int64_t)slices * kFWaves);
   a.nw[0] = (int32_t)((per_wave + kFColsMax - 1) / kFColsMax * kFColsMax);
   const int jtmax = (ldt + 15) / 16;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);

@@ -46,12 +46,13 @@ from . import _native
 _DEFAULT_BUDGET_FRACTION = 4  # default weights budget: a quarter of the device's memory
 
 
-def _ident(t: torch.Tensor) -> tuple:
-    return (t.data_ptr(), tuple(t.shape), t.stride(), t.dtype)
-
-
-def _versioned(t: torch.Tensor) -> bool:
-    return not t.is_inference()
+def _ident_version(t: torch.Tensor):
+    """(identity, version counter) of t, or None for a tensor without a version counter."""
+    try:
+        v = t._version
+    except RuntimeError:  # inference tensors track no version
+        return None
+    return (t.data_ptr(), t.shape, t.stride(), t.dtype), v
 
 
 def _aligned_buffer(nbytes: int, device: torch.device) -> torch.Tensor:
@@ -61,21 +62,23 @@ def _aligned_buffer(nbytes: int, device: torch.device) -> torch.Tensor:
 
 
 class _PlanEntry:
-    __slots__ = ("refs", "versions", "buf")
+    __slots__ = ("refs", "versions", "buf", "ptr")
 
-    def __init__(self, refs: tuple, buf: torch.Tensor) -> None:
+    def __init__(self, refs: tuple, versions: tuple, buf: torch.Tensor) -> None:
         self.refs = refs  # strong: the storage cannot be recycled while the entry lives
-        self.versions = tuple(t._version for t in refs)
+        self.versions = versions
         self.buf = buf
+        self.ptr = buf.data_ptr()
 
 
 class _WeightsEntry:
-    __slots__ = ("refs", "versions", "buf", "marks_bytes", "epoch", "stage", "nbytes")
+    __slots__ = ("refs", "versions", "buf", "ptr", "marks_bytes", "epoch", "stage", "nbytes")
 
     def __init__(self, refs: tuple, buf: torch.Tensor, marks_bytes: int) -> None:
         self.refs = refs  # weak references
         self.versions = None
         self.buf = buf
+        self.ptr = buf.data_ptr()
         self.marks_bytes = marks_bytes
         self.epoch = 0
         self.stage = 0  # 0: nothing packed, 1: the adapters of one call packed, 2: all packed
@@ -95,6 +98,7 @@ class ReferenceOpCache:
         self.max_bytes: int | None = None  # None: a quarter of the device's memory
         self.bytes: dict = {}
         self._dead: list = []
+        self._device_budget: dict = {}
         self.stats = dict(plan_builds=0, plan_hits=0, pack_used=0, pack_all=0, weights_hits=0, uncached=0)
 
     def clear(self) -> None:
@@ -106,7 +110,11 @@ class ReferenceOpCache:
     def _budget(self, device: torch.device) -> int:
         if self.max_bytes is not None:
             return self.max_bytes
-        return torch.cuda.get_device_properties(device).total_memory // _DEFAULT_BUDGET_FRACTION
+        got = self._device_budget.get(device)
+        if got is None:
+            got = torch.cuda.get_device_properties(device).total_memory // _DEFAULT_BUDGET_FRACTION
+            self._device_budget[device] = got
+        return got
 
     def _drop(self, key) -> None:
         e = self.weights.pop(key, None)
@@ -119,40 +127,44 @@ class ReferenceOpCache:
 
     def plan(self, device: torch.device, stream: int, B: int, M: int, num_adapters: int, seq_lens: torch.Tensor,
              weight_indices: torch.Tensor, nbytes: int) -> tuple:
-        """(plan buffer, whether the call must build it)."""
-        if not (_versioned(seq_lens) and _versioned(weight_indices)):
+        """(plan buffer, its address, whether the call must build it)."""
+        a, b = _ident_version(seq_lens), _ident_version(weight_indices)
+        if a is None or b is None:
             self.stats["plan_builds"] += 1
-            return _aligned_buffer(nbytes, device), True
-        key = (device, stream, B, M, num_adapters, nbytes, _ident(seq_lens), _ident(weight_indices))
+            buf = _aligned_buffer(nbytes, device)
+            return buf, buf.data_ptr(), True
+        key = (device, stream, B, M, num_adapters, nbytes, a[0], b[0])
+        now = (a[1], b[1])
         e = self.plans.get(key)
         if e is not None:
             self.plans.move_to_end(key)
-            now = (seq_lens._version, weight_indices._version)
             if now == e.versions:
                 self.stats["plan_hits"] += 1
-                return e.buf, False
+                return e.buf, e.ptr, False
             e.versions = now
             self.stats["plan_builds"] += 1
-            return e.buf, True
-        e = _PlanEntry((seq_lens, weight_indices), _aligned_buffer(nbytes, device))
+            return e.buf, e.ptr, True
+        e = _PlanEntry((seq_lens, weight_indices), now, _aligned_buffer(nbytes, device))
         self.plans[key] = e
         while len(self.plans) > self.max_plans:
             self.plans.popitem(last=False)
         self.stats["plan_builds"] += 1
-        return e.buf, True
+        return e.buf, e.ptr, True
 
     def weights_part(self, device: torch.device, stream: int, which: int, weights: torch.Tensor,
                      lora_ranks: torch.Tensor, scalings: torch.Tensor | None, stack_num: int, dims: tuple,
                      nbytes: int, marks_bytes: int) -> tuple:
-        """(weights buffer, build flags, epoch) for this call."""
-        self._reap()
+        """(weights buffer, its address, build flags, epoch) for this call."""
+        if self._dead:
+            self._reap()
         srcs = (weights, lora_ranks) if scalings is None else (weights, lora_ranks, scalings)
-        budget = self._budget(device)
-        if not all(_versioned(t) for t in srcs) or nbytes > budget:
+        ivs = [_ident_version(t) for t in srcs]
+        if None in ivs or nbytes > self._budget(device):
             self.stats["uncached"] += 1
             self.stats["pack_used"] += 1
-            return _aligned_buffer(nbytes, device), _native.PL_REF_PACK_USED, 0
-        key = (device, stream, which, stack_num, dims, nbytes) + tuple(_ident(t) for t in srcs)
+            buf = _aligned_buffer(nbytes, device)
+            return buf, buf.data_ptr(), _native.PL_REF_PACK_USED, 0
+        key = (device, stream, which, stack_num, dims, nbytes) + tuple(iv[0] for iv in ivs)
         e = self.weights.get(key)
         if e is not None and not e.alive():
             self._drop(key)
@@ -163,6 +175,7 @@ class ReferenceOpCache:
             e = _WeightsEntry(refs, _aligned_buffer(nbytes, device), marks_bytes)
             self.weights[key] = e
             self.bytes[device] = self.bytes.get(device, 0) + e.nbytes
+            budget = self._budget(device)
             for old in list(self.weights):
                 if self.bytes[device] <= budget:
                     break
@@ -170,7 +183,7 @@ class ReferenceOpCache:
                     self._drop(old)
         else:
             self.weights.move_to_end(key)
-        now = tuple(t._version for t in srcs)
+        now = tuple(iv[1] for iv in ivs)
         if e.versions != now or e.epoch >= 0x7FFFFFF0:
             e.versions = now
             e.stage = 0
@@ -178,15 +191,15 @@ class ReferenceOpCache:
             e.buf[: e.marks_bytes].zero_()
         if e.stage == 2:
             self.stats["weights_hits"] += 1
-            return e.buf, 0, 0
+            return e.buf, e.ptr, 0, 0
         e.epoch += 1
         if e.stage == 0:
             e.stage = 1
             self.stats["pack_used"] += 1
-            return e.buf, _native.PL_REF_PACK_USED | _native.PL_REF_KEEP_PACKED, e.epoch
+            return e.buf, e.ptr, _native.PL_REF_PACK_USED | _native.PL_REF_KEEP_PACKED, e.epoch
         e.stage = 2
         self.stats["pack_all"] += 1
-        return e.buf, _native.PL_REF_PACK_ALL | _native.PL_REF_KEEP_PACKED, e.epoch
+        return e.buf, e.ptr, _native.PL_REF_PACK_ALL | _native.PL_REF_KEEP_PACKED, e.epoch
 
 
 CACHE = ReferenceOpCache()

@@ -855,8 +855,8 @@ def _check_row_meta(B: int, num_adapters: int, seq_lens, weight_indices, lora_ra
 _REF_SIZES: dict = {}
 
 
-def _ref_parts(lib, x: torch.Tensor, which: int, B: int, M: int, K: int, n: int, weights: torch.Tensor,
-               seq_lens: torch.Tensor, weight_indices: torch.Tensor, lora_ranks: torch.Tensor,
+def _ref_parts(lib, dt: int, stream: int, x: torch.Tensor, which: int, B: int, M: int, K: int, n: int,
+               weights: torch.Tensor, seq_lens: torch.Tensor, weight_indices: torch.Tensor, lora_ranks: torch.Tensor,
                scalings: torch.Tensor | None, stack_num: int):
     """The parts of the operator API's MFMA path for this call, as the
     pl_sgmv_lora_*_ref_parts arguments (plan, plan bytes, weights, weights
@@ -870,7 +870,6 @@ def _ref_parts(lib, x: torch.Tensor, which: int, B: int, M: int, K: int, n: int,
     taken for one call come from torch's caching allocator, which hands a
     block to later work on the same stream only after this call's kernels.
     """
-    dt = _native.dtype_code(x.dtype)
     num_adapters = int(weights.shape[0])
     skey = (dt, which, B, M, K, n, num_adapters)
     sizes = _REF_SIZES.get(skey)
@@ -885,19 +884,19 @@ def _ref_parts(lib, x: torch.Tensor, which: int, B: int, M: int, K: int, n: int,
     if torch.cuda.is_current_stream_capturing():
         plan = refop_cache._aligned_buffer(plan_bytes, device)
         wpart = refop_cache._aligned_buffer(weights_bytes, device)
+        plan_ptr, w_ptr = plan.data_ptr(), wpart.data_ptr()
         flags, epoch = _native.PL_REF_BUILD_PLAN | _native.PL_REF_PACK_USED, 0
     else:
-        stream = _stream(device)
-        plan, build = refop_cache.CACHE.plan(device, stream, B, M, num_adapters, seq_lens, weight_indices,
-                                             plan_bytes)
-        wpart, flags, epoch = refop_cache.CACHE.weights_part(
-            device, stream, which, weights, lora_ranks, scalings, int(stack_num), (K, n), weights_bytes,
+        plan, plan_ptr, build = refop_cache.CACHE.plan(device, stream, B, M, num_adapters, seq_lens, weight_indices,
+                                                       plan_bytes)
+        wpart, w_ptr, flags, epoch = refop_cache.CACHE.weights_part(
+            device, stream, which, weights, lora_ranks, scalings, stack_num, (K, n), weights_bytes,
             refop_cache.marks_bytes(num_adapters))
         if build:
             flags |= _native.PL_REF_BUILD_PLAN
     keep = (plan, wpart, scratch)
-    return (plan.data_ptr(), plan_bytes, wpart.data_ptr(), weights_bytes,
-            0 if scratch is None else scratch.data_ptr(), scratch_bytes, flags, epoch), keep
+    return (plan_ptr, plan_bytes, w_ptr, weights_bytes, 0 if scratch is None else scratch.data_ptr(), scratch_bytes,
+            flags, epoch), keep
 
 
 def sgmv_lora_a_fwd(
@@ -930,15 +929,15 @@ def sgmv_lora_a_fwd(
         raise ValueError(f"weights are on {weights.device}, x on {x.device}")
     _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, device=x.device)
     lib = _native.load()
-    head = (_native.dtype_code(x.dtype), x.data_ptr(), B, M, K, weights.data_ptr(), weights.stride(0),
-            weights.stride(1), weights.stride(2), int(weights.shape[0]), N_max, seq_lens.data_ptr(),
-            weight_indices.data_ptr(), lora_ranks.data_ptr(), int(stack_num), output.data_ptr())
-    parts = _ref_parts(lib, x, 0, B, M, K, N_max, weights, seq_lens_in, weight_indices_in, lora_ranks_in, None,
-                       stack_num)
+    dt, stream, stack_num = _native.dtype_code(x.dtype), _stream(x.device), int(stack_num)
+    head = (dt, x.data_ptr(), B, M, K, weights.data_ptr(), *weights.stride(), int(weights.shape[0]), N_max,
+            seq_lens.data_ptr(), weight_indices.data_ptr(), lora_ranks.data_ptr(), stack_num, output.data_ptr())
+    parts = _ref_parts(lib, dt, stream, x, 0, B, M, K, N_max, weights, seq_lens_in, weight_indices_in, lora_ranks_in,
+                       None, stack_num)
     if parts is None:
-        _native.check(lib.pl_sgmv_lora_a_ref(*head, 0, 0, _stream(x.device)), "pl_sgmv_lora_a_ref")
+        _native.check(lib.pl_sgmv_lora_a_ref(*head, 0, 0, stream), "pl_sgmv_lora_a_ref")
     else:
-        _native.check(lib.pl_sgmv_lora_a_ref_parts(*head, *parts[0], _stream(x.device)), "pl_sgmv_lora_a_ref_parts")
+        _native.check(lib.pl_sgmv_lora_a_ref_parts(*head, *parts[0], stream), "pl_sgmv_lora_a_ref_parts")
     return output
 
 
@@ -975,15 +974,16 @@ def sgmv_lora_b_fwd(
         raise ValueError("x, weights and base_output must be on one device")
     _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, scalings, device=x.device)
     lib = _native.load()
-    head = (_native.dtype_code(x.dtype), x.data_ptr(), B, M, K_max, weights.data_ptr(), weights.stride(0),
-            weights.stride(1), weights.stride(2), int(weights.shape[0]), N, seq_lens.data_ptr(),
-            weight_indices.data_ptr(), lora_ranks.data_ptr(), scalings.data_ptr(), work.data_ptr())
-    parts = _ref_parts(lib, x, 1, B, M, K_max, N, weights, seq_lens_in, weight_indices_in, lora_ranks_in,
+    dt, stream = _native.dtype_code(x.dtype), _stream(x.device)
+    head = (dt, x.data_ptr(), B, M, K_max, weights.data_ptr(), *weights.stride(), int(weights.shape[0]), N,
+            seq_lens.data_ptr(), weight_indices.data_ptr(), lora_ranks.data_ptr(), scalings.data_ptr(),
+            work.data_ptr())
+    parts = _ref_parts(lib, dt, stream, x, 1, B, M, K_max, N, weights, seq_lens_in, weight_indices_in, lora_ranks_in,
                        scalings_in, 1)
     if parts is None:
-        _native.check(lib.pl_sgmv_lora_b_ref(*head, 0, 0, _stream(x.device)), "pl_sgmv_lora_b_ref")
+        _native.check(lib.pl_sgmv_lora_b_ref(*head, 0, 0, stream), "pl_sgmv_lora_b_ref")
     else:
-        _native.check(lib.pl_sgmv_lora_b_ref_parts(*head, *parts[0], _stream(x.device)), "pl_sgmv_lora_b_ref_parts")
+        _native.check(lib.pl_sgmv_lora_b_ref_parts(*head, *parts[0], stream), "pl_sgmv_lora_b_ref_parts")
     if work is not output:
         output.copy_(work)
     return output

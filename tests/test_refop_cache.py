@@ -21,7 +21,16 @@ def _cache(max_bytes=1 << 20, max_plans=16):
 
 
 def _part(c, w, r, s=None, stream=0, nbytes=4096, which=0):
-    return c.weights_part(CPU, stream, which, w, r, s, 1, (64, 16), nbytes, 256)
+    """(buffer, flags, epoch) of a weights-part lookup; the buffer's address comes back with it."""
+    buf, ptr, flags, epoch = c.weights_part(CPU, stream, which, w, r, s, 1, (64, 16), nbytes, 256)
+    assert ptr == buf.data_ptr()
+    return buf, flags, epoch
+
+
+def _plan(c, *args):
+    buf, ptr, build = c.plan(CPU, 0, *args)
+    assert ptr == buf.data_ptr()
+    return buf, build
 
 
 def test_weights_part_packs_used_then_all_then_nothing_and_rebuilds_on_a_write():
@@ -92,19 +101,19 @@ def test_budget_evicts_least_recently_used_and_dead_tensors_drop_their_entry():
 def test_plan_entries_are_reused_rebuilt_in_place_and_bounded():
     c = _cache(max_plans=2)
     seq, idx = torch.ones(8, dtype=torch.int32), torch.zeros(8, dtype=torch.int32)
-    p, build = c.plan(CPU, 0, 8, 1, 4, seq, idx, 1024)
+    p, build = _plan(c, 8, 1, 4, seq, idx, 1024)
     assert build and p.numel() == 1024
-    p2, build = c.plan(CPU, 0, 8, 1, 4, seq, idx, 1024)
+    p2, build = _plan(c, 8, 1, 4, seq, idx, 1024)
     assert not build and p2.data_ptr() == p.data_ptr()
     idx[3] = 2
-    p3, build = c.plan(CPU, 0, 8, 1, 4, seq, idx, 1024)
+    p3, build = _plan(c, 8, 1, 4, seq, idx, 1024)
     assert build and p3.data_ptr() == p.data_ptr()
-    assert c.plan(CPU, 0, 8, 2, 4, seq, idx, 1024)[1], "another row length is another plan"
-    assert c.plan(CPU, 0, 8, 1, 4, seq.clone(), idx, 1024)[1]  # a third entry: the oldest goes
-    assert len(c.plans) == 2 and c.plan(CPU, 0, 8, 1, 4, seq, idx, 1024)[1]
+    assert _plan(c, 8, 2, 4, seq, idx, 1024)[1], "another row length is another plan"
+    assert _plan(c, 8, 1, 4, seq.clone(), idx, 1024)[1]  # a third entry: the oldest goes
+    assert len(c.plans) == 2 and _plan(c, 8, 1, 4, seq, idx, 1024)[1]
     with torch.inference_mode():
         si = torch.ones(8, dtype=torch.int32)
-    assert c.plan(CPU, 0, 8, 1, 4, si, idx, 1024)[1] and c.plan(CPU, 0, 8, 1, 4, si, idx, 1024)[1]
+    assert _plan(c, 8, 1, 4, si, idx, 1024)[1] and _plan(c, 8, 1, 4, si, idx, 1024)[1]
 
 
 def test_marks_bytes():
