@@ -128,6 +128,36 @@ _lib = None
 _checked_runtime = False
 
 
+_raw: dict = {}
+
+
+def raw(name: str):
+    """Entry point `name` without ctypes argument conversion.
+
+    Every argument must already be a ctypes object of the declared type
+    (c_int32, c_int64, c_void_p); arguments that do not change between calls
+    can then be built once and passed as they are, which saves the per-call
+    conversion of the declared-argtypes binding.  Returns int32.
+    """
+    f = _raw.get(name)
+    if f is None:
+        f = load()[name]  # a separate function object with no argtypes
+        f.restype = c_int32
+        _raw[name] = f
+    return f
+
+
+_c32: dict = {}
+
+
+def c32(v: int) -> ctypes.c_int32:
+    """A shared c_int32 for a small constant argument (dtype codes, flags, counts)."""
+    got = _c32.get(v)
+    if got is None:
+        got = _c32[v] = c_int32(v)
+    return got
+
+
 class NativeLibraryMissing(RuntimeError):
     """The HIP library has not been built (run ``python -m polylora_amd.build``)."""
 

@@ -79,7 +79,7 @@ class SgmvPlan:
     """
 
     __slots__ = ("rows", "row_len", "num_slots", "group_tokens", "tokens_cap", "group_cap", "tok", "groups", "meta",
-                 "row_slot", "seq_lens", "distinct_slots", "launch_args", "active", "_build")
+                 "row_slot", "seq_lens", "distinct_slots", "launch_args", "launch_args_c", "active", "_build")
 
     def __init__(self, row_slot: torch.Tensor, seq_lens: torch.Tensor, row_len: int, num_slots: int,
                  distinct_slots: int | None = None, group_tokens: int | None = None,
@@ -113,6 +113,9 @@ class SgmvPlan:
         # the plan's arguments of the fused entry points, in their order
         self.launch_args = (self.tok.data_ptr(), self.groups.data_ptr(), self.meta.data_ptr(), max(1, self.group_cap),
                             self.group_tokens)
+        self.launch_args_c = (ctypes.c_void_p(self.launch_args[0]), ctypes.c_void_p(self.launch_args[1]),
+                              ctypes.c_void_p(self.launch_args[2]), ctypes.c_int64(self.launch_args[3]),
+                              ctypes.c_int32(self.launch_args[4]))
         self.row_slot, self.seq_lens, self.active = row_slot, seq_lens, active
         out = (self.tok.data_ptr(), self.groups.data_ptr(), self.meta.data_ptr(), max(1, self.group_cap))
         if active is None:
@@ -563,17 +566,33 @@ def _cache_args(cache, module_name: str) -> tuple:
     return hit
 
 
+def _cache_args_c(cache, module_name: str) -> tuple:
+    """_cache_args as ctypes objects, built once per cache and module."""
+    args = cache.__dict__.setdefault("_launch_args_c", {})
+    hit = args.get(module_name)
+    if hit is None:
+        arena, table, n_modules, column, ldt = _cache_args(cache, module_name)
+        hit = args[module_name] = (ctypes.c_void_p(arena), ctypes.c_void_p(table), ctypes.c_int32(n_modules),
+                                   ctypes.c_int32(column), ctypes.c_int32(ldt))
+    return hit
+
+
 def _fused_launch(x, y, cache, module_name: str, plan: SgmvPlan, epilogue: int, slices, stream: int) -> None:
-    """pl_lora_fused on operands the caller has checked."""
+    """pl_lora_fused on operands the caller has checked.
+
+    The wrapped Linear's hot call: the cache's and the plan's arguments are
+    ctypes objects built once (per cache and module, per plan), and the
+    entry point is called without per-argument conversion.
+    """
     N = y.shape[1]
-    _native.check(
-        _native.load().pl_lora_fused(
-            _native.dtype_code(x.dtype), x.data_ptr(), x.stride(0), x.shape[1], y.data_ptr(), y.stride(0), N,
-            *_cache_args(cache, module_name), *plan.launch_args,
-            choose_slices(plan, N) if slices is None else slices, epilogue, stream,
-        ),
-        "pl_lora_fused",
-    )
+    c32 = _native.c32
+    rc = _native.raw("pl_lora_fused")(
+        c32(_native.dtype_code(x.dtype)), ctypes.c_void_p(x.data_ptr()), ctypes.c_int64(x.stride(0)),
+        c32(x.shape[1]), ctypes.c_void_p(y.data_ptr()), ctypes.c_int64(y.stride(0)), c32(N),
+        *_cache_args_c(cache, module_name), *plan.launch_args_c,
+        c32(choose_slices(plan, N) if slices is None else slices), c32(epilogue), ctypes.c_void_p(stream))
+    if rc:
+        _native.check(rc, "pl_lora_fused")
 
 
 def lora_fused_stacked(
