@@ -8,7 +8,8 @@ whole slot.
 Here the weights of slot s >= 1 fill one region of ``slot_bytes`` in a
 single device arena, found through the slot's table row (the kernels read
 every A and B offset from it).  The arena has more regions than slots (up to
-one spare per slot, within ``SPARE_REGION_BYTES``).  The store holds each
+one spare per slot, within ``PolyLoraConfig.spare_region_bytes``, by default
+4 GiB and an eighth of the free device memory).  The store holds each
 adapter as its slot image
 (``slot_image.AdapterImage``, pinned, model dtype): for each module it has
 weights for, A as ``[rank][in]`` (= PEFT lora_A) then B as ``[out][rank8]``
@@ -161,11 +162,24 @@ class GpuAdapterCache:
         self._allocate()
 
     # ------------------------------------------------------------------ storage
-    # Device memory for spare arena regions (at most one per slot): a load
-    # copies into a spare region while a running forward still reads the
-    # slot's current one.  0 turns them off (loads then rewrite a slot in
-    # place, after its readers).  Read when the arena is allocated.
+    # Default cap on the device memory for spare arena regions (at most one
+    # per slot): a load copies into a spare region while a running forward
+    # still reads the slot's current one.  PolyLoraConfig.spare_region_bytes
+    # overrides it; without that the spares also stay within an eighth of
+    # the device memory free at allocation.  0 turns them off (loads then
+    # rewrite a slot in place, after its readers).  Read when the arena is
+    # allocated.
     SPARE_REGION_BYTES = 4 << 30
+
+    def _spare_budget(self) -> int:
+        given = getattr(self.config, "spare_region_bytes", None)  # a reference config has no such field
+        if given is not None:
+            return int(given)
+        cap = int(self.SPARE_REGION_BYTES)
+        if self.device.type == "cuda" and cap > 0:
+            free, _ = torch.cuda.mem_get_info(self.device)
+            cap = min(cap, free // 8)
+        return cap
 
     def _allocate(self) -> None:
         self.layout = SlotLayout(list(self.module_specs.values()), self.dtype, self.config.max_rank)
@@ -173,7 +187,7 @@ class GpuAdapterCache:
         self.store.bind_layout(self.layout)
         n_mod = len(self.module_specs)
         slots = self.num_slots - 1
-        self.spare_regions = int(min(slots, self.SPARE_REGION_BYTES // max(1, self.layout.slot_bytes)))
+        self.spare_regions = int(min(slots, self._spare_budget() // max(1, self.layout.slot_bytes)))
         self.num_regions = slots + self.spare_regions
         arena_bytes = max(1, self.num_regions * self.layout.slot_bytes)
         self.arena = torch.empty(arena_bytes, dtype=torch.uint8, device=self.device)

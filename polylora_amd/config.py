@@ -23,6 +23,13 @@ class PolyLoraConfig:
     base_adapter_id: str = "__base__"
     enforce_right_padding: bool = True
     use_triton_kernels: bool = True
+    # Device memory for spare slot regions (not in the reference, which
+    # rewrites a slot in place): a load copies an adapter into a spare region
+    # while a forward still reads the slot's current one.  None: at most
+    # GpuAdapterCache.SPARE_REGION_BYTES (4 GiB) and at most an eighth of
+    # the device memory free when the cache allocates; 0: no spares (loads
+    # then rewrite a slot in place, after its readers).
+    spare_region_bytes: int | None = None
 
     def __post_init__(self) -> None:
         # Same checks and messages as config.py:17-29.
@@ -38,6 +45,8 @@ class PolyLoraConfig:
             raise ValueError("max_rank must be at least 1")
         if self.target_modules is not None and not self.target_modules:
             raise ValueError("target_modules must not be empty when provided")
+        if self.spare_region_bytes is not None and self.spare_region_bytes < 0:
+            raise ValueError("spare_region_bytes must be at least 0")
 
     @property
     def use_hip_kernels(self) -> bool:

@@ -137,3 +137,29 @@ def test_region_bookkeeping_over_random_batches():
         for aid in batch:
             slot = cache.adapter_to_slot[aid]
             assert int(cache.ranks["m"][slot]) == int(cache.store.adapters[aid].layers["m"].rank)
+
+
+def test_spare_region_budget_comes_from_the_config():
+    """PolyLoraConfig.spare_region_bytes sets the spare regions' budget (0: none; a value: as many whole
+    regions as it holds, at most one per slot); negative budgets are refused."""
+    import pytest
+
+    from polylora_amd.cache import ModuleSpec
+    from polylora_amd.config import PolyLoraConfig
+    from tests._util import make_store
+
+    g = torch.Generator().manual_seed(4)
+    adapters = {f"a{i}": {"m": peft_layer(g, 32, 24, 2, 4.0)} for i in range(4)}
+    specs = [ModuleSpec("m", 32, 24)]
+
+    def spares(budget):
+        cfg = PolyLoraConfig(max_gpu_adapters=3, max_rank=4, spare_region_bytes=budget)
+        cache = GpuAdapterCache(make_store(adapters), specs, cfg, torch.device("cpu"), torch.float32)
+        return cache.spare_regions, cache.layout.slot_bytes
+
+    assert spares(0)[0] == 0
+    n, slot_bytes = spares(None)
+    assert n == 3  # the default cap (4 GiB) holds a spare for every slot
+    assert spares(slot_bytes)[0] == 1 and spares(2 * slot_bytes + 1)[0] == 2
+    with pytest.raises(ValueError, match="spare_region_bytes"):
+        PolyLoraConfig(max_gpu_adapters=1, max_rank=4, spare_region_bytes=-1)
