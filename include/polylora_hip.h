@@ -149,7 +149,16 @@ int64_t pl_plan_group_capacity(int32_t rows, int32_t row_len, int32_t num_slots,
  * p % 8, so the slot-major list of the n groups is cut into 8 contiguous
  * chunks, chunk x = groups [x*n/8, (x+1)*n/8), and the i-th group of chunk
  * x is stored at position 8*i + x: an adapter's groups share one or two XCDs'
- * L2.  Every other record below group_cap is empty (slot 0, length 0). */
+ * L2.  Every other record below group_cap is empty (slot 0, length 0).
+ *
+ * Plan inputs of the kernels.  Every entry point below that takes tok,
+ * groups and meta (pl_sgmv_shrink(_stacked), pl_sgmv_expand(_stacked),
+ * pl_lora_apply, pl_lora_fused(_stacked), pl_lora_decode_stacked) reads
+ * them as pl_plan_build or pl_plan_build_active wrote them: it walks the
+ * group positions below meta[3] (records past the groups in use are empty)
+ * and gives position p to XCD p % 8.  A plan built another way must follow
+ * that format, meta[3] included: with meta[3] = 0 no group is read and the
+ * call adds no LoRA delta. */
 int pl_plan_build(const int32_t* row_slot, const int32_t* seq_lens, int32_t rows,
                   int32_t row_len, int32_t num_slots, int32_t group_tokens, int32_t* tok,
                   pl_group* groups, int32_t* meta, int64_t group_cap, void* stream);
@@ -180,6 +189,8 @@ int64_t pl_shrink_workspace_bytes(int32_t dtype, int32_t K, int32_t k_splits,
  * (no atomics); entries outside (p, j < rank) are not written and nothing
  * needs clearing between calls.
  *   x [*, ldx] of dtype; K = in_features
+ *   tok, groups, meta, group_cap: a plan of pl_plan_build or
+ *     pl_plan_build_active (group positions below meta[3] are read)
  *   group_tokens: the group size the plan was built with (16 or 64)
  *   ws / ws_bytes: at least pl_shrink_workspace_bytes(...) bytes
  *   tmp_rows >= the plan's token count; ldt a multiple of 8 and >= every
@@ -211,7 +222,9 @@ int pl_sgmv_shrink_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K,
  * planes[c][p][j]) * B_slot[n][j] rounded in the order of `epilogue`; the
  * `planes` partial sums the shrink left in `ws` are added in split order, so
  * results are bitwise reproducible.  y [*, ldy] of dtype; requires
- * N % 8 == 0 (bf16/f16) or N % 4 == 0 (f32) and 16-byte aligned y rows. */
+ * N % 8 == 0 (bf16/f16) or N % 4 == 0 (f32) and 16-byte aligned y rows.
+ * The plan (tok, groups, meta, group_cap) is the one the shrink walked, in
+ * the format of pl_plan_build. */
 int pl_sgmv_expand(int32_t dtype, const void* ws, int32_t ldt, int64_t tmp_rows, int32_t planes,
                    const void* arena, const pl_slot_entry* table, int32_t num_modules,
                    int32_t module, const int32_t* tok, const pl_group* groups,
@@ -262,7 +275,8 @@ int pl_lora_decode_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K,
  * counters. */
 int64_t pl_decode_counter_ints(int64_t group_cap, int32_t n_modules);
 
-/* Shrink followed by expand on one stream (one call per wrapped Linear). */
+/* Shrink followed by expand on one stream (one call per wrapped Linear),
+ * over a plan in the format of pl_plan_build. */
 int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y, int64_t ldy,
                   int32_t N, const void* arena, const pl_slot_entry* table,
                   int32_t num_modules, int32_t module, const int32_t* tok,
@@ -277,7 +291,8 @@ int pl_lora_apply(int32_t dtype, const void* x, int64_t ldx, int32_t K, void* y,
  * ranks up to 64 (ldt, the table's rank capacity, must be <= 64), 1..8
  * column slices per tile (each slice recomputes the tile's shrink; more
  * slices, more workgroups), the alignment rules of the tiled path, and a
- * plan of 16- or 64-token groups.  Pays off when groups are full (many
+ * plan of 16- or 64-token groups in the format of pl_plan_build (positions
+ * below meta[3] are read).  Pays off when groups are full (many
  * tokens per adapter); for a few tokens per adapter (decode) use
  * pl_sgmv_shrink + pl_sgmv_expand, which split K and N over many
  * workgroups. */

@@ -41,10 +41,16 @@ def _existing(lib, dt, x, y, cache, row_slot, seq, rows, row_len, group_tokens, 
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+# (rows, row_len) of two calls in a row, the second smaller: decode-like rows, and prefill-shaped rows longer
+# than 16 tokens (the plan places their tokens with one wave per row)
+CALLS = [((40, 16), (9, 5)), ((4, 300), (3, 120))]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("group_tokens,k_splits", [(16, 4), (64, 2)])
-def test_noalloc_equals_plan_build_plus_lora_apply(gpu, dtype, group_tokens, k_splits):
-    print(f"case: noalloc dtype={dtype} group_tokens={group_tokens} k_splits={k_splits}", flush=True)
+@pytest.mark.parametrize("calls", CALLS)
+def test_noalloc_equals_plan_build_plus_lora_apply(gpu, dtype, group_tokens, k_splits, calls):
+    print(f"case: noalloc dtype={dtype} group_tokens={group_tokens} k_splits={k_splits} calls={calls}", flush=True)
     lib = _native.load()
     dt = _native.dtype_code(dtype)
     g = torch.Generator().manual_seed(31)
@@ -52,7 +58,7 @@ def test_noalloc_equals_plan_build_plus_lora_apply(gpu, dtype, group_tokens, k_s
     cache = make_cache(adapters, {"m": (K, N)}, 5, 16, gpu, dtype)
     ids_pool = ["__base__", *adapters]
     stream = _native.current_stream_handle(gpu)
-    for rows, row_len in ((40, 16), (9, 5)):  # the second call is smaller
+    for rows, row_len in calls:
         ids = [ids_pool[int(i)] for i in torch.randint(0, len(ids_pool), (rows,), generator=g)]
         row_slot = cache.ensure_resident(ids)
         seq_cpu = torch.randint(0, row_len + 3, (rows,), generator=g, dtype=torch.int32)
@@ -89,3 +95,55 @@ def test_noalloc_rejects_a_batch_beyond_its_scratch(gpu):
                                    cache.num_slots, 64, cache.rank8_cap, 8, 0, _native.current_stream_handle(gpu))
     assert st == 4  # PL_ERR_LIMIT
     assert b"static scratch" in lib.pl_last_error()
+
+
+def _noalloc_need(lib, dt, rows, row_len, num_slots, group_tokens, ldt, k_splits):
+    """Scratch bytes a pl_lora_apply_noalloc call needs (the formula its declaration states)."""
+    a256 = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    T = max(1, rows * row_len)
+    cap = int(lib.pl_plan_group_capacity(rows, row_len, num_slots, group_tokens))
+    return 256 + a256(16 * cap) + a256(4 * T) + int(lib.pl_shrink_workspace_bytes(dt, K, k_splits, group_tokens, T, ldt))
+
+
+def test_noalloc_just_under_its_scratch_limit(gpu):
+    """The largest batch of 64-token rows whose plan and planes fit the static scratch: bit for bit equal
+    to pl_plan_build + pl_lora_apply, then a smaller call, then one more row is refused."""
+    print("case: noalloc near the limit", flush=True)
+    lib = _native.load()
+    dt, gt, ks, row_len = _native.PL_BF16, 64, 2, 64
+    g = torch.Generator().manual_seed(33)
+    adapters = {f"n{i}": {"m": peft_layer(g, K, N, r, 2.0 * r)} for i, r in enumerate([4, 8, 16])}
+    cache = make_cache(adapters, {"m": (K, N)}, 3, 16, gpu, torch.bfloat16)
+    limit = _native.PL_NOALLOC_SCRATCH_BYTES
+    need = lambda r: _noalloc_need(lib, dt, r, row_len, cache.num_slots, gt, cache.rank8_cap, ks)  # noqa: E731
+    lo, hi = 1, 1 << 16
+    assert need(lo) <= limit < need(hi)
+    while hi - lo > 1:
+        mid = (lo + hi) // 2
+        lo, hi = (mid, hi) if need(mid) <= limit else (lo, mid)
+    rows = lo
+    assert need(rows) <= limit < need(rows + 1) and need(rows) > limit - (1 << 20)
+    stream = _native.current_stream_handle(gpu)
+    gd = torch.Generator(device=gpu).manual_seed(33)
+    ids_pool = ["__base__", *adapters]
+    for r in (rows, rows // 3):
+        ids = [ids_pool[int(i)] for i in torch.randint(0, len(ids_pool), (r,), generator=g)]
+        row_slot = cache.ensure_resident(ids)
+        seq = torch.randint(0, row_len + 3, (r,), generator=g, dtype=torch.int32).to(gpu)
+        x = torch.randn(r * row_len, K, generator=gd, device=gpu).bfloat16()
+        y_new = torch.randn(r * row_len, N, generator=gd, device=gpu).bfloat16()
+        y_old = y_new.clone()
+        torch.cuda.synchronize()
+        _native.check(lib.pl_lora_apply_noalloc(dt, x.data_ptr(), K, K, y_new.data_ptr(), N, N, cache.arena.data_ptr(),
+                                                cache.table.data_ptr(), 1, 0, row_slot.data_ptr(), seq.data_ptr(), r,
+                                                row_len, cache.num_slots, gt, cache.rank8_cap, ks,
+                                                _native.PL_EPI_FALLBACK, stream), "pl_lora_apply_noalloc")
+        torch.cuda.synchronize()
+        _existing(lib, dt, x, y_old, cache, row_slot, seq, r, row_len, gt, ks, stream)
+        assert torch.equal(y_new, y_old), r
+        del x, y_new, y_old
+    x = torch.empty(8, K, dtype=torch.bfloat16, device=gpu)  # never read: the size check fails first
+    st = lib.pl_lora_apply_noalloc(dt, x.data_ptr(), K, K, x.data_ptr(), N, N, cache.arena.data_ptr(),
+                                   cache.table.data_ptr(), 1, 0, x.data_ptr(), x.data_ptr(), rows + 1, row_len,
+                                   cache.num_slots, gt, cache.rank8_cap, ks, 0, stream)
+    assert st == _native.PL_ERR_LIMIT
