@@ -567,13 +567,19 @@ def _cache_args(cache, module_name: str) -> tuple:
 
 
 def _cache_args_c(cache, module_name: str) -> tuple:
-    """_cache_args as ctypes objects, built once per cache and module."""
-    args = cache.__dict__.setdefault("_launch_args_c", {})
-    hit = args.get(module_name)
+    """_cache_args as ctypes objects, built once per cache and module.
+
+    Kept in the same memo as _cache_args, which the cache drops whenever it
+    allocates a new arena and table (GpuAdapterCache.to), so neither form
+    can outlive the memory it points at.
+    """
+    args = cache.__dict__.setdefault("_launch_args", {})
+    key = ("ctypes", module_name)
+    hit = args.get(key)
     if hit is None:
         arena, table, n_modules, column, ldt = _cache_args(cache, module_name)
-        hit = args[module_name] = (ctypes.c_void_p(arena), ctypes.c_void_p(table), ctypes.c_int32(n_modules),
-                                   ctypes.c_int32(column), ctypes.c_int32(ldt))
+        hit = args[key] = (ctypes.c_void_p(arena), ctypes.c_void_p(table), ctypes.c_int32(n_modules),
+                           ctypes.c_int32(column), ctypes.c_int32(ldt))
     return hit
 
 

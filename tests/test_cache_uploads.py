@@ -163,3 +163,21 @@ def test_spare_region_budget_comes_from_the_config():
     assert spares(slot_bytes)[0] == 1 and spares(2 * slot_bytes + 1)[0] == 2
     with pytest.raises(ValueError, match="spare_region_bytes"):
         PolyLoraConfig(max_gpu_adapters=1, max_rank=4, spare_region_bytes=-1)
+
+
+def test_bound_launch_arguments_follow_a_reallocated_arena():
+    """The fused launch's prebuilt arguments (arena and table addresses) are rebuilt after the cache
+    allocates a new arena and table on a dtype change, never reused from the freed ones."""
+    from polylora_amd import sgmv
+
+    cache = _cache(4, 3)
+    cache.ensure_resident(["a0", "a1"])
+    before = sgmv._cache_args_c(cache, "m")
+    assert before[0].value == cache.arena.data_ptr() and before[1].value == cache.table.data_ptr()
+    assert sgmv._cache_args(cache, "m")[0] == cache.arena.data_ptr()
+    old_arena = cache.arena
+    cache.to(torch.device("cpu"), torch.float16)
+    assert cache.arena is not old_arena
+    after = sgmv._cache_args_c(cache, "m")
+    assert after[0].value == cache.arena.data_ptr() and after[1].value == cache.table.data_ptr()
+    assert sgmv._cache_args(cache, "m")[:2] == (cache.arena.data_ptr(), cache.table.data_ptr())
