@@ -1304,25 +1304,16 @@ def reduce_graph_trace(args) -> int:
     return 0
 
 
-def operator_api_decode_layer(pm, adapter_ids: list, reps: int = 30) -> dict:
-    """One decode layer's seven wrapped Linears through the reference's operator API.
+def operator_decode_layer_tensors(pm, adapter_ids: list) -> tuple:
+    """One decode layer's seven wrapped Linears in the reference cache's own layout (cache.py:37-58).
 
-    As MultiLoraLinear calls it (layers.py:42-58: sgmv_lora_a_fwd then
-    sgmv_lora_b_fwd per Linear) on the reference cache's own layout
-    (cache.py:37-58): per module A [65, K, 64] and B [65, 64, N] bf16 (slot 0
-    the base adapter with rank 0, the decode batch's 64 adapters at their
-    slots and ranks, zero past each rank), ranks [65] int32 and scales [65]
-    fp32; weight_indices is the batch's row -> slot map, seq_lens ones, and
-    each Linear gets x [256, 1, K] and its base output [256, 1, N].  Weight
-    values are random: no timing depends on them.
-
-    Times one layer on its first call (the plan built, each module's used
-    adapters packed), its second (the rest packed), then layers back to back
-    with the plan and packed weights kept, and the same with nothing kept
-    (every call builds the plan and repacks the adapters its rows use).
+    Per module A [65, K, 64] and B [65, 64, N] bf16 (slot 0 the base adapter
+    with rank 0, the decode batch's 64 adapters at their slots and ranks,
+    zero past each rank), ranks [65] int32 and scales [65] fp32, and the
+    Linear's x [256, 1, K] and base output [256, 1, N].  Weight values are
+    random: no timing depends on them.  Returns (modules, seq_lens,
+    weight_indices) with modules a list of (module name, A, B, ranks, scales, x, y).
     """
-    from polylora_amd import refop_cache, sgmv
-
     cache = pm.adapter_cache
     device = cache.device
     B = len(adapter_ids)
@@ -1330,9 +1321,9 @@ def operator_api_decode_layer(pm, adapter_ids: list, reps: int = 30) -> dict:
     gen = torch.Generator(device=device).manual_seed(7)
     widx = cache.ensure_resident(adapter_ids)
     seq = torch.ones(B, dtype=torch.int32, device=device)
-    mods = []
     layer0 = [s for s in pm.module_specs if re.search(r"(^|\.)layers\.0\.", s.name)]
     assert len(layer0) == 7, [s.name for s in pm.module_specs[:8]]
+    mods = []
     for spec in layer0:
         K, N = spec.in_features, spec.out_features
         ranks = torch.zeros(S, dtype=torch.int32)
@@ -1347,10 +1338,26 @@ def operator_api_decode_layer(pm, adapter_ids: list, reps: int = 30) -> dict:
         sc = torch.where(rk > 0, 2.0, 0.0).float()
         x = torch.randn(B, 1, K, generator=gen, device=device).bfloat16()
         y = torch.randn(B, 1, N, generator=gen, device=device).bfloat16()
-        mods.append((A, Bw, rk, sc, x, y))
+        mods.append((spec.name, A, Bw, rk, sc, x, y))
+    return mods, seq, widx
+
+
+def operator_api_decode_layer(pm, adapter_ids: list, reps: int = 30) -> dict:
+    """One decode layer's seven wrapped Linears through the reference's operator API.
+
+    As MultiLoraLinear calls it (layers.py:42-58: sgmv_lora_a_fwd then
+    sgmv_lora_b_fwd per Linear) on operator_decode_layer_tensors.  Times one
+    layer on its first call (the plan built, each module's used adapters
+    packed), its second (the rest packed), then layers back to back with the
+    plan and packed weights kept, and the same with nothing kept (every call
+    builds the plan and repacks the adapters its rows use).
+    """
+    from polylora_amd import refop_cache, sgmv
+
+    mods, seq, widx = operator_decode_layer_tensors(pm, adapter_ids)
 
     def layer():
-        for A, Bw, rk, sc, x, y in mods:
+        for _, A, Bw, rk, sc, x, y in mods:
             tmp = sgmv.sgmv_lora_a_fwd(x, A, seq, widx, rk)
             sgmv.sgmv_lora_b_fwd(tmp, Bw, seq, widx, rk, sc, y)
 
@@ -1780,6 +1787,34 @@ def launch_profile(args) -> int:
             desc = ("reference operator API (sgmv_lora_a_fwd + sgmv_lora_b_fwd) on the isolated op's shapes, "
                     "reference slot layout, 9 rotated input sets, plan and packed weights kept across calls")
         cache, row_slot, seq_lens, tpr, distinct = base_set.cache, base_set.row_slot, base_set.seq_lens, 1, 16
+    elif kind == "operator-decode":
+        from polylora_amd import refop_cache
+
+        wl = decode_workload(device, layers=args.decode_layers, kv_cache=False)
+        pm, ids = wl.model, wl.adapter_ids
+        mods, op_seq, op_widx = operator_decode_layer_tensors(pm, ids)
+        refop_cache.configure()
+        seq = []
+        for name, A, Bw, rk, sc, x, y in mods:
+            def pair(A=A, Bw=Bw, rk=rk, sc=sc, x=x, y=y):
+                tmp = sgmv.sgmv_lora_a_fwd(x, A, op_seq, op_widx, rk)
+                sgmv.sgmv_lora_b_fwd(tmp, Bw, op_seq, op_widx, rk, sc, y)
+
+            leaf = name.rsplit(".", 1)[-1]
+            # one host call pair issues 3 dispatches once the plan and packed weights are kept (the first
+            # two layers' pl_refop_prep dispatches fall in the first warm-up pass): the split shrink, its
+            # finish, and the fused kernel's expand phase; the first entry issues them all
+            seq += [(f"{leaf} shrink: split shrink", "shrink", pair,
+                     launch_bytes(pm, [name], "shrink", ids, [1] * len(ids))),
+                    (f"{leaf} shrink: finish", "operator", lambda: None, 0),
+                    (f"{leaf} expand: fused phase", "expand", lambda: None,
+                     launch_bytes(pm, [name], "expand", ids, [1] * len(ids)))]
+        desc = ("reference operator API (sgmv_lora_a_fwd + sgmv_lora_b_fwd) on one Llama-3-8B-shaped decode "
+                "layer's 7 Linears, 256 rows x 1 token, reference layout [65, K, 64] / [65, 64, N] bf16, 64 "
+                "adapters of ranks {8,16,32,64}, Zipf(1.1) with 10% base rows, plan and packed weights kept "
+                "across calls")
+        cache, row_slot, seq_lens, tpr = pm.adapter_cache, op_widx, op_seq, 1
+        distinct = len({a for a in ids if a != pm.config.base_adapter_id})
     else:
         if kind == "decode":
             wl = decode_workload(device, layers=args.decode_layers, kv_cache=False)
@@ -2030,7 +2065,7 @@ def main(argv=None) -> int:
                    help="most distinct adapters per churn sub-batch (the cache has 32 slots)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                    help="only copy a BYTES-sized device buffer 5 times (calibrates HBM byte counters) and exit")
-    p.add_argument("--launch-profile", choices=["isolated", "decode", "prefill", "operator"],
+    p.add_argument("--launch-profile", choices=["isolated", "decode", "prefill", "operator", "operator-decode"],
                    help="only issue this workload's LoRA launches in fixed passes (for rocprofv3) and write --manifest")
     p.add_argument("--manifest", default="launch_profile/manifest.json")
     p.add_argument("--profile-passes", type=int, default=20)
