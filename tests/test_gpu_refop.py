@@ -413,3 +413,25 @@ def test_part_entry_points_reject_bad_flags(gpu):
     assert b"parts" in lib.pl_last_error()
     assert call(_native.PL_REF_BUILD_PLAN | _native.PL_REF_PACK_ALL | _native.PL_REF_KEEP_PACKED, 1) == 0
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16])
+def test_kept_parts_with_int64_indices_and_stacked_columns(gpu, dtype):
+    """The reference passes int64 index and length tensors and may stack modules along n (stack_num 2): the
+    parts are kept by the caller's own tensors (not the int32 copies made per call), and every call still
+    equals a fresh-workspace call bit for bit."""
+    _announce(test="refop_kept_int64_stack2", dtype=dtype)
+    _fresh_cache()
+    st = refop_cache.CACHE.stats
+    g = torch.Generator().manual_seed(34)
+    Bt, M, K, N, S, R = 48, 1, 512, 256, 6, 16
+    _, (dx, dwa, dwb, dranks, dscal, dseq, dwidx) = _case(g, Bt, M, K, N, S, R, 2, dtype, gpu)
+    widx64, seq64 = dwidx.long(), dseq.long()
+    for step in range(3):
+        want = _call_a(dx, dwa, dseq, dwidx, dranks, 2, mfma=True)
+        got = sgmv.sgmv_lora_a_fwd(dx, dwa, seq64, widx64, dranks, stack_num=2)
+        valid = _valid(dseq.cpu(), dwidx.cpu(), dranks.cpu(), M, 2 * R, stack_num=2).to(gpu)
+        assert torch.equal(got[valid], want[valid]), step
+    torch.cuda.synchronize()
+    assert (st["plan_builds"], st["plan_hits"]) == (1, 2), st
+    assert (st["pack_used"], st["pack_all"], st["weights_hits"]) == (1, 1, 1), st
