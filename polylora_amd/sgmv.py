@@ -45,6 +45,8 @@ def _require_gpu(t: torch.Tensor, what: str) -> None:
 
 
 def _i32(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype is torch.int32 and t.is_contiguous():
+        return t
     return t.to(torch.int32).contiguous()
 
 
@@ -994,7 +996,8 @@ def sgmv_lora_b_fwd(
     work = output if output.is_contiguous() else output.contiguous()
     seq_lens_in, weight_indices_in, lora_ranks_in, scalings_in = seq_lens, weight_indices, lora_ranks, scalings
     seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
-    scalings = scalings.to(torch.float32).contiguous()
+    if not (scalings.dtype is torch.float32 and scalings.is_contiguous()):
+        scalings = scalings.to(torch.float32).contiguous()
     if weights.device != x.device or output.device != x.device:
         raise ValueError("x, weights and base_output must be on one device")
     _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, scalings, device=x.device)
