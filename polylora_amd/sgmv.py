@@ -27,7 +27,8 @@ from . import _native, refop_cache
 
 __all__ = ["SgmvPlan", "lora_apply", "lora_apply_rows", "lora_shrink", "lora_expand", "sgmv_lora_a_fwd",
            "sgmv_lora_b_fwd", "choose_k_splits", "choose_group_tokens", "side_stream", "lora_shrink_stacked",
-           "lora_fused", "fused_ok", "choose_slices", "lora_expand_stacked"]
+           "lora_fused", "fused_ok", "choose_slices", "lora_expand_stacked", "lora_decode_stacked", "decode_ok",
+           "decode_waits_timed_out"]
 
 
 def _stream(device: torch.device) -> int:
@@ -742,6 +743,24 @@ def handoff_counters(device: torch.device, stream: int) -> _HandoffCounters:
     hit = _COUNTERS.get(key)
     if hit is None:
         hit = _COUNTERS[key] = _HandoffCounters(device)
+    return hit
+
+
+def decode_waits_timed_out(device: torch.device | None = None, clear: bool = True) -> bool:
+    """Whether a pl_lora_decode_stacked wait on `device` (all devices when None) ran out of polls since the
+    status words were last cleared: the results of that launch are then undefined.  Waits for the work
+    queued so far on each counter set's device; with `clear`, resets the status words (on the current
+    stream) for the next check.  A timed-out wait is not expected on a GPU this process has to itself:
+    the limit is far above what a launch's shrink takes."""
+    hit = False
+    for (index, _), c in _COUNTERS.items():
+        if c.buf is None or (device is not None and c.device != torch.device(device)):
+            continue
+        torch.cuda.synchronize(c.device)
+        if int(c.buf[0]) != 0:
+            hit = True
+            if clear:
+                c.buf[0].zero_()
     return hit
 
 

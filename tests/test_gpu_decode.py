@@ -124,6 +124,7 @@ def test_decode_config_layer_repeated_launches(gpu):
         for m in shapes:
             assert torch.equal(outs[m], want[m]), (m, rep)
         _counters_clear(gpu)
+    assert not sgmv.decode_waits_timed_out(gpu)
     for r in runs:
         for m in r:
             fi, fo = shapes[m]
