@@ -606,3 +606,26 @@ def test_sibling_shrinks_are_stacked(gpu, handoff):
         want = oracle_model.run(om, bank, adapter_ids, input_ids=ids).last_hidden_state
     assert torch.equal(first, second)
     torch.testing.assert_close(second.float(), want.float(), **BF16)
+
+
+@pytest.mark.parametrize("rows,seq", [(64, 1), (16, 64), (4, 600)])
+def test_batches_without_lora_work_equal_the_base_model(gpu, rows, seq):
+    """Every row on the base adapter: the wrapped Linears still run their LoRA launches, on a plan with no
+    groups (64 x 1: the one-launch decode kernel; 16 x 64: the fused kernel; 4 x 600: the fused kernel past
+    the side-stream overlap threshold), and the output equals the base model's bit for bit."""
+    _announce(test="no_lora_work", rows=rows, seq=seq)
+    base, cfg = _tiny_llama(21, torch.bfloat16, gpu)
+    pm = PolyLoraModel(copy.deepcopy(base), PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=2,
+                                                           max_rank=16)).eval()
+    g = torch.Generator().manual_seed(21)
+    w = _peft.make_lora_weights(g, _shapes(pm), 8, std=0.05)
+    pm.adapter_store.add_adapter_from_peft_state_dict("a", _peft.state_dict(w), pm.target_module_names, 16.0)
+    ids = torch.randint(0, 211, (rows, seq), generator=g).to(gpu)
+    mask = torch.ones(rows, seq, dtype=torch.long, device=gpu)
+    with torch.inference_mode():
+        pm(input_ids=ids, attention_mask=mask, adapter_ids=["a"] * rows)  # the adapter resident, siblings learned
+        for _ in range(2):
+            got = pm(input_ids=ids, attention_mask=mask, adapter_ids=["__base__"] * rows).last_hidden_state
+            plain = base(input_ids=ids, attention_mask=mask).last_hidden_state
+            assert torch.equal(got, plain)
+    assert not sgmv.decode_waits_timed_out(gpu)
