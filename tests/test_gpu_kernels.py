@@ -58,6 +58,22 @@ def test_plan_matches_oracle(gpu, rows, row_len, num_slots, seed, group_tokens):
     )
 
 
+@pytest.mark.parametrize("rows,row_len,num_slots,group_tokens", [(4096, 1, 17, 16), (2049, 16, 3, 64), (8192, 4, 65, 16)])
+def test_plan_of_sorted_rows_matches_oracle(gpu, rows, row_len, num_slots, group_tokens):
+    """Rows sorted by slot: whole waves of one slot claim their counts and places with one atomic, and
+    waves that straddle two slots take the per-thread path; 2049 rows leave the last wave one row, 8192 rows
+    take two passes of the workgroup."""
+    _announce(test="plan_sorted", rows=rows, row_len=row_len, num_slots=num_slots, group_tokens=group_tokens)
+    g = torch.Generator().manual_seed(rows)
+    row_slot = torch.sort(torch.randint(0, num_slots, (rows,), generator=g, dtype=torch.int32)).values
+    seq_lens = torch.randint(0, row_len + 1, (rows,), generator=g, dtype=torch.int32)
+    seq_lens[: rows // 2] = row_len  # half the rows full: runs of equal lengths as well as ragged ones
+    plan = sgmv.SgmvPlan(row_slot.to(gpu), seq_lens.to(gpu), row_len, num_slots, group_tokens=group_tokens)
+    torch.cuda.synchronize()
+    check_plan(plan.tok.cpu().numpy(), plan.groups.cpu().numpy(), plan.meta.cpu().numpy(), row_slot.tolist(),
+               seq_lens.tolist(), row_len, num_slots, group_tokens=group_tokens)
+
+
 @pytest.mark.parametrize("rows,row_len,num_slots,group_tokens,seed",
                          [(4096, 1, 17, 16, 20), (300, 3, 40, 16, 21), (32, 1024, 9, 64, 22), (9000, 1, 70, 16, 23)])
 def test_plan_active_mask_matches_oracle(gpu, rows, row_len, num_slots, group_tokens, seed):
