@@ -8,7 +8,10 @@
   store's PEFT path, some held in pageable memory (their loads go through the
   staging ring), batches of 128 rows drawn Zipf(0.9) and split into
   sub-batches of at most 24 distinct adapters, every wrapped layer of every
-  sub-batch against the oracle on the inputs it saw.
+  sub-batch against the oracle on the inputs it saw; and at the catalog's own
+  size, 1024 adapters (images built as the churn bench builds them, half of
+  them pageable), steps of 128 rows, sub-batches of up to 32 distinct: 8 steps
+  on 2 layers, and 3 steps on the configuration's 32 layers.
 * Decode (32 Llama-3-8B layers, 64 slots, ranks {8,16,32,64}, 256 rows over
   a 512-token KV cache, Zipf(1.1) with 10% base rows): one decode step with
   all 224 wrapped layers checked.
@@ -134,6 +137,61 @@ class _StoreWeights(dict):
     def get(self, module, default=None):
         got = self.adapter.peft_tensors(module)
         return default if got is None else (got[0], got[1])
+
+
+@pytest.mark.parametrize("layers,n_steps", [(2, 8), (32, 3)])
+def test_churn_catalog_of_1024_adapters_every_layer_against_the_oracle(gpu, layers, n_steps):
+    """Config 5 at its catalog size: 1024 rank-16 adapters on all 7 targets (images as the churn bench builds
+    them; about half of them pageable, loaded through the staging ring), 32 slots with spare regions, steps of
+    128 rows drawn Zipf(0.9) over the catalog, each cut into sub-batches of at most 32 distinct adapters; every
+    wrapped layer of every sub-batch against the oracle, with the weights read back from the store's images.
+    On 2 layers for more steps, and on the configuration's 32 layers (an 86 GB catalog) for 3 steps."""
+    _announce(test="churn_catalog", catalog=1024, layers=layers, steps=n_steps)
+    import gc
+
+    from transformers import DynamicCache
+
+    from bench import build_llama, random_image_catalog
+    from polylora_amd.slot_image import release_locked_free
+
+    n_cat, rows = 1024, 128
+    model = build_llama(gpu, layers=layers, seed=1006)
+    pm = PolyLoraModel(model, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=32, max_rank=16)).eval()
+    assert pm.adapter_cache.spare_regions == 32
+    shapes = {s.name: (s.in_features, s.out_features) for s in pm.module_specs}
+    image_bytes = sum(16 * (fi + fo) * 2 for fi, fo in shapes.values())
+    store = pm.adapter_store
+    store.pinned_bytes_limit = n_cat // 2 * (image_bytes + (1 << 16))  # room for about half of the images
+    catalog = random_image_catalog(pm, n_cat, rank=16, seed=1006)
+    pinned = sum(1 for a in catalog if store.adapters[a].image.pinned)
+    assert 0 < pinned < n_cat, pinned
+    ads = {aid: (_StoreWeights(store.adapters[aid]), 32.0) for aid in catalog}  # alpha = 2 r
+    rng = np.random.default_rng(1006)
+    w = 1.0 / np.arange(1, n_cat + 1) ** 0.9
+    w /= w.sum()
+    vocab = model.config.vocab_size
+    gen = torch.Generator(device=gpu).manual_seed(1006)
+    loads0, forwards, distinct = pm.adapter_cache.loads, 0, set()
+    with torch.inference_mode(), _per_layer_check(pm, ads, torch.bfloat16, "churn catalog") as checked:
+        for step in range(n_steps):
+            ids = [catalog[int(i)] for i in rng.choice(n_cat, size=rows, p=w)]
+            distinct.update(ids)
+            for sub in _sub_batches(ids, 32):
+                x = torch.randint(0, vocab, (len(sub), 1), generator=gen, device=gpu)
+                pm(input_ids=x, adapter_ids=sub, past_key_values=DynamicCache(config=model.config), use_cache=True)
+                forwards += 1
+            print(f"step {step + 1}/{n_steps}: {forwards} forwards, {pm.adapter_cache.loads - loads0} loads", flush=True)
+    assert checked.count == len(pm.target_module_names) == 7 * layers
+    assert checked.calls == 7 * layers * forwards
+    loads = pm.adapter_cache.loads - loads0
+    # every step meets more distinct adapters than there are slots: loads far beyond the slot count
+    assert len(distinct) > 150 and loads > 4 * 32, (len(distinct), loads)
+    print(f"churn catalog: {forwards} forwards, {loads} loads, {len(distinct)} distinct adapters", flush=True)
+    # the catalog's page-locked images back to the system before the next test pins its own
+    del ads, catalog, store, pm, model, checked
+    gc.collect()
+    torch.cuda.synchronize()
+    release_locked_free()
 
 
 def test_decode_config_step_every_layer_against_the_oracle(gpu):
