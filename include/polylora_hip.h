@@ -255,12 +255,15 @@ int pl_sgmv_expand_stacked(int32_t dtype, void* const* ws, int32_t ldt, int64_t 
  * that no 128-byte line of the planes holds rows of two groups).  `counters`
  * holds counter_ints >= pl_decode_counter_ints(group_cap, n_modules) int32s,
  * must be all zero before the first call and is all zero again after each
- * call (the last reader of each counter resets it), so it is reused call
- * after call without a clear; calls that share it must not overlap (one
- * stream).  A wait gives up after spin_limit polls of its counter and then
- * sets counters[0] (the status word) to 1 (the results of that call are
- * undefined); otherwise it stays 0.  Every other argument is as for
- * pl_sgmv_shrink_stacked and pl_sgmv_expand_stacked. */
+ * call whose waits all end in time (the last reader of each counter resets
+ * it), so it is reused call after call without a clear; calls that share it
+ * must not overlap (one stream).  A wait gives up after spin_limit (>= 1)
+ * polls of its counter and then sets counters[0] (the status word) to 1:
+ * the results of that call are undefined, and a shrink workgroup that
+ * arrives after the wait gave up can leave its counter above zero, so the
+ * caller must zero all counter_ints words (with no call in flight) before
+ * the next call; otherwise the status word stays 0.  Every other argument
+ * is as for pl_sgmv_shrink_stacked and pl_sgmv_expand_stacked. */
 int pl_lora_decode_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K, const void* arena,
                            const pl_slot_entry* table, int32_t num_modules, int32_t n_modules,
                            const int32_t* modules, void* const* ws, const int32_t* tok,

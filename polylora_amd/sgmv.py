@@ -707,11 +707,13 @@ def lora_expand_stacked(results: list, ys: list, cache, module_names: list, *,
 class _HandoffCounters:
     """Zeroed int32 hand-off counters of pl_lora_decode_stacked for one (device, stream), grown on demand.
 
-    Every launch leaves them zero (each counter's last reader resets it), so
-    they are cleared only when allocated, on the current stream, which must be
-    the stream the launches run on; replaced buffers stay allocated for the
-    life of the process, so a HIP graph that recorded a launch keeps a valid
-    pointer.  Word 0 is the status a timed-out wait sets to 1.
+    Every launch whose waits all end in time leaves them zero (each counter's
+    last reader resets it), so they are cleared only when allocated, on the
+    current stream, which must be the stream the launches run on, and by
+    decode_waits_timed_out after a wait ran out; replaced buffers stay
+    allocated for the life of the process, so a HIP graph that recorded a
+    launch keeps a valid pointer.  Word 0 is the status a timed-out wait sets
+    to 1.
     """
 
     def __init__(self, device: torch.device) -> None:
@@ -749,9 +751,11 @@ def handoff_counters(device: torch.device, stream: int) -> _HandoffCounters:
 def decode_waits_timed_out(device: torch.device | None = None, clear: bool = True) -> bool:
     """Whether a pl_lora_decode_stacked wait on `device` (all devices when None) ran out of polls since the
     status words were last cleared: the results of that launch are then undefined.  Waits for the work
-    queued so far on each counter set's device; with `clear`, resets the status words (on the current
-    stream) for the next check.  A timed-out wait is not expected on a GPU this process has to itself:
-    the limit is far above what a launch's shrink takes."""
+    queued so far on each counter set's device.  With `clear`, a counter set whose status word is set is
+    zeroed whole (on the current stream) for the next launches: a shrink workgroup that arrived after a
+    wait gave up can leave its counter above zero, and a later launch's waits would then end early.  A
+    timed-out wait is not expected on a GPU this process has to itself: the limit is far above what a
+    launch's shrink takes."""
     hit = False
     for (index, _), c in _COUNTERS.items():
         if c.buf is None or (device is not None and c.device != torch.device(device)):
@@ -760,7 +764,7 @@ def decode_waits_timed_out(device: torch.device | None = None, clear: bool = Tru
         if int(c.buf[0]) != 0:
             hit = True
             if clear:
-                c.buf[0].zero_()
+                c.buf.zero_()  # no launch is in flight on the device: every counter can be reset
     return hit
 
 

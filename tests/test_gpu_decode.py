@@ -86,6 +86,42 @@ def test_decode_launch_equals_split_pair_and_oracle(gpu, dtype, rows, K, outs, r
         assert torch.equal(y.cpu()[untouched], b0.cpu()[untouched])
 
 
+def test_timed_out_waits_are_reported_and_clearing_restores_the_counters(gpu, monkeypatch):
+    """Waits forced to give up after one poll (a spin limit of 1, set from the host: every wave still
+    ends) set the status word and can leave counters above zero; decode_waits_timed_out reports them and
+    zeroes the counter set, after which launches with the normal limit equal the split pair bit for bit."""
+    _announce(test="decode_timeout_clear")
+    g = torch.Generator().manual_seed(77)
+    K, outs, ranks = 1024, [512, 256], [8, 16, 32, 64]
+    mods = ["m0", "m1"]
+    shapes = {m: (K, n) for m, n in zip(mods, outs)}
+    adapters = {f"a{i}": {m: peft_layer(g, K, n, r, 2.0 * r) for m, (_, n) in shapes.items()} for i, r in enumerate(ranks)}
+    cache = make_cache(adapters, shapes, len(adapters), 64, gpu, torch.bfloat16)
+    ids = [list(adapters)[i] for i in torch.randint(0, len(adapters), (256,), generator=g).tolist()]
+    row_slot = cache.ensure_resident(ids)
+    plan = sgmv.SgmvPlan(row_slot, torch.ones(256, dtype=torch.int32, device=gpu), 1, cache.num_slots, group_tokens=16)
+    x = torch.randn(256, K, generator=g).to(torch.bfloat16).to(gpu)
+    base = [torch.randn(256, n, generator=g).to(torch.bfloat16).to(gpu) for n in outs]
+    want = _split_pair(x, [b.clone() for b in base], cache, mods, plan)
+    torch.cuda.synchronize()
+    assert not sgmv.decode_waits_timed_out(gpu)
+    limit = sgmv.DECODE_SPIN_LIMIT
+    monkeypatch.setattr(sgmv, "DECODE_SPIN_LIMIT", 1)
+    for _ in range(3):
+        sgmv.lora_decode_stacked(x, [b.clone() for b in base], cache, mods, plan)
+    monkeypatch.setattr(sgmv, "DECODE_SPIN_LIMIT", limit)
+    # the expand workgroups resident at the start poll once, long before every shrink has arrived
+    assert sgmv.decode_waits_timed_out(gpu)
+    _counters_clear(gpu)  # status word and every counter back at zero
+    for rep in range(3):
+        got = sgmv.lora_decode_stacked(x, [b.clone() for b in base], cache, mods, plan)
+        torch.cuda.synchronize()
+        for m, a, b in zip(mods, got, want):
+            assert torch.equal(a, b), (m, rep)
+    _counters_clear(gpu)
+    assert not sgmv.decode_waits_timed_out(gpu)
+
+
 def test_decode_config_layer_repeated_launches(gpu):
     """The decode configuration's layer (256 rows, 64 adapters of ranks {8,16,32,64}, Zipf(1.1) with 10% base
     rows): q/k/v, o, gate/up and down each as one launch, 30 times over, every launch bitwise equal to the
