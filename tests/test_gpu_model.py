@@ -328,6 +328,11 @@ def test_deberta_base_shape_fp32_config(gpu):
         om, bank = _oracle(wl.base, TARGETS, wl.adapters, 16, torch.float32, gpu)
         want = oracle_model.run(om, bank, wl.adapter_ids, **wl.inputs).last_hidden_state
     torch.testing.assert_close(got, want, **FP32)
+    # and every one of the 72 wrapped Linears on the inputs it saw, at the fp32 tolerance
+    with torch.inference_mode(), _per_layer_check(wl.model, wl.adapters, torch.float32, "deberta") as checked:
+        again = wl.model(**wl.inputs, adapter_ids=wl.adapter_ids).last_hidden_state
+    assert checked.count == len(wl.model.target_module_names) == 72
+    assert torch.equal(again, got)
 
 
 def _tiny_llama(seed, dtype, device, attn="pl_safe_fp32"):
