@@ -12,9 +12,12 @@ call.  Their MFMA path works in three parts of device memory (the C ABI's
 * the weights part: the slot table and the weights repacked into the MFMA
   block layout, which depends on ``weights``, ``lora_ranks``, ``stack_num``
   and ``scalings``;
-* per-call scratch.
+* per-call scratch (the shrink's split planes).
 
-This module keeps the first two across calls.  An entry is found by what
+This module keeps the first two across calls, and one scratch buffer per
+device and stream that every call on that stream reuses (calls on one
+stream run in order, so a call's planes are written only after the
+previous call's kernels have read theirs).  An entry is found by what
 identifies the tensors it was built from (storage pointer, shape, strides,
 dtype, device, the stream) and is valid while their version counters are
 where they were when it was built; a changed counter (any in-place write
@@ -99,6 +102,7 @@ class ReferenceOpCache:
         self.bytes: dict = {}
         self._dead: list = []
         self._device_budget: dict = {}
+        self._scratch: dict = {}
         self.stats = dict(plan_builds=0, plan_hits=0, pack_used=0, pack_all=0, weights_hits=0, uncached=0)
 
     def clear(self) -> None:
@@ -106,6 +110,7 @@ class ReferenceOpCache:
         self.weights.clear()
         self.bytes.clear()
         self._dead.clear()
+        self._scratch.clear()
 
     def _budget(self, device: torch.device) -> int:
         if self.max_bytes is not None:
@@ -124,6 +129,18 @@ class ReferenceOpCache:
     def _reap(self) -> None:
         while self._dead:
             self._drop(self._dead.pop())
+
+    def scratch(self, device: torch.device, stream: int, nbytes: int) -> int:
+        """Address of at least nbytes of 256-byte aligned scratch for calls on `stream`, grown on demand
+        (a replaced buffer goes back to torch's allocator, which hands it to later work on the stream it
+        was allocated on, the same stream, only after the kernels queued so far)."""
+        key = (device, stream)
+        hit = self._scratch.get(key)
+        if hit is None or hit[1] < nbytes:
+            size = max(nbytes, 2 * hit[1]) if hit is not None else nbytes
+            buf = _aligned_buffer(size, device)
+            hit = self._scratch[key] = (buf.data_ptr(), size, buf)
+        return hit[0]
 
     def plan(self, device: torch.device, stream: int, B: int, M: int, num_adapters: int, seq_lens: torch.Tensor,
              weight_indices: torch.Tensor, nbytes: int) -> tuple:

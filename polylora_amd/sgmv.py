@@ -915,10 +915,11 @@ def _ref_parts(lib, dt: int, stream: int, x: torch.Tensor, which: int, B: int, M
     take the shape (the row kernels then run).
 
     The plan and weights parts come from refop_cache (kept across calls,
-    rebuilt when the tensors they depend on change) except while a HIP graph
-    is being captured, when every part is taken for this call only.  Parts
-    taken for one call come from torch's caching allocator, which hands a
-    block to later work on the same stream only after this call's kernels.
+    rebuilt when the tensors they depend on change) and the scratch is the
+    stream's reused buffer, except while a HIP graph is being captured, when
+    every part is taken for this call only.  Parts taken for one call come
+    from torch's caching allocator, which hands a block to later work on the
+    same stream only after this call's kernels.
     """
     num_adapters = int(weights.shape[0])
     skey = (dt, which, B, M, K, n, num_adapters)
@@ -930,13 +931,18 @@ def _ref_parts(lib, dt: int, stream: int, x: torch.Tensor, which: int, B: int, M
     if plan_bytes <= 0:
         return None
     device = x.device
-    scratch = refop_cache._aligned_buffer(scratch_bytes, device) if scratch_bytes else None
+    scratch, scratch_ptr = None, 0
     if torch.cuda.is_current_stream_capturing():
         plan = refop_cache._aligned_buffer(plan_bytes, device)
         wpart = refop_cache._aligned_buffer(weights_bytes, device)
         plan_ptr, w_ptr = plan.data_ptr(), wpart.data_ptr()
+        if scratch_bytes:
+            scratch = refop_cache._aligned_buffer(scratch_bytes, device)
+            scratch_ptr = scratch.data_ptr()
         flags, epoch = _native.PL_REF_BUILD_PLAN | _native.PL_REF_PACK_USED, 0
     else:
+        if scratch_bytes:
+            scratch_ptr = refop_cache.CACHE.scratch(device, stream, scratch_bytes)
         plan, plan_ptr, build = refop_cache.CACHE.plan(device, stream, B, M, num_adapters, seq_lens, weight_indices,
                                                        plan_bytes)
         wpart, w_ptr, flags, epoch = refop_cache.CACHE.weights_part(
@@ -945,8 +951,7 @@ def _ref_parts(lib, dt: int, stream: int, x: torch.Tensor, which: int, B: int, M
         if build:
             flags |= _native.PL_REF_BUILD_PLAN
     keep = (plan, wpart, scratch)
-    return (plan_ptr, plan_bytes, w_ptr, weights_bytes, 0 if scratch is None else scratch.data_ptr(), scratch_bytes,
-            flags, epoch), keep
+    return (plan_ptr, plan_bytes, w_ptr, weights_bytes, scratch_ptr, scratch_bytes, flags, epoch), keep
 
 
 def sgmv_lora_a_fwd(

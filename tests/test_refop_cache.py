@@ -120,3 +120,17 @@ def test_marks_bytes():
     assert refop_cache.marks_bytes(1) == 256 and refop_cache.marks_bytes(64) == 256
     assert refop_cache.marks_bytes(65) == 512
     refop_cache.configure()
+
+
+def test_scratch_is_one_aligned_buffer_per_stream_grown_on_demand():
+    c = _cache()
+    p = c.scratch(CPU, 0, 1000)
+    assert p % 256 == 0
+    assert c.scratch(CPU, 0, 1000) == p and c.scratch(CPU, 0, 10) == p  # reused while it is large enough
+    q = c.scratch(CPU, 7, 1000)  # another stream: its own buffer
+    assert q != p and c.scratch(CPU, 7, 500) == q
+    grown = c.scratch(CPU, 0, 1500)  # past its size: replaced by one at least twice as large
+    assert grown % 256 == 0 and c._scratch[(CPU, 0)][1] == 2000
+    assert c.scratch(CPU, 0, 2000) == grown
+    refop_cache.clear()
+    assert not c._scratch
