@@ -14,7 +14,8 @@
   on 2 layers, and 3 steps on the configuration's 32 layers.
 * Decode (32 Llama-3-8B layers, 64 slots, ranks {8,16,32,64}, 256 rows over
   a 512-token KV cache, Zipf(1.1) with 10% base rows): one decode step with
-  all 224 wrapped layers checked.
+  all 224 wrapped layers checked; and the same rows and adapters on two
+  layers in fp16 and in fp32 (the one-launch decode path in those dtypes).
 * Prefill through the model (2 Llama-3-8B layers, 32 rows x 1024, U[512,1024]
   right-padded lengths, 8 adapters of ranks 16 and 32, 4 rows each): two
   forwards of PolyLoraModel, one fused launch per Linear and then the stacked
@@ -210,6 +211,34 @@ def test_decode_config_step_every_layer_against_the_oracle(gpu):
                  adapter_ids=wl.adapter_ids).last_hidden_state
     assert checked.count == len(pm.target_module_names) == 224
     assert torch.isfinite(out.float()).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_decode_shapes_in_fp16_and_fp32_every_layer_against_the_oracle(gpu, dtype):
+    """The decode configuration's rows and adapters (256 rows of one token, 64 slots, ranks {8,16,32,64},
+    Zipf(1.1) with 10% base rows) on two Llama-3-8B-shaped layers in fp16 and in fp32: every wrapped Linear
+    runs the one-launch decode path (one module per launch, then the sibling sets stacked) and is checked
+    against the oracle at the dtype's tolerance."""
+    _announce(test="decode_shapes", dtype=dtype)
+    from bench import add_random_adapters, build_llama, zipf_ids
+
+    model = build_llama(gpu, layers=2, seed=1007, attn="pl_safe_fp32").to(dtype)  # attention in fp32, any dtype
+    pm = PolyLoraModel(model, PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=64, max_rank=64)).eval()
+    assert pm.adapter_cache.dtype == dtype and pm.adapter_cache.decode_handoff
+    rng = np.random.default_rng(1007)
+    names = [f"h{i:02d}" for i in range(64)]
+    ranks = add_random_adapters(pm, {n: int(rng.choice([8, 16, 32, 64])) for n in names}, seed=1007, device=gpu)
+    ids = zipf_ids(rng, 256, 64, 1.1, 0.10, names)
+    store = pm.adapter_store
+    ads = {aid: (_StoreWeights(store.adapters[aid]), 2.0 * r) for aid, r in ranks.items()}
+    x = torch.randint(0, model.config.vocab_size, (256, 1), generator=torch.Generator().manual_seed(1007)).to(gpu)
+    with torch.inference_mode(), _per_layer_check(pm, ads, dtype, f"decode shapes {dtype}") as checked:
+        # the first forward launches per Linear and learns the sibling runs; the second stacks q/k/v and gate/up
+        out = [pm(input_ids=x, adapter_ids=ids).last_hidden_state for _ in range(2)]
+    assert checked.count == len(pm.target_module_names) == 14 and checked.calls == 28
+    assert pm.adapter_cache.stacked_runs
+    assert torch.isfinite(out[0].float()).all() and torch.equal(out[0], out[1])
+    assert not sgmv.decode_waits_timed_out(gpu)
 
 
 def test_prefill_config_through_the_model_every_layer_against_the_oracle(gpu, monkeypatch):
