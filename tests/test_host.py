@@ -12,6 +12,8 @@ from __future__ import annotations
 
 import ctypes
 import re
+import shutil
+import subprocess
 from pathlib import Path
 
 import numpy as np
@@ -426,6 +428,28 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_native.EXPORTED_SYMBOLS)
+
+
+@pytest.mark.parametrize("compiler,std,suffix", [("gcc", "c99", "c"), ("g++", "c++17", "cpp")])
+def test_header_compiles_as_c_and_cpp_and_links(tmp_path, compiler, std, suffix):
+    """A C (cgo, FFI) or C++ client: a program that includes the public header, takes the address of every
+    declared entry point and links against the library compiles warning-free under -pedantic and runs."""
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} is not installed")
+    names = _header_functions()
+    src = tmp_path / f"client.{suffix}"
+    src.write_text(
+        '#include "polylora_hip.h"\n#include <stdio.h>\n'
+        "int main(void) {\n  void (*fns[])(void) = {\n"
+        + "".join(f"    (void (*)(void))&{n},\n" for n in names)
+        + '  };\n  printf("%d %d\\n", pl_version(), (int)(sizeof(fns) / sizeof(fns[0])));\n  return 0;\n}\n')
+    exe = tmp_path / "client"
+    lib_dir = _native.LIB_PATH.parent
+    subprocess.run([compiler, f"-std={std}", "-Wall", "-Wextra", "-pedantic", "-Werror", f"-I{ROOT / 'include'}",
+                    str(src), "-o", str(exe), f"-L{lib_dir}", "-lpolylora_hip", f"-Wl,-rpath,{lib_dir}"],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    assert out == [str(_native.load().pl_version()), str(len(names))]
 
 
 def test_library_host_side_errors_without_gpu():
