@@ -410,7 +410,10 @@ int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32
  *                        call's on that part (a counter).
  * A call without flags reads the plan and weights parts as earlier calls
  * left them: the caller must rebuild them (with the flags, after zeroing
- * the marks again) whenever what they depend on changes. */
+ * the marks again) whenever what they depend on changes.  The first call on
+ * a part must build it (PL_REF_BUILD_PLAN for a plan part, a PACK flag for a
+ * weights part): the kernels read offsets and lengths from the parts without
+ * checking them, so a part that no call has built is read as garbage. */
 #define PL_REF_PART_PLAN 0
 #define PL_REF_PART_WEIGHTS 1
 #define PL_REF_PART_SCRATCH 2
