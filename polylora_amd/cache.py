@@ -190,8 +190,11 @@ class GpuAdapterCache:
         self.spare_regions = int(min(slots, self._spare_budget() // max(1, self.layout.slot_bytes)))
         self.num_regions = slots + self.spare_regions
         arena_bytes = max(1, self.num_regions * self.layout.slot_bytes)
-        self.arena = torch.empty(arena_bytes, dtype=torch.uint8, device=self.device)
-        self.table = torch.zeros((self.num_slots, n_mod, _ENTRY_INTS), dtype=torch.int32, device=self.device)
+        # ordinary tensors even when the first forward under torch.inference_mode moves the cache: loads
+        # write into them with in-place copies, which an inference tensor refuses outside that mode
+        with torch.inference_mode(False):
+            self.arena = torch.empty(arena_bytes, dtype=torch.uint8, device=self.device)
+            self.table = torch.zeros((self.num_slots, n_mod, _ENTRY_INTS), dtype=torch.int32, device=self.device)
         self.table_host = np.zeros((self.num_slots, n_mod, _ENTRY_INTS), dtype=np.int32)
         table_f = self.table.view(torch.float32)
         self.ranks = {name: self.table[:, i, 0] for name, i in self.module_index.items()}

@@ -59,7 +59,10 @@ def _ident_version(t: torch.Tensor):
 
 
 def _aligned_buffer(nbytes: int, device: torch.device) -> torch.Tensor:
-    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+    """nbytes of device memory at a 256-byte aligned address; an ordinary tensor even under
+    torch.inference_mode, since a kept weights part's marks are cleared in place on later calls."""
+    with torch.inference_mode(False):
+        buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
     pad = (-buf.data_ptr()) % 256
     return buf[pad : pad + nbytes]
 

@@ -727,8 +727,11 @@ class _HandoffCounters:
                 self.retired.append(self.buf)
                 ints = max(ints, 2 * self.buf.numel())
             # cleared by a fill kernel on the current stream (the launch's stream),
-            # which a HIP graph being captured records like any other kernel
-            self.buf = torch.empty(max(64, ints), dtype=torch.int32, device=self.device).zero_()
+            # which a HIP graph being captured records like any other kernel; an
+            # ordinary tensor even under torch.inference_mode, so that
+            # decode_waits_timed_out can clear it outside that mode
+            with torch.inference_mode(False):
+                self.buf = torch.empty(max(64, ints), dtype=torch.int32, device=self.device).zero_()
         return self.buf
 
 

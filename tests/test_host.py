@@ -519,3 +519,21 @@ def test_group_size_choice():
     assert sgmv.choose_group_tokens(32 * 1024, 2048) == short  # many adapters, short segments
     assert sgmv.choose_k_splits(80, 4096, torch.bfloat16) == 4
     assert sgmv.choose_k_splits(4096, 4096, torch.bfloat16) == 1  # groups alone fill the GPU
+
+
+def test_cache_moved_under_inference_mode_still_loads_outside_it():
+    """A cache whose arena and table were (re)allocated inside torch.inference_mode (a first forward there moves
+    it) loads adapters outside that mode: they are ordinary tensors, written with in-place copies."""
+    g = torch.Generator().manual_seed(40)
+    w = _peft.make_lora_weights(g, _shapes(), rank=2)
+    store = CpuAdapterStore()
+    store.add_adapter_from_peft_state_dict("a", _peft.state_dict(w), list(_shapes()), 4)
+    cache = _cpu_cache(store, _shapes(), 1, 2)
+    with torch.inference_mode():
+        cache.to(torch.device("cpu"), torch.bfloat16)
+    assert not cache.arena.is_inference() and not cache.table.is_inference()
+    cache.ensure_resident(["a"])
+    slot = cache.adapter_to_slot["a"]
+    assert int(cache.ranks["enc.q_proj"][slot]) == 2
+    for mod, (a, b) in w.items():
+        assert torch.equal(cache.A[mod][slot, :, :2], a.t().to(torch.bfloat16))

@@ -134,3 +134,19 @@ def test_scratch_is_one_aligned_buffer_per_stream_grown_on_demand():
     assert c.scratch(CPU, 0, 2000) == grown
     refop_cache.clear()
     assert not c._scratch
+
+
+def test_parts_made_under_inference_mode_are_rebuilt_outside_it():
+    """A weights part first made inside torch.inference_mode is cleared in place (its pack marks) when its
+    tensors change outside that mode: its buffer is an ordinary tensor."""
+    c = _cache()
+    w, r = torch.zeros(5, 64, 16), torch.ones(5, dtype=torch.int32)
+    with torch.inference_mode():
+        buf, f, e = _part(c, w, r)
+        assert (f, e) == (USED, 1) and not buf.is_inference()
+        c.scratch(CPU, 0, 1000)
+        assert not c._scratch[(CPU, 0)][2].is_inference()
+    w.add_(1)  # a write the version counter sees
+    buf[:256].fill_(3)  # marks left by the earlier packing
+    buf2, f, e = _part(c, w, r)
+    assert buf2.data_ptr() == buf.data_ptr() and (f, e) == (USED, 1) and not buf2[:256].any()
