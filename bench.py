@@ -1801,12 +1801,12 @@ def launch_profile(args) -> int:
                 sgmv.sgmv_lora_b_fwd(tmp, Bw, op_seq, op_widx, rk, sc, y)
 
             leaf = name.rsplit(".", 1)[-1]
-            # one host call pair issues 3 dispatches once the plan and packed weights are kept (the first
-            # two layers' pl_refop_prep dispatches fall in the first warm-up pass): the split shrink, its
-            # finish, and the fused kernel's expand phase; the first entry issues them all
-            seq += [(f"{leaf} shrink: split shrink", "shrink", pair,
+            # one host call pair issues 2 dispatches once the plan and packed weights are kept (the first
+            # two layers' pl_refop_prep dispatches fall in the first warm-up pass): the split shrink,
+            # whose last K split of each tile writes the intermediate, and the fused kernel's expand
+            # phase; the first entry issues both
+            seq += [(f"{leaf} shrink: split shrink + finish", "shrink", pair,
                      launch_bytes(pm, [name], "shrink", ids, [1] * len(ids))),
-                    (f"{leaf} shrink: finish", "operator", lambda: None, 0),
                     (f"{leaf} expand: fused phase", "expand", lambda: None,
                      launch_bytes(pm, [name], "expand", ids, [1] * len(ids)))]
         desc = ("reference operator API (sgmv_lora_a_fwd + sgmv_lora_b_fwd) on one Llama-3-8B-shaped decode "

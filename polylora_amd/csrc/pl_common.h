@@ -204,6 +204,23 @@ struct pl_refop_parts {
   int32_t flags;  // PL_REF_* build flags
   int32_t epoch;
 };
+// pl_sgmv_shrink for one module (table column 0) of a plan of 16-token
+// groups, with each (group, rank pass) finished inside the launch: the last
+// of its K splits to store its plane writes out[tok][j] = T(sum of the planes
+// in split order) for j below the slot's rank and n_max, as a separate pass
+// over the planes would, and nothing else of out.  counters: counter_ints >=
+// group_cap * rank passes (ldt / 32 at most 2) * PL_FINISH_COUNTER_INTS
+// int32s, all zero, and all zero again when the launch has run.  Returns
+// PL_REFOP_DECLINED, having launched nothing, for plans of 64-token groups,
+// ldt not a multiple of 32 (each 128-byte line of the planes must hold one
+// row's ranks of one rank pass) or too few counters.
+constexpr int PL_FINISH_COUNTER_INTS = 16;  // int32s per counter: 64 bytes
+int pl_shrink_finish_launch(int32_t dtype, const void* x, int64_t ldx, int32_t K,
+                            const void* arena, const pl_slot_entry* table, const int32_t* tok,
+                            const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                            int32_t group_tokens, void* ws, int64_t ws_bytes, int32_t ldt,
+                            int64_t tmp_rows, int32_t k_splits, int32_t* counters,
+                            int64_t counter_ints, void* out, int32_t n_max, void* stream);
 int pl_refop_shrink(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K, const void* w,
                     int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t num_adapters,
                     int32_t n_max, const int32_t* seq_lens, const int32_t* weight_indices,

@@ -31,9 +31,13 @@
 //      consecutive lanes on consecutive elements of its fastest dimension,
 //      transposes it through LDS and writes 16 whole MFMA blocks.  Ranks,
 //      scales and indices stay on the device: no host synchronisation.
-//   2. shrink: pl_sgmv_shrink into fp32 split planes, then pl_refop_finish
-//      writes out[b][m][n] = T(sum of the planes) for n < rank * stack_num;
-//      with long adapter segments (at least 1024 rows and 64 per adapter)
+//   2. shrink: the split shrink into fp32 planes, and out[b][m][n] = T(sum
+//      of the planes) for n < rank * stack_num written by the last K split
+//      of each tile to finish, in the same launch (pl_shrink_finish_launch,
+//      16-token groups; its counters live in the plan part, zeroed by every
+//      plan build and left zero by every launch); with 64-token groups a
+//      second launch (pl_refop_finish) sums the planes; with long adapter
+//      segments (at least 1024 rows and 64 per adapter)
 //      one launch of the fused kernel's shrink phase (pl_fused_phase)
 //      instead reduces each 16-token tile in LDS and writes T(sum) straight
 //      into out.  expand: one launch of the fused kernel's expand phase
@@ -65,6 +69,7 @@ constexpr int kMaxRefRank = 64;  // rank capacity of the repacked slots (the til
 constexpr int kPackRows = 64;    // destination rows of one repack unit (4 MFMA tiles)
 constexpr int kPackBlocks = 4;   // 64-byte column blocks of one repack unit
 constexpr int kPackGridCap = 16; // repack workgroups per adapter (each loops over its units)
+constexpr int kMaxPlanes = 16;   // split planes a shrink writes at most (pl_shrink_planes)
 
 int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 int32_t round8(int32_t v) { return (v + 7) & ~7; }
@@ -73,12 +78,14 @@ struct refop_layout {
   int32_t group_tokens;
   int64_t group_cap;
   int32_t ldt;        // rank capacity of a slot, a multiple of 8
+  int32_t pldt;       // row stride of the split shrink's planes, a multiple of 32
   int32_t k_splits;   // shrink planes requested
   int32_t planes;     // planes the shrink writes (1 for the expand)
   int64_t tokens;     // B * M
   int64_t slot_bytes;
   // byte offsets inside the plan part
-  int64_t meta, groups, tok, plan_bytes;
+  int64_t meta, groups, tok, counters, plan_bytes;
+  int64_t counter_ints;  // the shrink's finish counters (pl_shrink_finish_launch)
   // byte offsets inside the weights part
   int64_t marks, table, arena, weights_bytes;
   int64_t scratch_bytes;  // the planes
@@ -104,6 +111,9 @@ bool refop_plan_layout(int32_t dtype, int which, int32_t B, int32_t M, int32_t K
   L.group_cap = pl_plan_group_capacity(B, M, num_adapters + 1, L.group_tokens);
   if (L.group_cap < 1) L.group_cap = 1;
   L.ldt = round8(rank_cap);
+  // the split shrink planes' row stride: whole 128-byte lines, as its
+  // in-launch finish needs
+  L.pldt = (rank_cap + 31) & ~31;
   if (which == 0) {
     const int64_t by_k = (K + 1023) / 1024;
     const int64_t by_groups = (2048 + L.group_cap - 1) / L.group_cap;
@@ -123,6 +133,12 @@ bool refop_plan_layout(int32_t dtype, int which, int32_t B, int32_t M, int32_t K
   o += align256(16 * L.group_cap);
   L.tok = o;
   o += align256(4 * T);
+  // counters of the split shrink's in-launch finish: one per (group, rank
+  // pass), at most 2 passes of 32 ranks for slots of up to 64; the same size
+  // for the shrink and the expand, so that their plans stay interchangeable
+  L.counters = o;
+  L.counter_ints = L.group_cap * 2 * PL_FINISH_COUNTER_INTS;
+  o += align256(4 * L.counter_ints);
   L.plan_bytes = o;
   o = 0;
   L.marks = o;
@@ -132,7 +148,7 @@ bool refop_plan_layout(int32_t dtype, int which, int32_t B, int32_t M, int32_t K
   L.arena = o;
   o += L.slot_bytes * num_adapters;
   L.weights_bytes = o;
-  L.scratch_bytes = align256((int64_t)L.planes * T * L.ldt * 4);
+  L.scratch_bytes = align256((int64_t)L.planes * T * L.pldt * 4);
   L.total = L.plan_bytes + L.weights_bytes + L.scratch_bytes;
   return true;
 }
@@ -166,6 +182,8 @@ struct refop_prep_args {
   int32_t* tok;
   pl_group* groups;
   int32_t* meta;
+  int32_t* counters;  // zeroed with every plan build
+  int64_t counter_ints;
 };
 
 // Rank a slot holds for adapter s: rank * stack_num columns of the shrink,
@@ -258,9 +276,13 @@ __global__ __launch_bounds__(kPlanThreads) void pl_refop_prep(refop_prep_args a)
         a.table[e] = en;
       }
     }
-    if (a.build_plan)
+    if (a.build_plan) {
+      // a new plan starts the shrink's finish counters at zero (each launch
+      // leaves them zero again)
+      for (int64_t i = threadIdx.x; i < a.counter_ints; i += kPlanThreads) a.counters[i] = 0;
       pl_plan_body<true>(a.widx, a.num_adapters, a.seq_lens, a.B, a.M, a.num_adapters + 1,
                          nullptr, 0, a.group_tokens, a.tok, a.groups, a.meta, a.group_cap);
+    }
     return;
   }
   const int s = blockIdx.y - 1;
@@ -311,8 +333,16 @@ __global__ __launch_bounds__(kThreads) void pl_refop_finish(const float* __restr
     const int i = idx / r;
     const int n = idx - i * r;
     const int64_t p = (int64_t)g.start + i;
+    // every plane's load before the first add (an index past the last plane
+    // reads the last one again): one round trip, not one per plane
+    const float* src = planes + p * ldt + n;
+    float v[kMaxPlanes];
+#pragma unroll
+    for (int c = 0; c < kMaxPlanes; ++c) v[c] = src[(int64_t)min(c, n_planes - 1) * plane];
     float acc = 0.f;
-    for (int c = 0; c < n_planes; ++c) acc += planes[c * plane + p * ldt + n];
+#pragma unroll
+    for (int c = 0; c < kMaxPlanes; ++c)
+      if (c < n_planes) acc += v[c];
     reinterpret_cast<T*>(out)[(int64_t)tok[p] * n_max + n] = (T)acc;
   }
 }
@@ -436,6 +466,8 @@ int refop_prep(int32_t dtype, const refop_layout& L, const pl_refop_parts& P, co
   a.tok = reinterpret_cast<int32_t*>(pp + L.tok);
   a.groups = reinterpret_cast<pl_group*>(pp + L.groups);
   a.meta = reinterpret_cast<int32_t*>(pp + L.meta);
+  a.counters = reinterpret_cast<int32_t*>(pp + L.counters);
+  a.counter_ints = L.counter_ints;
   // repack units of the largest matrix an adapter can have (rank = rank_cap)
   const int W = 4 * pl_chunk_elems(dtype);
   const int64_t Rmax = which == 0 ? rank_cap : width;
@@ -503,13 +535,20 @@ int pl_refop_shrink(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t 
                           L.ldt, tok, groups, meta, L.group_cap, L.group_tokens, 1, PL_EPI_FALLBACK,
                           stream);
   float* planes = reinterpret_cast<float*>(P.scratch);
+  // 16-token groups: the last K split of each tile writes its intermediate
+  // in the same launch
+  st = pl_shrink_finish_launch(dtype, x, K, K, wp + L.arena, table, tok, groups, meta, L.group_cap,
+                               L.group_tokens, planes, L.scratch_bytes, L.pldt, L.tokens,
+                               L.k_splits, reinterpret_cast<int32_t*>(pp + L.counters),
+                               L.counter_ints, out, n_max, stream);
+  if (st != PL_REFOP_DECLINED) return st;
   st = pl_sgmv_shrink(dtype, x, K, K, wp + L.arena, table, 1, 0, tok, groups, meta, L.group_cap,
-                      L.group_tokens, planes, L.scratch_bytes, L.ldt, L.tokens, L.k_splits,
+                      L.group_tokens, planes, L.scratch_bytes, L.pldt, L.tokens, L.k_splits,
                       stream);
   if (st) return st;
   refop_dispatch(dtype, [&](auto dt) {
     hipLaunchKernelGGL(pl_refop_finish<decltype(dt)::value>, dim3((unsigned)L.group_cap),
-                       dim3(kThreads), 0, s, planes, L.tokens * L.ldt, L.planes, L.ldt, groups, tok,
+                       dim3(kThreads), 0, s, planes, L.tokens * L.pldt, L.planes, L.pldt, groups, tok,
                        table, n_max, out);
   });
   return pl_launch_status("pl_refop_finish");

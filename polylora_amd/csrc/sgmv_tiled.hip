@@ -250,9 +250,26 @@ constexpr int pl_shrink_short_lds() {
   return kWaves * JT * 64 * (int)sizeof(pl_f32x4);
 }
 
-template <int DT, int JT, bool HANDOFF>
+// What a short-shrink workgroup does with its partial sums: store them as
+// the split planes (plain), store them for the decode launch's expand and
+// arrive on the hand-off counter (handoff), or store them, arrive on the
+// (group, rank pass) counter and, as the last of the K splits to arrive, sum
+// the planes and write the model-dtype intermediate (finish).
+enum { kShrinkPlain = 0, kShrinkHandoff = 1, kShrinkFinish = 2 };
+
+// The finish mode's counters and output: counter (g * rank_passes + rp) at
+// [(g * rank_passes + rp) * PL_FINISH_COUNTER_INTS], zero before the launch
+// and zero again after it (its last arrival resets it); out [tokens][n_max].
+struct pl_shrink_finish {
+  int32_t* counters;
+  void* out;
+  int32_t n_max;
+};
+
+template <int DT, int JT, int MODE>
 __device__ __forceinline__ void pl_shrink_short_body(const pl_shrink_args& a, int block,
-                                                     char* smem, const pl_handoff& h) {
+                                                     char* smem, const pl_handoff& h,
+                                                     const pl_shrink_finish& fin) {
   typedef typename pl_traits<DT>::T T;
   constexpr int E = pl_traits<DT>::E;
   constexpr int kInstr = 4 * E;
@@ -286,7 +303,7 @@ __device__ __forceinline__ void pl_shrink_short_body(const pl_shrink_args& a, in
   if (rb >= rank) {
     // a pass past the rank stores nothing; with a hand-off it still arrives
     // (the expand waits for every pass of a slot that has this module)
-    if constexpr (HANDOFF)
+    if constexpr (MODE == kShrinkHandoff)
       if (tid == 0 && rank > 0) pl_handoff_arrive(h, g * a.n_jobs + job);
     return;
   }
@@ -366,7 +383,7 @@ __device__ __forceinline__ void pl_shrink_short_body(const pl_shrink_args& a, in
       for (int v = 0; v < 4; ++v) {
         const int prow = (l >> 4) * 4 + v;
         if (prow < len) {
-          if constexpr (HANDOFF)
+          if constexpr (MODE != kShrinkPlain)
             pl_store_agent(out + (int64_t)(grp.start + prow) * a.ldt + j, s[v]);
           else
             out[(int64_t)(grp.start + prow) * a.ldt + j] = s[v];
@@ -374,17 +391,69 @@ __device__ __forceinline__ void pl_shrink_short_body(const pl_shrink_args& a, in
       }
     }
   }
-  if constexpr (HANDOFF) {
+  if constexpr (MODE == kShrinkHandoff) {
     pl_wait_stores();  // this thread's planes have reached the agent's coherence point
     __syncthreads();   // ... and every other thread's
     if (tid == 0) pl_handoff_arrive(h, g * a.n_jobs + job);
+  }
+  if constexpr (MODE == kShrinkFinish) {
+    pl_wait_stores();  // this thread's planes have reached the agent's coherence point
+    __syncthreads();   // ... and every other thread's; red[] is no longer read
+    int* last = reinterpret_cast<int*>(smem);
+    if (tid == 0) {
+      int32_t* ctr = fin.counters + (int64_t)(g * a.rank_passes + rp) * PL_FINISH_COUNTER_INTS;
+      const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int is_last = old == a.k_splits - 1;
+      if (is_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *last = is_last;
+    }
+    __syncthreads();
+    if (!*last) return;
+    // The last of the tile's K splits: T(sum of the planes in split order)
+    // for its rows and this pass's ranks, as a separate pass over the planes
+    // would write it.  Ordinary loads see every split's stores: with ldt a
+    // multiple of 32 each 128-byte line of a plane holds this pass's ranks of
+    // one row only, so its one writer is that plane's workgroup of this
+    // (group, rank pass), which stored it through its L2 before arriving;
+    // this XCD's L2 can hold the line only from that writer's own stores,
+    // since each launch starts with the L2s invalidated and no other
+    // workgroup reads it.
+    // Every plane's load is issued before the first add (an index past the
+    // last plane reads the last one again), so the sum waits one round trip,
+    // not one per plane.
+    const float* __restrict__ planes = a.planes[job];
+    T* __restrict__ o = reinterpret_cast<T*>(fin.out);
+    for (int idx = tid; idx < len * kShortRanks; idx += 256) {
+      const int i = idx / kShortRanks;
+      const int j = rb + (idx - i * kShortRanks);
+      if (j >= rank || j >= fin.n_max) continue;
+      const int64_t p = grp.start + i;
+      const float* src = planes + p * a.ldt + j;
+      float v[kShortMaxPlanes];
+#pragma unroll
+      for (int q = 0; q < kShortMaxPlanes; ++q) v[q] = src[(int64_t)min(q, a.k_splits - 1) * a.plane];
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < kShortMaxPlanes; ++q)
+        if (q < a.k_splits) acc += v[q];
+      o[(int64_t)a.tok[p] * fin.n_max + j] = (T)acc;
+    }
   }
 }
 
 template <int DT, int JT>
 __global__ __launch_bounds__(256, 2) void pl_shrink_short(pl_shrink_args a) {
   __shared__ __attribute__((aligned(16))) char smem[pl_shrink_short_lds<JT>()];
-  pl_shrink_short_body<DT, JT, false>(a, blockIdx.x, smem, pl_handoff{});
+  pl_shrink_short_body<DT, JT, kShrinkPlain>(a, blockIdx.x, smem, pl_handoff{}, pl_shrink_finish{});
+}
+
+// pl_shrink_short whose last K split of each (group, rank pass) also writes
+// the tile's model-dtype intermediate (pl_shrink_finish_launch).
+template <int DT, int JT>
+__global__ __launch_bounds__(256, 2) void pl_shrink_short_finish(pl_shrink_args a,
+                                                                 pl_shrink_finish f) {
+  __shared__ __attribute__((aligned(16))) char smem[pl_shrink_short_lds<JT>()];
+  pl_shrink_short_body<DT, JT, kShrinkFinish>(a, blockIdx.x, smem, pl_handoff{}, f);
 }
 
 // Long-group shrink (64-token groups, e.g. prefill): one workgroup per
@@ -947,7 +1016,7 @@ __global__ __launch_bounds__(256, (pl_decode_min_blocks<PMAX, RB>())) void pl_de
   __shared__ __attribute__((aligned(16))) char smem[kLds];
   const int b = (int)blockIdx.x;
   if (b < h.n_shrink)
-    pl_shrink_short_body<DT, JT, true>(sa, b, smem, h);
+    pl_shrink_short_body<DT, JT, kShrinkHandoff>(sa, b, smem, h, pl_shrink_finish{});
   else
     pl_expand_handoff_body<DT, PMAX, RB>(ea, b - h.n_shrink, smem, h);
 }
@@ -1236,6 +1305,15 @@ int dispatch_shrink(int32_t dtype, const pl_shrink_args& a, int64_t group_cap, h
   }
 }
 
+template <int DT>
+void launch_shrink_finish(const pl_shrink_args& a, const pl_shrink_finish& f, int64_t grid,
+                          hipStream_t s) {
+  if (a.rank_tiles == 4)
+    hipLaunchKernelGGL((pl_shrink_short_finish<DT, 4>), dim3((unsigned)grid), dim3(256), 0, s, a, f);
+  else
+    hipLaunchKernelGGL((pl_shrink_short_finish<DT, 2>), dim3((unsigned)grid), dim3(256), 0, s, a, f);
+}
+
 int dispatch_expand(int32_t dtype, const pl_expand_args& a, int64_t group_cap, hipStream_t s) {
   switch (dtype) {
     case PL_BF16: return launch_expand<PL_BF16>(a, group_cap, s);
@@ -1270,6 +1348,33 @@ extern "C" int pl_sgmv_shrink(int32_t dtype, const void* x, int64_t ldx, int32_t
   return pl_sgmv_shrink_stacked(dtype, x, ldx, K, arena, table, num_modules, 1, &module, &ws,
                                 tok, groups, meta, group_cap, group_tokens, ws_bytes, ldt,
                                 tmp_rows, k_splits, stream);
+}
+
+int pl_shrink_finish_launch(int32_t dtype, const void* x, int64_t ldx, int32_t K,
+                            const void* arena, const pl_slot_entry* table, const int32_t* tok,
+                            const pl_group* groups, const int32_t* meta, int64_t group_cap,
+                            int32_t group_tokens, void* ws, int64_t ws_bytes, int32_t ldt,
+                            int64_t tmp_rows, int32_t k_splits, int32_t* counters,
+                            int64_t counter_ints, void* out, int32_t n_max, void* stream) {
+  if (group_tokens != PL_GROUP_TOKENS_SHORT || !counters || !out || n_max < 1 || ldt % 32 != 0)
+    return PL_REFOP_DECLINED;
+  pl_shrink_args a;
+  const int32_t module = 0;
+  int st = prepare_shrink(a, dtype, x, ldx, K, arena, table, 1, 1, &module, &ws, tok, groups, meta,
+                          group_cap, group_tokens, ws_bytes, ldt, tmp_rows, k_splits);
+  if (st) return st;
+  if (a.sub != 1 || group_cap * a.rank_passes * PL_FINISH_COUNTER_INTS > counter_ints)
+    return PL_REFOP_DECLINED;
+  const int64_t grid = group_cap * a.k_splits * a.rank_passes;
+  if (grid <= 0) return PL_OK;
+  const pl_shrink_finish f{counters, out, n_max};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case PL_BF16: launch_shrink_finish<PL_BF16>(a, f, grid, s); break;
+    case PL_F16: launch_shrink_finish<PL_F16>(a, f, grid, s); break;
+    default: launch_shrink_finish<PL_F32>(a, f, grid, s); break;
+  }
+  return pl_launch_status("pl_sgmv_shrink (finish)");
 }
 
 extern "C" int pl_sgmv_shrink_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K,

@@ -435,3 +435,44 @@ def test_kept_parts_with_int64_indices_and_stacked_columns(gpu, dtype):
     torch.cuda.synchronize()
     assert (st["plan_builds"], st["plan_hits"]) == (1, 2), st
     assert (st["pack_used"], st["pack_all"], st["weights_hits"]) == (1, 1, 1), st
+
+
+@pytest.mark.parametrize("dtype,Bt,K,R,stack_num,S", [
+    (torch.bfloat16, 256, 4096, 64, 1, 17),  # 4 K splits, up to 64 ranks
+    (torch.float16, 200, 14336, 16, 1, 9),  # 8 K splits, 64-byte plane rows shared by neighbouring groups
+    (torch.float32, 96, 4096, 8, 2, 6),  # fp32, two stacked columns per rank
+    (torch.bfloat16, 2048, 4096, 32, 2, 40),  # ~170 groups, 64 columns
+    # 64-token groups (8192 tokens, ~41 per adapter: too few for the fused kernel): the split shrink with
+    # its planes summed by a second launch
+    (torch.bfloat16, 8192, 2048, 16, 1, 200),
+])
+def test_split_shrink_finishes_inside_its_launch(gpu, dtype, Bt, K, R, stack_num, S):
+    """Short adapter segments take the split shrink; with 16-token groups its last K split of each tile writes
+    the intermediate in the same launch on counters kept in the plan part.  Three calls with a kept plan (the
+    counters must be back at zero after each launch) and new x each time, every one against the oracle, and
+    equal bit for bit to the single-workspace entry (which builds the plan, and zeroes the counters, on every
+    call)."""
+    _announce(test="refop_split_finish", dtype=dtype, Bt=Bt, K=K, R=R, stack_num=stack_num, S=S)
+    g = torch.Generator().manual_seed(Bt + K + R)
+    M = 1
+    wa = (torch.randn(S, K, R * stack_num, generator=g) * 0.05).to(dtype)
+    ranks = torch.randint(0, R + 1, (S,), generator=g, dtype=torch.int32)
+    ranks[0], ranks[-1] = 0, R
+    seq = (torch.rand(Bt, generator=g) > 0.05).to(torch.int32)  # a few rows of length 0
+    widx = torch.randint(0, S, (Bt,), generator=g, dtype=torch.int32)
+    dwa, dranks, dseq, dwidx = (t.to(gpu) for t in (wa, ranks, seq, widx))
+    refop_cache.configure()
+    try:
+        for call in range(3):
+            x = torch.randn(Bt, M, K, generator=g).to(dtype)
+            exp, valid = sgmv_shrink_reference(x, wa, seq, widx, ranks, stack_num)
+            dx = x.to(gpu)
+            got = sgmv.sgmv_lora_a_fwd(dx, dwa, dseq, dwidx, dranks, stack_num).cpu()
+            torch.testing.assert_close(got[valid], exp[valid], **tol_for(dtype))
+            fresh = _call_a(dx, dwa, dseq, dwidx, dranks, stack_num, mfma=True).cpu()
+            assert torch.equal(fresh[valid], got[valid]), call
+            assert bool((fresh[~valid] == 7).all()), "entries outside the defined region were written"
+        st = refop_cache.CACHE.stats
+        assert (st["plan_builds"], st["plan_hits"]) == (1, 2), st
+    finally:
+        refop_cache.configure()
