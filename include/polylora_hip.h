@@ -383,8 +383,12 @@ int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32
 
 /* The operator API's MFMA path in three caller-kept parts (codes for
  * pl_sgmv_ref_part_bytes):
- *   PL_REF_PART_PLAN     the plan (meta, group records, token list).  It
- *                        depends on weight_indices, seq_lens, B, M and
+ *   PL_REF_PART_PLAN     the plan (meta, group records, token list) and the
+ *                        counters with which the split shrink's last K
+ *                        split of each tile finishes it in the same launch
+ *                        (zeroed by every plan build, left zero by every
+ *                        call; so calls that share a plan part must not
+ *                        overlap).  It depends on weight_indices, seq_lens, B, M and
  *                        num_adapters only (not on ranks, weights or
  *                        which), so one plan built by any call serves the
  *                        shrink and the expand of every module that shares
