@@ -348,13 +348,16 @@ def test_kept_weights_die_with_their_tensor(gpu):
     torch.cuda.synchronize()
 
 
-def test_operator_api_in_a_graph_replays(gpu):
+@pytest.mark.parametrize("K", [512, 4096])
+def test_operator_api_in_a_graph_replays(gpu, K):
     """Shrink then expand captured in a HIP graph (every part taken for the captured call, nothing kept):
-    each replay, with eager work between replays, equals the eager result bit for bit."""
-    _announce(test="refop_graph")
+    each replay, with eager work between replays, equals the eager result bit for bit.  32 rows take the
+    split shrink with its in-launch finish: one K split at K = 512, four at 4096 (each replay's plan build
+    zeroes the finish counters)."""
+    _announce(test="refop_graph", K=K)
     _fresh_cache()
     g = torch.Generator().manual_seed(33)
-    _, (dx, dwa, dwb, dranks, dscal, dseq, dwidx) = _case(g, 32, 1, 512, 256, 6, 16, 1, torch.bfloat16, gpu)
+    _, (dx, dwa, dwb, dranks, dscal, dseq, dwidx) = _case(g, 32, 1, K, 256, 6, 16, 1, torch.bfloat16, gpu)
     base = torch.randn(32, 1, 256, generator=g).bfloat16().to(gpu)
     out = torch.empty_like(base)
     tmp = torch.zeros(32, 1, 16, dtype=torch.bfloat16, device=gpu)
