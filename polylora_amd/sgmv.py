@@ -892,13 +892,14 @@ def lora_apply_rows(
 
 
 def _check_row_meta(B: int, num_adapters: int, seq_lens, weight_indices, lora_ranks, scalings=None,
-                    device=None) -> None:
-    """Per-row and per-adapter vectors must cover every row and adapter the kernels index, on `device`."""
-    if device is not None:
+                    device_index: int | None = None) -> None:
+    """Per-row and per-adapter vectors must cover every row and adapter the kernels index, on the GPU of
+    index `device_index` (compared as integers: no device objects on the per-call path)."""
+    if device_index is not None:
         for name, t in (("seq_lens", seq_lens), ("weight_indices", weight_indices), ("lora_ranks", lora_ranks),
                         ("scalings", scalings)):
-            if t is not None and t.device != device:
-                raise ValueError(f"{name} is on {t.device}; the kernels read it on {device}")
+            if t is not None and t.get_device() != device_index:
+                raise ValueError(f"{name} is on {t.device}; the kernels read it on cuda:{device_index}")
     if int(seq_lens.numel()) != B or int(weight_indices.numel()) != B:
         raise ValueError(f"seq_lens / weight_indices must have {B} entries")
     if int(lora_ranks.numel()) < num_adapters or (scalings is not None and int(scalings.numel()) < num_adapters):
@@ -935,7 +936,7 @@ def _ref_parts(lib, dt: int, stream: int, x: torch.Tensor, which: int, B: int, M
         return None
     device = x.device
     scratch, scratch_ptr = None, 0
-    if torch.cuda.is_current_stream_capturing():
+    if torch._C._cuda_isCurrentStreamCapturing():  # torch.cuda.is_current_stream_capturing without its wrapper
         plan = refop_cache._aligned_buffer(plan_bytes, device)
         wpart = refop_cache._aligned_buffer(weights_bytes, device)
         plan_ptr, w_ptr = plan.data_ptr(), wpart.data_ptr()
@@ -975,7 +976,7 @@ def sgmv_lora_a_fwd(
     B, M, K = x.shape
     _, Kw, N_max = weights.shape
     assert Kw == K, f"K mismatch: x={K}, weights={Kw}"
-    output = torch.empty((B, M, N_max), device=x.device, dtype=x.dtype)
+    output = x.new_empty((B, M, N_max))
     if B == 0 or M == 0 or N_max == 0:
         return output
     _require_gpu(x, "sgmv_lora_a_fwd")
@@ -983,11 +984,12 @@ def sgmv_lora_a_fwd(
         raise TypeError(f"weights dtype {weights.dtype} must match x dtype {x.dtype}")
     seq_lens_in, weight_indices_in, lora_ranks_in = seq_lens, weight_indices, lora_ranks
     seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
-    if weights.device != x.device:
+    dev = x.get_device()
+    if weights.get_device() != dev:
         raise ValueError(f"weights are on {weights.device}, x on {x.device}")
-    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, device=x.device)
+    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, device_index=dev)
     lib = _native.load()
-    dt, stream, stack_num = _native.dtype_code(x.dtype), _stream(x.device), int(stack_num)
+    dt, stream, stack_num = _native.dtype_code(x.dtype), torch._C._cuda_getCurrentRawStream(dev), int(stack_num)
     head = (dt, x.data_ptr(), B, M, K, weights.data_ptr(), *weights.stride(), int(weights.shape[0]), N_max,
             seq_lens.data_ptr(), weight_indices.data_ptr(), lora_ranks.data_ptr(), stack_num, output.data_ptr())
     parts = _ref_parts(lib, dt, stream, x, 0, B, M, K, N_max, weights, seq_lens_in, weight_indices_in, lora_ranks_in,
@@ -1029,11 +1031,12 @@ def sgmv_lora_b_fwd(
     seq_lens, weight_indices, lora_ranks = _i32(seq_lens), _i32(weight_indices), _i32(lora_ranks)
     if not (scalings.dtype is torch.float32 and scalings.is_contiguous()):
         scalings = scalings.to(torch.float32).contiguous()
-    if weights.device != x.device or output.device != x.device:
+    dev = x.get_device()
+    if weights.get_device() != dev or output.get_device() != dev:
         raise ValueError("x, weights and base_output must be on one device")
-    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, scalings, device=x.device)
+    _check_row_meta(B, weights.shape[0], seq_lens, weight_indices, lora_ranks, scalings, device_index=dev)
     lib = _native.load()
-    dt, stream = _native.dtype_code(x.dtype), _stream(x.device)
+    dt, stream = _native.dtype_code(x.dtype), torch._C._cuda_getCurrentRawStream(dev)
     head = (dt, x.data_ptr(), B, M, K_max, weights.data_ptr(), *weights.stride(), int(weights.shape[0]), N,
             seq_lens.data_ptr(), weight_indices.data_ptr(), lora_ranks.data_ptr(), scalings.data_ptr(),
             work.data_ptr())
