@@ -68,20 +68,24 @@ def _aligned_buffer(nbytes: int, device: torch.device) -> torch.Tensor:
 
 
 class _PlanEntry:
-    __slots__ = ("refs", "versions", "buf", "ptr")
+    __slots__ = ("refs", "versions", "buf", "ptr", "ptrs", "live")
 
     def __init__(self, refs: tuple, versions: tuple, buf: torch.Tensor) -> None:
         self.refs = refs  # strong: the storage cannot be recycled while the entry lives
         self.versions = versions
         self.buf = buf
         self.ptr = buf.data_ptr()
+        self.ptrs = tuple(t.data_ptr() for t in refs)
+        self.live = True  # False once the cache has dropped it
 
 
 class _WeightsEntry:
-    __slots__ = ("refs", "versions", "buf", "ptr", "marks_bytes", "epoch", "stage", "nbytes")
+    __slots__ = ("refs", "versions", "buf", "ptr", "marks_bytes", "epoch", "stage", "nbytes", "wmeta", "live", "key")
 
-    def __init__(self, refs: tuple, buf: torch.Tensor, marks_bytes: int) -> None:
+    def __init__(self, refs: tuple, buf: torch.Tensor, marks_bytes: int, wmeta: tuple) -> None:
         self.refs = refs  # weak references
+        self.wmeta = wmeta  # the weights' storage pointer and shape when the entry was made
+        self.live = True  # False once the cache has dropped it
         self.versions = None
         self.buf = buf
         self.ptr = buf.data_ptr()
@@ -106,14 +110,24 @@ class ReferenceOpCache:
         self._dead: list = []
         self._device_budget: dict = {}
         self._scratch: dict = {}
+        # Front memos of the lookups below, keyed by the tensors' identities: a hit is taken only for a
+        # live entry that holds these very tensor objects (weakly or strongly, so an id() reused by a
+        # later tensor never matches), at the same storage pointers and version counters; anything
+        # else goes through the full lookup.
+        self._recent_plans: dict = {}
+        self._recent_weights: dict = {}
         self.stats = dict(plan_builds=0, plan_hits=0, pack_used=0, pack_all=0, weights_hits=0, uncached=0)
 
     def clear(self) -> None:
+        for e in (*self.plans.values(), *self.weights.values()):
+            e.live = False
         self.plans.clear()
         self.weights.clear()
         self.bytes.clear()
         self._dead.clear()
         self._scratch.clear()
+        self._recent_plans.clear()
+        self._recent_weights.clear()
 
     def _budget(self, device: torch.device) -> int:
         if self.max_bytes is not None:
@@ -127,6 +141,7 @@ class ReferenceOpCache:
     def _drop(self, key) -> None:
         e = self.weights.pop(key, None)
         if e is not None:
+            e.live = False
             self.bytes[key[0]] = self.bytes.get(key[0], 0) - e.nbytes
 
     def _reap(self) -> None:
@@ -148,6 +163,17 @@ class ReferenceOpCache:
     def plan(self, device: torch.device, stream: int, B: int, M: int, num_adapters: int, seq_lens: torch.Tensor,
              weight_indices: torch.Tensor, nbytes: int) -> tuple:
         """(plan buffer, its address, whether the call must build it)."""
+        fast = (id(seq_lens), id(weight_indices), B, M, num_adapters, nbytes, stream)
+        e = self._recent_plans.get(fast)
+        if e is not None and e.live and e.refs[0] is seq_lens and e.refs[1] is weight_indices:
+            try:
+                same = (e.ptrs == (seq_lens.data_ptr(), weight_indices.data_ptr())
+                        and e.versions == (seq_lens._version, weight_indices._version))
+            except RuntimeError:
+                same = False
+            if same:
+                self.stats["plan_hits"] += 1
+                return e.buf, e.ptr, False
         a, b = _ident_version(seq_lens), _ident_version(weight_indices)
         if a is None or b is None:
             self.stats["plan_builds"] += 1
@@ -158,6 +184,7 @@ class ReferenceOpCache:
         e = self.plans.get(key)
         if e is not None:
             self.plans.move_to_end(key)
+            self._remember(self._recent_plans, fast, e)
             if now == e.versions:
                 self.stats["plan_hits"] += 1
                 return e.buf, e.ptr, False
@@ -167,9 +194,17 @@ class ReferenceOpCache:
         e = _PlanEntry((seq_lens, weight_indices), now, _aligned_buffer(nbytes, device))
         self.plans[key] = e
         while len(self.plans) > self.max_plans:
-            self.plans.popitem(last=False)
+            self.plans.popitem(last=False)[1].live = False
+        if e.live:
+            self._remember(self._recent_plans, fast, e)
         self.stats["plan_builds"] += 1
         return e.buf, e.ptr, True
+
+    @staticmethod
+    def _remember(memo: dict, fast: tuple, e) -> None:
+        if len(memo) >= 256:
+            memo.clear()
+        memo[fast] = e
 
     def weights_part(self, device: torch.device, stream: int, which: int, weights: torch.Tensor,
                      lora_ranks: torch.Tensor, scalings: torch.Tensor | None, stack_num: int, dims: tuple,
@@ -177,6 +212,20 @@ class ReferenceOpCache:
         """(weights buffer, its address, build flags, epoch) for this call."""
         if self._dead:
             self._reap()
+        fast = (id(weights), id(lora_ranks), id(scalings), which, stack_num, stream)
+        e = self._recent_weights.get(fast)
+        if e is not None and e.live and e.stage == 2 and e.refs[0]() is weights and e.refs[1]() is lora_ranks \
+                and (scalings is None or e.refs[2]() is scalings):
+            try:
+                now = (weights._version, lora_ranks._version) if scalings is None else (
+                    weights._version, lora_ranks._version, scalings._version)
+                same = now == e.versions and (weights.data_ptr(), weights.shape) == e.wmeta
+            except RuntimeError:
+                same = False
+            if same:
+                self.weights.move_to_end(e.key)
+                self.stats["weights_hits"] += 1
+                return e.buf, e.ptr, 0, 0
         srcs = (weights, lora_ranks) if scalings is None else (weights, lora_ranks, scalings)
         ivs = [_ident_version(t) for t in srcs]
         if None in ivs or nbytes > self._budget(device):
@@ -192,7 +241,8 @@ class ReferenceOpCache:
         if e is None:
             dead = self._dead
             refs = tuple(weakref.ref(t, lambda _r, k=key: dead.append(k)) for t in srcs)
-            e = _WeightsEntry(refs, _aligned_buffer(nbytes, device), marks_bytes)
+            e = _WeightsEntry(refs, _aligned_buffer(nbytes, device), marks_bytes, (weights.data_ptr(), weights.shape))
+            e.key = key
             self.weights[key] = e
             self.bytes[device] = self.bytes.get(device, 0) + e.nbytes
             budget = self._budget(device)
@@ -203,6 +253,8 @@ class ReferenceOpCache:
                     self._drop(old)
         else:
             self.weights.move_to_end(key)
+        if e.live:
+            self._remember(self._recent_weights, fast, e)
         now = tuple(iv[1] for iv in ivs)
         if e.versions != now or e.epoch >= 0x7FFFFFF0:
             e.versions = now

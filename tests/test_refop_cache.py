@@ -150,3 +150,57 @@ def test_parts_made_under_inference_mode_are_rebuilt_outside_it():
     buf[:256].fill_(3)  # marks left by the earlier packing
     buf2, f, e = _part(c, w, r)
     assert buf2.data_ptr() == buf.data_ptr() and (f, e) == (USED, 1) and not buf2[:256].any()
+
+
+def _steady(c, w, r, **kw):
+    """Lookups until the weights part needs nothing more (packed used, then all, then kept)."""
+    flags = None
+    for _ in range(3):
+        buf, flags, _ = _part(c, w, r, **kw)
+    assert flags == 0
+    return buf
+
+
+def test_identity_memo_never_serves_a_dropped_entry_or_another_tensor():
+    """The lookups' identity-keyed front memos: a kept part is served again without its full key, but
+    never after clear()/configure(), after the budget dropped it, after its tensor died and a new one
+    took its id(), or after the storage under the same tensor object changed."""
+    c = _cache(max_bytes=3 * 4096)
+    w, r = torch.zeros(5, 64, 16), torch.ones(5, dtype=torch.int32)
+    buf = _steady(c, w, r)
+    hits = c.stats["weights_hits"]
+    assert _part(c, w, r)[1] == 0 and c.stats["weights_hits"] == hits + 1  # served again, nothing to build
+    refop_cache.clear()
+    assert _part(c, w, r)[1] == USED  # a fresh entry: packs again
+    # the budget holds 3 parts of 4096 bytes: a fourth drops the oldest
+    _steady(c, w, r)
+    others = [(torch.zeros(5, 64, 16), torch.ones(5, dtype=torch.int32)) for _ in range(3)]
+    for wo, ro in others:
+        _part(c, wo, ro)
+    assert _part(c, w, r)[1] == USED  # dropped by the budget: built again
+    # a new tensor that reuses a dead one's id() is never taken for it
+    c = _cache()
+    w2 = torch.zeros(5, 64, 16)
+    _steady(c, w2, r)
+    ident = id(w2)
+    del w2
+    gc.collect()
+    for _ in range(50):
+        w3 = torch.zeros(5, 64, 16)
+        if id(w3) == ident:
+            break
+    assert _part(c, w3, r)[1] == USED
+    # the storage under one tensor object changed without a version bump (.data): not served
+    w4 = torch.zeros(5, 64, 16)
+    _steady(c, w4, r)
+    w4.data = torch.zeros(5, 64, 16)
+    assert _part(c, w4, r)[1] == USED
+    # plans: served from the memo while their tensors stand, rebuilt after an in-place write
+    c = _cache()
+    s, i = torch.ones(4, dtype=torch.int32), torch.zeros(4, dtype=torch.int32)
+    assert _plan(c, 4, 1, 5, s, i, 4096)[1] and not _plan(c, 4, 1, 5, s, i, 4096)[1]
+    i[0] = 2
+    assert _plan(c, 4, 1, 5, s, i, 4096)[1]
+    refop_cache.clear()
+    assert _plan(c, 4, 1, 5, s, i, 4096)[1]
+    del buf
