@@ -445,6 +445,9 @@ def test_kept_parts_with_int64_indices_and_stacked_columns(gpu, dtype):
     (torch.float16, 200, 14336, 16, 1, 9),  # 8 K splits, 64-byte plane rows shared by neighbouring groups
     (torch.float32, 96, 4096, 8, 2, 6),  # fp32, two stacked columns per rank
     (torch.bfloat16, 2048, 4096, 32, 2, 40),  # ~170 groups, 64 columns
+    (torch.bfloat16, 130, 1000, 24, 1, 7),  # one K split: every workgroup is its tile's last; K ends mid-step
+    (torch.float16, 300, 2048, 64, 1, 12),  # 2 K splits, two rank passes
+    (torch.float32, 77, 3000, 40, 1, 5),  # 3 K splits, the last one short; fp32 at 40 ranks
     # 64-token groups (8192 tokens, ~41 per adapter: too few for the fused kernel): the split shrink with
     # its planes summed by a second launch
     (torch.bfloat16, 8192, 2048, 16, 1, 200),
