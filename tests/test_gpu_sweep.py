@@ -1,0 +1,132 @@
+"""Seeded random shapes through every kernel path, against the oracle.
+
+Each case draws a dtype, a batch (rows x positions with ragged lengths, some
+rows of length 0, some on the base adapter), K and N (whole 16-byte chunks,
+mostly not multiples of the tile sizes), and adapters of random ranks up to a
+random max_rank (some lacking the module, so their rows stay untouched).  It
+then runs the split shrink + expand (16- and 64-token groups, the split count
+drawn too), the fused kernel (where its rank limit allows), the one-launch
+decode path (bit for bit against the split pair on the same plan and split
+count), the row kernels, and the operator API's sgmv_lora_a_fwd /
+sgmv_lora_b_fwd on the reference slot layout.  Every output is checked
+against the oracle at the dtype's tolerance (tests/_util.py: CountedParity for
+outputs that add into a base, the plain tolerance for the intermediate).
+
+Reference: the fallback of layers.py:112-134 (reference_forward), the
+operator signatures of sgmv.py:141-175 and :278-328.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.lora import reference_forward, sgmv_expand_reference, sgmv_shrink_reference
+from polylora_amd import refop_cache, sgmv
+from tests._util import CountedParity, make_cache, oracle_slot_tensors, peft_layer, tol_for
+
+pytestmark = pytest.mark.gpu
+
+_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def _announce(**kw):
+    print("case:", ", ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _draw(seed: int) -> dict:
+    r = np.random.default_rng(1000 + seed)
+    dtype = _DTYPES[int(r.integers(3))]
+    e = 4 if dtype == torch.float32 else 8  # elements per 16 bytes
+    M = int(r.choice([1, 1, 1, 2, 3, 17, 64]))
+    max_rank = int(r.choice([8, 16, 32, 64]))
+    n_ad = int(r.integers(1, 13))
+    ranks = [int(v) for v in r.integers(0, max_rank + 1, n_ad)]
+    ranks[-1] = max_rank
+    tokens = int(r.choice([2048, 2048, 8192]))  # at most, over rows x positions
+    return dict(dtype=dtype, K=e * int(r.integers(1, 513)), N=e * int(r.integers(1, 513)), M=M,
+                rows=int(r.integers(1, max(2, tokens // M))), ranks=ranks, max_rank=max_rank,
+                base_frac=float(r.uniform(0.0, 0.3)), k_splits=int(r.choice([1, 2, 3, 4, 8])))
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_random_shapes_every_path_against_the_oracle(gpu, seed):
+    c = _draw(seed)
+    dtype, K, N, M, rows = c["dtype"], c["K"], c["N"], c["M"], c["rows"]
+    _announce(test="sweep", seed=seed, **{k: v for k, v in c.items() if k != "dtype"}, dtype=dtype)
+    g = torch.Generator().manual_seed(seed)
+    adapters = {}
+    for i, rk in enumerate(c["ranks"]):
+        # rank 0: the adapter lacks the module (another module keeps it loadable)
+        adapters[f"a{i:02d}"] = ({"m": peft_layer(g, K, N, rk, 2.0 * rk)} if rk else
+                                 {"other": peft_layer(g, 8, 8, 2, 4.0)})
+    cache = make_cache(adapters, {"m": (K, N), "other": (8, 8)}, len(adapters), c["max_rank"], gpu, dtype)
+    names = list(adapters)
+    pick = torch.randint(0, len(names), (rows,), generator=g).tolist()
+    on_base = (torch.rand(rows, generator=g) < c["base_frac"]).tolist()
+    adapter_ids = ["__base__" if b else names[i] for i, b in zip(pick, on_base)]
+    row_slot = cache.ensure_resident(adapter_ids)
+    seq = torch.randint(0, M + 2, (rows,), generator=g, dtype=torch.int32)
+    x = torch.randn(rows, M, K, generator=g).to(dtype)
+    base = torch.randn(rows, M, N, generator=g).to(dtype)
+    A, B, rk, sc = oracle_slot_tensors(cache, adapters, "m", dtype)
+    slots = row_slot.cpu()
+    want = reference_forward(x, base, seq, slots, A, B, rk, sc)
+    untouched = torch.ones(rows, M, dtype=torch.bool)
+    for b in range(rows):
+        if int(rk[int(slots[b])]) > 0:
+            untouched[b, : min(int(seq[b]), M)] = False
+    dx, dseq = x.to(gpu).view(-1, K), seq.to(gpu)
+    parity = CountedParity(dtype, f"sweep seed {seed}")
+
+    def check(y: torch.Tensor, path: str) -> None:
+        got = y.cpu().view(rows, M, N)
+        parity.check(got, want, base, f" [{path}]")
+        assert torch.equal(got[untouched], base[untouched]), f"{path}: untouched rows were written"
+
+    # split shrink + expand, both group sizes, the drawn split count
+    for gt in (16, 64):
+        plan = sgmv.SgmvPlan(row_slot, dseq, M, cache.num_slots, group_tokens=gt)
+        _announce(path="split", group_tokens=gt)
+        y = base.to(gpu).view(-1, N)
+        sgmv.lora_apply(dx, y, cache, "m", plan, k_splits=c["k_splits"])
+        check(y, f"split gt{gt}")
+        if cache.rank8_cap <= sgmv.FUSED_MAX_RANK:
+            _announce(path="fused", group_tokens=gt)
+            y = base.to(gpu).view(-1, N)
+            sgmv.lora_fused(dx, y, cache, "m", plan)
+            check(y, f"fused gt{gt}")
+        if sgmv.decode_ok(plan):
+            _announce(path="decode", group_tokens=gt)
+            pair = base.to(gpu).view(-1, N)
+            res = sgmv.lora_shrink_stacked(dx, cache, ["m"], plan, k_splits=c["k_splits"])
+            sgmv.lora_expand_stacked(res, [pair], cache, ["m"])
+            y = base.to(gpu).view(-1, N)
+            sgmv.lora_decode_stacked(dx, [y], cache, ["m"], plan, k_splits=c["k_splits"])
+            torch.cuda.synchronize()
+            assert torch.equal(y, pair), "decode launch differs from the split pair"
+            assert not sgmv.decode_waits_timed_out(gpu)
+            check(y, f"decode gt{gt}")
+    _announce(path="rows")
+    y = base.to(gpu).view(-1, N)
+    sgmv.lora_apply_rows(dx, y, cache, "m", row_slot, dseq, M)
+    check(y, "rows")
+
+    # the operator API on the reference slot layout (slot 0 the base adapter, rank 0)
+    _announce(path="operator")
+    refop_cache.configure()
+    try:
+        dA, dB, drk, dsc, dslots = (t.to(gpu) for t in (A, B, rk, sc, slots))
+        exp_tmp, valid = sgmv_shrink_reference(x, A, seq, slots, rk)
+        for call in range(2):  # the second call runs on the kept parts
+            tmp = sgmv.sgmv_lora_a_fwd(x.to(gpu), dA, dseq, dslots, drk).cpu()
+            torch.testing.assert_close(tmp[valid], exp_tmp[valid], **tol_for(dtype))
+        exp_out = sgmv_expand_reference(exp_tmp, B, seq, slots, rk, sc, base)
+        for call in range(2):
+            out = sgmv.sgmv_lora_b_fwd(exp_tmp.to(gpu), dB, dseq, dslots, drk, dsc, base.to(gpu)).cpu()
+            parity.check(out, exp_out, base, " [operator b]")
+            assert torch.equal(out[untouched], base[untouched]), "operator b: untouched rows were written"
+    finally:
+        refop_cache.configure()
+    parity.finish()
