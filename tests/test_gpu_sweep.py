@@ -130,3 +130,81 @@ def test_random_shapes_every_path_against_the_oracle(gpu, seed):
     finally:
         refop_cache.configure()
     parity.finish()
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_sibling_modules_in_one_launch_against_the_oracle(gpu, seed):
+    """2..4 sibling modules fed the same x (different N, and adapters that have only some of them) through
+    the stacked launches: fused, split shrink + expand, and the decode launch (bit for bit against the
+    stacked split pair); each module's output against the oracle."""
+    r = np.random.default_rng(5000 + seed)
+    dtype = _DTYPES[int(r.integers(3))]
+    e = 4 if dtype == torch.float32 else 8
+    n_mod = int(r.integers(2, 5))
+    K = e * int(r.integers(1, 513))
+    outs = [e * int(r.integers(1, 513)) for _ in range(n_mod)]
+    M = int(r.choice([1, 1, 2, 9]))
+    rows = int(r.integers(1, max(2, 2048 // M)))
+    max_rank = int(r.choice([16, 32, 64]))
+    n_ad = int(r.integers(1, 9))
+    k_splits = int(r.choice([1, 2, 4, 8]))
+    mods = [f"m{i}" for i in range(n_mod)]
+    _announce(test="sweep_stacked", seed=seed, dtype=dtype, K=K, outs=outs, M=M, rows=rows, max_rank=max_rank,
+              adapters=n_ad, k_splits=k_splits)
+    g = torch.Generator().manual_seed(seed)
+    adapters = {}
+    for i in range(n_ad):
+        layers = {}
+        for m, n in zip(mods, outs):
+            rk = int(r.integers(0, max_rank + 1))
+            if rk:
+                layers[m] = peft_layer(g, K, n, rk, 2.0 * rk)
+        adapters[f"a{i:02d}"] = layers or {"other": peft_layer(g, 8, 8, 2, 4.0)}
+    shapes = dict({m: (K, n) for m, n in zip(mods, outs)}, other=(8, 8))
+    cache = make_cache(adapters, shapes, len(adapters), max_rank, gpu, dtype)
+    names = list(adapters) + ["__base__"]
+    ids = [names[i] for i in torch.randint(0, len(names), (rows,), generator=g).tolist()]
+    row_slot = cache.ensure_resident(ids)
+    seq = torch.randint(0, M + 2, (rows,), generator=g, dtype=torch.int32)
+    x = torch.randn(rows, M, K, generator=g).to(dtype)
+    bases = [torch.randn(rows, M, n, generator=g).to(dtype) for n in outs]
+    slots = row_slot.cpu()
+    wants, untouched = [], []
+    for m, b0 in zip(mods, bases):
+        A, B, rk, sc = oracle_slot_tensors(cache, adapters, m, dtype)
+        wants.append(reference_forward(x, b0, seq, slots, A, B, rk, sc))
+        u = torch.ones(rows, M, dtype=torch.bool)
+        for b in range(rows):
+            if int(rk[int(slots[b])]) > 0:
+                u[b, : min(int(seq[b]), M)] = False
+        untouched.append(u)
+    dx, dseq = x.to(gpu).view(-1, K), seq.to(gpu)
+    parity = CountedParity(dtype, f"stacked sweep seed {seed}")
+
+    def check(ys, path):
+        for m, y, w, b0, u in zip(mods, ys, wants, bases, untouched):
+            got = y.cpu().view(rows, M, -1)
+            parity.check(got, w, b0, f" [{path} {m}]")
+            assert torch.equal(got[u], b0[u]), f"{path} {m}: untouched rows were written"
+
+    for gt in (16, 64):
+        plan = sgmv.SgmvPlan(row_slot, dseq, M, cache.num_slots, group_tokens=gt)
+        _announce(path="stacked split", group_tokens=gt)
+        pair = [b.to(gpu).view(-1, b.shape[-1]) for b in bases]
+        res = sgmv.lora_shrink_stacked(dx, cache, mods, plan, k_splits=k_splits)
+        sgmv.lora_expand_stacked(res, pair, cache, mods)
+        check(pair, f"split gt{gt}")
+        if cache.rank8_cap <= sgmv.FUSED_MAX_RANK:
+            _announce(path="stacked fused", group_tokens=gt)
+            ys = [b.to(gpu).view(-1, b.shape[-1]) for b in bases]
+            sgmv.lora_fused_stacked(dx, ys, cache, mods, plan)
+            check(ys, f"fused gt{gt}")
+        if sgmv.decode_ok(plan):
+            _announce(path="stacked decode", group_tokens=gt)
+            ys = [b.to(gpu).view(-1, b.shape[-1]) for b in bases]
+            sgmv.lora_decode_stacked(dx, ys, cache, mods, plan, k_splits=k_splits)
+            torch.cuda.synchronize()
+            for m, a, b in zip(mods, ys, pair):
+                assert torch.equal(a, b), f"decode launch differs from the split pair ({m})"
+            assert not sgmv.decode_waits_timed_out(gpu)
+    parity.finish()
