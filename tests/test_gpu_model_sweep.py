@@ -95,3 +95,47 @@ def test_random_models_every_layer_against_the_oracle(gpu, seed):
     for b, aid in enumerate(adapter_ids):
         if aid == "__base__":
             assert torch.equal(first[b][valid[b]], plain[b][valid[b]]), b
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_churn_every_layer_against_the_oracle(gpu, seed):
+    """A catalog larger than the slots through random batches: each step loads the adapters it lacks into
+    free or evicted slots (spare regions on or off, so loads copy beside the readers or rewrite a slot in
+    place after them), and every wrapped Linear of every step is checked against the oracle on the
+    cache's slot assignment at that step."""
+    r = np.random.default_rng(8000 + seed)
+    dtype = (torch.bfloat16, torch.float16)[int(r.integers(2))]
+    slots = int(r.integers(2, 6))
+    catalog = int(r.integers(slots + 1, 3 * slots + 2))
+    max_rank = int(r.choice([8, 16]))
+    spare = int(r.choice([0, 1 << 30]))
+    steps = 6
+    _announce(test="churn_sweep", seed=seed, dtype=dtype, slots=slots, catalog=catalog, max_rank=max_rank,
+              spare_bytes=spare)
+    base = _llama(seed, dtype, gpu, 128, 256)
+    pm = PolyLoraModel(copy.deepcopy(base), PolyLoraConfig(target_modules=LLAMA_TARGETS, max_gpu_adapters=slots,
+                                                           max_rank=max_rank, spare_region_bytes=spare)).eval()
+    shapes = _shapes(pm)
+    g = torch.Generator().manual_seed(seed)
+    ads = {}
+    for i in range(catalog):
+        weights = {}
+        for m in shapes:
+            if r.random() < 0.85:
+                weights.update(_peft.make_lora_weights(g, shapes, int(r.integers(1, max_rank + 1)), std=0.05,
+                                                       modules=[m]))
+        weights = weights or _peft.make_lora_weights(g, shapes, max_rank, std=0.05, modules=[next(iter(shapes))])
+        ads[f"c{i:02d}"] = (weights, 2.0 * max_rank)
+        pm.adapter_store.add_adapter_from_peft_state_dict(f"c{i:02d}", _peft.state_dict(weights),
+                                                          pm.target_module_names, 2.0 * max_rank)
+    names = list(ads)
+    with torch.inference_mode(), _per_layer_check(pm, ads, dtype, f"churn sweep seed {seed}") as checked:
+        for step in range(steps):
+            B = int(r.integers(1, 9))
+            S = int(r.choice([1, 1, 5, 40]))
+            pick = r.choice(len(names), size=int(r.integers(1, slots + 1)), replace=False)
+            adapter_ids = [names[int(pick[int(i)])] if r.random() > 0.15 else "__base__"
+                           for i in r.integers(0, len(pick), B)]
+            ids = torch.randint(0, 211, (B, S), generator=g).to(gpu)
+            pm(input_ids=ids, adapter_ids=adapter_ids)
+    assert checked.calls == steps * len(pm.target_module_names)
