@@ -537,3 +537,41 @@ def test_cache_moved_under_inference_mode_still_loads_outside_it():
     assert int(cache.ranks["enc.q_proj"][slot]) == 2
     for mod, (a, b) in w.items():
         assert torch.equal(cache.A[mod][slot, :, :2], a.t().to(torch.bfloat16))
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="fake device pointers: run only where no GPU can be reached")
+def test_decode_launch_refuses_bad_arguments_before_any_launch():
+    """pl_lora_decode_stacked checks its plan geometry, workspaces, hand-off counters and spin limit on the
+    host and returns PL_ERR_ARG with a message before any HIP call; each call below breaks one rule."""
+    import ctypes
+
+    lib = _native.load()
+    fake = [ctypes.c_void_p(4096 * (i + 1)) for i in range(8)]  # 16-byte aligned, never dereferenced
+    dt, K, n, cap, rows, ldt, splits = _native.PL_BF16, 1024, 2, 40, 256, 64, 4
+    ws_bytes = int(lib.pl_shrink_workspace_bytes(dt, K, splits, 16, rows, ldt))
+    ints = int(lib.pl_decode_counter_ints(cap, n))
+    assert ws_bytes > 0 and ints > 0
+
+    def call(gt=16, ldt_=ldt, ws=(fake[5], fake[6]), counters=fake[7], counter_ints=ints, spin=1 << 16):
+        mods = (ctypes.c_int32 * n)(0, 1)
+        wsp = (ctypes.c_void_p * n)(*ws)
+        yp = (ctypes.c_void_p * n)(fake[3], fake[4])
+        ldy = (ctypes.c_int64 * n)(512, 512)
+        nn = (ctypes.c_int32 * n)(512, 512)
+        return lib.pl_lora_decode_stacked(dt, fake[0], K, K, fake[1], fake[2], 2, n, mods, wsp, fake[1], fake[2],
+                                          fake[1], cap, gt, ws_bytes, ldt_, rows, splits, yp, ldy, nn,
+                                          _native.PL_EPI_FALLBACK, counters, counter_ints, spin, None)
+
+    cases = [
+        (dict(gt=64), b"16-token groups"),
+        (dict(ldt_=40), b"multiple of 32"),
+        (dict(ws=(fake[5], fake[5])), b"its own workspace"),
+        (dict(counters=None), b"null or misaligned hand-off counters"),
+        (dict(counters=ctypes.c_void_p(4096 * 8 + 2)), b"null or misaligned hand-off counters"),
+        (dict(counter_ints=ints - 1), b"needed"),
+        (dict(spin=0), b"spin_limit"),
+    ]
+    for kw, msg in cases:
+        st = call(**kw)
+        assert st == 1, (kw, st, lib.pl_last_error())
+        assert msg in lib.pl_last_error(), (kw, lib.pl_last_error())
