@@ -575,3 +575,29 @@ def test_decode_launch_refuses_bad_arguments_before_any_launch():
         st = call(**kw)
         assert st == 1, (kw, st, lib.pl_last_error())
         assert msg in lib.pl_last_error(), (kw, lib.pl_last_error())
+
+
+def test_operator_part_sizes_depend_only_on_what_their_keys_hold():
+    """The kept operator parts are looked up by keys that leave some sizes out, so their byte counts must not
+    depend on those: the weights part depends on the weights' shape and dtype only (not on the batch), and
+    the plan part on the batch geometry and adapter count only (not on K, n, dtype or which call), so one
+    plan serves the shrink and the expand of every Linear of a forward.  Shapes the MFMA path declines
+    (ranks above 64, K or N not whole 16-byte chunks) report 0 bytes."""
+    lib = _native.load()
+
+    def size(dt, which, B, M, K, n, S, part):
+        return int(lib.pl_sgmv_ref_part_bytes(dt, which, B, M, K, n, S, part))
+
+    bf, f32 = _native.PL_BF16, _native.PL_F32
+    for which, (K, n) in ((0, (4096, 64)), (1, (64, 4096)), (0, (14336, 16)), (1, (32, 1024))):
+        w = {size(dt, which, B, M, K, n, 65, 1) for dt in (bf,) for B, M in ((1, 1), (256, 1), (32, 1024), (8192, 1), (7, 33))}
+        assert len(w) == 1 and w.pop() > 0, (which, K, n)
+    for B, M, S in ((256, 1, 65), (32, 1024, 9), (4096, 1, 17), (3, 7, 2)):
+        p = {size(dt, which, B, M, K, n, S, 0) for dt in (bf, f32) for which, (K, n) in
+             ((0, (4096, 64)), (1, (64, 4096)), (0, (1024, 8)), (1, (16, 768)))}
+        assert len(p) == 1 and p.pop() > 0, (B, M, S)
+    assert size(bf, 0, 256, 1, 4096, 128, 65, 0) == 0  # n_max above 64: the row kernels
+    assert size(bf, 0, 256, 1, 4100, 64, 65, 1) == 0  # K not whole 16-byte chunks
+    assert size(bf, 1, 256, 1, 64, 1001, 65, 0) == 0  # N not whole 16-byte chunks
+    # the expand reads the caller's intermediate directly: no scratch; the shrink's split planes need some
+    assert size(bf, 1, 256, 1, 64, 1000, 65, 2) == 0 and size(bf, 0, 256, 1, 4096, 64, 65, 2) > 0
