@@ -12,7 +12,7 @@ import torch
 
 from oracle.lora import reference_forward
 from polylora_amd import _native
-from tests._util import make_cache, oracle_slot_tensors, peft_layer, tol_for
+from tests._util import CountedParity, make_cache, oracle_slot_tensors, peft_layer, tol_for
 
 pytestmark = pytest.mark.gpu
 
@@ -22,6 +22,7 @@ K, N = 512, 384
 def _existing(lib, dt, x, y, cache, row_slot, seq, rows, row_len, group_tokens, k_splits, stream):
     """pl_plan_build + pl_lora_apply with torch-allocated plan and workspace."""
     dev = x.device
+    K, N = int(x.shape[1]), int(y.shape[1])
     cap = int(lib.pl_plan_group_capacity(rows, row_len, cache.num_slots, group_tokens))
     T = max(1, rows * row_len)
     tok = torch.empty(T, dtype=torch.int32, device=dev)
@@ -147,3 +148,53 @@ def test_noalloc_just_under_its_scratch_limit(gpu):
                                    cache.table.data_ptr(), 1, 0, x.data_ptr(), x.data_ptr(), rows + 1, row_len,
                                    cache.num_slots, gt, cache.rank8_cap, ks, 0, stream)
     assert st == _native.PL_ERR_LIMIT
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_noalloc_random_shapes_equal_the_existing_entry_points(gpu, seed):
+    """Seeded random dtype, K, N, ranks, batch geometry, group size and split count, two calls in a row (the
+    second smaller), each bit for bit against pl_plan_build + pl_lora_apply and within tolerance of the oracle."""
+    import numpy as np
+
+    r = np.random.default_rng(9000 + seed)
+    dtype = (torch.bfloat16, torch.float16, torch.float32)[int(r.integers(3))]
+    e = 4 if dtype == torch.float32 else 8
+    k, n = e * int(r.integers(1, 257)), e * int(r.integers(1, 257))
+    max_rank = int(r.choice([8, 16, 32, 64]))
+    ranks = [int(v) for v in r.integers(1, max_rank + 1, int(r.integers(1, 9)))]
+    group_tokens = int(r.choice([16, 64]))
+    k_splits = int(r.choice([1, 2, 3, 4, 8]))
+    print(f"case: noalloc sweep seed={seed} dtype={dtype} K={k} N={n} ranks={ranks} group_tokens={group_tokens} "
+          f"k_splits={k_splits}", flush=True)
+    lib = _native.load()
+    dt = _native.dtype_code(dtype)
+    g = torch.Generator().manual_seed(seed)
+    adapters = {f"n{i}": {"m": peft_layer(g, k, n, rk, 2.0 * rk)} for i, rk in enumerate(ranks)}
+    cache = make_cache(adapters, {"m": (k, n)}, len(adapters), max_rank, gpu, dtype)
+    ids_pool = ["__base__", *adapters]
+    stream = _native.current_stream_handle(gpu)
+    parity = CountedParity(dtype, f"noalloc sweep seed {seed}")
+    row_len = int(r.choice([1, 1, 3, 40]))
+    rows = int(r.integers(2, max(3, 2048 // row_len)))
+    for rows_i in (rows, max(1, rows // 3)):
+        ids = [ids_pool[int(i)] for i in r.integers(0, len(ids_pool), rows_i)]
+        row_slot = cache.ensure_resident(ids)
+        seq_cpu = torch.randint(0, row_len + 2, (rows_i,), generator=g, dtype=torch.int32)
+        seq = seq_cpu.to(gpu)
+        x_cpu = torch.randn(rows_i * row_len, k, generator=g).to(dtype)
+        base_cpu = torch.randn(rows_i * row_len, n, generator=g).to(dtype)
+        x, y_new, y_old = x_cpu.to(gpu), base_cpu.to(gpu), base_cpu.to(gpu)
+        torch.cuda.synchronize()
+        st = lib.pl_lora_apply_noalloc(dt, x.data_ptr(), x.stride(0), k, y_new.data_ptr(), y_new.stride(0), n,
+                                       cache.arena.data_ptr(), cache.table.data_ptr(), len(cache.module_index), 0,
+                                       row_slot.data_ptr(), seq.data_ptr(), rows_i, row_len, cache.num_slots,
+                                       group_tokens, cache.rank8_cap, k_splits, _native.PL_EPI_FALLBACK, stream)
+        _native.check(st, "pl_lora_apply_noalloc")
+        torch.cuda.synchronize()
+        _existing(lib, dt, x, y_old, cache, row_slot, seq, rows_i, row_len, group_tokens, k_splits, stream)
+        assert torch.equal(y_new, y_old), (rows_i, row_len)
+        A, B, rk, sc = oracle_slot_tensors(cache, adapters, "m", dtype)
+        want = reference_forward(x_cpu.view(rows_i, row_len, k), base_cpu.view(rows_i, row_len, n), seq_cpu,
+                                 row_slot.cpu().long(), A, B, rk, sc)
+        parity.check(y_new.cpu().view(rows_i, row_len, n), want, base_cpu.view(rows_i, row_len, n))
+    parity.finish()
