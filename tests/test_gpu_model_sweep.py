@@ -139,3 +139,45 @@ def test_random_churn_every_layer_against_the_oracle(gpu, seed):
             ids = torch.randint(0, 211, (B, S), generator=g).to(gpu)
             pm(input_ids=ids, adapter_ids=adapter_ids)
     assert checked.calls == steps * len(pm.target_module_names)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_debertas_every_layer_against_the_oracle(gpu, seed):
+    """Tiny fp32 DeBERTas (the reference tests' fixture shape), relative attention on or off (with it the
+    shared relative-position projections reach the wrapped Linears as [1, M, K] inputs and take row 0's
+    adapter, layers.py:91-97), random target subsets, adapters over random modules and ranks, right-padded
+    batches; every wrapped Linear against the oracle at fp32 tolerance."""
+    from tests.test_gpu_model import TARGETS
+
+    r = np.random.default_rng(9500 + seed)
+    rel = bool(r.integers(2))
+    k = int(r.integers(1, len(TARGETS) + 1))
+    targets = sorted(r.choice(TARGETS, size=k, replace=False).tolist(), key=TARGETS.index)
+    max_rank = int(r.choice([4, 8, 16]))
+    n_ad = int(r.integers(1, 5))
+    B, S = int(r.integers(1, 9)), int(r.integers(2, 33))
+    _announce(test="deberta_sweep", seed=seed, relative_attention=rel, targets=targets, max_rank=max_rank,
+              adapters=n_ad, B=B, S=S)
+    base = _peft.tiny_deberta(seed, relative_attention=rel).to(gpu)
+    pm = PolyLoraModel(copy.deepcopy(base), PolyLoraConfig(target_modules=targets, max_gpu_adapters=n_ad,
+                                                           max_rank=max_rank)).eval()
+    shapes = _shapes(pm)
+    names = list(shapes)
+    g = torch.Generator().manual_seed(seed)
+    ads = {}
+    for i in range(n_ad):
+        mods = [m for m in names if r.random() < 0.75] or [names[-1]]
+        weights = {}
+        for m in mods:
+            weights.update(_peft.make_lora_weights(g, shapes, int(r.integers(1, max_rank + 1)), std=0.05, modules=[m]))
+        ads[f"d{i}"] = (weights, 2.0 * max_rank)
+        pm.adapter_store.add_adapter_from_peft_state_dict(f"d{i}", _peft.state_dict(weights), pm.target_module_names,
+                                                          2.0 * max_rank)
+    pool = ["__base__", *ads]
+    adapter_ids = [pool[int(i)] for i in r.integers(0, len(pool), B)]
+    ids = torch.randint(1, 90, (B, S), generator=g).to(gpu)
+    lens = torch.randint(1, S + 1, (B,), generator=g)
+    mask = (torch.arange(S)[None, :] < lens[:, None]).long().to(gpu)
+    with torch.inference_mode(), _per_layer_check(pm, ads, torch.float32, f"deberta sweep seed {seed}") as checked:
+        pm(input_ids=ids, attention_mask=mask, adapter_ids=adapter_ids)
+    assert checked.calls >= len(pm.target_module_names), (checked.calls, len(pm.target_module_names))
