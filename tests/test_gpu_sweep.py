@@ -208,3 +208,64 @@ def test_random_sibling_modules_in_one_launch_against_the_oracle(gpu, seed):
                 assert torch.equal(a, b), f"decode launch differs from the split pair ({m})"
             assert not sgmv.decode_waits_timed_out(gpu)
     parity.finish()
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_operator_calls_against_the_oracle(gpu, seed):
+    """The reference operator API (sgmv_lora_a_fwd / sgmv_lora_b_fwd) on seeded random reference-layout
+    tensors: stack_num 1..3, int32 or int64 indices (some out of range, which the kernels skip), rows whose
+    seq_len exceeds M, rank caps up to 96 (above 64 the row kernels run), base_output given or not.  Each
+    call is made twice (the second on the kept parts), then again after an in-place write to the weights
+    (which must rebuild what was kept); every result against the oracle."""
+    r = np.random.default_rng(6000 + seed)
+    dtype = _DTYPES[int(r.integers(3))]
+    e = 4 if dtype == torch.float32 else 8
+    stack = int(r.integers(1, 4))
+    R = int(r.choice([4, 8, 16, 32, 64, 96 // stack]))  # R * stack above 64: the row kernels
+    S = int(r.integers(2, 20))
+    M = int(r.choice([1, 1, 4, 33]))
+    Bt = int(r.integers(1, max(2, 1536 // M)))
+    K, N = e * int(r.integers(1, 385)), e * int(r.integers(1, 385))
+    idx_dtype = (torch.int32, torch.int64)[int(r.integers(2))]
+    with_base = bool(r.integers(2))
+    _announce(test="sweep_operator", seed=seed, dtype=dtype, stack=stack, R=R, S=S, M=M, Bt=Bt, K=K, N=N,
+              idx=idx_dtype, with_base=with_base)
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(Bt, M, K, generator=g).to(dtype)
+    wa = (torch.randn(S, K, R * stack, generator=g) * 0.05).to(dtype)
+    wb = (torch.randn(S, R, N, generator=g) * 0.05).to(dtype)
+    ranks = torch.randint(0, R + 1, (S,), generator=g, dtype=torch.int32)
+    ranks[0] = 0
+    scal = torch.rand(S, generator=g) * 4
+    seq = torch.randint(0, M + 3, (Bt,), generator=g, dtype=torch.int32)
+    widx = torch.randint(-1, S + 1, (Bt,), generator=g).to(idx_dtype)  # -1 and S: out of range, skipped
+    ok = (widx >= 0) & (widx < S)
+    base = torch.randn(Bt, M, N, generator=g).to(dtype)
+    dx, dwa, dwb, dranks, dscal, dseq, dwidx = (t.to(gpu) for t in (x, wa, wb, ranks, scal, seq, widx))
+    tol = tol_for(dtype)
+    refop_cache.configure()
+    try:
+        for phase in range(2):
+            if phase == 1:  # an in-place write, as the reference cache's slot loads make
+                wa[1:] *= 0.5
+                wb[1:] *= 2.0
+                dwa.mul_(torch.tensor([1.0] + [0.5] * (S - 1), dtype=dtype, device=gpu).view(S, 1, 1))
+                dwb.mul_(torch.tensor([1.0] + [2.0] * (S - 1), dtype=dtype, device=gpu).view(S, 1, 1))
+                torch.testing.assert_close(dwa.cpu(), wa, rtol=0, atol=0)
+            # the oracle takes the rows whose index is in range; the kernels leave the others untouched
+            exp_tmp, valid = sgmv_shrink_reference(x[ok], wa, seq[ok], widx[ok], ranks, stack)
+            for call in range(2):
+                tmp = sgmv.sgmv_lora_a_fwd(dx, dwa, dseq, dwidx, dranks, stack).cpu()
+                torch.testing.assert_close(tmp[ok][valid], exp_tmp[valid], **tol)
+            xb = torch.zeros(Bt, M, R, dtype=dtype)
+            xb[ok] = exp_tmp[:, :, :R]
+            start = base if with_base else torch.zeros_like(base)
+            exp_out = start.clone()
+            exp_out[ok] = sgmv_expand_reference(xb[ok], wb, seq[ok], widx[ok], ranks, scal, start[ok])
+            for call in range(2):
+                out = sgmv.sgmv_lora_b_fwd(xb.to(gpu), dwb, dseq, dwidx, dranks, dscal,
+                                           base.to(gpu) if with_base else None).cpu()
+                torch.testing.assert_close(out, exp_out, **tol)
+                assert torch.equal(out[~ok], start[~ok])
+    finally:
+        refop_cache.configure()
