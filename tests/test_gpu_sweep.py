@@ -8,9 +8,12 @@ then runs the split shrink + expand (16- and 64-token groups, the split count
 drawn too), the fused kernel (where its rank limit allows), the one-launch
 decode path (bit for bit against the split pair on the same plan and split
 count), the row kernels, and the operator API's sgmv_lora_a_fwd /
-sgmv_lora_b_fwd on the reference slot layout.  Every output is checked
-against the oracle at the dtype's tolerance (tests/_util.py: CountedParity for
-outputs that add into a base, the plain tolerance for the intermediate).
+sgmv_lora_b_fwd on the reference slot layout.  Further cases run 2..4 sibling
+modules through the stacked launches, and the operator API alone with its
+stack_num, index types, out-of-range indices and kept-part rebuilds.  Every
+output is checked against the oracle at the dtype's tolerance (tests/_util.py:
+CountedParity for outputs that add into a base, the plain tolerance for the
+intermediate).
 
 Reference: the fallback of layers.py:112-134 (reference_forward), the
 operator signatures of sgmv.py:141-175 and :278-328.
