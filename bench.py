@@ -1803,11 +1803,11 @@ def launch_profile(args) -> int:
             leaf = name.rsplit(".", 1)[-1]
             # one host call pair issues 2 dispatches once the plan and packed weights are kept (the first
             # two layers' pl_refop_prep dispatches fall in the first warm-up pass): the split shrink,
-            # whose last K split of each tile writes the intermediate, and the fused kernel's expand
-            # phase; the first entry issues both
+            # whose last K split of each tile writes the intermediate, and the short expand reading
+            # that intermediate; the first entry issues both
             seq += [(f"{leaf} shrink: split shrink + finish", "shrink", pair,
                      launch_bytes(pm, [name], "shrink", ids, [1] * len(ids))),
-                    (f"{leaf} expand: fused phase", "expand", lambda: None,
+                    (f"{leaf} expand: short expand", "expand", lambda: None,
                      launch_bytes(pm, [name], "expand", ids, [1] * len(ids)))]
         desc = ("reference operator API (sgmv_lora_a_fwd + sgmv_lora_b_fwd) on one Llama-3-8B-shaped decode "
                 "layer's 7 Linears, 256 rows x 1 token, reference layout [65, K, 64] / [65, 64, N] bf16, 64 "

@@ -221,6 +221,16 @@ int pl_shrink_finish_launch(int32_t dtype, const void* x, int64_t ldx, int32_t K
                             int32_t group_tokens, void* ws, int64_t ws_bytes, int32_t ldt,
                             int64_t tmp_rows, int32_t k_splits, int32_t* counters,
                             int64_t counter_ints, void* out, int32_t n_max, void* stream);
+
+// The short expand (16-token groups) staging the caller's model-dtype
+// intermediate inter[token][ldi] instead of split planes, for the operator
+// API's expand: one workgroup per (group, 256- or 128-column chunk).  Returns
+// PL_REFOP_DECLINED for arguments it does not take (the caller then runs
+// another kernel); ranks in the slot table must not exceed ldi.
+int pl_expand_inter_launch(int32_t dtype, const void* inter, int64_t ldi, const void* arena,
+                           const pl_slot_entry* table, const int32_t* tok, const pl_group* groups,
+                           const int32_t* meta, int64_t group_cap, int32_t group_tokens, void* y,
+                           int64_t ldy, int32_t N, int32_t ldt, int32_t epilogue, void* stream);
 int pl_refop_shrink(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t K, const void* w,
                     int64_t w_s0, int64_t w_s1, int64_t w_s2, int32_t num_adapters,
                     int32_t n_max, const int32_t* seq_lens, const int32_t* weight_indices,

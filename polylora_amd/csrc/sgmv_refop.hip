@@ -40,15 +40,18 @@
 //      segments (at least 1024 rows and 64 per adapter)
 //      one launch of the fused kernel's shrink phase (pl_fused_phase)
 //      instead reduces each 16-token tile in LDS and writes T(sum) straight
-//      into out.  expand: one launch of the fused kernel's expand phase
-//      stages the caller's model-dtype intermediate in LDS (zero past each
-//      row's rank) and adds T(scale * sum) into the output in the
-//      reference's rounding order, the columns cut into slices so that the
-//      launch has about 1024 workgroups.  (On the Llama-3-8B decode layer,
-//      256 rows over 64 adapters, that phase took 9.3 us per module against
-//      12.1 us for a gather launch and the split expand; the fused shrink
+//      into out.  expand: one launch that stages the caller's model-dtype
+//      intermediate in LDS (zero past each row's rank) and adds
+//      T(scale * sum) into the output in the reference's rounding order:
+//      where the shrink took the split kernels (16-token groups), the short
+//      expand reading the intermediate by token (pl_expand_inter_launch);
+//      with long segments, the fused kernel's expand phase, its columns cut
+//      into slices so that the launch has about 1024 workgroups.  (On the
+//      Llama-3-8B decode layer, 256 rows over 64 adapters, the fused shrink
 //      phase took 18.8 us against 13.6 us for the split shrink and its
-//      finish, so short segments keep the split shrink.)
+//      finish, so short segments keep the split shrink; the short expand
+//      there takes 4.5-13.2 us per module against 5.8-14.3 us for the fused
+//      expand phase.)
 //
 // The plan gives every row with an adapter index in range its slot, rank 0
 // or not: every kernel of step 2 returns at once for a slot whose table
@@ -577,6 +580,18 @@ int pl_refop_expand(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t 
   pl_group* groups = reinterpret_cast<pl_group*>(pp + L.groups);
   int32_t* tok = reinterpret_cast<int32_t*>(pp + L.tok);
   const pl_slot_entry* table = reinterpret_cast<const pl_slot_entry*>(wp + L.table);
+  // Few tokens per adapter (the shrink took the split kernels) with 16-token
+  // groups: the short expand staging the caller's intermediate, one workgroup
+  // per group and 256-column chunk (decode layer: 133.5 -> 125.5 us of
+  // kernels for its 7 pairs).  Long segments keep the fused kernel's expand
+  // phase, whose non-temporal y stores leave no dirty lines behind (the short
+  // expand there: 15.9 -> 18.4 us, and the next call's shrink 10.3 -> 12.3 us);
+  // so do 64-token groups and calls the short expand declines.
+  if (L.group_tokens == PL_GROUP_TOKENS_SHORT && !refop_fused(L, num_adapters, k_max)) {
+    st = pl_expand_inter_launch(dtype, x, k_max, wp + L.arena, table, tok, groups, meta, L.group_cap,
+                                L.group_tokens, out, N, N, L.ldt, PL_EPI_TRITON, stream);
+    if (st != PL_REFOP_DECLINED) return st;
+  }
   return pl_fused_phase(PL_FUSED_EXPAND, dtype, x, k_max, k_max, out, N, N, wp + L.arena, table,
                         L.ldt, tok, groups, meta, L.group_cap, L.group_tokens,
                         refop_expand_slices(L, N), PL_EPI_TRITON, stream);

@@ -92,6 +92,8 @@ struct pl_expand_args {
   void* y[kMaxJobs];              // its output
   int64_t ldy[kMaxJobs];
   int32_t N[kMaxJobs];
+  const void* inter;  // the caller's model-dtype intermediate [tokens][ldi] (pl_expand_inter_launch)
+  int64_t ldi;
 };
 
 // Columns of y one expand wave owns: 128 bytes of each row (64 for 2-byte
@@ -594,7 +596,11 @@ __global__ __launch_bounds__(256, 2) void pl_shrink_long(pl_shrink_args a) {
   }
 }
 
-template <int DT, int PMAX, int RB>
+// INTER: the intermediate is the caller's model-dtype tensor a.inter, row
+// (token) stride a.ldi, staged as it is (it already holds T(x·A)), instead
+// of the sum of the split planes; otherwise the same work, the same MFMA
+// order and the same epilogue.
+template <int DT, int PMAX, int RB, bool INTER = false>
 __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   typedef typename pl_traits<DT>::T T;
   typedef typename pl_traits<DT>::T4 T4;
@@ -665,9 +671,13 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
   const int sp = tid / kStageLanes;
   const int sq = (tid % kStageLanes) * 4;
   const float* srow = a.planes[job] + (int64_t)(grp.start + (sp < len ? sp : 0)) * a.ldt;
+  // INTER: the stager's row is token tok[grp.start + sp] of the intermediate
+  int st_tok = 0;
+  if constexpr (INTER) st_tok = a.tok[grp.start + min(sp, len - 1)];
 
   pl_u32x4 bf[kSteps][S::kCT];
   pl_u32x4 pv[PMAX];
+  T4 iv;
   // B rows n0 + ct*16 + li and the planes of ranks rb .. rb+63
   auto load_block = [&](int rb) {
 #pragma unroll
@@ -688,11 +698,19 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
     // only the first k_splits are summed
     if (stager) {
       const int jr = rb + sq;
-      const bool sok = sp < len && jr < rank;
-      const float* sbase = srow + jr;
+      if constexpr (INTER) {
+        // four elements of the token's row (the row stride need not keep
+        // them 8-byte aligned); ranks past the slot's rank read as zeros
+        const T* ip = reinterpret_cast<const T*>(a.inter) + (int64_t)st_tok * a.ldi + jr;
 #pragma unroll
-      for (int q = 0; q < PMAX; ++q)
-        pv[q] = pl_ld16_or0(sbase + (int64_t)min(q, a.k_splits - 1) * a.plane, sok);
+        for (int i = 0; i < 4; ++i) iv[i] = (sp < len && jr + i < rank) ? ip[i] : (T)0.f;
+      } else {
+        const bool sok = sp < len && jr < rank;
+        const float* sbase = srow + jr;
+#pragma unroll
+        for (int q = 0; q < PMAX; ++q)
+          pv[q] = pl_ld16_or0(sbase + (int64_t)min(q, a.k_splits - 1) * a.plane, sok);
+      }
     }
   };
 
@@ -707,13 +725,17 @@ __global__ __launch_bounds__(256, 2) void pl_expand_short(pl_expand_args a) {
     if (stager) {
       const int jr = rb + sq;
       const bool sok = sp < len && jr < rank;
-      pl_f32x4 sum = __builtin_bit_cast(pl_f32x4, pv[0]);
-#pragma unroll
-      for (int q = 1; q < PMAX; ++q)
-        if (q < a.k_splits) sum += __builtin_bit_cast(pl_f32x4, pv[q]);
       T4 tv;
+      if constexpr (INTER) {
+        tv = iv;
+      } else {
+        pl_f32x4 sum = __builtin_bit_cast(pl_f32x4, pv[0]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) tv[i] = (T)((sok && jr + i < rank) ? sum[i] : 0.f);
+        for (int q = 1; q < PMAX; ++q)
+          if (q < a.k_splits) sum += __builtin_bit_cast(pl_f32x4, pv[q]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tv[i] = (T)((sok && jr + i < rank) ? sum[i] : 0.f);
+      }
       *reinterpret_cast<T4*>(tt + sp * kTRow + sq) = tv;
     }
     __syncthreads();
@@ -1275,6 +1297,8 @@ int prepare_expand(pl_expand_args& a, int32_t dtype, void* const* ws, int32_t ld
   a.ldt = ldt;
   a.k_splits = planes;
   a.plane = tmp_rows * ldt;
+  a.inter = nullptr;
+  a.ldi = 0;
   a.arena = reinterpret_cast<const char*>(arena);
   a.table = table;
   a.num_modules = num_modules;
@@ -1375,6 +1399,57 @@ int pl_shrink_finish_launch(int32_t dtype, const void* x, int64_t ldx, int32_t K
     default: launch_shrink_finish<PL_F32>(a, f, grid, s); break;
   }
   return pl_launch_status("pl_sgmv_shrink (finish)");
+}
+
+int pl_expand_inter_launch(int32_t dtype, const void* inter, int64_t ldi, const void* arena,
+                           const pl_slot_entry* table, const int32_t* tok, const pl_group* groups,
+                           const int32_t* meta, int64_t group_cap, int32_t group_tokens, void* y,
+                           int64_t ldy, int32_t N, int32_t ldt, int32_t epilogue, void* stream) {
+  const int E = pl_chunk_elems(dtype);
+  const int es = pl_elem_size(dtype);
+  if (group_tokens != PL_GROUP_TOKENS_SHORT || !inter || !y || !arena || !table || !tok ||
+      !groups || !meta || ldi < 1 || N < 1 || ldy < N || ldt < 1 || group_cap < 1 ||
+      group_cap > ((int64_t)1 << 24) || N % E != 0 || (ldy * es) % 16 != 0 || !aligned16(y) ||
+      !aligned16(arena) || (epilogue != PL_EPI_FALLBACK && epilogue != PL_EPI_TRITON))
+    return PL_REFOP_DECLINED;
+  const int chunk = dtype == PL_F32 ? (int)pl_expand_shape<PL_F32>::kChunk
+                                    : (int)pl_expand_shape<PL_BF16>::kChunk;
+  const int64_t n_chunks = (N + chunk - 1) / chunk;
+  const int64_t grid = group_cap * n_chunks;
+  if (!pl_grid_fits(grid, 256)) return PL_REFOP_DECLINED;
+  pl_expand_args a;
+  a.ldt = ldt;
+  a.k_splits = 1;
+  a.plane = 0;
+  a.arena = reinterpret_cast<const char*>(arena);
+  a.table = table;
+  a.num_modules = 1;
+  a.tok = tok;
+  a.groups = groups;
+  a.meta = meta;
+  a.epilogue = epilogue;
+  a.sub = 1;
+  a.n_jobs = 1;
+  a.n_chunks = (int32_t)n_chunks;
+  for (int j = 0; j < kMaxJobs; ++j) {
+    const bool on = j == 0;
+    a.chunk0[j] = on ? 0 : (int32_t)n_chunks;
+    a.module[j] = 0;
+    a.planes[j] = nullptr;
+    a.y[j] = on ? y : nullptr;
+    a.ldy[j] = on ? ldy : 0;
+    a.N[j] = on ? N : 0;
+  }
+  a.inter = inter;
+  a.ldi = ldi;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 g((unsigned)grid);
+  switch (dtype) {
+    case PL_BF16: hipLaunchKernelGGL((pl_expand_short<PL_BF16, 1, 64, true>), g, dim3(256), 0, s, a); break;
+    case PL_F16: hipLaunchKernelGGL((pl_expand_short<PL_F16, 1, 64, true>), g, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((pl_expand_short<PL_F32, 1, 64, true>), g, dim3(256), 0, s, a); break;
+  }
+  return pl_launch_status("pl_sgmv_lora_b (short expand)");
 }
 
 extern "C" int pl_sgmv_shrink_stacked(int32_t dtype, const void* x, int64_t ldx, int32_t K,
