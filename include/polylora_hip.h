@@ -350,8 +350,9 @@ int64_t pl_sgmv_ref_workspace_bytes(int32_t dtype, int32_t which, int32_t B, int
  * repacks the weights of every adapter some row uses into the slot arena's
  * block layout inside the workspace (reading the reference layout with
  * consecutive lanes on consecutive elements) and builds the device plan
- * that groups the rows by adapter, then the tiled shrink and a finish
- * kernel write out (3 launches,
+ * that groups the rows by adapter, then the tiled shrink writes out, its
+ * last K split of each 16-token tile summing the splits in the same launch
+ * (2 launches; with 64-token groups a finish kernel sums them, 3 launches;
  * no host synchronisation); with long adapter segments (B*M >= 1024 and >=
  * 64 rows per adapter, K <= 16384) one launch of the fused kernel's shrink
  * phase writes out instead (2 launches).  Otherwise, or with a null
@@ -371,9 +372,10 @@ int pl_sgmv_lora_a_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32
  * (updated in place).  Rows with widx outside [0, num_adapters) are
  * skipped.  Workspace and paths as for pl_sgmv_lora_a_ref (which = 1; the
  * MFMA path needs a 16-byte aligned out), except that after the repack +
- * plan launch one launch of the fused kernel's expand phase reads x
- * directly and adds the scaled delta into out, whatever the segment
- * lengths. */
+ * plan launch one launch reads x directly and adds the scaled delta into
+ * out: the short expand (one workgroup per 16-token group and column
+ * chunk) where the shrink would take the split kernels, the fused kernel's
+ * expand phase for long adapter segments or 64-token groups. */
 int pl_sgmv_lora_b_ref(int32_t dtype, const void* x, int32_t B, int32_t M, int32_t k_max,
                        const void* w, int64_t w_s0, int64_t w_s1, int64_t w_s2,
                        int32_t num_adapters, int32_t N,
